@@ -1,0 +1,137 @@
+"""ctypes binding of libflashdp_hip.so (declared in include/flashdp_hip.h).
+
+The library is built in-tree by ``flashdp4review_amd.build``.  There is no
+fallback: if the library is missing, or a tensor is not on a HIP device, the
+call raises.  Status codes map to the exception types the reference raises
+for the same condition (flashdp/core/linear_clip.py:69-73,
+flashdp/core/layernorm_clip.py:207,221): dtype -> KeyError, sizes/arguments ->
+ValueError, everything else -> RuntimeError.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libflashdp_hip.so")
+
+FDP_F32, FDP_F16, FDP_BF16 = 0, 1, 2
+LAYOUT_TN, LAYOUT_NN = 0, 1
+NORM_SUM, NORM_FROB = 0, 1
+WGRAD_NOCLIP = 1
+
+_DTYPE_CODES = {torch.float32: FDP_F32, torch.float16: FDP_F16, torch.bfloat16: FDP_BF16}
+
+_c_i64 = ctypes.c_int64
+_c_int = ctypes.c_int
+_c_f = ctypes.c_float
+_c_p = ctypes.c_void_p
+_c_sz_p = ctypes.POINTER(ctypes.c_size_t)
+
+# Every exported symbol with its (restype, argtypes); tests check this list
+# against include/flashdp_hip.h.
+SIGNATURES = {
+    "fdp_strerror": (ctypes.c_char_p, [_c_int]),
+    "fdp_version": (_c_int, []),
+    "fdp_wgrad_clip_workspace_size": (_c_int, [_c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int,
+                                               _c_sz_p]),
+    "fdp_wgrad_clip": (_c_int, [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+                                _c_i64, _c_i64, _c_int, _c_int, _c_f, _c_f, _c_p, _c_f, _c_p,
+                                _c_f, _c_p, _c_i64, _c_int, _c_p, _c_p, _c_int, _c_p,
+                                ctypes.c_size_t, _c_p]),
+    "fdp_colsum_clip_workspace_size": (_c_int, [_c_i64, _c_i64, _c_i64, _c_int, _c_sz_p]),
+    "fdp_colsum_clip": (_c_int, [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_f, _c_f,
+                                 _c_p, _c_f, _c_p, _c_f, _c_p, _c_int, _c_p, _c_p, _c_p,
+                                 ctypes.c_size_t, _c_p]),
+    "fdp_layernorm_fwd": (_c_int, [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_f, _c_int, _c_int, _c_p,
+                                   _c_p, _c_p, _c_p]),
+    "fdp_layernorm_bwd_clip_workspace_size": (_c_int, [_c_i64, _c_i64, _c_i64, _c_int, _c_sz_p]),
+    "fdp_layernorm_bwd_clip": (_c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64,
+                                        _c_int, _c_int, _c_f, _c_f, _c_p, _c_f, _c_p, _c_p, _c_f,
+                                        _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, ctypes.c_size_t,
+                                        _c_p]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+class FlashDPError(RuntimeError):
+    """A HIP-side failure reported by libflashdp_hip.so."""
+
+
+def lib() -> ctypes.CDLL:
+    """Load (once) and return the HIP library; raises if it was not built."""
+    global _lib
+    if _lib is None:
+        with _lock:
+            if _lib is None:
+                if not os.path.exists(LIB_PATH):
+                    raise RuntimeError(
+                        f"{LIB_PATH} is missing: build it with `python -m flashdp4review_amd.build` "
+                        "(flashdp4review_amd has no CPU fallback)")
+                handle = ctypes.CDLL(LIB_PATH)
+                for name, (res, args) in SIGNATURES.items():
+                    fn = getattr(handle, name)
+                    fn.restype = res
+                    fn.argtypes = args
+                _lib = handle
+    return _lib
+
+
+def check(status: int, what: str) -> None:
+    if status == 0:
+        return
+    msg = f"{what}: {lib().fdp_strerror(status).decode()} (status {status})"
+    if status == 1:
+        raise KeyError(msg)
+    if status in (2, 3, 6):
+        raise ValueError(msg)
+    raise FlashDPError(msg)
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return _DTYPE_CODES[dtype]
+    except KeyError:
+        raise KeyError(f"The type of input mat is not supported: {dtype}") from None
+
+
+def require_hip(*tensors: torch.Tensor | None) -> torch.device:
+    """All tensors must live on one HIP device; returns it."""
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise RuntimeError(
+                "flashdp4review_amd kernels run on the GPU only; got a tensor on "
+                f"{t.device} (there is no CPU fallback)")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} and {t.device}")
+    if dev is None:
+        raise ValueError("no tensor arguments")
+    return dev
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    """Caller-owned workspace from the torch caching allocator (256-byte aligned)."""
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+def size_query(fn, *args) -> int:
+    out = ctypes.c_size_t(0)
+    check(fn(*args, ctypes.byref(out)), fn.__name__)
+    return out.value

@@ -1,0 +1,147 @@
+"""Clipped per-sample product sums on the HIP kernels (fdp_wgrad_clip).
+
+Operator names and argument meanings follow flashdp/core/__init__.py:1-13:
+bmtm_clip (bmtm_clip_loop.py:162-173), bmm_clip (bmm_clip_loop.py:150-162),
+mm_clip (mm_clip_loop.py:127-139), mm_fused (linear_clip.py:64-91) and
+linear_weight_flashdp (linear_clip.py:107-113).  All of them call one entry
+point, ``wgrad_clip``, which never materialises a per-sample gradient.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from .. import _lib
+from .clip_fn import clip_args_of
+from .utils import RuntimeAutoTuner
+
+
+def _inner_contig(t: torch.Tensor) -> torch.Tensor:
+    if t.dim() != 3:
+        raise ValueError(f"expected a 3-D tensor, got shape {tuple(t.shape)}")
+    if t.stride(2) != 1 or (t.shape[1] > 1 and t.stride(1) < t.shape[2]):
+        t = t.contiguous()
+    return t
+
+
+def wgrad_clip(a: torch.Tensor, b: torch.Tensor, C: float = 1.0, clamp_value: float = 1.0, *,
+               layout: str = "tn", clip_args=None, out_scale: float = 1.0,
+               noise: torch.Tensor | None = None, noise_scale: float = 1.0,
+               out_dtype: torch.dtype | None = None, out: torch.Tensor | None = None,
+               return_stats: bool = False, noclip: bool = False):
+    """out = out_scale * sum_b c_b G_b + noise_scale * noise, c_b = clip(||G_b||_F).
+
+    layout "tn": a [B,K,M], b [B,K,N], G_b = a_b^T b_b;
+    layout "nn": a [B,M,K], b [B,K,N], G_b = a_b b_b.
+    ``clip_args`` (tensor [C, clamp] or pair) overrides C / clamp_value.
+    With ``return_stats`` also returns the fp32 per-sample norms and factors.
+    """
+    dev = _lib.require_hip(a, b, noise, out)
+    if a.dtype != b.dtype:
+        raise KeyError(f"operand dtypes differ: {a.dtype} vs {b.dtype}")
+    dt = _lib.dtype_code(a.dtype)
+    a, b = _inner_contig(a), _inner_contig(b)
+    if layout == "tn":
+        Bn, K, M = a.shape
+        lay = _lib.LAYOUT_TN
+    elif layout == "nn":
+        Bn, M, K = a.shape
+        lay = _lib.LAYOUT_NN
+    else:
+        raise ValueError(f"unknown layout {layout!r}")
+    if b.shape[0] != Bn or b.shape[1] != K:
+        raise ValueError(f"operand shapes {tuple(a.shape)} and {tuple(b.shape)} do not match "
+                         f"for layout {layout}")
+    N = b.shape[2]
+    if Bn == 0:
+        raise ValueError("batch size must be at least 1")
+    if out_dtype is None:
+        out_dtype = out.dtype if out is not None else a.dtype
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype, device=dev)
+    elif out.shape != (M, N) or out.stride(1) != 1 or out.dtype != out_dtype:
+        raise ValueError("out must be an [M, N] row-major tensor of out_dtype")
+    odt = _lib.dtype_code(out_dtype)
+    if noise is not None:
+        if noise.shape != (M, N):
+            raise ValueError(f"noise must have shape {(M, N)}, got {tuple(noise.shape)}")
+        noise = noise.to(out_dtype).contiguous()
+    C_, clamp_, cad = clip_args_of(clip_args, dev) if clip_args is not None else (
+        float(C), float(clamp_value), None)
+    norms = factors = None
+    if return_stats:
+        factors = torch.empty(Bn, dtype=torch.float32, device=dev)
+        norms = None if noclip else torch.empty(Bn, dtype=torch.float32, device=dev)
+    flags = _lib.WGRAD_NOCLIP if noclip else 0
+    L = _lib.lib()
+    nbytes = _lib.size_query(L.fdp_wgrad_clip_workspace_size, Bn, K, M, N, dt, flags)
+    ws = _lib.workspace(nbytes, dev)
+    st = L.fdp_wgrad_clip(
+        _lib.ptr(a), _lib.ptr(b), Bn, K, M, N, a.stride(0), a.stride(1), b.stride(0), b.stride(1),
+        lay, dt, ctypes.c_float(C_), ctypes.c_float(clamp_), _lib.ptr(cad),
+        ctypes.c_float(out_scale), _lib.ptr(noise), ctypes.c_float(noise_scale), out.data_ptr(),
+        out.stride(0), odt, _lib.ptr(norms), _lib.ptr(factors), flags, ws.data_ptr(), ws.numel(),
+        _lib.stream_handle(dev))
+    _lib.check(st, "fdp_wgrad_clip")
+    if return_stats:
+        return out, norms, factors
+    return out
+
+
+def bmtm_clip(tensor1: torch.Tensor, tensor2: torch.Tensor, clip_args=None) -> torch.Tensor:
+    """sum_b clip(||t1_b^T t2_b||) t1_b^T t2_b; t1 [B,K,M], t2 [B,K,N] -> [M,N] in t1's dtype."""
+    return wgrad_clip(tensor1, tensor2.to(tensor1.dtype), layout="tn",
+                      clip_args=clip_args if clip_args is not None else (1.0, 1.0))
+
+
+def bmm_clip(tensor1: torch.Tensor, tensor2: torch.Tensor, clip_args=None) -> torch.Tensor:
+    """sum_b clip(||t1_b t2_b||) t1_b t2_b; t1 [B,M,K], t2 [B,K,N] -> [M,N] fp32
+    (the reference accumulates this operator in its fp32 acc dtype, bmm_clip_loop.py:138)."""
+    return wgrad_clip(tensor1, tensor2.to(tensor1.dtype), layout="nn",
+                      clip_args=clip_args if clip_args is not None else (1.0, 1.0),
+                      out_dtype=torch.float32)
+
+
+def mm_clip(mat1: torch.Tensor, mat2: torch.Tensor, clip_args=None) -> torch.Tensor:
+    """sum_k clip(||a_k (x) b_k||) a_k (x) b_k with a_k = mat1[:,k], b_k = mat2[k,:] -> [M,N]:
+    one rank-1 "sample" per k, i.e. the clipped product sum with B=K and K=1."""
+    if mat1.dim() != 2 or mat2.dim() != 2 or mat1.shape[1] != mat2.shape[0]:
+        raise ValueError("mm_clip expects mat1 [M,K] and mat2 [K,N]")
+    a = mat1.t().contiguous().unsqueeze(1)             # [K,1,M]
+    b = mat2.to(mat1.dtype).contiguous().unsqueeze(1)  # [K,1,N]
+    return wgrad_clip(a, b, layout="tn",
+                      clip_args=clip_args if clip_args is not None else (1.0, 1.0))
+
+
+def mm_fused(tensor1: torch.Tensor, tensor2: torch.Tensor) -> torch.Tensor:
+    """Plain product tensor1 @ tensor2 in the fp32 accumulation dtype
+    (flashdp/core/linear_clip.py:64-91): the product sum with one sample and no clip."""
+    if tensor1.dim() < 2 or tensor2.dim() < 2:
+        raise KeyError("The dimensions of input tensors must be at least 2.")
+    if tensor1.shape[-1] != tensor2.shape[0]:
+        raise ValueError("tensor1 last dimension must match tensor2 first dimension")
+    s1, s2 = tensor1.shape, tensor2.shape
+    a = tensor1.reshape(1, -1, s1[-1])
+    b = tensor2.to(tensor1.dtype).reshape(1, s2[0], -1)
+    out = wgrad_clip(a, b, layout="nn", clip_args=(float("inf"), 1.0), noclip=True,
+                     out_dtype=torch.float32)
+    return out.reshape(tuple(s1[:-1]) + tuple(s2[1:]))
+
+
+def linear_weight_flashdp(input: torch.Tensor, grad_output: torch.Tensor, C: float,
+                          clamp_value: float, runtime_tuner: RuntimeAutoTuner | None = None):
+    """sum_b clip(||g_b^T x_b||) g_b^T x_b -> [O, I] in grad_output's dtype
+    (flashdp/core/linear_clip.py:107-113; the tuner argument is accepted only)."""
+    if runtime_tuner is not None:
+        runtime_tuner.choose_function([bmtm_clip])
+    return wgrad_clip(grad_output, input.to(grad_output.dtype), C, clamp_value, layout="tn")
+
+
+def conv1d_weight_flashdp(input: torch.Tensor, grad_output: torch.Tensor, C: float,
+                          clamp_value: float, runtime_tuner: RuntimeAutoTuner | None = None):
+    """sum_b clip(||x_b^T g_b||) x_b^T g_b -> [I, O]
+    (flashdp/core/transformers_conv1d_clip.py:22-28)."""
+    if runtime_tuner is not None:
+        runtime_tuner.choose_function([bmtm_clip])
+    return wgrad_clip(input.to(grad_output.dtype), grad_output, C, clamp_value, layout="tn")

@@ -1,0 +1,101 @@
+"""DPLinear: nn.Linear whose backward clips per-sample weight/bias gradients.
+
+Reference: flashdp/layers/linear.py:11-106.  Backward math (per parameter tensor):
+  dX = g W                                                       (unclipped)
+  dW = (1/B) sum_b clip(||g_b^T x_b||_F) g_b^T x_b + (sigma/sqrt(B)) z_W
+  db = (1/(B*T)) sum_b clip(||g_b||_F) sum_t g_bt  + (sigma/sqrt(B)) z_b
+with clip(n) = min(clamp_value, C/(n + 1e-10)).  dW and db each run as one fused
+HIP call (fdp_wgrad_clip / fdp_colsum_clip): norm, clip, 1/B and noise add
+happen on the device, and grad_output is never modified.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+from torch.autograd.function import Function
+
+from ..core import colsum_clip, wgrad_clip
+from ..core.utils import RuntimeAutoTuner
+from .utils import DPParameter as Parameter
+from .utils import as_btf, draw_noise, noise_std
+
+
+class DPLinear(nn.Linear):
+    def __init__(self, in_features: int, out_features: int, bias: bool = True, device=None,
+                 dtype=None, C: float = 1.0, clamp_value: float = 1.0,
+                 noise_multiplier: float = 1.0, auto_tune: bool = True):
+        # bias may be a bool or (as wrap_with_flashdp_layers passes it) a tensor/None;
+        # False and None both mean "no bias" (the reference keeps a bias for False).
+        use_bias = not (bias is None or bias is False)
+        super().__init__(in_features, out_features, use_bias, device=device, dtype=dtype)
+        factory_kwargs = {"device": device, "dtype": dtype}
+        self.dp = True
+        self.C = C
+        self.clamp_value = clamp_value
+        self.noise_multiplier = noise_multiplier
+        self.runtime_tuner = RuntimeAutoTuner(enable=auto_tune)
+        self.weight = Parameter(torch.empty((out_features, in_features), **factory_kwargs))
+        if use_bias:
+            self.bias = Parameter(torch.empty(out_features, **factory_kwargs))
+        else:
+            self.register_parameter("bias", None)
+        self.reset_parameters()
+        # Optional torch.Generator for the noise draws (z_W first, then z_b).
+        self.noise_generator = None
+        # When True, backward stores per-sample norms / clip factors in last_stats.
+        self.record_stats = False
+        self.last_stats = None
+
+    def forward(self, input: torch.Tensor) -> torch.Tensor:
+        self.runtime_tuner.final_tune()
+        return _DPLinearFunction.apply(input, self.weight, self.bias, self)
+
+
+class _DPLinearFunction(Function):
+    @staticmethod
+    def forward(ctx, input, weight, bias, module):
+        ctx.save_for_backward(input, weight)
+        ctx.has_bias = bias is not None
+        ctx.bias_dtype = bias.dtype if bias is not None else None
+        ctx.cfg = (float(module.C), float(module.clamp_value), float(module.noise_multiplier),
+                   module.noise_generator)
+        ctx.module = module if module.record_stats else None
+        w = weight if weight.dtype == input.dtype else weight.to(input.dtype)
+        b = None if bias is None else (bias if bias.dtype == input.dtype else bias.to(input.dtype))
+        return F.linear(input, w, b)
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        input, weight = ctx.saved_tensors
+        C, clamp_value, sigma, gen = ctx.cfg
+        x3, g3 = as_btf(input), as_btf(grad_output)
+        B, T = x3.shape[0], x3.shape[1]
+        std = noise_std(sigma, B)
+        stats = {} if ctx.module is not None else None
+        grad_input = grad_weight = grad_bias = None
+        if ctx.needs_input_grad[0]:
+            w = weight if weight.dtype == g3.dtype else weight.to(g3.dtype)
+            grad_input = (g3 @ w).reshape(input.shape)
+        if ctx.needs_input_grad[1]:
+            z = draw_noise(weight.shape, weight.dtype, weight.device, gen) if std > 0 else None
+            r = wgrad_clip(g3, x3.to(g3.dtype), C, clamp_value, layout="tn", out_scale=1.0 / B,
+                           noise=z, noise_scale=std, out_dtype=weight.dtype,
+                           return_stats=stats is not None)
+            if stats is not None:
+                grad_weight, stats["norms_w"], stats["fac_w"] = r
+            else:
+                grad_weight = r
+        if ctx.has_bias and ctx.needs_input_grad[2]:
+            O = g3.shape[-1]
+            z = draw_noise((O,), ctx.bias_dtype, g3.device, gen) if std > 0 else None
+            r = colsum_clip(g3, None, C, clamp_value, norm="frob", out_scale=1.0 / (B * T),
+                            noise=z, noise_scale=std, out_dtype=ctx.bias_dtype,
+                            return_stats=stats is not None)
+            if stats is not None:
+                grad_bias, stats["norms_b"], stats["fac_b"] = r
+            else:
+                grad_bias = r
+        if stats is not None:
+            ctx.module.last_stats = stats
+        return grad_input, grad_weight, grad_bias, None

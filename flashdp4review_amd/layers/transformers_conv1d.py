@@ -1,0 +1,115 @@
+"""DPConv1D: HuggingFace Conv1D (y = x W + b, W is [nx, nf]) with per-sample clipping.
+
+Reference: flashdp/layers/transformers_conv1d.py:12-101 and the intended math of
+flashdp/core/transformers_conv1d_clip.py:22-39.  The reference layer routes its
+weight gradient through the Linear helper, which yields g^T x ([nf, nx]) for a
+[nx, nf] weight and fails unless nx == nf, and clips the bias first, in place,
+so that dX and dW see the scaled grad_output.  Here:
+  dX = g W^T                                                     (unclipped)
+  dW = (1/B) sum_b clip(||x_b^T g_b||_F) x_b^T g_b + (sigma/sqrt(B)) z_W
+  db = (1/(B*T)) sum_b clip(||g_b||_F) sum_t g_bt  + (sigma/sqrt(B)) z_b
+so DPConv1D(W) computes exactly DPLinear(W^T)'s gradients, transposed.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+from torch.autograd.function import Function
+
+from ..core import colsum_clip, wgrad_clip
+from ..core.utils import RuntimeAutoTuner
+from .utils import DPParameter as Parameter
+from .utils import as_btf, draw_noise, noise_std
+
+try:  # the HF module type is what wrap_with_flashdp_layers replaces
+    from transformers.pytorch_utils import Conv1D as _HFConv1D
+except Exception:  # pragma: no cover - transformers is part of the image
+    _HFConv1D = None
+
+
+class _Conv1DBase(nn.Module):
+    """Stand-in base with HF Conv1D's attributes when transformers is absent."""
+
+    def __init__(self, nf, nx):
+        super().__init__()
+        self.nf = nf
+        self.nx = nx
+        self.weight = nn.Parameter(torch.empty(nx, nf))
+        self.bias = nn.Parameter(torch.zeros(nf))
+        nn.init.normal_(self.weight, std=0.02)
+
+
+_Base = _HFConv1D if _HFConv1D is not None else _Conv1DBase
+
+
+class DPConv1D(_Base):
+    def __init__(self, nf, nx, C: float = 1.0, clamp_value: float = 1.0,
+                 noise_multiplier: float = 1.0, auto_tune: bool = True):
+        super().__init__(nf, nx)
+        self.dp = True
+        self.C = C
+        self.clamp_value = clamp_value
+        self.noise_multiplier = noise_multiplier
+        self.nf = nf
+        self.nx = nx
+        self.runtime_tuner = RuntimeAutoTuner(enable=auto_tune)
+        self.weight = Parameter(torch.empty(nx, nf))
+        self.bias = Parameter(torch.zeros(nf))
+        nn.init.normal_(self.weight, std=0.02)
+        self.noise_generator = None
+        self.record_stats = False
+        self.last_stats = None
+
+    def forward(self, x):
+        self.runtime_tuner.final_tune()
+        size_out = x.size()[:-1] + (self.nf,)
+        y = _DPConv1DFunction.apply(x, self.weight, self.bias, self)
+        return y.view(size_out)
+
+
+class _DPConv1DFunction(Function):
+    @staticmethod
+    def forward(ctx, input, weight, bias, module):
+        ctx.save_for_backward(input, weight)
+        ctx.bias_dtype = bias.dtype
+        ctx.cfg = (float(module.C), float(module.clamp_value), float(module.noise_multiplier),
+                   module.noise_generator)
+        ctx.module = module if module.record_stats else None
+        w = weight if weight.dtype == input.dtype else weight.to(input.dtype)
+        b = bias if bias.dtype == input.dtype else bias.to(input.dtype)
+        x2 = input.reshape(-1, input.shape[-1])
+        return torch.addmm(b, x2, w).view(input.shape[:-1] + (w.shape[1],))
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        input, weight = ctx.saved_tensors
+        C, clamp_value, sigma, gen = ctx.cfg
+        x3, g3 = as_btf(input), as_btf(grad_output)
+        B, T = x3.shape[0], x3.shape[1]
+        std = noise_std(sigma, B)
+        stats = {} if ctx.module is not None else None
+        grad_input = grad_weight = grad_bias = None
+        if ctx.needs_input_grad[0]:
+            w = weight if weight.dtype == g3.dtype else weight.to(g3.dtype)
+            grad_input = (g3 @ w.t()).reshape(input.shape)
+        if ctx.needs_input_grad[1]:
+            z = draw_noise(weight.shape, weight.dtype, weight.device, gen) if std > 0 else None
+            r = wgrad_clip(x3.to(g3.dtype), g3, C, clamp_value, layout="tn", out_scale=1.0 / B,
+                           noise=z, noise_scale=std, out_dtype=weight.dtype,
+                           return_stats=stats is not None)
+            if stats is not None:
+                grad_weight, stats["norms_w"], stats["fac_w"] = r
+            else:
+                grad_weight = r
+        if ctx.needs_input_grad[2]:
+            z = draw_noise((g3.shape[-1],), ctx.bias_dtype, g3.device, gen) if std > 0 else None
+            r = colsum_clip(g3, None, C, clamp_value, norm="frob", out_scale=1.0 / (B * T),
+                            noise=z, noise_scale=std, out_dtype=ctx.bias_dtype,
+                            return_stats=stats is not None)
+            if stats is not None:
+                grad_bias, stats["norms_b"], stats["fac_b"] = r
+            else:
+                grad_bias = r
+        if stats is not None:
+            ctx.module.last_stats = stats
+        return grad_input, grad_weight, grad_bias, None

@@ -1,0 +1,46 @@
+"""DPParameter marker and helpers shared by the DP layers.
+
+Reference: flashdp/layers/utils.py:6-11 (DPParameter), flashdp/layers/linear.py:51-58
+(per-sample reshape).
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn as nn
+
+
+class DPParameter(nn.Parameter):
+    """nn.Parameter carrying ``requires_dp`` (flashdp/layers/utils.py:6-11)."""
+
+    def __new__(cls, data=None, requires_grad=True, requires_dp=True):
+        t = nn.Parameter.__new__(cls, data, requires_grad)
+        t.requires_dp = requires_dp
+        return t
+
+
+def as_btf(t: torch.Tensor) -> torch.Tensor:
+    """[B, F] -> [B, 1, F]; [B, ..., F] -> [B, T, F] with T the product of the middle axes.
+
+    The reference reshapes this way (flashdp/layers/linear.py:51-58) but then
+    returns the reshaped gradient; the layers here return it in the input's shape.
+    """
+    if t.dim() == 2:
+        return t.unsqueeze(1)
+    if t.dim() > 3:
+        return t.reshape(t.shape[0], -1, t.shape[-1])
+    if t.dim() < 2:
+        raise ValueError(f"DP layers need a leading batch axis; got shape {tuple(t.shape)}")
+    return t
+
+
+def noise_std(noise_multiplier: float, batch: int) -> float:
+    """Standard deviation of the Gaussian noise: noise_multiplier / sqrt(B), added
+    after the 1/B average (flashdp/layers/linear.py:74-80)."""
+    return float(noise_multiplier) / math.sqrt(batch)
+
+
+def draw_noise(shape, dtype, device, generator) -> torch.Tensor:
+    """Standard-normal draw on the device; scaled by noise_std inside the kernels."""
+    return torch.randn(shape, dtype=dtype, device=device, generator=generator)

@@ -1,0 +1,190 @@
+/*
+ * flashdp_hip.h - C ABI of libflashdp_hip.so, the MI355X (gfx950) kernels
+ * behind the FlashDP DP-SGD hot path.
+ *
+ * The reference exposes only a Python operator API (flashdp/core/__init__.py:1-11)
+ * whose functions launch Triton kernels; these entry points are the device work
+ * those operators stand for.  Each declaration names the reference function it
+ * replaces.  The host side (flashdp4review_amd/_lib.py) binds them with ctypes.
+ *
+ * Conventions shared by every entry point:
+ *   - All tensor pointers are device pointers (HBM) of contiguous row-major
+ *     tensors unless a stride argument says otherwise.  Sizes are elements.
+ *   - The caller owns every buffer, including the workspace; the library never
+ *     allocates device memory and never synchronises the host.
+ *   - Work is enqueued on `stream` (a hipStream_t; NULL = the default stream)
+ *     in stream order.  Entry points keep no global mutable state, so calls on
+ *     different streams may run concurrently with distinct workspaces.
+ *   - Return 0 (FDP_OK) or a positive fdp_status; fdp_strerror() names it.
+ *   - Clip factor: c = min(clamp, C / (norm + 1e-10))      (clip_fn.py:6-8).
+ *     When `clip_args_dev` is non-NULL it points at two device floats
+ *     {C, clamp} and overrides the scalar C/clamp arguments, the same device
+ *     layout the reference's Triton kernels read (clip_fn.py:21-25).
+ *   - Optional outputs (norms, factors, noise) may be NULL.
+ */
+#ifndef FLASHDP_HIP_H
+#define FLASHDP_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum fdp_dtype {
+  FDP_F32 = 0,
+  FDP_F16 = 1,
+  FDP_BF16 = 2
+} fdp_dtype;
+
+typedef enum fdp_status {
+  FDP_OK = 0,
+  FDP_ERR_DTYPE = 1,     /* unsupported dtype            -> KeyError     */
+  FDP_ERR_SHAPE = 2,     /* bad / unsupported sizes       -> ValueError   */
+  FDP_ERR_ARG = 3,       /* NULL pointer, bad flag        -> ValueError   */
+  FDP_ERR_WORKSPACE = 4, /* workspace too small           -> RuntimeError */
+  FDP_ERR_HIP = 5,       /* HIP launch error              -> RuntimeError */
+  FDP_ERR_ALIGN = 6      /* pointer alignment violated    -> ValueError   */
+} fdp_status;
+
+/* Operand layouts of the per-sample product G_b (b = 0..B-1).
+ *   FDP_LAYOUT_TN: a is [B, K, M], b is [B, K, N]:  G_b = a_b^T b_b
+ *                  (bmtm_clip, flashdp/core/bmtm_clip_loop.py:162-173;
+ *                   Linear weight grad g^T x, flashdp/core/linear_clip.py:94-113)
+ *   FDP_LAYOUT_NN: a is [B, M, K], b is [B, K, N]:  G_b = a_b b_b
+ *                  (bmm_clip, flashdp/core/bmm_clip_loop.py:150-162)          */
+typedef enum fdp_layout {
+  FDP_LAYOUT_TN = 0,
+  FDP_LAYOUT_NN = 1
+} fdp_layout;
+
+/* Which per-sample norm drives the clip of a column-sum reduction.
+ *   FDP_NORM_SUM:  || sum_t u_bt (.* v_bt) ||_2       (LayerNorm dgamma/dbeta,
+ *                  flashdp/core/layernorm_clip.py:163-198)
+ *   FDP_NORM_FROB: || u_b ||_F over all T*H entries   (Linear/Conv1D bias,
+ *                  flashdp/core/linear_clip.py:116-123)                     */
+typedef enum fdp_norm_kind {
+  FDP_NORM_SUM = 0,
+  FDP_NORM_FROB = 1
+} fdp_norm_kind;
+
+const char* fdp_strerror(int status);
+/* Library version, e.g. 100 for 0.1.0. */
+int fdp_version(void);
+
+/* ------------------------------------------------------------------------
+ * Clipped per-sample product sum (the DP-SGD weight-gradient hot path):
+ *
+ *   out[m,n] = out_scale * sum_b c_b * G_b[m,n] + noise_scale * noise[m,n]
+ *   c_b      = min(clamp, C / (||G_b||_F + 1e-10))
+ *
+ * Replaces: bmtm_clip_triton / mtm_clip (flashdp/core/bmtm_clip_loop.py:137-173),
+ *           bmm_clip_triton / mm_clip (flashdp/core/bmm_clip_loop.py:129-162),
+ *           mm_clip_triton (flashdp/core/mm_clip_loop.py:127-139, as B=K, K=1),
+ *           _weight_grad_block_clip + linear_weight_flashdp
+ *           (flashdp/core/linear_clip.py:94-113) and the .div_(B) + noise add_
+ *           of _DPLinearFunc.backward (flashdp/layers/linear.py:72-80).
+ *
+ * a, b     : input dtype `dtype` (F32, F16 or BF16), batch strides
+ *            stride_ab / stride_bb and row strides lda / ldb in elements
+ *            (row = the contiguous dimension's parent: for TN, a row of a_b
+ *            is one k; for NN, one m).  The innermost dimension must be
+ *            contiguous.
+ * out      : [M, N] row-major with row stride ldo, dtype `out_dtype`.
+ * noise    : NULL or [M, N] contiguous, dtype `out_dtype`.
+ * norms    : NULL or [B] fp32, ||G_b||_F.
+ * factors  : NULL or [B] fp32, c_b.
+ * flags    : bit 0 (FDP_WGRAD_NOCLIP) skips the norm pass and uses c_b = clamp
+ *            (a plain batched product sum; `norms` must then be NULL).
+ * workspace: device buffer of at least fdp_wgrad_clip_workspace_size() bytes.
+ * ---------------------------------------------------------------------- */
+#define FDP_WGRAD_NOCLIP 1
+
+int fdp_wgrad_clip_workspace_size(int64_t B, int64_t K, int64_t M, int64_t N,
+                                  int dtype, int flags, size_t* bytes);
+
+int fdp_wgrad_clip(const void* a, const void* b, int64_t B, int64_t K, int64_t M,
+                   int64_t N, int64_t stride_ab, int64_t lda, int64_t stride_bb,
+                   int64_t ldb, int layout, int dtype, float C, float clamp,
+                   const float* clip_args_dev, float out_scale, const void* noise,
+                   float noise_scale, void* out, int64_t ldo, int out_dtype,
+                   float* norms, float* factors, int flags, void* workspace,
+                   size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Clipped per-sample column sums over the middle axis:
+ *
+ *   S_b[h]  = sum_t u[b,t,h] * (v ? v[b,t,h] : 1)
+ *   n_b     = ||S_b||_2 (FDP_NORM_SUM) or ||u_b||_F (FDP_NORM_FROB)
+ *   out[h]  = out_scale * sum_b c_b S_b[h] + noise_scale * noise[h]
+ *
+ * Replaces: linear_bias_grad_clip (flashdp/core/linear_clip.py:116-123, with
+ *           out_scale = 1/(B*T), without its in-place write to grad_output),
+ *           conv1d_bias_grad_clip (flashdp/core/transformers_conv1d_clip.py:31-39),
+ *           layernorm_dw_clip (v = x_hat) and layernorm_db_clip (v = NULL)
+ *           (flashdp/core/layernorm_clip.py:163-198, out_scale = 1/B) and the
+ *           noise add_ of the layers (flashdp/layers/linear.py:84-92,
+ *           flashdp/layers/layernorm.py:139-155).
+ * u, v     : [B, T, H] contiguous, dtype `dtype`; v may be NULL.
+ * out      : [H], dtype `out_dtype`; noise NULL or [H] of `out_dtype`.
+ * ---------------------------------------------------------------------- */
+int fdp_colsum_clip_workspace_size(int64_t B, int64_t T, int64_t H, int dtype,
+                                   size_t* bytes);
+
+int fdp_colsum_clip(const void* u, const void* v, int64_t B, int64_t T, int64_t H,
+                    int dtype, int norm_kind, float C, float clamp,
+                    const float* clip_args_dev, float out_scale, const void* noise,
+                    float noise_scale, void* out, int out_dtype, float* norms,
+                    float* factors, void* workspace, size_t workspace_bytes,
+                    void* stream);
+
+/* ------------------------------------------------------------------------
+ * LayerNorm forward over the last axis, fp32 statistics:
+ *   mean_r = mean(x_r), rstd_r = 1/sqrt(var_r + eps) (biased var),
+ *   y_r = (x_r - mean_r) * rstd_r * w + b
+ * Replaces: layernorm_fwd_fused_triton / _layer_norm_fwd_fused
+ *           (flashdp/core/layernorm_clip.py:11-60,201-239).
+ * x, y     : [rows, H] contiguous, dtype `dtype`.
+ * w, b     : [H] of `w_dtype`; either may be NULL (weight 1 / bias 0).
+ * mean,rstd: [rows] fp32 (either may be NULL).
+ * ---------------------------------------------------------------------- */
+int fdp_layernorm_fwd(const void* x, const void* w, const void* b, int64_t rows,
+                      int64_t H, float eps, int dtype, int w_dtype, void* y,
+                      float* mean, float* rstd, void* stream);
+
+/* ------------------------------------------------------------------------
+ * LayerNorm backward with per-sample clipped gamma/beta gradients:
+ *   x_hat = (x - mean) * rstd
+ *   dx    = rstd * (w.dy - mean_h(w.dy) - x_hat * mean_h(w.dy.x_hat))
+ *   P_b   = sum_t dy.x_hat,  Q_b = sum_t dy                  (per sample)
+ *   dw    = out_scale * sum_b clip(||P_b||) P_b + noise_scale * noise_w
+ *   db    = out_scale * sum_b clip(||Q_b||) Q_b + noise_scale * noise_b
+ * Replaces: layernorm_bwd_clip_fused_triton + layernorm_dwdb_fused_triton
+ *           (flashdp/core/layernorm_clip.py:63-160,241-315) with the per-sample
+ *           math of layernorm_dw_clip / layernorm_db_clip
+ *           (flashdp/core/layernorm_clip.py:163-198) and one noise draw each
+ *           (flashdp/layers/layernorm.py:139-155).
+ * dy, x, dx: [B, T, H] contiguous, dtype `dtype` (dx may alias nothing).
+ * w        : [H] of `w_dtype` or NULL (weight 1).
+ * mean,rstd: [B*T] fp32 from fdp_layernorm_fwd.
+ * dw, db   : [H] of `w_dtype`; either may be NULL to skip it.
+ * norms    : NULL or [2*B] fp32 (||P_b|| then ||Q_b||); factors likewise.
+ * ---------------------------------------------------------------------- */
+int fdp_layernorm_bwd_clip_workspace_size(int64_t B, int64_t T, int64_t H,
+                                          int dtype, size_t* bytes);
+
+int fdp_layernorm_bwd_clip(const void* dy, const void* x, const void* w,
+                           const float* mean, const float* rstd, int64_t B,
+                           int64_t T, int64_t H, int dtype, int w_dtype, float C,
+                           float clamp, const float* clip_args_dev,
+                           float out_scale, const void* noise_w,
+                           const void* noise_b, float noise_scale, void* dx,
+                           void* dw, void* db, float* norms, float* factors,
+                           void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLASHDP_HIP_H */

@@ -1,0 +1,98 @@
+"""C ABI of libflashdp_hip.so: the library loads, exports exactly what
+include/flashdp_hip.h declares with the argument counts the ctypes binding uses,
+and argument validation returns the documented status codes.  No kernel is
+launched here (validation happens before any launch)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from flashdp4review_amd import _lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include",
+                      "flashdp_hip.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    out = {}
+    for m in re.finditer(r"(?:const\s+char\s*\*|int)\s+(fdp_\w+)\s*\(([^)]*)\)\s*;", text):
+        params = [p.strip() for p in m.group(2).split(",") if p.strip() and p.strip() != "void"]
+        out[m.group(1)] = len(params)
+    return out
+
+
+def test_library_loads():
+    L = _lib.lib()
+    assert L.fdp_version() == 100
+    assert L.fdp_strerror(0) == b"ok"
+    assert L.fdp_strerror(4).startswith(b"workspace")
+
+
+def test_header_matches_exports_and_binding():
+    decl = header_functions()
+    assert decl, "no declarations parsed"
+    assert set(decl) == set(_lib.SIGNATURES), (set(decl) ^ set(_lib.SIGNATURES))
+    L = _lib.lib()
+    for name, nargs in decl.items():
+        fn = getattr(L, name)  # raises AttributeError if not exported
+        assert fn is not None
+        assert len(_lib.SIGNATURES[name][1]) == nargs, name
+
+
+def _wgrad(**kw):
+    args = dict(a=1, b=1, B=2, K=4, M=8, N=8, sab=32, lda=8, sbb=32, ldb=8, layout=0, dtype=2,
+                C=1.0, clamp=1.0, cad=None, out_scale=1.0, noise=None, noise_scale=0.0, out=1,
+                ldo=8, odt=2, norms=None, factors=None, flags=0, ws=None, wsb=0, stream=None)
+    args.update(kw)
+    return _lib.lib().fdp_wgrad_clip(*args.values())
+
+
+def test_wgrad_validation_codes():
+    assert _wgrad(dtype=7) == 1
+    assert _wgrad(odt=-1) == 1
+    assert _wgrad(layout=5) == 3
+    assert _wgrad(B=0) == 2
+    assert _wgrad(lda=4) == 2          # row stride shorter than M
+    assert _wgrad(out=None) == 3
+    assert _wgrad(flags=4) == 3
+    assert _wgrad(flags=1, norms=16) == 3  # norms undefined without the norm pass
+    assert _wgrad() == 4               # workspace missing
+
+
+def test_workspace_queries():
+    L = _lib.lib()
+    n = _lib.size_query(L.fdp_wgrad_clip_workspace_size, 8, 1024, 3072, 768, 2, 0)
+    assert n >= 8 * 4
+    with pytest.raises(KeyError):
+        _lib.size_query(L.fdp_wgrad_clip_workspace_size, 8, 1024, 3072, 768, 9, 0)
+    with pytest.raises(ValueError):
+        _lib.size_query(L.fdp_colsum_clip_workspace_size, 0, 4, 4, 2)
+    with pytest.raises(ValueError):  # rows longer than one wavefront holds
+        _lib.size_query(L.fdp_layernorm_bwd_clip_workspace_size, 2, 4, 8192, 2)
+    assert _lib.size_query(L.fdp_layernorm_bwd_clip_workspace_size, 16, 1024, 1024, 2) > 0
+
+
+def test_other_validation_codes():
+    L = _lib.lib()
+    st = L.fdp_colsum_clip(1, None, 2, 3, 4, 2, 9, 1.0, 1.0, None, 1.0, None, 0.0, 1, 2, None,
+                           None, None, 0, None)
+    assert st == 3  # bad norm kind
+    st = L.fdp_layernorm_fwd(1, None, None, 4, 8192, 1e-5, 2, 2, 1, None, None, None)
+    assert st == 2
+    st = L.fdp_layernorm_fwd(1, None, None, 4, 64, 1e-5, 5, 2, 1, None, None, None)
+    assert st == 1
+    st = L.fdp_layernorm_bwd_clip(1, 1, None, 1, 1, 2, 4, 64, 2, 2, 1.0, 1.0, None, 0.5, None,
+                                  None, 0.0, 1, None, None, None, None, None, 0, None)
+    assert st == 4
+
+
+def test_status_to_exception_mapping():
+    with pytest.raises(KeyError):
+        _lib.check(1, "x")
+    with pytest.raises(ValueError):
+        _lib.check(2, "x")
+    with pytest.raises(RuntimeError):
+        _lib.check(5, "x")

@@ -1,0 +1,140 @@
+"""GPU parity of the DP layers (DPLinear, DPConv1D, DPLayerNorm) end to end
+through autograd, against the float64 oracle, with seeded injected noise."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import dp_clip as O
+from tests._tol import assert_close, assert_elementwise
+
+from flashdp4review_amd import DPConv1D, DPLayerNorm, DPLinear, wrap_with_flashdp_layers
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def draws(seed, shapes, dtype):
+    """The layers draw z_W then z_b with torch.randn from their noise_generator."""
+    gen = torch.Generator(device=DEV).manual_seed(seed)
+    return [torch.randn(s, dtype=dtype, device=DEV, generator=gen) for s in shapes]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=str)
+@pytest.mark.parametrize("sigma", [0.0, 1.0])
+def test_dplinear_cfg1(dtype, sigma):
+    """cfg1: Linear 768->768 with bias, x [4,128,768] ~ N(0,1), g ~ N(0, 0.01^2)."""
+    torch.manual_seed(0)
+    lin = DPLinear(768, 768, bias=True, C=1.0, noise_multiplier=sigma).to(DEV, dtype)
+    lin.record_stats = True
+    lin.noise_generator = torch.Generator(device=DEV).manual_seed(1234)
+    x = torch.randn(4, 128, 768, device=DEV).to(dtype).requires_grad_(True)
+    g = (torch.randn(4, 128, 768, device=DEV) * 0.01).to(dtype)
+    g0 = g.clone()
+    lin(x).backward(g)
+    assert torch.equal(g, g0)
+    zw, zb = draws(1234, [(768, 768), (768,)], dtype) if sigma > 0 else (None, None)
+    ref = O.linear_backward(x.detach(), g, lin.weight.detach(), 1.0, 1.0, sigma, zw, zb)
+    assert_close(x.grad, ref["dx"], dtype, "dx")
+    assert_close(lin.weight.grad, ref["dw"], dtype, "dW")
+    assert_close(lin.bias.grad, ref["db"], dtype, "db")
+    st = lin.last_stats
+    assert_elementwise(st["norms_w"], ref["norms_w"], dtype, "weight norms")
+    assert_elementwise(st["fac_w"], ref["fac_w"], dtype, "weight factors")
+    assert_elementwise(st["norms_b"], ref["norms_b"], dtype, "bias norms")
+    assert_elementwise(st["fac_b"], ref["fac_b"], dtype, "bias factors")
+    assert np.all(ref["norms_w"] > 1.0)  # all samples clipped at this config
+
+
+@pytest.mark.parametrize("shape", [(6, 20), (3, 4, 5, 20)], ids=["2d", "4d"])
+def test_dplinear_other_ranks(shape):
+    """2-D inputs (T=1) and >3-D inputs (T = product of middle axes) return
+    gradients in the input's shape."""
+    lin = DPLinear(20, 12, C=0.05, noise_multiplier=0.0).to(DEV)
+    x = torch.randn(*shape, device=DEV, requires_grad=True)
+    g = torch.randn(*shape[:-1], 12, device=DEV)
+    lin(x).backward(g)
+    assert x.grad.shape == x.shape
+    ref = O.linear_backward(x.detach(), g, lin.weight.detach(), 0.05, 1.0)
+    assert_close(x.grad, ref["dx"], torch.float32, "dx")
+    assert_close(lin.weight.grad, ref["dw"], torch.float32, "dW")
+    assert_close(lin.bias.grad, ref["db"], torch.float32, "db")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=str)
+def test_dpconv1d_matches_linear_transposed(dtype):
+    """cfg3-style Conv1D (nx=768 -> nf=2304 scaled down in T) with log-uniform per-sample
+    norms: DPConv1D(W) == DPLinear(W^T) transposed, and both match the oracle."""
+    torch.manual_seed(4)
+    B, T, nx, nf = 4, 64, 768, 2304
+    conv = DPConv1D(nf, nx, C=1.0, noise_multiplier=0.0).to(DEV, dtype)
+    conv.record_stats = True
+    x = torch.randn(B, T, nx, device=DEV).to(dtype).requires_grad_(True)
+    gh = torch.randn(B, T, nf, device=DEV) * 0.02
+    # scale each sample so that ||x_b^T g_b|| = 10^u_b, u_b ~ U(-1, 1)
+    G = torch.einsum("btm,btn->bmn", x.detach().float(), gh)
+    u = torch.rand(B, generator=torch.Generator().manual_seed(4)) * 2 - 1
+    r = (10 ** u).to(DEV)
+    g = (gh * (r / G.flatten(1).norm(dim=1))[:, None, None]).to(dtype)
+    conv(x).backward(g)
+    ref = O.conv1d_backward(x.detach(), g, conv.weight.detach(), 1.0, 1.0)
+    assert_close(x.grad, ref["dx"], dtype, "dx")
+    assert_close(conv.weight.grad, ref["dw"], dtype, "dW")
+    assert_close(conv.bias.grad, ref["db"], dtype, "db")
+    f = conv.last_stats["fac_w"].cpu().numpy()
+    assert np.any(f < 1.0) and np.any(f >= 1.0 - 1e-6)  # partially clipped
+    lin = DPLinear(nx, nf, C=1.0, noise_multiplier=0.0).to(DEV, dtype)
+    with torch.no_grad():
+        lin.weight.copy_(conv.weight.t())
+        lin.bias.copy_(conv.bias)
+    x2 = x.detach().clone().requires_grad_(True)
+    lin(x2).backward(g)
+    assert_close(conv.weight.grad.t(), lin.weight.grad.double().cpu().numpy(), dtype, "W^T")
+    assert_close(conv.bias.grad, lin.bias.grad.double().cpu().numpy(), dtype, "bias")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=str)
+@pytest.mark.parametrize("use_fused", [True, False])
+def test_dplayernorm(dtype, use_fused):
+    """cfg4-style LayerNorm (H=1024, gamma=1, beta=0) with seeded noise."""
+    B, T, H = 4, 128, 1024
+    ln = DPLayerNorm(H, use_fused=use_fused, C=1.0, noise_multiplier=1.0).to(DEV, dtype)
+    ln.record_stats = True
+    ln.noise_generator = torch.Generator(device=DEV).manual_seed(77)
+    x = torch.randn(B, T, H, device=DEV).to(dtype).requires_grad_(True)
+    g = (torch.randn(B, T, H, device=DEV) * 0.01).to(dtype)
+    y = ln(x)
+    yr, _, _ = O.layernorm_fwd(x.detach(), ln.weight.detach(), ln.bias.detach(), 1e-5)
+    assert_close(y, yr, dtype, "y")
+    y.backward(g)
+    zw, zb = draws(77, [(H,), (H,)], dtype)
+    ref = O.layernorm_bwd_clip(g, x.detach(), ln.weight.detach(), 1e-5, C=1.0,
+                               noise_multiplier=1.0, z_w=zw, z_b=zb)
+    assert_close(x.grad, ref["dx"], dtype, "dx")
+    assert_close(ln.weight.grad, ref["dw"], dtype, "dgamma")
+    assert_close(ln.bias.grad, ref["db"], dtype, "dbeta")
+    assert_elementwise(ln.last_stats["norms_w"], ref["norms_w"], dtype, "gamma norms")
+    assert_elementwise(ln.last_stats["norms_b"], ref["norms_b"], dtype, "beta norms")
+
+
+def test_wrapped_mlp_trains():
+    """A wrapped 2-layer MLP with LayerNorm steps under Adam and its loss decreases
+    with sigma = 0 (sanity of the whole backward wiring)."""
+    torch.manual_seed(0)
+    m = torch.nn.Sequential(torch.nn.LayerNorm(64), torch.nn.Linear(64, 128), torch.nn.GELU(),
+                            torch.nn.Linear(128, 64)).to(DEV)
+    wrap_with_flashdp_layers(m, target_modules=[torch.nn.Linear, torch.nn.LayerNorm], C=10.0,
+                             noise_multiplier=0.0, feedback=False)
+    assert all(type(mod).__name__.startswith("DP") for mod in (m[0], m[1], m[3]))
+    opt = torch.optim.Adam(m.parameters(), lr=1e-2)
+    x = torch.randn(16, 8, 64, device=DEV)
+    target = torch.randn(16, 8, 64, device=DEV)
+    losses = []
+    for _ in range(20):
+        loss = ((m(x) - target) ** 2).mean()
+        opt.zero_grad()
+        loss.backward()
+        opt.step()
+        losses.append(loss.item())
+    assert losses[-1] < 0.8 * losses[0]

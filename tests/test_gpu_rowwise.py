@@ -1,0 +1,156 @@
+"""GPU parity of the bandwidth-bound kernels (fdp_colsum_clip, fdp_layernorm_fwd,
+fdp_layernorm_bwd_clip) against the float64 oracle."""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import dp_clip as O
+from tests._tol import assert_close, assert_elementwise
+
+from flashdp4review_amd import core
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+DTYPES = [torch.float32, torch.bfloat16, torch.float16]
+
+
+def randn(shape, dtype, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(shape, generator=g) * scale).to(dtype).to(DEV)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+@pytest.mark.parametrize("shape", [(8, 1024, 768), (3, 7, 100), (2, 33, 2304), (5, 1, 9),
+                                   (16, 64, 3072)], ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("norm", ["frob", "sum"])
+def test_colsum_parity(shape, norm, dtype):
+    B, T, H = shape
+    u = randn(shape, dtype, 1, 0.02)
+    v = randn(shape, dtype, 2) if norm == "sum" else None
+    _, n0, _ = O.colsum_clip(u, v, 1.0, 1.0, norm)
+    C = float(np.median(n0))
+    ref, nref, fref = O.colsum_clip(u, v, C, 1.0, norm, out_scale=1.0 / B)
+    out, n, f = core.colsum_clip(u, v, C, 1.0, norm=norm, out_scale=1.0 / B,
+                                 out_dtype=torch.float32, return_stats=True)
+    assert_close(out, ref, dtype, "colsum")
+    assert_elementwise(n, nref, dtype, "norms")
+    assert_elementwise(f, fref, dtype, "factors")
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+def test_bias_ops(dtype):
+    g = randn((4, 50, 96), dtype, 3, 0.05)
+    g0 = g.clone()
+    ref, _, _ = O.colsum_clip(g, None, 0.5, 1.0, "frob", out_scale=1.0 / 200)
+    assert_close(core.linear_bias_grad_clip(g, 0.5, 1.0), ref, dtype, "linear_bias_grad_clip")
+    assert torch.equal(g, g0), "grad_output must not be modified"
+    assert_close(core.conv1d_bias_grad_clip(g, 0.5, 1.0), ref, dtype, "conv1d_bias_grad_clip")
+    z = randn((96,), dtype, 4)
+    out = core.colsum_clip(g, None, 0.5, 1.0, norm="frob", out_scale=1.0 / 200, noise=z,
+                           noise_scale=0.25, out_dtype=torch.float32)
+    ref, _, _ = O.colsum_clip(g, None, 0.5, 1.0, "frob", 1.0 / 200, z, 0.25)
+    assert_close(out, ref, dtype, "bias + noise")
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+@pytest.mark.parametrize("H", [1024, 768, 2048, 100, 4096, 8])
+def test_layernorm_fwd_parity(H, dtype):
+    x = randn((3, 37, H), dtype, 5)
+    w = randn((H,), dtype, 6)
+    b = randn((H,), dtype, 7)
+    y, mean, rstd = core.layernorm_fwd(x, w, b, 1e-5)
+    yr, mr, rr = O.layernorm_fwd(x, w, b, 1e-5)
+    assert_close(y, yr, dtype, "y")
+    assert_close(mean.reshape(mr.shape), mr, dtype, "mean")
+    assert_elementwise(rstd.reshape(rr.shape), rr, dtype, "rstd")
+    # torch's own layer_norm on the same inputs (fp32 math)
+    yt = F.layer_norm(x.float(), (H,), w.float(), b.float(), 1e-5)
+    assert_close(y, yt.double().cpu().numpy(), dtype, "y vs torch")
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+@pytest.mark.parametrize("shape", [(16, 1024, 1024), (4, 33, 768), (2, 5, 100), (3, 64, 4096),
+                                   (1, 1, 64)], ids=lambda s: "x".join(map(str, s)))
+def test_layernorm_bwd_parity(shape, dtype):
+    B, T, H = shape
+    x = randn(shape, dtype, 8)
+    w = randn((H,), dtype, 9)
+    g = randn(shape, dtype, 10, 0.01)
+    _, mean, rstd = core.layernorm_fwd(x, w, None, 1e-5)
+    r0 = O.layernorm_bwd_clip(g, x, w, 1e-5, C=1.0, mean=mean, rstd=rstd)
+    C = float(np.median(r0["norms_w"]))
+    zw = randn((H,), dtype, 11)
+    zb = randn((H,), dtype, 12)
+    std = 0.7 / np.sqrt(B)
+    dx, dw, db, norms, fac = core.layernorm_bwd_clip(
+        g, x, w, mean, rstd, C, 1.0, noise_w=zw, noise_b=zb, noise_scale=std,
+        param_dtype=torch.float32, return_stats=True)
+    ref = O.layernorm_bwd_clip(g, x, w, 1e-5, C=C, noise_multiplier=0.7, z_w=zw, z_b=zb,
+                               mean=mean, rstd=rstd)
+    assert_close(dx, ref["dx"], dtype, "dx")
+    assert_close(dw, ref["dw"], dtype, "dgamma")
+    assert_close(db, ref["db"], dtype, "dbeta")
+    assert_elementwise(norms[:B], ref["norms_w"], dtype, "norms gamma")
+    assert_elementwise(norms[B:], ref["norms_b"], dtype, "norms beta")
+    assert_elementwise(fac[:B], ref["fac_w"], dtype, "factors gamma")
+    assert_elementwise(fac[B:], ref["fac_b"], dtype, "factors beta")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=str)
+def test_layernorm_no_clip_matches_torch_autograd(dtype):
+    """C -> inf: dgamma/dbeta are torch autograd's divided by B, dx is autograd's."""
+    B, T, H = 4, 40, 512
+    x = randn((B, T, H), dtype, 13)
+    w = randn((H,), dtype, 14)
+    b = randn((H,), dtype, 15)
+    g = randn((B, T, H), dtype, 16, 0.1)
+    y, mean, rstd = core.layernorm_fwd(x, w, b, 1e-5)
+    dx, dw, db = core.layernorm_bwd_clip(g, x, w, mean, rstd, 1e30, 1.0, param_dtype=torch.float32)
+    xr = x.float().cpu().double().requires_grad_(True)
+    wr = w.float().cpu().double().requires_grad_(True)
+    br = b.float().cpu().double().requires_grad_(True)
+    gx, gw, gb = torch.autograd.grad(F.layer_norm(xr, (H,), wr, br, 1e-5), (xr, wr, br),
+                                     g.cpu().double())
+    assert_close(dx, gx.numpy(), dtype, "dx")
+    assert_close(dw, gw.numpy() / B, dtype, "dgamma")
+    assert_close(db, gb.numpy() / B, dtype, "dbeta")
+
+
+def test_layernorm_operator_api():
+    dtype = torch.bfloat16
+    B, T, H = 4, 32, 256
+    x = randn((B, T, H), dtype, 17)
+    w = randn((H,), dtype, 18)
+    b = randn((H,), dtype, 19)
+    g = randn((B, T, H), dtype, 20, 0.05)
+    y, buf, args = core.layernorm_fwd_fused(x, w, b, 1e-5)
+    assert args["BLOCK_SIZE"] == 256 and set(buf) == {"mean", "rstd"}
+    ca = torch.tensor([0.5, 1.0], device=DEV)
+    dx, dw_, db_, a2 = core.layernorm_bwd_clip_fused(g, x, w, b, ca, buf, args)
+    dw, db = core.layernorm_dwdb_fused(w, b, dw_, db_, a2)
+    ref = O.layernorm_bwd_clip(g, x, w, 1e-5, C=0.5, mean=buf["mean"], rstd=buf["rstd"])
+    assert dw.dtype == dtype and dw.shape == (H,)
+    assert_close(dx, ref["dx"], dtype, "dx")
+    assert_close(dw, ref["dw"], dtype, "dw")
+    assert_close(db, ref["db"], dtype, "db")
+    # per-sample clip ops on x_hat (layernorm_clip.py:163-198)
+    xhat, _, _ = O.layernorm_fwd(x, None, None, 1e-5)
+    xh = torch.tensor(xhat, dtype=dtype, device=DEV)
+    r = core.layernorm_dw_clip(xh, g, w, torch.tensor([0.5]), torch.tensor([1.0]))
+    assert r.shape == (1, 1, H)
+    ref_dw, _, _ = O.colsum_clip(g, xh, 0.5, 1.0, "sum", out_scale=1.0 / B)
+    assert_close(r.reshape(-1), ref_dw, dtype, "layernorm_dw_clip")
+    r = core.layernorm_db_clip(g, b, 0.5, 1.0)
+    ref_db, _, _ = O.colsum_clip(g, None, 0.5, 1.0, "sum", out_scale=1.0 / B)
+    assert_close(r.reshape(-1), ref_db, dtype, "layernorm_db_clip")
+
+
+def test_layernorm_bwd_deterministic():
+    x = randn((16, 256, 1024), torch.bfloat16, 21)
+    g = randn((16, 256, 1024), torch.bfloat16, 22, 0.01)
+    _, mean, rstd = core.layernorm_fwd(x, None, None, 1e-5)
+    a = core.layernorm_bwd_clip(g, x, None, mean, rstd, 1.0, 1.0)
+    b = core.layernorm_bwd_clip(g, x, None, mean, rstd, 1.0, 1.0)
+    for u, v in zip(a, b):
+        assert torch.equal(u, v)

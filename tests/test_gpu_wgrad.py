@@ -1,0 +1,163 @@
+"""GPU parity of the clipped per-sample product sum (fdp_wgrad_clip) against the
+float64 oracle on the same dtype-rounded inputs.  Tolerances: tests/_tol.py."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import dp_clip as O
+from tests._tol import assert_close, assert_elementwise
+
+from flashdp4review_amd import core
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+DTYPES = [torch.float32, torch.bfloat16, torch.float16]
+
+
+def make(B, K, M, N, dtype, layout, seed=0, scale_b=0.02):
+    g = torch.Generator().manual_seed(seed)
+    a = torch.randn((B, K, M) if layout == "tn" else (B, M, K), generator=g)
+    b = torch.randn((B, K, N), generator=g) * scale_b
+    return a.to(dtype).to(DEV), b.to(dtype).to(DEV)
+
+
+SHAPES = [
+    (4, 128, 768, 768),   # cfg1 per-layer shape
+    (3, 37, 100, 70),     # ragged in every dimension
+    (2, 64, 130, 257),    # odd N: unaligned rows, scalar loads
+    (1, 1, 16, 16),       # B = 1, T = 1
+    (5, 200, 64, 300),
+    (16, 16, 256, 256),   # many samples, short contraction
+]
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+@pytest.mark.parametrize("layout", ["tn", "nn"])
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_wgrad_parity(shape, layout, dtype):
+    B, K, M, N = shape
+    a, b = make(B, K, M, N, dtype, layout)
+    _, norms_ref, _ = O.wgrad_clip(a, b, 1.0, 1.0, layout)
+    # choose C inside the norm range so that some samples clip and some do not
+    C = float(np.median(norms_ref)) if B > 1 else float(norms_ref[0]) * 0.5
+    ref, norms_ref, fac_ref = O.wgrad_clip(a, b, C, 1.0, layout)
+    out, norms, fac = core.wgrad_clip(a, b, C, 1.0, layout=layout, out_dtype=torch.float32,
+                                      return_stats=True)
+    assert_close(out, ref, dtype, "out")
+    assert_elementwise(norms, norms_ref, dtype, "norms")
+    assert_elementwise(fac, fac_ref, dtype, "factors")
+    # output in the input dtype (what the layers write)
+    out2 = core.wgrad_clip(a, b, C, 1.0, layout=layout)
+    assert out2.dtype == dtype
+    assert_close(out2, ref, dtype, "out (input dtype)")
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+def test_wgrad_scale_noise_and_device_clip_args(dtype):
+    B, K, M, N = 4, 96, 192, 160
+    a, b = make(B, K, M, N, dtype, "tn", seed=3)
+    z = torch.randn(M, N, generator=torch.Generator().manual_seed(9)).to(dtype).to(DEV)
+    clip_args = torch.tensor([0.05, 0.9], device=DEV)
+    out = core.wgrad_clip(a, b, layout="tn", clip_args=clip_args, out_scale=1.0 / B, noise=z,
+                          noise_scale=0.5, out_dtype=torch.float32)
+    ref, _, _ = O.wgrad_clip(a, b, 0.05, 0.9, "tn", out_scale=1.0 / B, noise=z, noise_scale=0.5)
+    assert_close(out, ref, dtype, "scaled+noise")
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+def test_wgrad_special_cases(dtype):
+    B, K, M, N = 3, 50, 70, 90
+    a, b = make(B, K, M, N, dtype, "tn", seed=5)
+    # C = 0: every factor is 0
+    out, _, fac = core.wgrad_clip(a, b, 0.0, 1.0, return_stats=True)
+    assert torch.count_nonzero(out) == 0 and torch.count_nonzero(fac) == 0
+    # C huge: plain product sum == torch fp32 batched product
+    out = core.wgrad_clip(a, b, 1e30, 1.0, out_dtype=torch.float32)
+    ref = torch.einsum("bkm,bkn->mn", a.double().cpu(), b.double().cpu()).numpy()
+    assert_close(out, ref, dtype, "no clip")
+    # huge norms: each clipped term has norm C, single sample -> ||out|| = C
+    out = core.wgrad_clip(a[:1] * 8, b[:1] * 8, 0.25, 1.0, out_dtype=torch.float32)
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    assert abs(out.double().norm().item() - 0.25) / 0.25 < tol
+    # noclip flag = clamp everywhere
+    out = core.wgrad_clip(a, b, 5.0, 0.5, noclip=True, out_dtype=torch.float32)
+    ref, _, _ = O.wgrad_clip(a, b, 5.0, 0.5, "tn", noclip=True)
+    assert_close(out, ref, dtype, "noclip")
+
+
+def test_wgrad_deterministic():
+    a, b = make(8, 256, 512, 384, torch.bfloat16, "tn", seed=7)
+    o1 = core.wgrad_clip(a, b, 0.5, 1.0)
+    o2 = core.wgrad_clip(a, b, 0.5, 1.0)
+    assert torch.equal(o1, o2)
+
+
+def test_wgrad_does_not_modify_inputs():
+    a, b = make(4, 64, 128, 128, torch.bfloat16, "tn", seed=8)
+    a0, b0 = a.clone(), b.clone()
+    core.wgrad_clip(a, b, 0.1, 1.0)
+    assert torch.equal(a, a0) and torch.equal(b, b0)
+
+
+def test_operator_api():
+    dtype = torch.bfloat16
+    B, K, M, N = 4, 64, 96, 80
+    t1, t2 = make(B, K, M, N, dtype, "tn", seed=11)
+    ca = torch.tensor([0.3, 1.0], device=DEV)
+    ref, _, _ = O.wgrad_clip(t1, t2, 0.3, 1.0, "tn")
+    assert_close(core.bmtm_clip(t1, t2, ca), ref, dtype, "bmtm_clip")
+    t1n = t1.transpose(1, 2).contiguous()
+    r = core.bmm_clip(t1n, t2, ca)
+    assert r.dtype == torch.float32
+    assert_close(r, ref, dtype, "bmm_clip")
+    m1 = torch.randn(M, K, device=DEV, dtype=torch.float32)
+    m2 = torch.randn(K, N, device=DEV, dtype=torch.float32) * 0.1
+    assert_close(core.mm_clip(m1, m2, ca), O.mm_clip(m1, m2, 0.3, 1.0), torch.float32, "mm_clip")
+    mf = core.mm_fused(m1, m2)
+    assert_close(mf, m1.double().cpu().numpy() @ m2.double().cpu().numpy(), torch.float32,
+                 "mm_fused")
+    x = torch.randn(B, K, 48, device=DEV, dtype=dtype)
+    g = torch.randn(B, K, 40, device=DEV, dtype=dtype) * 0.01
+    ref, _, _ = O.wgrad_clip(g, x, 0.2, 1.0, "tn")
+    assert_close(core.linear_weight_flashdp(x, g, 0.2, 1.0, core.RuntimeAutoTuner()), ref, dtype,
+                 "linear_weight_flashdp")
+    ref, _, _ = O.wgrad_clip(x, g, 0.2, 1.0, "tn")
+    assert_close(core.conv1d_weight_flashdp(x, g, 0.2, 1.0), ref, dtype, "conv1d_weight_flashdp")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16], ids=str)
+def test_wgrad_cfg2_full_size(dtype):
+    """cfg2 (Linear 768->3072, B=8, T=1024): norms and the clipped sum against an fp32
+    torch reference on the GPU (per-sample bmm in fp32), all samples clipped."""
+    torch.manual_seed(0)
+    x = torch.randn(8, 1024, 768, device=DEV).to(dtype)
+    g = (torch.randn(8, 1024, 3072, device=DEV) * 0.02).to(dtype)
+    out, norms, fac = core.wgrad_clip(g, x, 1.0, 1.0, out_dtype=torch.float32, return_stats=True)
+    G = torch.bmm(g.float().transpose(1, 2).contiguous(), x.float())  # [8, 3072, 768]
+    n_ref = G.flatten(1).norm(dim=1)
+    c_ref = torch.clamp(1.0 / (n_ref + 1e-10), max=1.0)
+    ref = (c_ref[:, None, None] * G).sum(0)
+    assert torch.all(n_ref > 1.0)
+    assert_elementwise(norms, n_ref.double().cpu().numpy(), dtype, "norms")
+    assert_elementwise(fac, c_ref.double().cpu().numpy(), dtype, "factors")
+    assert_close(out, ref.double().cpu().numpy(), dtype, "clipped sum")
+    # with every sample clipped, the 1/B-free sum has norm <= B*C
+    assert out.norm().item() <= 8.0 * (1 + 1e-3)
+
+
+def test_wgrad_memory_no_per_sample_materialisation():
+    """Peak extra memory of the call stays below B*M*N*elt (what materialising
+    one bf16 gradient per sample would take)."""
+    B, K, M, N = 8, 1024, 3072, 768
+    x = torch.randn(B, K, N, device=DEV, dtype=torch.bfloat16)
+    g = torch.randn(B, K, M, device=DEV, dtype=torch.bfloat16) * 0.02
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats()
+    base = torch.cuda.memory_allocated()
+    out = core.wgrad_clip(g, x, 1.0, 1.0)
+    torch.cuda.synchronize()
+    extra = torch.cuda.max_memory_allocated() - base
+    assert extra < B * M * N * 2, extra
+    del out

@@ -1,0 +1,168 @@
+"""Host-side logic that runs without a GPU: the wrap API's selection rules
+(flashdp/api/wrap_model.py:17-211), layer constructors and attributes, and the
+absence of any CPU fallback."""
+import pytest
+import torch
+import torch.nn as nn
+
+import flashdp4review_amd as fdp
+from flashdp4review_amd import DPConv1D, DPLayerNorm, DPLinear, wrap_with_flashdp_layers
+from flashdp4review_amd.core import bmtm_clip, colsum_clip, wgrad_clip
+from flashdp4review_amd.core.clip_fn import clip_args_of
+from flashdp4review_amd.layers.utils import DPParameter, as_btf, noise_std
+
+transformers = pytest.importorskip("transformers.pytorch_utils")
+Conv1D = transformers.Conv1D
+
+
+class Block(nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.ln = nn.LayerNorm(8)
+        self.fc = nn.Linear(8, 16)
+        self.proj = nn.Linear(16, 8, bias=False)
+        self.attn = Conv1D(24, 8)
+
+
+class Net(nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.h = nn.ModuleList([Block(), Block()])
+        self.ln_f = nn.LayerNorm(8)
+        self.lm_head = nn.Linear(8, 10, bias=False)
+
+
+def kinds(model):
+    return {n: type(m).__name__ for n, m in model.named_modules() if n}
+
+
+def test_public_surface():
+    for name in ["DPLinear", "DPLayerNorm", "DPConv1D", "wrap_with_flashdp_layers",
+                 "dp_supported_modules"]:
+        assert hasattr(fdp, name)
+    assert fdp.dp_supported_modules[nn.Linear] is DPLinear
+    assert fdp.dp_supported_modules[nn.LayerNorm] is DPLayerNorm
+    assert fdp.dp_supported_modules[Conv1D] is DPConv1D
+
+
+def test_wrap_skip_lm_head_and_copy_weights():
+    torch.manual_seed(0)
+    m = Net()
+    before = {k: v.clone() for k, v in m.state_dict().items()}
+    wrap_with_flashdp_layers(m, target_modules=[nn.Linear, nn.LayerNorm, Conv1D],
+                             skip_layers=["lm_head"], C=0.5, noise_multiplier=0.3)
+    k = kinds(m)
+    assert k["lm_head"] == "Linear"
+    assert k["h.0.fc"] == "DPLinear" and k["h.1.proj"] == "DPLinear"
+    assert k["h.0.ln"] == "DPLayerNorm" and k["ln_f"] == "DPLayerNorm"
+    assert k["h.0.attn"] == "DPConv1D"
+    assert m.h[0].proj.bias is None and m.h[0].fc.bias is not None
+    assert m.h[0].fc.C == 0.5 and m.h[0].fc.noise_multiplier == 0.3
+    assert m.h[0].attn.weight.shape == (8, 24)
+    for key, val in m.state_dict().items():
+        assert torch.equal(val, before[key]), key
+    assert isinstance(m.h[0].fc.weight, DPParameter) and m.h[0].fc.weight.requires_dp
+
+
+def test_wrap_only_selected_types():
+    m = Net()
+    wrap_with_flashdp_layers(m, target_modules=[nn.LayerNorm])
+    k = kinds(m)
+    assert k["h.0.ln"] == "DPLayerNorm" and k["h.0.fc"] == "Linear" and k["lm_head"] == "Linear"
+
+
+def test_wrap_skip_parent_does_not_skip_children():
+    """Selection matches names exactly (wrap_model.py:169-182): skipping 'h.0'
+    still wraps 'h.0.fc'."""
+    m = Net()
+    wrap_with_flashdp_layers(m, target_modules=[nn.Linear], skip_layers=["h.0"])
+    assert kinds(m)["h.0.fc"] == "DPLinear"
+
+
+def test_wrap_target_layers_and_priority():
+    m = Net()
+    wrap_with_flashdp_layers(m, target_modules=[nn.Linear], target_layers=["h.0.fc", "lm_head"],
+                             skip_layers=["lm_head"])
+    k = kinds(m)
+    assert k["h.0.fc"] == "DPLinear" and k["lm_head"] == "Linear" and k["h.1.fc"] == "Linear"
+    m = Net()
+    wrap_with_flashdp_layers(m, target_modules=[nn.Linear], target_layers=["lm_head"],
+                             skip_layers=["lm_head"], priority_to_target=True)
+    assert kinds(m)["lm_head"] == "Linear"  # set difference either way (wrap_model.py:177-180)
+
+
+def test_wrap_errors():
+    with pytest.raises(ValueError):
+        wrap_with_flashdp_layers(Net())
+    with pytest.raises(ValueError):
+        wrap_with_flashdp_layers(Net(), target_modules=[])
+    with pytest.raises(ValueError):
+        wrap_with_flashdp_layers(Net(), target_modules=[nn.Conv2d])
+
+
+def test_wrap_messages(capsys):
+    """Skip names are validated after prefix expansion against the model's own
+    names (wrap_model.py:83,91-92), so an unknown name expands to nothing and
+    draws no warning; an unused module type does."""
+    wrap_with_flashdp_layers(Net(), target_modules=[nn.Linear], skip_layers=["nope"])
+    out = capsys.readouterr().out
+    assert "Warning" not in out
+    assert "Layers Skipped: nope" in out and "Model wrapped with FlashDP." in out
+
+    class Tiny(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.fc = nn.Linear(2, 2)
+
+    wrap_with_flashdp_layers(Tiny(), target_modules=[nn.Linear, nn.LayerNorm])
+    assert "Module type 'LayerNorm' specified in target_modules is not used" in capsys.readouterr().out
+
+
+def test_wrap_preserves_dtype():
+    m = Net().to(torch.bfloat16)
+    wrap_with_flashdp_layers(m, target_modules=[nn.Linear, nn.LayerNorm, Conv1D])
+    for p in m.parameters():
+        assert p.dtype == torch.bfloat16
+
+
+def test_layer_constructors():
+    lin = DPLinear(4, 3, bias=False)
+    assert lin.bias is None and lin.dp and lin.C == 1.0
+    lin = DPLinear(4, 3, bias=None)
+    assert lin.bias is None
+    lin = DPLinear(4, 3, bias=torch.zeros(3), C=2.0, clamp_value=0.5, noise_multiplier=0.1)
+    assert lin.bias is not None and lin.clamp_value == 0.5
+    ln = DPLayerNorm(8)
+    assert ln.use_fused and ln.normalized_shape == (8,)
+    with pytest.raises(NotImplementedError):
+        DPLayerNorm(8, bias=False)  # fused mode needs a bias (layers/layernorm.py:44-45)
+    ln = DPLayerNorm(8, bias=False, use_fused=False)
+    assert ln.bias is None
+    conv = DPConv1D(6, 4)
+    assert conv.weight.shape == (4, 6) and conv.bias.shape == (6,)
+
+
+def test_no_cpu_fallback():
+    a = torch.randn(2, 4, 3)
+    b = torch.randn(2, 4, 5)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        wgrad_clip(a, b)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        bmtm_clip(a, b, torch.tensor([1.0, 1.0]))
+    with pytest.raises(RuntimeError, match="GPU only"):
+        colsum_clip(a)
+    lin = DPLinear(3, 5)
+    x = torch.randn(2, 4, 3, requires_grad=True)
+    y = lin(x)  # forward is a plain GEMM
+    with pytest.raises(RuntimeError, match="GPU only"):
+        y.sum().backward()
+
+
+def test_helpers():
+    assert as_btf(torch.zeros(3, 5)).shape == (3, 1, 5)
+    assert as_btf(torch.zeros(3, 2, 4, 5)).shape == (3, 8, 5)
+    assert noise_std(1.0, 4) == 0.5
+    assert clip_args_of(torch.tensor([2.0, 0.5]), torch.device("cuda", 0))[:2] == (2.0, 0.5)
+    assert clip_args_of((3, 1), torch.device("cpu")) == (3.0, 1.0, None)
+    with pytest.raises(ValueError):
+        clip_args_of(torch.tensor([1.0, 2.0, 3.0]), torch.device("cpu"))
