@@ -21,6 +21,7 @@ FDP_F32, FDP_F16, FDP_BF16 = 0, 1, 2
 LAYOUT_TN, LAYOUT_NN = 0, 1
 NORM_SUM, NORM_FROB = 0, 1
 WGRAD_NOCLIP = 1
+WGRAD_TWO_PASS = 2
 
 _DTYPE_CODES = {torch.float32: FDP_F32, torch.float16: FDP_F16, torch.bfloat16: FDP_BF16}
 

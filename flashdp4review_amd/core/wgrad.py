@@ -29,13 +29,17 @@ def wgrad_clip(a: torch.Tensor, b: torch.Tensor, C: float = 1.0, clamp_value: fl
                layout: str = "tn", clip_args=None, out_scale: float = 1.0,
                noise: torch.Tensor | None = None, noise_scale: float = 1.0,
                out_dtype: torch.dtype | None = None, out: torch.Tensor | None = None,
-               return_stats: bool = False, noclip: bool = False):
+               return_stats: bool = False, noclip: bool = False, two_pass: bool = False,
+               check: bool = False):
     """out = out_scale * sum_b c_b G_b + noise_scale * noise, c_b = clip(||G_b||_F).
 
     layout "tn": a [B,K,M], b [B,K,N], G_b = a_b^T b_b;
     layout "nn": a [B,M,K], b [B,K,N], G_b = a_b b_b.
     ``clip_args`` (tensor [C, clamp] or pair) overrides C / clamp_value.
     With ``return_stats`` also returns the fp32 per-sample norms and factors.
+    ``two_pass`` forces the norm-pass + clipped-sum-pass schedule instead of the
+    single-pass cooperative kernel.  ``check`` synchronises and raises if a
+    bounded inter-workgroup wait of the single-pass kernel expired.
     """
     dev = _lib.require_hip(a, b, noise, out)
     if a.dtype != b.dtype:
@@ -73,7 +77,7 @@ def wgrad_clip(a: torch.Tensor, b: torch.Tensor, C: float = 1.0, clamp_value: fl
     if return_stats:
         factors = torch.empty(Bn, dtype=torch.float32, device=dev)
         norms = None if noclip else torch.empty(Bn, dtype=torch.float32, device=dev)
-    flags = _lib.WGRAD_NOCLIP if noclip else 0
+    flags = (_lib.WGRAD_NOCLIP if noclip else 0) | (_lib.WGRAD_TWO_PASS if two_pass else 0)
     L = _lib.lib()
     nbytes = _lib.size_query(L.fdp_wgrad_clip_workspace_size, Bn, K, M, N, dt, flags)
     ws = _lib.workspace(nbytes, dev)
@@ -84,6 +88,8 @@ def wgrad_clip(a: torch.Tensor, b: torch.Tensor, C: float = 1.0, clamp_value: fl
         out.stride(0), odt, _lib.ptr(norms), _lib.ptr(factors), flags, ws.data_ptr(), ws.numel(),
         _lib.stream_handle(dev))
     _lib.check(st, "fdp_wgrad_clip")
+    if check and int(ws[:4].view(torch.int32).item()) != 0:
+        raise _lib.FlashDPError("fdp_wgrad_clip: an inter-workgroup wait timed out")
     if return_stats:
         return out, norms, factors
     return out

@@ -96,10 +96,17 @@ int fdp_version(void);
  * norms    : NULL or [B] fp32, ||G_b||_F.
  * factors  : NULL or [B] fp32, c_b.
  * flags    : bit 0 (FDP_WGRAD_NOCLIP) skips the norm pass and uses c_b = clamp
- *            (a plain batched product sum; `norms` must then be NULL).
+ *            (a plain batched product sum; `norms` must then be NULL);
+ *            bit 1 (FDP_WGRAD_TWO_PASS) forces the two-pass schedule (norm
+ *            pass, then clipped-sum pass) instead of the single-pass
+ *            cooperative kernel the library uses whenever the problem fits it.
  * workspace: device buffer of at least fdp_wgrad_clip_workspace_size() bytes.
+ *            Its first int is a status word: nonzero after the call completes
+ *            means a bounded inter-workgroup wait of the single-pass kernel
+ *            expired (results are then invalid).
  * ---------------------------------------------------------------------- */
 #define FDP_WGRAD_NOCLIP 1
+#define FDP_WGRAD_TWO_PASS 2
 
 int fdp_wgrad_clip_workspace_size(int64_t B, int64_t K, int64_t M, int64_t N,
                                   int dtype, int flags, size_t* bytes);

@@ -24,32 +24,36 @@ def make(B, K, M, N, dtype, layout, seed=0, scale_b=0.02):
 
 
 SHAPES = [
-    (4, 128, 768, 768),   # cfg1 per-layer shape
-    (3, 37, 100, 70),     # ragged in every dimension
+    (4, 128, 768, 768),   # cfg1 per-layer shape; one unit per workgroup, 4-way tile hand-over
+    (3, 37, 100, 70),     # ragged in every dimension, unaligned rows
+    (3, 37, 104, 72),     # ragged tiles, aligned rows (single-pass kernel)
     (2, 64, 130, 257),    # odd N: unaligned rows, scalar loads
     (1, 1, 16, 16),       # B = 1, T = 1
     (5, 200, 64, 300),
-    (16, 16, 256, 256),   # many samples, short contraction
+    (16, 16, 256, 256),   # many samples, short contraction; 16-way tile hand-over
+    (8, 64, 392, 520),    # several units per workgroup
 ]
 
 
+@pytest.mark.parametrize("path", ["auto", "two_pass"])
 @pytest.mark.parametrize("dtype", DTYPES, ids=str)
 @pytest.mark.parametrize("layout", ["tn", "nn"])
 @pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
-def test_wgrad_parity(shape, layout, dtype):
+def test_wgrad_parity(shape, layout, dtype, path):
     B, K, M, N = shape
     a, b = make(B, K, M, N, dtype, layout)
     _, norms_ref, _ = O.wgrad_clip(a, b, 1.0, 1.0, layout)
     # choose C inside the norm range so that some samples clip and some do not
     C = float(np.median(norms_ref)) if B > 1 else float(norms_ref[0]) * 0.5
     ref, norms_ref, fac_ref = O.wgrad_clip(a, b, C, 1.0, layout)
+    tp = path == "two_pass"
     out, norms, fac = core.wgrad_clip(a, b, C, 1.0, layout=layout, out_dtype=torch.float32,
-                                      return_stats=True)
+                                      return_stats=True, two_pass=tp, check=True)
     assert_close(out, ref, dtype, "out")
     assert_elementwise(norms, norms_ref, dtype, "norms")
     assert_elementwise(fac, fac_ref, dtype, "factors")
     # output in the input dtype (what the layers write)
-    out2 = core.wgrad_clip(a, b, C, 1.0, layout=layout)
+    out2 = core.wgrad_clip(a, b, C, 1.0, layout=layout, two_pass=tp, check=True)
     assert out2.dtype == dtype
     assert_close(out2, ref, dtype, "out (input dtype)")
 
@@ -87,11 +91,13 @@ def test_wgrad_special_cases(dtype):
     assert_close(out, ref, dtype, "noclip")
 
 
-def test_wgrad_deterministic():
+@pytest.mark.parametrize("two_pass", [False, True])
+def test_wgrad_deterministic(two_pass):
     a, b = make(8, 256, 512, 384, torch.bfloat16, "tn", seed=7)
-    o1 = core.wgrad_clip(a, b, 0.5, 1.0)
-    o2 = core.wgrad_clip(a, b, 0.5, 1.0)
-    assert torch.equal(o1, o2)
+    o1 = core.wgrad_clip(a, b, 0.5, 1.0, two_pass=two_pass, check=True)
+    for _ in range(3):
+        o2 = core.wgrad_clip(a, b, 0.5, 1.0, two_pass=two_pass, check=True)
+        assert torch.equal(o1, o2)
 
 
 def test_wgrad_does_not_modify_inputs():
@@ -134,7 +140,8 @@ def test_wgrad_cfg2_full_size(dtype):
     torch.manual_seed(0)
     x = torch.randn(8, 1024, 768, device=DEV).to(dtype)
     g = (torch.randn(8, 1024, 3072, device=DEV) * 0.02).to(dtype)
-    out, norms, fac = core.wgrad_clip(g, x, 1.0, 1.0, out_dtype=torch.float32, return_stats=True)
+    out, norms, fac = core.wgrad_clip(g, x, 1.0, 1.0, out_dtype=torch.float32, return_stats=True,
+                                      check=True)
     G = torch.bmm(g.float().transpose(1, 2).contiguous(), x.float())  # [8, 3072, 768]
     n_ref = G.flatten(1).norm(dim=1)
     c_ref = torch.clamp(1.0 / (n_ref + 1e-10), max=1.0)
