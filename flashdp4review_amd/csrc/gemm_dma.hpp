@@ -1,0 +1,255 @@
+// Asynchronous MFMA tile product for gfx950: LDS-DMA operand ring +
+// transposing LDS reads.
+//
+// Computes acc += A^T B for one BM x BN output tile where both operands are
+// stored with the contraction axis k as the strided axis (A: [K, M], B: [K, N],
+// the layout of every per-sample weight gradient g_b^T x_b).  Four waves split
+// the tile 2 x 2; each wave owns (BM/2) x (BN/2) outputs as blocks of 32x32
+// v_mfma_f32_32x32x16_{bf16,f16} accumulators.
+//
+//  * Global -> LDS: buffer_load_dwordx4 ... lds (16 bytes per lane straight into
+//    LDS, no VGPR staging).  A 64(k) x R tile of 16-bit values is rows of R/8
+//    chunks of 16 bytes; lane l of a wave's load j fills the next 64 slots in
+//    order, i.e. slot -> row k = slot / (R/8), physical chunk slot % (R/8), and
+//    the lane loads logical chunk (physical ^ swz(k)) of that row: every row is
+//    still one contiguous read, and the XOR swizzle puts the 4 rows x 4 chunks
+//    that half a wave reads in one transposing read onto 16 distinct 16-byte
+//    bank groups.  The buffer resource's record count is the sample's K*ld*2
+//    bytes, so rows past K read as zeros (columns past M/N may carry the next
+//    row's values; callers ignore those rows/columns).
+//  * S LDS stages, each a separate __shared__ object so that the compiler's
+//    wait-count pass can tell the stage being filled from the one being read:
+//    while stage kt is consumed, the loads of the next S-2 k-tiles are in flight
+//    and waits are explicit s_waitcnt vmcnt(n).
+//  * LDS -> MFMA: ds_read_b64_tr_b16.  In a group of 16 lanes, lane r fetches 4
+//    consecutive 16-bit values at its address and lane i receives value i%4 of
+//    the fetches of lanes i/4, 4+i/4, 8+i/4, 12+i/4.  With lane r pointing at
+//    row k0 + r/4, column m0 + 4(r%4), lane i thus holds rows k0..k0+3 of
+//    column m0 + i: two such reads give the 8 consecutive k-values one lane
+//    contributes to a 32x32x16 MFMA operand.
+#pragma once
+
+#include "fdp_common.hpp"
+
+namespace fdp {
+namespace dma {
+
+#define FDP_LDS __attribute__((address_space(3)))
+
+typedef __attribute__((__vector_size__(4 * sizeof(short)))) short i16x4;
+
+constexpr int kBK = 64;
+constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, 32-bit records
+
+__device__ __forceinline__ int swz(int k) { return (k & 3) << 2; }
+
+// Tile geometry: BM x BN outputs, 4 waves in 2 x 2, each (BM/2) x (BN/2).
+template <int BM_, int BN_>
+struct Geom {
+  static constexpr int BM = BM_;
+  static constexpr int BN = BN_;
+  static constexpr int WM = BM / 2;       // wave tile rows
+  static constexpr int WN = BN / 2;       // wave tile columns
+  static constexpr int FI = WM / 32;      // 32-row MFMA blocks per wave
+  static constexpr int FJ = WN / 32;      // 32-column MFMA blocks per wave
+  static constexpr int TILE_A = kBK * BM * 2;
+  static constexpr int TILE_B = kBK * BN * 2;
+  static constexpr int STAGE = TILE_A + TILE_B;
+  static constexpr int LOADS_A = TILE_A / (4 * 64 * 16);  // per wave per k-tile
+  static constexpr int LOADS_B = TILE_B / (4 * 64 * 16);
+  static constexpr int LOADS = LOADS_A + LOADS_B;
+};
+
+// One operand's per-thread load state: L buffer loads per k-tile.
+template <int L>
+struct Operand {
+  __amdgpu_buffer_rsrc_t rsrc;
+  uint32_t voff[L];  // byte offsets of this thread's loads for k-tile 0
+  uint32_t step;     // bytes per k-tile (64 rows)
+
+  // base: the sample's operand [K, ld] (16-bit); R: tile width; r0: first column.
+  template <int R>
+  __device__ inline void init(const uint16_t* base, int64_t ld, int64_t K, int64_t r0) {
+    constexpr int CPR = R / 8;  // 16-byte chunks per row
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), static_cast<short>(0),
+                                             static_cast<int>(K * ld * 2), kRsrcWord3);
+#pragma unroll
+    for (int j = 0; j < L; ++j) {
+      const int slot = (wave * L + j) * 64 + lane;
+      const int k = slot / CPR;
+      const int c = (slot % CPR) ^ swz(k);
+      voff[j] = static_cast<uint32_t>((int64_t(k) * ld + r0 + 8 * c) * 2);
+    }
+    step = static_cast<uint32_t>(kBK * ld * 2);
+  }
+
+  __device__ __forceinline__ void issue(FDP_LDS char* tile, int kt) const {
+    const int wave = threadIdx.x >> 6;
+    const uint32_t add = step * static_cast<uint32_t>(kt);
+#pragma unroll
+    for (int j = 0; j < L; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rsrc, reinterpret_cast<FDP_LDS void*>(tile + (wave * L + j) * 1024), 16, voff[j] + add,
+          0, 0, 0);
+  }
+};
+
+// Byte offset (inside a tile of row width R, k-step 0) of this lane's
+// transposing read for MFMA rows w0 + 32i .. +31, k sub-group h.
+template <int R>
+__device__ __forceinline__ uint32_t frag_off(int w0, int i, int h) {
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 4, r = lane & 15;
+  const int m = w0 + 32 * i + 16 * (g & 1) + 4 * (r & 3);
+  const int k = 8 * (g >> 1) + 4 * h + (r >> 2);
+  return static_cast<uint32_t>(k * (R * 2) + (((m >> 3) ^ swz(k)) * 16) + ((m >> 2) & 1) * 8);
+}
+
+template <class G>
+struct FragOffsets {
+  uint32_t a[G::FI][2], b[G::FJ][2];
+  __device__ __forceinline__ void init(int wm, int wn) {
+#pragma unroll
+    for (int i = 0; i < G::FI; ++i)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) a[i][h] = frag_off<G::BM>(wm, i, h);
+#pragma unroll
+    for (int j = 0; j < G::FJ; ++j)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) b[j][h] = frag_off<G::BN>(wn, j, h) + G::TILE_A;
+  }
+};
+
+__device__ __forceinline__ uint4 read_frag(const FDP_LDS char* stage, uint32_t o0, uint32_t o1) {
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      reinterpret_cast<FDP_LDS i16x4*>(const_cast<FDP_LDS char*>(stage) + o0));
+  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      reinterpret_cast<FDP_LDS i16x4*>(const_cast<FDP_LDS char*>(stage) + o1));
+  uint4 v;
+  v.x = uint32_t(uint16_t(lo[0])) | (uint32_t(uint16_t(lo[1])) << 16);
+  v.y = uint32_t(uint16_t(lo[2])) | (uint32_t(uint16_t(lo[3])) << 16);
+  v.z = uint32_t(uint16_t(hi[0])) | (uint32_t(uint16_t(hi[1])) << 16);
+  v.w = uint32_t(uint16_t(hi[2])) | (uint32_t(uint16_t(hi[3])) << 16);
+  return v;
+}
+
+template <class DT>
+__device__ __forceinline__ f32x16 mfma16(uint4 a, uint4 b, f32x16 c) {
+  if constexpr (DT::code == FDP_BF16) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+}
+
+// Fragments of one 16-deep k-step.
+template <class G>
+struct Frags {
+  uint4 a[G::FI], b[G::FJ];
+  __device__ __forceinline__ void load(const FDP_LDS char* st, const FragOffsets<G>& fo, int ks) {
+#pragma unroll
+    for (int j = 0; j < G::FJ; ++j)
+      b[j] = read_frag(st, fo.b[j][0] + ks * 16 * G::BN * 2, fo.b[j][1] + ks * 16 * G::BN * 2);
+#pragma unroll
+    for (int i = 0; i < G::FI; ++i)
+      a[i] = read_frag(st, fo.a[i][0] + ks * 16 * G::BM * 2, fo.a[i][1] + ks * 16 * G::BM * 2);
+  }
+};
+
+// One 64-deep k-tile of the wave's sub-tile from LDS stage `st`.
+template <class DT, class G>
+__device__ __forceinline__ void compute_stage(const FDP_LDS char* st, const FragOffsets<G>& fo,
+                                              f32x16 (&acc)[G::FI][G::FJ]) {
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    Frags<G> f;
+    f.load(st, fo, ks);
+#pragma unroll
+    for (int i = 0; i < G::FI; ++i)
+#pragma unroll
+      for (int j = 0; j < G::FJ; ++j) acc[i][j] = mfma16<DT>(f.a[i], f.b[j], acc[i][j]);
+  }
+}
+
+// s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xf) | (0x7 << 4) | (0xf << 8) | ((N >> 4) << 14));
+}
+// Wait until at most `tiles` k-tiles (L loads each) of this thread's loads are outstanding.
+template <int L>
+__device__ __forceinline__ void wait_tiles(int tiles) {
+  switch (tiles) {
+    case 0: wait_vm<0>(); break;
+    case 1: wait_vm<L>(); break;
+    default: wait_vm<2 * L>(); break;
+  }
+}
+
+// Workgroup barrier that also completes this wave's LDS reads and keeps the
+// compiler from moving memory operations across it.  (A __syncthreads() would
+// add a vmcnt(0) wait for the in-flight LDS-DMA loads, serialising the ring.)
+__device__ __forceinline__ void barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// The S stages live in separate __shared__ objects owned by the kernel.
+struct Stages {
+  FDP_LDS char* s[4];
+  __device__ __forceinline__ FDP_LDS char* get(int i) const {
+    switch (i) {
+      case 0: return s[0];
+      case 1: return s[1];
+      case 2: return s[2];
+      default: return s[3];
+    }
+  }
+};
+
+// Per-thread state of one (tile, sample) product.
+template <class G>
+struct Job {
+  Operand<G::LOADS_A> a;
+  Operand<G::LOADS_B> b;
+  __device__ __forceinline__ void init(const uint16_t* pa, int64_t lda, const uint16_t* pb,
+                                       int64_t ldb, int64_t K, int64_t m0, int64_t n0) {
+    a.template init<G::BM>(pa, lda, K, m0);
+    b.template init<G::BN>(pb, ldb, K, n0);
+  }
+  __device__ __forceinline__ void issue(FDP_LDS char* stage, int kt) const {
+    a.issue(stage, kt);
+    b.issue(stage + G::TILE_A, kt);
+  }
+};
+
+// acc += A_tile^T B_tile over nk k-tiles with an S-stage ring (S in {2, 3, 4}).
+template <class DT, class G, int S>
+__device__ inline void gemm(const Job<G>& job, int nk, const FragOffsets<G>& fo, const Stages& st,
+                            f32x16 (&acc)[G::FI][G::FJ]) {
+  static_assert(S >= 2 && S <= 4, "stages");
+  wait_vm<0>();  // no older vector-memory operation may confuse the counting below
+#pragma unroll
+  for (int s = 0; s < S - 1; ++s)
+    if (s < nk) job.issue(st.get(s), s);
+  for (int base = 0; base < nk; base += S) {
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const int kt = base + s;
+      if (kt < nk) {
+        const int ahead = nk - 1 - kt;
+        wait_tiles<G::LOADS>(ahead < S - 2 ? ahead : S - 2);
+        barrier();
+        if (kt + S - 1 < nk) job.issue(st.get((s + S - 1) % S), kt + S - 1);
+        compute_stage<DT, G>(st.get(s), fo, acc);
+      }
+    }
+  }
+  barrier();  // every wave is done reading before the ring is reused
+}
+
+}  // namespace dma
+}  // namespace fdp

@@ -182,18 +182,19 @@ namespace {
 constexpr size_t kAlign = 256;
 inline size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
-constexpr int64_t kMaxFusedB = 16384;  // clip factors staged in 64 KB of LDS
 
-// Workspace layout (both paths):
+// Workspace layout (both schedules):
 //   [0, 256)            err word (int), barrier word (uint)
-//   off_turn            tile_turn [tiles] (uint)
+//   off_turn            per-tile counters [tiles] (uint)
 //   off_partials        partials [B, tiles] (fp32)
 //   two-pass:  off_factors [B], off_group [groups, M, N] (fp32)
-//   one-pass:  off_acc [tiles, BM*BN] (fp32) for tiles shared by workgroups
+//   one-pass:  off_slots [groups, tiles, BM*BN] (fp32) per-group tile sums,
+//              off_chunk [M, N] (fp32) running sum when the batch needs
+//              more than one launch
 struct Plan {
   int tiles_m, tiles_n, tiles;
   int spg, groups;
-  size_t off_turn, off_partials, off_factors, off_group, off_acc;
+  size_t off_turn, off_partials, off_factors, off_group, off_slots, off_chunk;
   size_t total_two_pass, total_fused, total;
 };
 
@@ -221,15 +222,21 @@ Plan make_plan(int64_t B, int64_t M, int64_t N, int cus) {
   if (want < 1) want = 1;
   pl.spg = static_cast<int>((B + want - 1) / want);
   pl.groups = static_cast<int>((B + pl.spg - 1) / pl.spg);
-  pl.off_turn = kAlign;
+  pl.off_turn = kWsHead;
   pl.off_partials = pl.off_turn + align_up(sizeof(unsigned) * size_t(pl.tiles));
   const size_t after_partials = pl.off_partials + align_up(sizeof(float) * size_t(B) * pl.tiles);
   pl.off_factors = after_partials;
   pl.off_group = pl.off_factors + align_up(sizeof(float) * size_t(B));
   pl.total_two_pass =
       pl.off_group + (pl.groups > 1 ? align_up(sizeof(float) * size_t(pl.groups) * M * N) : 0);
-  pl.off_acc = after_partials;
-  pl.total_fused = pl.off_acc + sizeof(float) * size_t(pl.tiles) * BM * BN;
+  const GroupPlan gp = group_plan(B, pl.tiles, 2 * cus);
+  pl.off_slots = after_partials;
+  pl.off_chunk = pl.off_slots;
+  pl.total_fused = 0;
+  if (gp.groups > 0) {
+    pl.off_chunk += gp.groups > 1 ? sizeof(float) * size_t(gp.groups) * pl.tiles * BM * BN : 0;
+    pl.total_fused = pl.off_chunk + (gp.chunk < B ? sizeof(float) * size_t(M) * N : 0);
+  }
   pl.total = pl.total_two_pass > pl.total_fused ? pl.total_two_pass : pl.total_fused;
   return pl;
 }
@@ -343,7 +350,8 @@ extern "C" int fdp_wgrad_clip(const void* a, const void* b, int64_t B, int64_t K
   args.err = reinterpret_cast<int*>(ws);
   args.bar = reinterpret_cast<unsigned*>(ws) + 1;
   args.tile_turn = reinterpret_cast<unsigned*>(ws + pl.off_turn);
-  args.tile_acc = reinterpret_cast<float*>(ws + pl.off_acc);
+  args.tile_acc = reinterpret_cast<float*>(ws + pl.off_slots);
+  args.chunk_acc = reinterpret_cast<float*>(ws + pl.off_chunk);
   args.C = C;
   args.clamp = clamp;
   args.clip_args_dev = clip_args_dev;
@@ -358,13 +366,11 @@ extern "C" int fdp_wgrad_clip(const void* a, const void* b, int64_t B, int64_t K
                    ldb % vel == 0 && stride_ab % vel == 0 && stride_bb % vel == 0;
 
   hipStream_t s = static_cast<hipStream_t>(stream);
-  // Single pass: TN layout, aligned rows, a clip to compute, K > 0.
+  // Single pass: 16-bit inputs, TN layout, aligned rows, a clip to compute, K > 0.
   if (!noclip && (flags & FDP_WGRAD_TWO_PASS) == 0 && layout == FDP_LAYOUT_TN && vec && K > 0 &&
-      B <= kMaxFusedB) {
-    hipError_t e;
-    if (dtype == FDP_BF16) e = launch_fused_bf16(args, cus, s);
-    else if (dtype == FDP_F16) e = launch_fused_f16(args, cus, s);
-    else e = launch_fused_f32(args, cus, s);
+      dtype != FDP_F32 && pl.total_fused > 0) {
+    const hipError_t e = dtype == FDP_BF16 ? launch_grouped_bf16(args, cus, s)
+                                           : launch_grouped_f16(args, cus, s);
     if (e == hipSuccess) return FDP_OK;
     if (e != hipErrorNotSupported && e != hipErrorCooperativeLaunchTooLarge) {
       (void)hipGetLastError();

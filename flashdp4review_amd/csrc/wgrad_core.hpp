@@ -5,6 +5,7 @@
 #pragma once
 
 #include "fdp_common.hpp"
+#include "gemm_dma.hpp"
 
 namespace fdp {
 namespace wg {
@@ -41,6 +42,10 @@ struct Args {
   const float* clip_args_dev;
   float* norms_out;       // optional [B]
   float* factors_out;     // optional [B]
+  // grouped single-pass kernel: this launch covers samples [chunk_b0, chunk_b0+chunk_nb)
+  int64_t chunk_b0, chunk_nb;
+  int chunk_first, chunk_last;
+  float* chunk_acc;       // [M, N] fp32 running sum carried between chunks
 };
 
 // ------------------------------------------------------------------ 16-bit
@@ -52,6 +57,7 @@ __device__ __forceinline__ int lds16_off(int row, int chunk) {
 
 template <class DT>
 struct Core16 {
+  using dtype = DT;
   static constexpr int BK = 64;
   static constexpr int TILE_BYTES = 128 * 128;  // one operand tile
   static constexpr int SMEM = 4 * TILE_BYTES;   // 2 operands x 2 buffers
@@ -362,51 +368,36 @@ __device__ __forceinline__ void tile_coords(const Args& p, int tile, int64_t& m0
 }
 
 // ============================================================ single pass
-// Persistent cooperative kernel.  The tiles*B units (tile, sample) are split
-// into nwg contiguous ranges, sample-minor, so a workgroup's units cover a few
-// consecutive tiles for consecutive samples.  Logical workgroup ids are laid out
-// so that each of the 8 XCDs runs a contiguous block of ranges (the hardware
-// deals workgroups round-robin over the XCDs), which keeps a block's operand
-// rows in that XCD's L2.
-//
-// Phase 1: every unit's 128x128 tile of G_b is computed on MFMA; its sum of
-//   squares goes to partials[b, tile] and the tile itself stays in registers
-//   (packed to bf16 pairs for 16-bit inputs, fp32 otherwise).
-// Grid barrier (all workgroups are co-resident: cooperative launch).
-// Phase 2: every workgroup derives all c_b from the partials (same fixed order
-//   everywhere), sums c_b * G_b over its units tile by tile and writes tiles it
-//   owns entirely.  A tile split between consecutive workgroups is handed from
-//   one to the next through tile_acc with a ticket (tile_turn), so its sum is
-//   always formed in workgroup order: deterministic, no float atomics.  Each
-//   workgroup first finishes the tiles where it is the first contributor and
-//   only then waits for its first tile, so hand-over chains are at most as
-//   long as the number of workgroups sharing one tile.
-// Every wait is bounded (kSpinLimit polls); on expiry err is set and the
-// kernel runs to completion, so no wave can be left spinning.
-constexpr unsigned kSpinLimit = 1u << 21;
+// Cross-workgroup exchange in the single-pass kernel.  Values that another
+// workgroup reads (per-tile partial norms, per-group tile sums) are written and
+// read as relaxed agent-scope atomics: on gfx950 these are coherent (sc1)
+// accesses that bypass the per-XCD L2s, so no L2 write-back / invalidate fence
+// is needed; ordering against the counters comes from an explicit
+// s_waitcnt vmcnt(0) before each counter update.  Every wait is bounded
+// (kSpinLimit polls); on expiry err is set and the kernel runs to completion,
+// so no wave is ever left spinning.
+constexpr unsigned kSpinLimit = 1u << 22;
 constexpr int kXcds = 8;
 
-__device__ __forceinline__ int64_t unit_begin(int64_t w, int64_t units, int nwg) {
-  return w * units / nwg;
+__device__ __forceinline__ void st_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-// The workgroup whose range holds unit u.
-__device__ inline int owner_of(int64_t u, int64_t units, int nwg) {
-  int w = static_cast<int>((u * nwg) / units);
-  while (w > 0 && unit_begin(w, units, nwg) > u) --w;
-  while (w + 1 < nwg && unit_begin(w + 1, units, nwg) <= u) ++w;
-  return w;
+__device__ __forceinline__ float ld_coherent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ int logical_wg(int hw, int nwg) {
-  if (nwg % kXcds != 0) return hw;
-  return (hw % kXcds) * (nwg / kXcds) + hw / kXcds;
+__device__ __forceinline__ void wait_stores() {
+  __builtin_amdgcn_s_waitcnt((0 & 0xf) | (0x7 << 4) | (0xf << 8));  // vmcnt(0)
 }
 
-// Thread 0 polls *p until it reaches `target`; acquire for the whole group.
-__device__ inline void wait_at_least(unsigned* p, unsigned target, int* err) {
+// All workgroups of the (co-resident) grid arrive before any leaves.
+__device__ inline void grid_barrier(unsigned* bar, unsigned n, int* err) {
+  wait_stores();
+  __syncthreads();
   if (threadIdx.x == 0) {
+    __hip_atomic_fetch_add(bar, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     unsigned spins = 0;
-    while (__hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) < target) {
-      __builtin_amdgcn_s_sleep(4);
+    while (__hip_atomic_load(bar, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < n) {
+      __builtin_amdgcn_s_sleep(1);
       if (++spins > kSpinLimit) {
         atomicOr(err, 1);
         break;
@@ -414,14 +405,13 @@ __device__ inline void wait_at_least(unsigned* p, unsigned target, int* err) {
     }
   }
   __syncthreads();
-  __threadfence();
 }
 
-__device__ inline void grid_barrier(unsigned* bar, unsigned nwg, int* err) {
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) atomicAdd(bar, 1u);
-  wait_at_least(bar, nwg, err);
+// Workgroups are dealt round-robin to the 8 XCDs; give each XCD a contiguous
+// block of logical ids so that neighbouring work shares that XCD's L2.
+__device__ __forceinline__ int logical_wg(int hw, int nwg) {
+  if (nwg % kXcds != 0) return hw;
+  return (hw % kXcds) * (nwg / kXcds) + hw / kXcds;
 }
 
 template <bool PACK>
@@ -512,126 +502,275 @@ __device__ __forceinline__ int tl_index(int wm, int wn, int i, int j, int lane, 
   return acc_row(wm, i, lane, r) * BN + acc_col(wn, j, lane);
 }
 
-// Finish one tile of this workgroup's range: write it if owned, otherwise take
-// part in the ordered hand-over between the workgroups that share it.
-__device__ inline void finish_tile(const Args& p, int lw, int64_t u0, int64_t u1, int tile,
-                                   f32x16 (&tot)[2][2]) {
-  const int64_t tu0 = int64_t(tile) * p.B, tu1 = tu0 + p.B;
-  if (tu0 >= u0 && tu1 <= u1) {
-    store_tile(p, tile, tot);
-    return;
-  }
-  const int w0 = owner_of(tu0, p.units, p.nwg);
-  const int w1 = owner_of(tu1 - 1, p.units, p.nwg);
-  const int k = lw - w0;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
-  float* buf = p.tile_acc + int64_t(tile) * (BM * BN);
-  if (k > 0) {
-    wait_at_least(p.tile_turn + tile, unsigned(k), p.err);
+#ifdef FDP_PHASE_TIMING
+extern __device__ unsigned long long fdp_phase_ts[1024 * 16];
+#define FDP_TS(slot)                                                  \
+  do {                                                                \
+    if (threadIdx.x == 0 && blockIdx.x < 1024)                        \
+      fdp_phase_ts[blockIdx.x * 16 + (slot)] = wall_clock64();        \
+  } while (0)
+#else
+#define FDP_TS(slot) \
+  do {               \
+  } while (0)
+#endif
+
+
+// 16-byte coherent (sc1) stores/loads for the per-group slot exchange.  A slot
+// is one 128x128 fp32 tile kept in "thread-major" order: float4 q (0..15) of
+// thread t sits at byte (q*256 + t)*16, which makes every wave instruction one
+// contiguous 1 KB access.
+typedef __attribute__((__vector_size__(4 * sizeof(unsigned)))) unsigned u32x4;
+constexpr int kCoherent = 0x10;  // buffer cache policy bit: sc1
+
+__device__ inline void slot_store(float* slot, const f32x16 (&v)[2][2]) {
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(slot, static_cast<short>(0), BM * BN * 4, dma::kRsrcWord3);
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+  for (int a = 0; a < 2; ++a)
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+    for (int c = 0; c < 2; ++c)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) tot[i][j][r] = buf[tl_index(wm, wn, i, j, lane, r)] + tot[i][j][r];
-  }
-  if (lw == w1) {
-    store_tile(p, tile, tot);
-    return;
-  }
+      for (int q = 0; q < 4; ++q) {
+        const int idx = (a * 2 + c) * 4 + q;
+        const f32x4 x = {v[a][c][4 * q], v[a][c][4 * q + 1], v[a][c][4 * q + 2], v[a][c][4 * q + 3]};
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), r,
+                                               (idx * NT + threadIdx.x) * 16, 0, kCoherent);
+      }
+}
+__device__ inline void slot_add(const float* slot, f32x16 (&v)[2][2]) {
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(slot), static_cast<short>(0), BM * BN * 4, dma::kRsrcWord3);
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int a = 0; a < 2; ++a)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int c = 0; c < 2; ++c)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) buf[tl_index(wm, wn, i, j, lane, r)] = tot[i][j][r];
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) atomicAdd(p.tile_turn + tile, 1u);
+      for (int q = 0; q < 4; ++q) {
+        const int idx = (a * 2 + c) * 4 + q;
+        const f32x4 x = __builtin_bit_cast(
+            f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (idx * NT + threadIdx.x) * 16, 0,
+                                                         kCoherent));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[a][c][4 * q + e] += x[e];
+      }
 }
 
-template <class Core, int U, bool PACK>
-__global__ __launch_bounds__(NT) void wgrad_fused_kernel(Args p) {
-  extern __shared__ __attribute__((aligned(16))) char smem[];
-  __shared__ float red[NT / kWave];
+// out[m, n] = out_scale * tot + noise_scale * noise for one 128x128 tile, staged
+// through LDS (rows 0..63 in lo, 64..127 in hi, 32 KB each, fp32) so that the
+// global stores and noise loads are 16-byte row chunks.
+template <class OT>
+__device__ inline void store_tile_staged(const Args& p, int64_t m0, int64_t n0,
+                                         const f32x16 (&tot)[2][2], float* lo, float* hi) {
+  using S = typename OT::storage;
+  constexpr int E = 16 / sizeof(S);  // elements per 16-byte chunk
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int lw = logical_wg(blockIdx.x, p.nwg);
-  const int64_t u0 = unit_begin(lw, p.units, p.nwg);
-  const int64_t u1 = unit_begin(lw + 1, p.units, p.nwg);
-  const int nu = static_cast<int>(u1 - u0);
-  const int tiles = p.tiles_m * p.tiles_n;
+  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+  float* half = wm == 0 ? lo : hi;
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        half[(acc_row(0, a, lane, r)) * BN + acc_col(wn, c, lane)] = tot[a][c][r];
+  __syncthreads();
+  S* out = static_cast<S*>(p.out);
+  const S* noise = static_cast<const S*>(p.noise);
+  const bool vec = (reinterpret_cast<uintptr_t>(out) % 16 == 0) && (p.ldo % E == 0) &&
+                   (noise == nullptr || (reinterpret_cast<uintptr_t>(noise) % 16 == 0 && p.N % E == 0));
+  constexpr int CPR = BN / E;  // chunks per tile row
+  for (int q = threadIdx.x; q < BM * CPR; q += NT) {
+    const int row = q / CPR, col = (q % CPR) * E;
+    const int64_t m = m0 + row, n = n0 + col;
+    if (m >= p.M || n >= p.N) continue;
+    const float* src = (row < 64 ? lo : hi) + (row & 63) * BN + col;
+    float v[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) v[e] = src[e] * p.out_scale;
+    if (vec && n + E <= p.N) {
+      if (noise) {
+        const uint4 nz = *reinterpret_cast<const uint4*>(noise + m * p.N + n);
+        const S* ns = reinterpret_cast<const S*>(&nz);
+#pragma unroll
+        for (int e = 0; e < E; ++e) v[e] += p.noise_scale * OT::to_f32(ns[e]);
+      }
+      uint4 o;
+      S* os = reinterpret_cast<S*>(&o);
+#pragma unroll
+      for (int e = 0; e < E; ++e) os[e] = OT::from_f32(v[e]);
+      *reinterpret_cast<uint4*>(out + m * p.ldo + n) = o;
+    } else {
+      for (int e = 0; e < E && n + e < p.N; ++e) {
+        float x = v[e];
+        if (noise) x += p.noise_scale * OT::to_f32(noise[m * p.N + n + e]);
+        out[m * p.ldo + n + e] = OT::from_f32(x);
+      }
+    }
+  }
+}
 
-  // ---- phase 1: per-unit tile products, partial norms, tiles kept in registers.
-  // One copy of the product loop; the finished tile goes to held[i] through a
-  // branch per slot so that every held[] index is a compile-time constant.
-  Held<PACK> held[U];
-  for (int i = 0; i < nu; ++i) {
-    const int64_t u = u0 + i;
-    const int tile = static_cast<int>(u / p.B);
-    const int64_t bidx = u - int64_t(tile) * p.B;
-    int64_t m0, n0;
-    tile_coords(p, tile, m0, n0);
-    f32x16 acc[2][2];
+// ------------------------------------------------------ grouped single pass
+// Workgroup (tile, g) of a grid of groups x tiles workgroups, two per CU: it
+// runs the 128x128 tile products of the chunk's samples
+// chunk_b0 + g*spg .. + spg-1 on the LDS-DMA core (gemm_dma.hpp), keeping the
+// finished ones packed in AGPRs and the last one live in its accumulators.
+// Each product's sum of squares goes to partials[b, tile]; after the grid
+// barrier every workgroup knows the norms of its own samples, forms
+// sum_b c_b G_b for its tile in sample order and leaves it in its group's
+// slot.  The last group to arrive at a tile sums the slots in group order
+// (deterministic) and writes the output (or the running chunk sum).
+template <class DT, int U>
+__global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
+  using G = dma::Geom<BM, BN>;
+  __shared__ __attribute__((aligned(16))) char st0[G::STAGE];
+  __shared__ __attribute__((aligned(16))) char st1[G::STAGE];
+  __shared__ float red[NT / kWave];
+  __shared__ float fac[U];
+  __shared__ int is_last;
+  const dma::Stages stages{{(FDP_LDS char*)(st0), (FDP_LDS char*)(st1),
+                            (FDP_LDS char*)(st0), (FDP_LDS char*)(st1)}};
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+  const int tiles = p.tiles_m * p.tiles_n;
+  const int lw = logical_wg(blockIdx.x, p.nwg);
+  const int g = lw / tiles, tile = lw % tiles;
+  const int64_t b0 = p.chunk_b0 + int64_t(g) * p.spg;
+  const int64_t bend = p.chunk_b0 + p.chunk_nb;
+  const int nb = static_cast<int>((b0 + p.spg < bend ? b0 + p.spg : bend) - b0);
+  int64_t m0, n0;
+  tile_coords(p, tile, m0, n0);
+  const int nk = static_cast<int>((p.K + dma::kBK - 1) / dma::kBK);
+  dma::FragOffsets<G> fo;
+  fo.init(wm, wn);
+  FDP_TS(0);
+
+  // ---- phase 1
+  Held<true> held[U > 1 ? U - 1 : 1];
+  f32x16 acc[2][2];
+  for (int i = 0; i < nb; ++i) {
+    const int64_t bidx = b0 + i;
+    dma::Job<G> job;
+    job.init(static_cast<const uint16_t*>(p.a) + bidx * p.sab, p.lda,
+             static_cast<const uint16_t*>(p.b) + bidx * p.sbb, p.ldb, p.K, m0, n0);
+#pragma unroll
+    for (int j = 0; j < U - 1; ++j)
+      if (j == i - 1) held[j].put(acc);  // park the previous product
     zero(acc);
-    Core::template gemm<FDP_LAYOUT_TN, true>(p, bidx, m0, n0, acc, smem);
+    dma::gemm<DT, G, 2>(job, nk, fo, stages, acc);
+    // Rows/columns past M/N may hold the next row's values: leave them out.
     float s = 0.f;
 #pragma unroll
     for (int a = 0; a < 2; ++a)
 #pragma unroll
-      for (int c = 0; c < 2; ++c)
+      for (int c = 0; c < 2; ++c) {
+        const bool ncol = n0 + acc_col(wn, c, lane) < p.N;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) s += acc[a][c][r] * acc[a][c][r];
+        for (int r = 0; r < 16; ++r) {
+          const bool in = ncol && (m0 + acc_row(wm, a, lane, r) < p.M);
+          s += in ? acc[a][c][r] * acc[a][c][r] : 0.f;
+        }
+      }
     s = wave_sum(s);
     if (lane == 0) red[wave] = s;
     __syncthreads();
-    if (threadIdx.x == 0) p.partials[bidx * tiles + tile] = (red[0] + red[1]) + (red[2] + red[3]);
-#pragma unroll
-    for (int j = 0; j < U; ++j)
-      if (j == i) held[j].put(acc);
+    if (threadIdx.x == 0)
+      st_coherent(p.partials + bidx * tiles + tile, (red[0] + red[1]) + (red[2] + red[3]));
+    FDP_TS(1 + i);
   }
 
   grid_barrier(p.bar, unsigned(p.nwg), p.err);
+  FDP_TS(9);
 
-  // ---- clip factors of every sample (identical in every workgroup)
+  // ---- clip factors of this group's samples: all partials in one sweep
   float C = p.C, clamp = p.clamp;
   if (p.clip_args_dev != nullptr) {
     C = p.clip_args_dev[0];
     clamp = p.clip_args_dev[1];
   }
-  float* fac = reinterpret_cast<float*>(smem);
-  for (int64_t b = wave; b < p.B; b += NT / kWave) {
-    float s = 0.f;
-    for (int t = lane; t < tiles; t += kWave) s += p.partials[b * tiles + t];
-    const float n = sqrtf(wave_sum(s));
-    if (lane == 0) {
-      const float c = clip_factor(n, C, clamp);
-      fac[b] = c;
-      if (lw == 0) {
-        if (p.norms_out) p.norms_out[b] = n;
-        if (p.factors_out) p.factors_out[b] = c;
+  float ps[U];
+#pragma unroll
+  for (int i = 0; i < U; ++i) {
+    ps[i] = 0.f;
+    if (i < nb)
+      for (int t = threadIdx.x; t < tiles; t += NT) ps[i] += ld_coherent(p.partials + (b0 + i) * tiles + t);
+  }
+#pragma unroll
+  for (int i = 0; i < U; ++i) {
+    const float s = wave_sum(ps[i]);
+    if (lane == 0) red[wave] = s;
+    __syncthreads();
+    if (threadIdx.x == 0 && i < nb) {
+      const float n = sqrtf((red[0] + red[1]) + (red[2] + red[3]));
+      const float cf = clip_factor(n, C, clamp);
+      fac[i] = cf;
+      if (tile == 0) {
+        if (p.norms_out) p.norms_out[b0 + i] = n;
+        if (p.factors_out) p.factors_out[b0 + i] = cf;
       }
     }
+    __syncthreads();
   }
-  __syncthreads();
 
-  // ---- phase 2: clipped sums per tile.  Tiles whose first unit lies in this
-  // range come first (no waiting), the tile begun by an earlier range last.
-  const int t_first = static_cast<int>(u0 / p.B);
-  const int t_last = nu > 0 ? static_cast<int>((u1 - 1) / p.B) : t_first - 1;
-  const bool first_late = (u0 % p.B) != 0 && nu > 0;
-  const int t_begin = first_late ? t_first + 1 : t_first;
-  const int ntiles = t_last - t_first + 1;
-  for (int q = 0; q < ntiles; ++q) {
-    const int tile = (t_begin + q <= t_last) ? t_begin + q : t_first;
-    f32x16 tot[2][2];
-    zero(tot);
+  // ---- phase 2: sum_b c_b G_b, formed in place in the live accumulators as
+  // c_last G_last + c_0 G_0 + c_1 G_1 + ... (a fixed order: deterministic)
+  if (nb > 0) {
+    const float cl = fac[nb - 1];
 #pragma unroll
-    for (int i = 0; i < U; ++i) {
-      const int64_t u = u0 + i;
-      if (i < nu && u / p.B == tile) held[i].add_to(tot, fac[u - int64_t(tile) * p.B]);
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[a][c][r] *= cl;
+  } else {
+    zero(acc);
+  }
+#pragma unroll
+  for (int j = 0; j < U - 1; ++j)
+    if (j < nb - 1) held[j].add_to(acc, fac[j]);
+
+  // ---- combine the groups of this tile: the last to arrive sums the slots
+  const int ngroups = p.groups;
+  if (ngroups > 1) {
+    slot_store(p.tile_acc + (int64_t(g) * tiles + tile) * (BM * BN), acc);
+    wait_stores();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const unsigned old = __hip_atomic_fetch_add(p.tile_turn + tile, 1u, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT);
+      is_last = old == unsigned(ngroups - 1);
     }
-    finish_tile(p, lw, u0, u1, tile, tot);
+    __syncthreads();
+    FDP_TS(10);
+    if (!is_last) return;
+    zero(acc);
+    for (int gg = 0; gg < ngroups; ++gg) slot_add(p.tile_acc + (int64_t(gg) * tiles + tile) * (BM * BN), acc);
+  }
+  FDP_TS(11);
+  // running sum across chunks, then the output
+  if (!p.chunk_first || !p.chunk_last) {
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const int64_t n = n0 + acc_col(wn, c, lane);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t m = m0 + acc_row(wm, a, lane, r);
+          if (m < p.M && n < p.N) {
+            if (!p.chunk_first) acc[a][c][r] += p.chunk_acc[m * p.N + n];
+            if (!p.chunk_last) p.chunk_acc[m * p.N + n] = acc[a][c][r];
+          }
+        }
+      }
+  }
+  if (p.chunk_last) {
+    float* lo = reinterpret_cast<float*>(st0);
+    float* hi = reinterpret_cast<float*>(st1);
+    if (p.out_dtype == FDP_BF16) store_tile_staged<BF16>(p, m0, n0, acc, lo, hi);
+    else if (p.out_dtype == FDP_F16) store_tile_staged<F16>(p, m0, n0, acc, lo, hi);
+    else store_tile_staged<F32>(p, m0, n0, acc, lo, hi);
+    FDP_TS(12);
   }
 }
 
@@ -643,73 +782,69 @@ __global__ __launch_bounds__(NT) void clear_words_kernel(unsigned* p, int64_t n)
 }
 
 // ---------------------------------------------------------- single-pass launch
-constexpr int kMaxUnits16 = 7;  // 8 would spill (AGPRs full)
-constexpr int kMaxUnits32 = 4;
-constexpr size_t kWsHead = 256;  // err / barrier words at the head of the workspace
-
 using KernelFn = void (*)(Args);
+constexpr size_t kWsHead = 256;   // err / barrier words at the head of the workspace
+constexpr int kGroupUnits = 3;    // samples per group held by one workgroup
 
-template <class Core, int U>
-KernelFn fused_fn() {
-  return &wgrad_fused_kernel<Core, U, (U > 2 && Core::SMEM == Core16<BF16>::SMEM)>;
+// Grouped single-pass geometry for B samples over `tiles` 128x128 tiles on
+// `slots` co-resident workgroups: groups per chunk and samples per group.
+struct GroupPlan {
+  int groups, spg;
+  int64_t chunk;  // samples per launch
+};
+inline GroupPlan group_plan(int64_t B, int tiles, int slots) {
+  GroupPlan g{};
+  int64_t G = slots / tiles;
+  if (G < 1) G = 0;
+  if (G > B) G = B;
+  g.groups = static_cast<int>(G);
+  if (G == 0) return g;
+  const int64_t per = (B + G - 1) / G;
+  g.spg = static_cast<int>(per < kGroupUnits ? per : kGroupUnits);
+  // fewest groups that still cover the chunk with spg samples each
+  g.chunk = G * g.spg < B ? G * g.spg : B;
+  g.groups = static_cast<int>((g.chunk + g.spg - 1) / g.spg);
+  return g;
 }
 
-template <class Core>
-KernelFn fused_for_units(int u) {
-  if constexpr (Core::SMEM == Core32::SMEM) {
-    switch (u) {
-      case 1: return fused_fn<Core, 1>();
-      case 2: return fused_fn<Core, 2>();
-      case 3: return fused_fn<Core, 3>();
-      case 4: return fused_fn<Core, 4>();
-      default: return nullptr;
-    }
-  } else {
-    switch (u) {
-      case 1: return fused_fn<Core, 1>();
-      case 2: return fused_fn<Core, 2>();
-      case 3: return fused_fn<Core, 3>();
-      case 4: return fused_fn<Core, 4>();
-      case 5: return fused_fn<Core, 5>();
-      case 6: return fused_fn<Core, 6>();
-      case 7: return fused_fn<Core, 7>();
-      case 8: return fused_fn<Core, 8>();
-      default: return nullptr;
-    }
-  }
-}
-
-// Tries the single-pass kernel; returns hipErrorNotSupported when the problem
-// does not fit it (the caller then runs the two-pass path).
-template <class Core>
-hipError_t try_fused(Args a, int cus, int max_units, hipStream_t s) {
-  const int64_t units = a.units;
-  int64_t nwg = units < cus ? units : cus;
-  if (nwg >= kXcds) nwg -= nwg % kXcds;
-  const int64_t per = (units + nwg - 1) / nwg;
-  if (per > max_units) return hipErrorNotSupported;
-  KernelFn fn = fused_for_units<Core>(static_cast<int>(per));
-  if (fn == nullptr) return hipErrorNotSupported;
+template <class DT>
+hipError_t try_grouped(Args a, int cus, hipStream_t s) {
+  const int tiles = a.tiles_m * a.tiles_n;
+  if (a.K * a.lda * 2 >= (int64_t(1) << 31) || a.K * a.ldb * 2 >= (int64_t(1) << 31))
+    return hipErrorNotSupported;
+  const GroupPlan gp = group_plan(a.B, tiles, 2 * cus);
+  if (gp.groups == 0) return hipErrorNotSupported;
+  KernelFn fns[kGroupUnits] = {&wgrad_group_kernel<DT, 1>, &wgrad_group_kernel<DT, 2>,
+                               &wgrad_group_kernel<DT, 3>};
+  KernelFn fn = fns[gp.spg - 1];
   int occ = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void*>(fn), NT,
-                                                   Core::SMEM) != hipSuccess ||
-      occ < 1)
+                                                   0) != hipSuccess ||
+      occ < 2)
     return hipErrorNotSupported;
-  a.nwg = static_cast<int>(nwg);
-  // Zero the err / barrier words and the tile tickets (one kernel, graph-safe).
-  const int64_t words = int64_t(kWsHead / sizeof(unsigned)) + (a.tiles_m * a.tiles_n);
-  hipLaunchKernelGGL(clear_words_kernel<0>, dim3(static_cast<unsigned>((words + NT - 1) / NT)),
-                     dim3(NT), 0, s, reinterpret_cast<unsigned*>(a.err), words);
-  void* params[] = {&a};
-  return hipLaunchCooperativeKernel(reinterpret_cast<const void*>(fn), dim3(a.nwg), dim3(NT),
-                                    params, Core::SMEM, s);
+  a.spg = gp.spg;
+  const int64_t words = int64_t(kWsHead / sizeof(unsigned)) + tiles;
+  for (int64_t b0 = 0; b0 < a.B; b0 += gp.chunk) {
+    Args c = a;
+    c.chunk_b0 = b0;
+    c.chunk_nb = a.B - b0 < gp.chunk ? a.B - b0 : gp.chunk;
+    c.groups = static_cast<int>((c.chunk_nb + gp.spg - 1) / gp.spg);
+    c.nwg = c.groups * tiles;
+    c.chunk_first = b0 == 0;
+    c.chunk_last = b0 + c.chunk_nb >= a.B;
+    hipLaunchKernelGGL(clear_words_kernel<0>, dim3(static_cast<unsigned>((words + NT - 1) / NT)),
+                       dim3(NT), 0, s, reinterpret_cast<unsigned*>(a.err), words);
+    void* params[] = {&c};
+    const hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(fn),
+                                                    dim3(c.nwg), dim3(NT), params, 0, s);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
-
 // Per-dtype launchers (wgrad_fused_{bf16,f16,f32}.hip).
-hipError_t launch_fused_bf16(Args a, int cus, hipStream_t s);
-hipError_t launch_fused_f16(Args a, int cus, hipStream_t s);
-hipError_t launch_fused_f32(Args a, int cus, hipStream_t s);
+hipError_t launch_grouped_bf16(Args a, int cus, hipStream_t s);
+hipError_t launch_grouped_f16(Args a, int cus, hipStream_t s);
 
 }  // namespace wg
 }  // namespace fdp

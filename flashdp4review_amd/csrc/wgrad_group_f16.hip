@@ -1,0 +1,11 @@
+// Grouped single-pass clipped weight-gradient kernel instantiations for f16
+// inputs (one translation unit per dtype so that the builds run in parallel).
+#include "wgrad_core.hpp"
+
+namespace fdp {
+namespace wg {
+
+hipError_t launch_grouped_f16(Args a, int cus, hipStream_t s) { return try_grouped<F16>(a, cus, s); }
+
+}  // namespace wg
+}  // namespace fdp
