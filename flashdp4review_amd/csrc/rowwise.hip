@@ -180,35 +180,53 @@ __global__ __launch_bounds__(NT) void colsum_partials_kernel(
 }
 
 // ============================================================ per-stream reduce
-// grid (S): stream s sums its chunk partials in chunk order into sums[s, :],
-// derives ||.|| (sum vector or Frobenius partials) and c_s.
-__global__ __launch_bounds__(NT) void stream_reduce_kernel(
-    const float* partials, const float* frob, int64_t H, int chunks, int frob_per_chunk,
-    float C, float clamp, const float* clip_args_dev, float* sums, float* fac, float* norms,
-    float* factors) {
+// grid (ceil(H/NT), S): column h of stream s is summed over the chunk partials
+// in chunk order (loads unrolled for memory-level parallelism, additions kept
+// in order) into sums[s, h]; each block also writes the sum of squares of its
+// columns to sq_part[s, block] for the ||S_s|| norm.
+__global__ __launch_bounds__(NT) void chunk_reduce_kernel(const float* partials, int64_t H,
+                                                          int chunks, float* sums, float* sq_part) {
   __shared__ float red[NT / kWave];
-  const int64_t s = blockIdx.x;
+  const int64_t s = blockIdx.y;
+  const int64_t h = int64_t(blockIdx.x) * NT + threadIdx.x;
+  float acc = 0.f;
+  if (h < H) {
+    const float* src = partials + s * chunks * H + h;
+    int c = 0;
+    for (; c + 8 <= chunks; c += 8) {
+      float v[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) v[q] = src[int64_t(c + q) * H];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) acc += v[q];
+    }
+    for (; c < chunks; ++c) acc += src[int64_t(c) * H];
+    sums[s * H + h] = acc;
+  }
+  const float sq = wave_sum(acc * acc);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = sq;
+  __syncthreads();
+  if (threadIdx.x == 0) sq_part[s * gridDim.x + blockIdx.x] = (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+// One wavefront per stream: n_s = sqrt(sum of its squared-norm parts), c_s.
+// The parts are the per-block sums of squares of S_s (FDP_NORM_SUM) or the
+// per-(chunk, column block) sums of u^2 (FDP_NORM_FROB), nparts per stream.
+__global__ __launch_bounds__(NT) void stream_factor_kernel(const float* parts, int64_t S,
+                                                           int nparts, float C, float clamp,
+                                                           const float* clip_args_dev, float* fac,
+                                                           float* norms, float* factors) {
   if (clip_args_dev != nullptr) {
     C = clip_args_dev[0];
     clamp = clip_args_dev[1];
   }
-  float sq = 0.f;
-  for (int64_t h = threadIdx.x; h < H; h += NT) {
-    float acc = 0.f;
-    for (int c = 0; c < chunks; ++c) acc += partials[(s * chunks + c) * H + h];
-    sums[s * H + h] = acc;
-    sq += acc * acc;
-  }
-  if (frob != nullptr) {
-    sq = 0.f;
-    const int nf = chunks * frob_per_chunk;
-    for (int i = threadIdx.x; i < nf; i += NT) sq += frob[s * nf + i];
-  }
-  sq = wave_sum(sq);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = sq;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const float n = sqrtf((red[0] + red[1]) + (red[2] + red[3]));
+  const int lane = threadIdx.x & 63;
+  const int64_t s = int64_t(blockIdx.x) * (NT / kWave) + (threadIdx.x >> 6);
+  if (s >= S) return;
+  float q = 0.f;
+  for (int i = lane; i < nparts; i += kWave) q += parts[s * nparts + i];
+  const float n = sqrtf(wave_sum(q));
+  if (lane == 0) {
     const float c = clip_factor(n, C, clamp);
     fac[s] = c;
     if (norms) norms[s] = n;
@@ -287,7 +305,70 @@ __global__ __launch_bounds__(NT) void ln_fwd_kernel(const typename DT::storage* 
   }
 }
 
-// grid (chunks, B).  Each wave handles rows t = chunk*rows + wave, +4, ...:
+// Raw (undecoded) row fragment of one lane: lets the next row's loads be in
+// flight while the current row is processed.
+template <class DT, int EPL, int VEC>
+struct RawRow;
+template <class DT, int EPL>
+struct RawRow<DT, EPL, 8> {  // 16-bit, 16-byte vectors
+  uint4 q[EPL / 8];
+  __device__ __forceinline__ void load(const uint16_t* row, int64_t H, int lane) {
+#pragma unroll
+    for (int i = 0; i < EPL / 8; ++i) {
+      const int64_t e = wave_elem<EPL, 8>(lane, i);
+      q[i] = e < H ? *reinterpret_cast<const uint4*>(row + e) : make_uint4(0, 0, 0, 0);
+    }
+  }
+  __device__ __forceinline__ void decode(float (&o)[EPL]) const {
+#pragma unroll
+    for (int i = 0; i < EPL / 8; ++i) {
+      const uint32_t w[4] = {q[i].x, q[i].y, q[i].z, q[i].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        o[i * 8 + 2 * j] = DT::to_f32(static_cast<uint16_t>(w[j] & 0xffffu));
+        o[i * 8 + 2 * j + 1] = DT::to_f32(static_cast<uint16_t>(w[j] >> 16));
+      }
+    }
+  }
+};
+template <int EPL>
+struct RawRow<F32, EPL, 4> {  // fp32, 16-byte vectors
+  float4 q[EPL / 4];
+  __device__ __forceinline__ void load(const float* row, int64_t H, int lane) {
+#pragma unroll
+    for (int i = 0; i < EPL / 4; ++i) {
+      const int64_t e = wave_elem<EPL, 4>(lane, i);
+      q[i] = e < H ? *reinterpret_cast<const float4*>(row + e) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+  __device__ __forceinline__ void decode(float (&o)[EPL]) const {
+#pragma unroll
+    for (int i = 0; i < EPL / 4; ++i) {
+      o[4 * i] = q[i].x;
+      o[4 * i + 1] = q[i].y;
+      o[4 * i + 2] = q[i].z;
+      o[4 * i + 3] = q[i].w;
+    }
+  }
+};
+template <class DT, int EPL>
+struct RawRow<DT, EPL, 1> {  // any dtype, element loads (unaligned rows)
+  typename DT::storage q[EPL];
+  __device__ __forceinline__ void load(const typename DT::storage* row, int64_t H, int lane) {
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      const int64_t e = wave_elem<EPL, 1>(lane, i);
+      q[i] = e < H ? row[e] : typename DT::storage(0);
+    }
+  }
+  __device__ __forceinline__ void decode(float (&o)[EPL]) const {
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) o[i] = DT::to_f32(q[i]);
+  }
+};
+
+// grid (chunks, B).  Each wave handles rows t = chunk*rows + wave, +4, ...
+// with the next row's x / dy loads issued before the current row is used:
 // writes dx and accumulates P = sum dy*x_hat, Q = sum dy in registers; the four
 // waves are then folded in wave order through LDS into one partial per chunk.
 template <class DT, int EPL, int VEC>
@@ -314,12 +395,23 @@ __global__ __launch_bounds__(NT) void ln_bwd_kernel(const typename DT::storage* 
     Q[i] = 0.f;
   }
   const float inv_h = 1.f / static_cast<float>(H);
-  for (int64_t t = t0 + wave; t < t1; t += NT / kWave) {
+  RawRow<DT, EPL, VEC> rx, rg;
+  int64_t t = t0 + wave;
+  if (t < t1) {
+    rx.load(x + (b * T + t) * H, H, lane);
+    rg.load(dy + (b * T + t) * H, H, lane);
+  }
+  for (; t < t1; t += NT / kWave) {
     const int64_t r = b * T + t;
     float xv[EPL], gv[EPL];
-    load_row<DT, EPL, VEC>(x + r * H, H, lane, xv);
-    load_row<DT, EPL, VEC>(dy + r * H, H, lane, gv);
+    rx.decode(xv);
+    rg.decode(gv);
     const float mu = mean[r], rs = rstd[r];
+    const int64_t tn = t + NT / kWave;
+    if (tn < t1) {  // next row in flight while this one is processed
+      rx.load(x + (b * T + tn) * H, H, lane);
+      rg.load(dy + (b * T + tn) * H, H, lane);
+    }
     float s1 = 0.f, s2 = 0.f;
 #pragma unroll
     for (int i = 0; i < EPL / VEC; ++i)
@@ -392,9 +484,9 @@ int num_cus() {
 
 // ---------------------------------------------------------- column sums
 struct ColPlan {
-  int vec, bs, cblocks, chunks;
+  int vec, bs, cblocks, chunks, nblk;
   int64_t rows;
-  size_t off_part, off_frob, off_sums, off_fac, total;
+  size_t off_part, off_frob, off_sums, off_fac, off_sq, total;
 };
 
 ColPlan col_plan(int64_t B, int64_t T, int64_t H, int dtype, int cus, bool aligned) {
@@ -418,7 +510,9 @@ ColPlan col_plan(int64_t B, int64_t T, int64_t H, int dtype, int cus, bool align
   p.off_frob = align_up(sizeof(float) * size_t(B) * p.chunks * H);
   p.off_sums = p.off_frob + align_up(sizeof(float) * size_t(B) * p.chunks * p.cblocks);
   p.off_fac = p.off_sums + align_up(sizeof(float) * size_t(B) * H);
-  p.total = p.off_fac + align_up(sizeof(float) * size_t(B));
+  p.nblk = static_cast<int>((H + NT - 1) / NT);
+  p.off_sq = p.off_fac + align_up(sizeof(float) * size_t(B));
+  p.total = p.off_sq + align_up(sizeof(float) * size_t(B) * p.nblk);
   return p;
 }
 
@@ -486,9 +580,9 @@ void launch_ln_fwd(bool vec, int epl, const void* x, const void* w, const void* 
 }
 
 struct LnPlan {
-  int chunks;
+  int chunks, nblk;
   int64_t rows;
-  size_t off_part, off_sums, off_fac, total;
+  size_t off_part, off_sums, off_fac, off_sq, total;
 };
 
 LnPlan ln_plan(int64_t B, int64_t T, int64_t H, int cus) {
@@ -504,7 +598,9 @@ LnPlan ln_plan(int64_t B, int64_t T, int64_t H, int cus) {
   p.off_part = 0;
   p.off_sums = align_up(sizeof(float) * size_t(2 * B) * p.chunks * H);
   p.off_fac = p.off_sums + align_up(sizeof(float) * size_t(2 * B) * H);
-  p.total = p.off_fac + align_up(sizeof(float) * size_t(2 * B));
+  p.nblk = static_cast<int>((H + NT - 1) / NT);
+  p.off_sq = p.off_fac + align_up(sizeof(float) * size_t(2 * B));
+  p.total = p.off_sq + align_up(sizeof(float) * size_t(2 * B) * p.nblk);
   return p;
 }
 
@@ -574,7 +670,8 @@ extern "C" int fdp_colsum_clip(const void* u, const void* v, int64_t B, int64_t 
   if (!valid_dtype(dtype) || !valid_dtype(out_dtype)) return FDP_ERR_DTYPE;
   if (norm_kind != FDP_NORM_SUM && norm_kind != FDP_NORM_FROB) return FDP_ERR_ARG;
   if (B < 1 || T < 0 || H < 1) return FDP_ERR_SHAPE;
-  if (B > (int64_t(1) << 31) || H > (int64_t(1) << 31)) return FDP_ERR_SHAPE;
+  // samples index grid.y / grid.z (at most 65535)
+  if (B > 32767 || H > (int64_t(1) << 31)) return FDP_ERR_SHAPE;
   if ((T > 0 && u == nullptr) || out == nullptr) return FDP_ERR_ARG;
   const bool aligned = aligned16(u) && (v == nullptr || aligned16(v)) &&
                        (H * esize(dtype)) % 16 == 0;
@@ -596,8 +693,12 @@ extern "C" int fdp_colsum_clip(const void* u, const void* v, int64_t B, int64_t 
     zero_fill(part, int64_t(B) * p.chunks * H, s);
     if (frob) zero_fill(frob, int64_t(B) * p.chunks * p.cblocks, s);
   }
-  hipLaunchKernelGGL(stream_reduce_kernel, dim3(static_cast<unsigned>(B)), dim3(NT), 0, s, part,
-                     frob, H, p.chunks, p.cblocks, C, clamp, clip_args_dev, sums, fac, norms,
+  float* sq = reinterpret_cast<float*>(ws + p.off_sq);
+  hipLaunchKernelGGL(chunk_reduce_kernel, dim3(static_cast<unsigned>(p.nblk), static_cast<unsigned>(B)),
+                     dim3(NT), 0, s, part, H, p.chunks, sums, sq);
+  hipLaunchKernelGGL(stream_factor_kernel, dim3(static_cast<unsigned>((B + 3) / 4)), dim3(NT), 0, s,
+                     frob ? static_cast<const float*>(frob) : static_cast<const float*>(sq), B,
+                     frob ? p.chunks * p.cblocks : p.nblk, C, clamp, clip_args_dev, fac, norms,
                      factors);
   hipLaunchKernelGGL(combine_kernel, dim3(static_cast<unsigned>((H + NT - 1) / NT)), dim3(NT), 0,
                      s, sums, fac, B, H, out_scale, noise, static_cast<const void*>(nullptr),
@@ -641,7 +742,7 @@ extern "C" int fdp_layernorm_bwd_clip(const void* dy, const void* x, const void*
                                       size_t workspace_bytes, void* stream) {
   if (!valid_dtype(dtype) || !valid_dtype(w_dtype)) return FDP_ERR_DTYPE;
   if (B < 1 || T < 0 || H < 1 || H > kMaxLnH) return FDP_ERR_SHAPE;
-  if (B > (int64_t(1) << 30)) return FDP_ERR_SHAPE;
+  if (B > 32767) return FDP_ERR_SHAPE;  // 2B streams index grid.y
   if (T > 0 && (dy == nullptr || x == nullptr || dx == nullptr || mean == nullptr ||
                 rstd == nullptr))
     return FDP_ERR_ARG;
@@ -663,9 +764,13 @@ extern "C" int fdp_layernorm_bwd_clip(const void* dy, const void* x, const void*
   } else {
     zero_fill(part, int64_t(2 * B) * p.chunks * H, s);
   }
-  hipLaunchKernelGGL(stream_reduce_kernel, dim3(static_cast<unsigned>(2 * B)), dim3(NT), 0, s,
-                     part, static_cast<const float*>(nullptr), H, p.chunks, 0, C, clamp,
-                     clip_args_dev, sums, fac, norms, factors);
+  float* sq = reinterpret_cast<float*>(ws + p.off_sq);
+  hipLaunchKernelGGL(chunk_reduce_kernel,
+                     dim3(static_cast<unsigned>(p.nblk), static_cast<unsigned>(2 * B)), dim3(NT), 0,
+                     s, part, H, p.chunks, sums, sq);
+  hipLaunchKernelGGL(stream_factor_kernel, dim3(static_cast<unsigned>((2 * B + 3) / 4)), dim3(NT),
+                     0, s, static_cast<const float*>(sq), 2 * B, p.nblk, C, clamp, clip_args_dev,
+                     fac, norms, factors);
   if (dw != nullptr || db != nullptr) {
     // combine_kernel writes out0 from streams [0,B) and out1 from [B,2B).
     hipLaunchKernelGGL(combine_kernel, dim3(static_cast<unsigned>((H + NT - 1) / NT)), dim3(NT),
