@@ -4,18 +4,21 @@ Default workload ("cfg2"): the clipped per-sample weight
 gradient of a DP Linear 768 -> 3072 in bf16 with x [8,1024,768] ~ N(0,1),
 grad_out [8,1024,3072] ~ N(0,0.02^2), C = 1, sigma = 1:
     dW = (1/B) sum_b clip(||g_b^T x_b||) g_b^T x_b + (sigma/sqrt(B)) z
-One step = one noise draw + one fdp_wgrad_clip call (norm pass, factors,
-clipped-sum pass, epilogue with 1/B and the noise add), inputs resident in HBM.
+One step = one noise draw + one fdp_wgrad_clip call (single-pass kernel:
+per-sample products, norms, factors, clipped sum, 1/B and the noise add in
+its epilogue), inputs resident in HBM, default (cooperative) launch.
 
 value = algorithmic TFLOP/s = 2*B*T*M*N / step time (norm, scale and recompute
 flops are not credited).  The JSON line also carries the roofline of the
-clipped-GEMM call (timed alone with HIP events on the launch stream), the
-reference's torch op sequence timed on the host CPU (cpu_baseline), and extra
-measurements: the DP Linear layer fwd+bwd vs a plain nn.Linear, the Conv1D
-(cfg3) and LayerNorm (cfg4) paths.
+dominant kernel (wgrad_group_kernel: HIP events on the launch stream around
+back-to-back calls in ordinary-dispatch mode, where one call is exactly one
+launch of that kernel), the reference's torch op sequence timed on the host CPU
+(cpu_baseline), and extra measurements: the same step with the ordinary
+dispatch, the DP Linear layer fwd+bwd vs a plain nn.Linear, the Conv1D (cfg3)
+and LayerNorm (cfg4) paths.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload cfg2|cfg3|cfg4]
-                       [--no-cpu-baseline] [--no-extra]
+                       [--no-cpu-baseline] [--no-extra] [--copy-calibration MiB]
 """
 from __future__ import annotations
 
@@ -35,6 +38,12 @@ sys.path.insert(0, ROOT)
 
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+# HBM bytes per launch of the dominant kernel, from rocprofv3 --pmc FETCH_SIZE
+# and WRITE_SIZE runs of this script (profiles/*_traffic.md), each scaled by the
+# factor the same counter reads on a plain copy of known size.  None = not
+# measured for that workload.
+TRAFFIC_BYTES = {"cfg2": None, "cfg3": None, "cfg4": None}
 
 
 def cuda_time(fn, steps, warmup, stream=None):
@@ -78,7 +87,7 @@ def cfg3_inputs(dev):
     return x, go
 
 
-def run_wgrad(x, go, out_dtype, sigma=1.0, transpose=False):
+def run_wgrad(x, go, out_dtype, sigma=1.0, transpose=False, launch=None):
     """One DP weight-gradient step: noise draw + fused clipped product sum."""
     from flashdp4review_amd.core import wgrad_clip
     B = x.shape[0]
@@ -89,10 +98,11 @@ def run_wgrad(x, go, out_dtype, sigma=1.0, transpose=False):
     def step():
         z = torch.randn(M, N, device=x.device, dtype=out_dtype)
         return wgrad_clip(a, b, 1.0, 1.0, layout="tn", out_scale=1.0 / B, noise=z,
-                          noise_scale=std, out_dtype=out_dtype)
+                          noise_scale=std, out_dtype=out_dtype, launch=launch)
 
     def gemm_only():
-        return wgrad_clip(a, b, 1.0, 1.0, layout="tn", out_scale=1.0 / B, out_dtype=out_dtype)
+        return wgrad_clip(a, b, 1.0, 1.0, layout="tn", out_scale=1.0 / B, out_dtype=out_dtype,
+                          launch=launch)
 
     return step, gemm_only
 
@@ -110,7 +120,8 @@ def cpu_baseline_cfg2():
     F = 2.0 * 8 * 1024 * 3072 * 768
     torch_ref.linear_weight_backward(x, go, 1.0, 1.0, 1.0)  # warm-up
     ts = []
-    for _ in range(3):
+    t_start = time.perf_counter()
+    while len(ts) < 3 or (time.perf_counter() - t_start < 10.0 and len(ts) < 500):
         t0 = time.perf_counter()
         torch_ref.linear_weight_backward(x, go, 1.0, 1.0, 1.0)
         ts.append(time.perf_counter() - t0)
@@ -118,8 +129,8 @@ def cpu_baseline_cfg2():
     return {"value": round(F / t / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
             "kind": "port",
             "sample": "cfg2 full batch (B=8,T=1024,768->3072), fp32 on CPU, reference torch op "
-                      "sequence (per-sample einsum/norm/clamp/mul/sum, /B, normal add), "
-                      f"median of 3 after 1 warm-up, {t:.3f} s/step",
+                      "sequence (per-sample einsum/norm/clamp/mul/sum, /B, normal add); "
+                      f"median of {len(ts)} steps (~10 s) after 1 warm-up, {t:.4f} s/step",
             "cpu_model": platform.processor() or platform.machine()}
 
 
@@ -175,6 +186,8 @@ def main():
     ap.add_argument("--workload", default="cfg2", choices=["cfg2", "cfg3", "cfg4"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MiB",
+                    help="also run one plain device copy of this size (for PMC byte calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the DP hot path here is single-GPU "
@@ -188,27 +201,46 @@ def main():
     from flashdp4review_amd import _lib
     _lib.lib()  # fail loudly if the HIP library is missing
 
+    if args.copy_calibration > 0:
+        n = args.copy_calibration * (1 << 20) // 4
+        src = torch.ones(n, device=dev, dtype=torch.float32)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
     if args.workload == "cfg2":
         x, go, _ = cfg2_inputs(dev)
         B, T, I, O = 8, 1024, 768, 3072
-        step, gemm_only = run_wgrad(x, go, torch.bfloat16)
-        workload = "cfg2: DP Linear 768->3072 clipped per-sample weight grad, B=8 T=1024, C=1, sigma=1"
+        step, _ = run_wgrad(x, go, torch.bfloat16)
+        step_plain, kernel_call = run_wgrad(x, go, torch.bfloat16, launch="plain")
+        workload = ("cfg2: DP Linear 768->3072 clipped per-sample weight grad, B=8 T=1024, "
+                    "C=1, sigma=1")
     elif args.workload == "cfg3":
         x, go = cfg3_inputs(dev)
         B, T, I, O = 16, 1024, 768, 2304
-        step, gemm_only = run_wgrad(x, go, torch.bfloat16, transpose=True)
+        step, _ = run_wgrad(x, go, torch.bfloat16, transpose=True)
+        step_plain, kernel_call = run_wgrad(x, go, torch.bfloat16, transpose=True,
+                                            launch="plain")
         workload = "cfg3: DP Conv1D 768->2304 clipped per-sample weight grad, B=16 T=1024"
     else:
-        step = gemm_only = None
-    if args.workload == "cfg4":
         from flashdp4review_amd.core import layernorm_bwd_clip, layernorm_fwd
         g4 = torch.Generator(device=dev).manual_seed(5)
         xl = torch.randn(16, 1024, 1024, device=dev, generator=g4).to(torch.bfloat16)
         gl = (torch.randn(16, 1024, 1024, device=dev, generator=g4) * 0.01).to(torch.bfloat16)
         w = torch.ones(1024, device=dev, dtype=torch.bfloat16)
         _, mean, rstd = layernorm_fwd(xl, w, torch.zeros_like(w), 1e-5)
-        step = gemm_only = (lambda: layernorm_bwd_clip(gl, xl, w, mean, rstd, 1.0, 1.0))
 
+        def step():
+            zw = torch.randn(1024, device=dev, dtype=torch.bfloat16)
+            zb = torch.randn(1024, device=dev, dtype=torch.bfloat16)
+            return layernorm_bwd_clip(gl, xl, w, mean, rstd, 1.0, 1.0, out_scale=1.0 / 16,
+                                      noise_w=zw, noise_b=zb, noise_scale=0.25)
+
+        step_plain = None
+        kernel_call = lambda: layernorm_bwd_clip(gl, xl, w, mean, rstd, 1.0, 1.0)  # noqa: E731
+
+    # ---- timed region: K steps bracketed by synchronisation
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -220,24 +252,33 @@ def main():
     torch.cuda.synchronize()
     ms = s.elapsed_time(e) / args.steps
 
+    calls = max(args.steps, 20)
     if args.workload == "cfg4":
+        # algorithmic bytes: read x, dy, write dx (bf16) + mean/rstd (fp32)
         nbytes = 3 * 2 * 16 * 1024 * 1024 + 8 * 16 * 1024
+        call_ms = median_cuda_time(kernel_call, calls, 3, reps=3)
         res = {"metric": "DP LayerNorm per-sample grad GB/s", "value": round(nbytes / ms / 1e6, 1),
                "unit": "GB/s", "dtype": "bf16",
-               "config": {"workload": "cfg4: DP LayerNorm H=1024 bwd, B=16 T=1024"}}
-        gemm_ms = ms
-        roof = {"bound": "hbm", "achieved": round(nbytes / ms / 1e6, 1), "peak": PEAK_HBM_GBS,
-                "unit": "GB/s", "frac": round(nbytes / ms / 1e6 / PEAK_HBM_GBS, 4),
-                "traffic": None}
+               "config": {"workload": "cfg4: DP LayerNorm H=1024 bwd incl. dx, B=16 T=1024, "
+                                      "per-sample gamma/beta clip, 1/B, noise"}}
+        roof = {"bound": "hbm", "achieved": round(nbytes / call_ms / 1e6, 1),
+                "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(nbytes / call_ms / 1e6 / PEAK_HBM_GBS, 4),
+                "traffic": TRAFFIC_BYTES["cfg4"],
+                "kernel": "fdp_layernorm_bwd_clip (ln_bwd_kernel + reductions), one call",
+                "bytes_per_launch": nbytes, "avg_ms": round(call_ms, 4)}
     else:
         F = 2.0 * B * T * I * O
-        gemm_ms = median_cuda_time(gemm_only, args.steps, 3, reps=3)
+        call_ms = median_cuda_time(kernel_call, calls, 3, reps=3)
         res = {"metric": "clipped per-sample-grad GEMM TFLOP/s", "value": round(F / ms / 1e9, 2),
                "unit": "TFLOP/s", "dtype": "bf16", "config": {"workload": workload}}
-        roof = {"bound": "mfma", "achieved": round(F / gemm_ms / 1e9, 2), "peak": PEAK_BF16_TFLOPS,
-                "unit": "TFLOP/s", "frac": round(F / gemm_ms / 1e9 / PEAK_BF16_TFLOPS, 4),
-                "traffic": None, "kernel": "fdp_wgrad_clip (norm pass + factors + clipped-sum pass)",
-                "flops_per_launch": F, "avg_ms": round(gemm_ms, 4)}
+        roof = {"bound": "mfma", "achieved": round(F / call_ms / 1e9, 2),
+                "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(F / call_ms / 1e9 / PEAK_BF16_TFLOPS, 4),
+                "traffic": TRAFFIC_BYTES[args.workload],
+                "kernel": "wgrad_group_kernel (fdp_wgrad_clip calls back to back, ordinary "
+                          "dispatch; the call is this one kernel)",
+                "flops_per_launch": F, "avg_ms": round(call_ms, 4)}
     out = {"metric": res["metric"], "value": res["value"], "unit": res["unit"], "n_gpus": 1,
            "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
            "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
@@ -246,7 +287,13 @@ def main():
     if not args.no_cpu_baseline and args.workload == "cfg2":
         out["cpu_baseline"] = cpu_baseline_cfg2()
     if not args.no_extra and args.workload == "cfg2":
-        out["extra"] = extra_measurements(dev, max(5, args.steps // 5), 3)
+        extra = {}
+        t_plain = median_cuda_time(step_plain, args.steps, 3, reps=3)
+        F = 2.0 * B * T * I * O
+        extra["cfg2_step_plain_dispatch"] = {"ms": round(t_plain, 4),
+                                             "tflops": round(F / t_plain / 1e9, 2)}
+        extra.update(extra_measurements(dev, max(5, args.steps // 5), 3))
+        out["extra"] = extra
     out["device"] = torch.cuda.get_device_name(dev)
     print(json.dumps(out), flush=True)
 

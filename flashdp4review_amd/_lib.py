@@ -22,6 +22,8 @@ LAYOUT_TN, LAYOUT_NN = 0, 1
 NORM_SUM, NORM_FROB = 0, 1
 WGRAD_NOCLIP = 1
 WGRAD_TWO_PASS = 2
+WGRAD_PLAIN_LAUNCH = 4
+WGRAD_CLEAN_WORKSPACE = 8
 
 _DTYPE_CODES = {torch.float32: FDP_F32, torch.float16: FDP_F16, torch.bfloat16: FDP_BF16}
 

@@ -9,12 +9,61 @@ point, ``wgrad_clip``, which never materialises a per-sample gradient.
 from __future__ import annotations
 
 import ctypes
+import os
+import threading
 
 import torch
 
 from .. import _lib
 from .clip_fn import clip_args_of
 from .utils import RuntimeAutoTuner
+
+
+_LAUNCH_MODES = ("cooperative", "plain")
+_launch_mode = os.environ.get("FDP_WGRAD_LAUNCH", "cooperative")
+if _launch_mode not in _LAUNCH_MODES:
+    raise ValueError(f"FDP_WGRAD_LAUNCH must be one of {_LAUNCH_MODES}, got {_launch_mode!r}")
+_ws_sizes: dict = {}
+_ws_lock = threading.Lock()
+_ws_cache: dict = {}
+
+
+def _persistent_workspace(nbytes: int, dev: torch.device, stream: int) -> torch.Tensor:
+    """Zero-filled workspace kept per (device, stream).  Calls on one stream run in
+    order and each leaves the control words zero, so the buffer is reused with
+    FDP_WGRAD_CLEAN_WORKSPACE and no clearing kernel."""
+    key = (dev.index, stream)
+    with _ws_lock:
+        ws = _ws_cache.get(key)
+        if ws is None or ws.numel() < nbytes:
+            if len(_ws_cache) >= 16:
+                _ws_cache.clear()
+            ws = torch.zeros(max(int(nbytes), 4096), dtype=torch.uint8, device=dev)
+            _ws_cache[key] = ws
+        return ws
+
+
+def release_workspaces() -> None:
+    """Drop the cached per-stream workspaces (they are re-made on the next call)."""
+    with _ws_lock:
+        _ws_cache.clear()
+
+
+def set_wgrad_launch(mode: str) -> str:
+    """Default launch of the single-pass kernel; returns the previous mode.
+
+    "cooperative" (default) is safe whatever else runs on the device.  "plain"
+    dispatches it as an ordinary kernel, which saves the runtime's
+    cooperative-launch synchronisation (about 15 us per call) but requires
+    that nothing else occupies the device during the call (no concurrent
+    streams, e.g. collectives); a violated guarantee is reported through the
+    workspace status word (``check=True``), never a hang.
+    """
+    global _launch_mode
+    if mode not in _LAUNCH_MODES:
+        raise ValueError(f"launch mode must be one of {_LAUNCH_MODES}, got {mode!r}")
+    prev, _launch_mode = _launch_mode, mode
+    return prev
 
 
 def _inner_contig(t: torch.Tensor) -> torch.Tensor:
@@ -30,7 +79,7 @@ def wgrad_clip(a: torch.Tensor, b: torch.Tensor, C: float = 1.0, clamp_value: fl
                noise: torch.Tensor | None = None, noise_scale: float = 1.0,
                out_dtype: torch.dtype | None = None, out: torch.Tensor | None = None,
                return_stats: bool = False, noclip: bool = False, two_pass: bool = False,
-               check: bool = False):
+               launch: str | None = None, check: bool = False):
     """out = out_scale * sum_b c_b G_b + noise_scale * noise, c_b = clip(||G_b||_F).
 
     layout "tn": a [B,K,M], b [B,K,N], G_b = a_b^T b_b;
@@ -38,8 +87,10 @@ def wgrad_clip(a: torch.Tensor, b: torch.Tensor, C: float = 1.0, clamp_value: fl
     ``clip_args`` (tensor [C, clamp] or pair) overrides C / clamp_value.
     With ``return_stats`` also returns the fp32 per-sample norms and factors.
     ``two_pass`` forces the norm-pass + clipped-sum-pass schedule instead of the
-    single-pass cooperative kernel.  ``check`` synchronises and raises if a
-    bounded inter-workgroup wait of the single-pass kernel expired.
+    single-pass kernel; ``launch`` ("cooperative" / "plain", default: the
+    mode of ``set_wgrad_launch``) picks how that kernel is dispatched.
+    ``check`` synchronises and raises if a bounded inter-workgroup wait of the
+    single-pass kernel expired.
     """
     dev = _lib.require_hip(a, b, noise, out)
     if a.dtype != b.dtype:
@@ -77,19 +128,31 @@ def wgrad_clip(a: torch.Tensor, b: torch.Tensor, C: float = 1.0, clamp_value: fl
     if return_stats:
         factors = torch.empty(Bn, dtype=torch.float32, device=dev)
         norms = None if noclip else torch.empty(Bn, dtype=torch.float32, device=dev)
-    flags = (_lib.WGRAD_NOCLIP if noclip else 0) | (_lib.WGRAD_TWO_PASS if two_pass else 0)
+    mode = _launch_mode if launch is None else launch
+    if mode not in _LAUNCH_MODES:
+        raise ValueError(f"launch must be one of {_LAUNCH_MODES}, got {mode!r}")
+    flags = ((_lib.WGRAD_NOCLIP if noclip else 0) | (_lib.WGRAD_TWO_PASS if two_pass else 0)
+             | (_lib.WGRAD_PLAIN_LAUNCH if mode == "plain" else 0) | _lib.WGRAD_CLEAN_WORKSPACE)
     L = _lib.lib()
-    nbytes = _lib.size_query(L.fdp_wgrad_clip_workspace_size, Bn, K, M, N, dt, flags)
-    ws = _lib.workspace(nbytes, dev)
+    key = (dev.index, Bn, K, M, N, dt, flags)
+    nbytes = _ws_sizes.get(key)
+    if nbytes is None:
+        nbytes = _lib.size_query(L.fdp_wgrad_clip_workspace_size, Bn, K, M, N, dt, flags)
+        _ws_sizes[key] = nbytes
+    stream = _lib.stream_handle(dev)
+    ws = _persistent_workspace(nbytes, dev, stream)
     st = L.fdp_wgrad_clip(
         _lib.ptr(a), _lib.ptr(b), Bn, K, M, N, a.stride(0), a.stride(1), b.stride(0), b.stride(1),
         lay, dt, ctypes.c_float(C_), ctypes.c_float(clamp_), _lib.ptr(cad),
         ctypes.c_float(out_scale), _lib.ptr(noise), ctypes.c_float(noise_scale), out.data_ptr(),
         out.stride(0), odt, _lib.ptr(norms), _lib.ptr(factors), flags, ws.data_ptr(), ws.numel(),
-        _lib.stream_handle(dev))
+        stream)
     _lib.check(st, "fdp_wgrad_clip")
-    if check and int(ws[:4].view(torch.int32).item()) != 0:
-        raise _lib.FlashDPError("fdp_wgrad_clip: an inter-workgroup wait timed out")
+    if check:
+        status = ws[:4].view(torch.int32)
+        if int(status.item()) != 0:
+            status.zero_()  # the status word is sticky on a reused workspace
+            raise _lib.FlashDPError("fdp_wgrad_clip: an inter-workgroup wait timed out")
     if return_stats:
         return out, norms, factors
     return out

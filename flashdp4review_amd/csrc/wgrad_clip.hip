@@ -184,7 +184,9 @@ inline size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 
 // Workspace layout (both schedules):
-//   [0, 256)            err word (int), barrier word (uint)
+//   [0, 256)            status word (int), barrier and finished-workgroup
+//                       counters (uint); zero between calls, except a status set
+//                       by an expired wait
 //   off_turn            per-tile counters [tiles] (uint)
 //   off_partials        partials [B, tiles] (fp32)
 //   two-pass:  off_factors [B], off_group [groups, M, N] (fp32)
@@ -311,7 +313,9 @@ extern "C" int fdp_wgrad_clip(const void* a, const void* b, int64_t B, int64_t K
   if (layout == FDP_LAYOUT_NN && (lda < K || ldb < N)) return FDP_ERR_SHAPE;
   if (M * N > (int64_t(1) << 40) || B > (int64_t(1) << 31)) return FDP_ERR_SHAPE;
   if ((K > 0 && (a == nullptr || b == nullptr)) || out == nullptr) return FDP_ERR_ARG;
-  if ((flags & ~(FDP_WGRAD_NOCLIP | FDP_WGRAD_TWO_PASS)) != 0) return FDP_ERR_ARG;
+  if ((flags & ~(FDP_WGRAD_NOCLIP | FDP_WGRAD_TWO_PASS | FDP_WGRAD_PLAIN_LAUNCH |
+                 FDP_WGRAD_CLEAN_WORKSPACE)) != 0)
+    return FDP_ERR_ARG;
   const bool noclip = (flags & FDP_WGRAD_NOCLIP) != 0;
   if (noclip && norms != nullptr) return FDP_ERR_ARG;
 
@@ -349,6 +353,7 @@ extern "C" int fdp_wgrad_clip(const void* a, const void* b, int64_t B, int64_t K
   args.units = int64_t(pl.tiles) * B;
   args.err = reinterpret_cast<int*>(ws);
   args.bar = reinterpret_cast<unsigned*>(ws) + 1;
+  args.done = reinterpret_cast<unsigned*>(ws) + 2;
   args.tile_turn = reinterpret_cast<unsigned*>(ws + pl.off_turn);
   args.tile_acc = reinterpret_cast<float*>(ws + pl.off_slots);
   args.chunk_acc = reinterpret_cast<float*>(ws + pl.off_chunk);
@@ -369,8 +374,10 @@ extern "C" int fdp_wgrad_clip(const void* a, const void* b, int64_t B, int64_t K
   // Single pass: 16-bit inputs, TN layout, aligned rows, a clip to compute, K > 0.
   if (!noclip && (flags & FDP_WGRAD_TWO_PASS) == 0 && layout == FDP_LAYOUT_TN && vec && K > 0 &&
       dtype != FDP_F32 && pl.total_fused > 0) {
-    const hipError_t e = dtype == FDP_BF16 ? launch_grouped_bf16(args, cus, s)
-                                           : launch_grouped_f16(args, cus, s);
+    const bool plain = (flags & FDP_WGRAD_PLAIN_LAUNCH) != 0;
+    const bool clean = (flags & FDP_WGRAD_CLEAN_WORKSPACE) != 0;
+    const hipError_t e = dtype == FDP_BF16 ? launch_grouped_bf16(args, cus, plain, clean, s)
+                                           : launch_grouped_f16(args, cus, plain, clean, s);
     if (e == hipSuccess) return FDP_OK;
     if (e != hipErrorNotSupported && e != hipErrorCooperativeLaunchTooLarge) {
       (void)hipGetLastError();

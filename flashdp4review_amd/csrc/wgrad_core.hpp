@@ -35,6 +35,7 @@ struct Args {
   int64_t units;          // tiles * B work units, unit u = (tile u/B, sample u%B)
   int nwg;                // workgroups of the cooperative grid
   unsigned* bar;          // grid barrier arrivals
+  unsigned* done;         // workgroups finished (the last one re-zeroes bar / done)
   unsigned* tile_turn;    // [tiles] hand-over tickets for tiles shared by workgroups
   float* tile_acc;        // [tiles, BM*BN] fp32 running sums of shared tiles
   int* err;               // set when a bounded wait gives up
@@ -731,6 +732,7 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
 
   // ---- combine the groups of this tile: the last to arrive sums the slots
   const int ngroups = p.groups;
+  bool owner = true;
   if (ngroups > 1) {
     slot_store(p.tile_acc + (int64_t(g) * tiles + tile) * (BM * BN), acc);
     wait_stores();
@@ -739,38 +741,56 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
       const unsigned old = __hip_atomic_fetch_add(p.tile_turn + tile, 1u, __ATOMIC_RELAXED,
                                                   __HIP_MEMORY_SCOPE_AGENT);
       is_last = old == unsigned(ngroups - 1);
+      // every group has taken its ticket: leave the counter zeroed
+      if (is_last)
+        __hip_atomic_store(p.tile_turn + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
     FDP_TS(10);
-    if (!is_last) return;
-    zero(acc);
-    for (int gg = 0; gg < ngroups; ++gg) slot_add(p.tile_acc + (int64_t(gg) * tiles + tile) * (BM * BN), acc);
+    owner = is_last != 0;
+    if (owner) {
+      zero(acc);
+      for (int gg = 0; gg < ngroups; ++gg)
+        slot_add(p.tile_acc + (int64_t(gg) * tiles + tile) * (BM * BN), acc);
+    }
   }
   FDP_TS(11);
-  // running sum across chunks, then the output
-  if (!p.chunk_first || !p.chunk_last) {
+  if (owner) {
+    // running sum across chunks, then the output
+    if (!p.chunk_first || !p.chunk_last) {
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+      for (int a = 0; a < 2; ++a)
 #pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        const int64_t n = n0 + acc_col(wn, c, lane);
+        for (int c = 0; c < 2; ++c) {
+          const int64_t n = n0 + acc_col(wn, c, lane);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int64_t m = m0 + acc_row(wm, a, lane, r);
-          if (m < p.M && n < p.N) {
-            if (!p.chunk_first) acc[a][c][r] += p.chunk_acc[m * p.N + n];
-            if (!p.chunk_last) p.chunk_acc[m * p.N + n] = acc[a][c][r];
+          for (int r = 0; r < 16; ++r) {
+            const int64_t m = m0 + acc_row(wm, a, lane, r);
+            if (m < p.M && n < p.N) {
+              if (!p.chunk_first) acc[a][c][r] += p.chunk_acc[m * p.N + n];
+              if (!p.chunk_last) p.chunk_acc[m * p.N + n] = acc[a][c][r];
+            }
           }
         }
-      }
+    }
+    if (p.chunk_last) {
+      float* lo = reinterpret_cast<float*>(st0);
+      float* hi = reinterpret_cast<float*>(st1);
+      if (p.out_dtype == FDP_BF16) store_tile_staged<BF16>(p, m0, n0, acc, lo, hi);
+      else if (p.out_dtype == FDP_F16) store_tile_staged<F16>(p, m0, n0, acc, lo, hi);
+      else store_tile_staged<F32>(p, m0, n0, acc, lo, hi);
+      FDP_TS(12);
+    }
   }
-  if (p.chunk_last) {
-    float* lo = reinterpret_cast<float*>(st0);
-    float* hi = reinterpret_cast<float*>(st1);
-    if (p.out_dtype == FDP_BF16) store_tile_staged<BF16>(p, m0, n0, acc, lo, hi);
-    else if (p.out_dtype == FDP_F16) store_tile_staged<F16>(p, m0, n0, acc, lo, hi);
-    else store_tile_staged<F32>(p, m0, n0, acc, lo, hi);
-    FDP_TS(12);
+  // ---- leave the control words zeroed for the next launch on this
+  // workspace: every workgroup has passed the barrier once `done` reaches nwg.
+  if (threadIdx.x == 0) {
+    const unsigned old =
+        __hip_atomic_fetch_add(p.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (old == unsigned(p.nwg - 1)) {
+      __hip_atomic_store(p.bar, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(p.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
 }
 
@@ -807,8 +827,13 @@ inline GroupPlan group_plan(int64_t B, int tiles, int slots) {
   return g;
 }
 
+// `plain`: ordinary dispatch instead of a cooperative launch (the caller
+// guarantees that nothing else occupies the device during the call, so the
+// grid, sized to the computed occupancy, is resident at once).  `clean`: the
+// control words are already zero (every launch of the kernel leaves them so),
+// which makes the clearing kernel unnecessary.
 template <class DT>
-hipError_t try_grouped(Args a, int cus, hipStream_t s) {
+hipError_t try_grouped(Args a, int cus, bool plain, bool clean, hipStream_t s) {
   const int tiles = a.tiles_m * a.tiles_n;
   if (a.K * a.lda * 2 >= (int64_t(1) << 31) || a.K * a.ldb * 2 >= (int64_t(1) << 31))
     return hipErrorNotSupported;
@@ -832,19 +857,23 @@ hipError_t try_grouped(Args a, int cus, hipStream_t s) {
     c.nwg = c.groups * tiles;
     c.chunk_first = b0 == 0;
     c.chunk_last = b0 + c.chunk_nb >= a.B;
-    hipLaunchKernelGGL(clear_words_kernel<0>, dim3(static_cast<unsigned>((words + NT - 1) / NT)),
-                       dim3(NT), 0, s, reinterpret_cast<unsigned*>(a.err), words);
+    if (b0 == 0 && !clean)
+      hipLaunchKernelGGL(clear_words_kernel<0>,
+                         dim3(static_cast<unsigned>((words + NT - 1) / NT)), dim3(NT), 0, s,
+                         reinterpret_cast<unsigned*>(a.err), words);
     void* params[] = {&c};
-    const hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(fn),
-                                                    dim3(c.nwg), dim3(NT), params, 0, s);
+    const hipError_t e =
+        plain ? hipLaunchKernel(reinterpret_cast<const void*>(fn), dim3(c.nwg), dim3(NT), params, 0, s)
+              : hipLaunchCooperativeKernel(reinterpret_cast<const void*>(fn), dim3(c.nwg),
+                                           dim3(NT), params, 0, s);
     if (e != hipSuccess) return e;
   }
   return hipSuccess;
 }
 
-// Per-dtype launchers (wgrad_fused_{bf16,f16,f32}.hip).
-hipError_t launch_grouped_bf16(Args a, int cus, hipStream_t s);
-hipError_t launch_grouped_f16(Args a, int cus, hipStream_t s);
+// Per-dtype launchers (wgrad_group_{bf16,f16}.hip).
+hipError_t launch_grouped_bf16(Args a, int cus, bool plain, bool clean, hipStream_t s);
+hipError_t launch_grouped_f16(Args a, int cus, bool plain, bool clean, hipStream_t s);
 
 }  // namespace wg
 }  // namespace fdp

@@ -5,7 +5,9 @@
 namespace fdp {
 namespace wg {
 
-hipError_t launch_grouped_f16(Args a, int cus, hipStream_t s) { return try_grouped<F16>(a, cus, s); }
+hipError_t launch_grouped_f16(Args a, int cus, bool plain, bool clean, hipStream_t s) {
+  return try_grouped<F16>(a, cus, plain, clean, s);
+}
 
 }  // namespace wg
 }  // namespace fdp

@@ -99,14 +99,30 @@ int fdp_version(void);
  *            (a plain batched product sum; `norms` must then be NULL);
  *            bit 1 (FDP_WGRAD_TWO_PASS) forces the two-pass schedule (norm
  *            pass, then clipped-sum pass) instead of the single-pass
- *            cooperative kernel the library uses whenever the problem fits it.
- * workspace: device buffer of at least fdp_wgrad_clip_workspace_size() bytes.
- *            Its first int is a status word: nonzero after the call completes
- *            means a bounded inter-workgroup wait of the single-pass kernel
- *            expired (results are then invalid).
+ *            cooperative kernel the library uses whenever the problem fits it;
+ *            bit 2 (FDP_WGRAD_PLAIN_LAUNCH) dispatches the single-pass kernel
+ *            as an ordinary launch instead of a cooperative one, saving the
+ *            runtime's cooperative-launch synchronisation (about 15 us per
+ *            call on MI355X).  The caller then guarantees that nothing else
+ *            occupies the device during the call, so that the grid (sized to
+ *            the kernel's occupancy) is resident at once; if that fails, a
+ *            bounded wait expires and the status word below is set;
+ *            bit 3 (FDP_WGRAD_CLEAN_WORKSPACE) states that the workspace's
+ *            control words (its first 256 bytes and the per-tile tickets after
+ *            them) are zero -- a zero-filled buffer, or one whose last use was
+ *            a completed fdp_wgrad_clip call, which always leaves them zero
+ *            (the status word excepted) -- so the library skips clearing them.
+ * workspace: device buffer of at least fdp_wgrad_clip_workspace_size() bytes,
+ *            16-byte aligned.  Its first int is a status word: nonzero after
+ *            the call completes means a bounded inter-workgroup wait of the
+ *            single-pass kernel expired (results are then invalid).  With
+ *            FDP_WGRAD_CLEAN_WORKSPACE the word is sticky: the caller resets
+ *            it after reading a nonzero value.
  * ---------------------------------------------------------------------- */
 #define FDP_WGRAD_NOCLIP 1
 #define FDP_WGRAD_TWO_PASS 2
+#define FDP_WGRAD_PLAIN_LAUNCH 4
+#define FDP_WGRAD_CLEAN_WORKSPACE 8
 
 int fdp_wgrad_clip_workspace_size(int64_t B, int64_t K, int64_t M, int64_t N,
                                   int dtype, int flags, size_t* bytes);

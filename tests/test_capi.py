@@ -57,7 +57,7 @@ def test_wgrad_validation_codes():
     assert _wgrad(B=0) == 2
     assert _wgrad(lda=4) == 2          # row stride shorter than M
     assert _wgrad(out=None) == 3
-    assert _wgrad(flags=4) == 3
+    assert _wgrad(flags=16) == 3
     assert _wgrad(flags=1, norms=16) == 3  # norms undefined without the norm pass
     assert _wgrad() == 4               # workspace missing
 

@@ -35,7 +35,7 @@ SHAPES = [
 ]
 
 
-@pytest.mark.parametrize("path", ["auto", "two_pass"])
+@pytest.mark.parametrize("path", ["auto", "plain", "two_pass"])
 @pytest.mark.parametrize("dtype", DTYPES, ids=str)
 @pytest.mark.parametrize("layout", ["tn", "nn"])
 @pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
@@ -47,13 +47,14 @@ def test_wgrad_parity(shape, layout, dtype, path):
     C = float(np.median(norms_ref)) if B > 1 else float(norms_ref[0]) * 0.5
     ref, norms_ref, fac_ref = O.wgrad_clip(a, b, C, 1.0, layout)
     tp = path == "two_pass"
+    launch = "plain" if path == "plain" else "cooperative"
     out, norms, fac = core.wgrad_clip(a, b, C, 1.0, layout=layout, out_dtype=torch.float32,
-                                      return_stats=True, two_pass=tp, check=True)
+                                      return_stats=True, two_pass=tp, launch=launch, check=True)
     assert_close(out, ref, dtype, "out")
     assert_elementwise(norms, norms_ref, dtype, "norms")
     assert_elementwise(fac, fac_ref, dtype, "factors")
     # output in the input dtype (what the layers write)
-    out2 = core.wgrad_clip(a, b, C, 1.0, layout=layout, two_pass=tp, check=True)
+    out2 = core.wgrad_clip(a, b, C, 1.0, layout=layout, two_pass=tp, launch=launch, check=True)
     assert out2.dtype == dtype
     assert_close(out2, ref, dtype, "out (input dtype)")
 
@@ -95,9 +96,47 @@ def test_wgrad_special_cases(dtype):
 def test_wgrad_deterministic(two_pass):
     a, b = make(8, 256, 512, 384, torch.bfloat16, "tn", seed=7)
     o1 = core.wgrad_clip(a, b, 0.5, 1.0, two_pass=two_pass, check=True)
-    for _ in range(3):
-        o2 = core.wgrad_clip(a, b, 0.5, 1.0, two_pass=two_pass, check=True)
+    for launch in ("cooperative", "plain", "cooperative"):
+        o2 = core.wgrad_clip(a, b, 0.5, 1.0, two_pass=two_pass, launch=launch, check=True)
         assert torch.equal(o1, o2)
+
+
+@pytest.mark.parametrize("shape", [(8, 64, 392, 520), (16, 16, 256, 256), (20, 32, 3072, 1536)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_wgrad_reused_workspace_stays_clean(shape):
+    """Calls that reuse one workspace without clearing it (FDP_WGRAD_CLEAN_WORKSPACE)
+    match a call on a garbage-filled workspace that the library clears, and leave
+    the control words zero (tiles shared by groups; several launches per call)."""
+    import ctypes
+    from flashdp4review_amd import _lib
+    B, K, M, N = shape
+    a, b = make(B, K, M, N, torch.bfloat16, "tn", seed=12)
+    L = _lib.lib()
+    nb = _lib.size_query(L.fdp_wgrad_clip_workspace_size, B, K, M, N, _lib.FDP_BF16, 0)
+    tiles = ((M + 127) // 128) * ((N + 127) // 128)
+
+    def call(ws, flags):
+        out = torch.empty(M, N, dtype=torch.float32, device=DEV)
+        st = L.fdp_wgrad_clip(a.data_ptr(), b.data_ptr(), B, K, M, N, a.stride(0), a.stride(1),
+                              b.stride(0), b.stride(1), _lib.LAYOUT_TN, _lib.FDP_BF16,
+                              ctypes.c_float(0.05), ctypes.c_float(1.0), None, ctypes.c_float(1.0),
+                              None, ctypes.c_float(1.0), out.data_ptr(), N, _lib.FDP_F32, None,
+                              None, flags, ws.data_ptr(), ws.numel(),
+                              _lib.stream_handle(torch.device(DEV)))
+        assert st == 0
+        return out
+
+    dirty = torch.full((nb,), 0xA5, dtype=torch.uint8, device=DEV)
+    ref = call(dirty, 0)
+    clean = torch.zeros(nb, dtype=torch.uint8, device=DEV)
+    for _ in range(3):
+        out = call(clean, _lib.WGRAD_CLEAN_WORKSPACE)
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref)
+        assert torch.count_nonzero(clean[:256]) == 0
+        assert torch.count_nonzero(clean[256:256 + 4 * tiles]) == 0
+    exp, _, _ = O.wgrad_clip(a, b, 0.05, 1.0, "tn")
+    assert_close(ref, exp, torch.bfloat16, "clipped sum")
 
 
 def test_wgrad_does_not_modify_inputs():
