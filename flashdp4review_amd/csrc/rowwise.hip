@@ -10,10 +10,11 @@
 //              rstd = 1/sqrt(var+eps), y = x_hat*w + b)
 //   LN dx:     flashdp/core/layernorm_clip.py:98-107
 //
-// All reductions are fixed-order (no float atomics): per-(sample, row-chunk)
-// partial vectors go to a workspace, a per-sample kernel sums the chunks in
-// chunk order and derives the clip factor, and a combine kernel sums the
-// clipped samples in sample order.  Rows are read with 16-byte loads, one
+// All reductions are fixed-order (no float atomics): the row kernel writes
+// per-(sample, row-chunk) partial vectors to the workspace, chunk_sum_kernel
+// adds each sample's chunks in chunk order (and the squares for the norm), and
+// combine_kernel derives the clip factors and adds the clipped samples in
+// sample order into the output.  Rows are read with 16-byte loads, one
 // wavefront per row for the LayerNorm kernels (row statistics are wavefront
 // shuffles, no LDS), 64..256 threads across the columns for the column sums.
 #include "fdp_common.hpp"
@@ -110,13 +111,17 @@ __device__ inline void load_param(const void* p, int dtype, int64_t H, int lane,
   }
 }
 
-// ======================================================= column-sum partials
+// ========================================================== column sums
 // grid (col_blocks, chunks, B); thread owns VEC consecutive columns of one
-// 16-byte vector and walks `rows` rows of one sample.
+// 16-byte vector and walks `rows` rows of one sample.  Writes the chunk's
+// partial column sums partials[b][chunk][h] and, for FDP_NORM_FROB, the
+// workgroup's sum of u^2 to frob[b][chunk * col_blocks + col_block].
 template <class DT, int VEC>
-__global__ __launch_bounds__(NT) void colsum_partials_kernel(
-    const typename DT::storage* u, const typename DT::storage* v, int64_t T, int64_t H,
-    int64_t rows, int chunks, float* partials, float* frob) {
+__global__ __launch_bounds__(NT) void colsum_kernel(const typename DT::storage* u,
+                                                    const typename DT::storage* v, int64_t T,
+                                                    int64_t H, int64_t rows, int chunks,
+                                                    float* partials, float* frob) {
+  __shared__ float red[NT / kWave];
   const int64_t b = blockIdx.z;
   const int chunk = blockIdx.y;
   const int64_t vi = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -166,144 +171,177 @@ __global__ __launch_bounds__(NT) void colsum_partials_kernel(
     for (int j = 0; j < VEC; ++j) dst[j] = acc[j];
   }
   if (frob) {
-    __shared__ float red[NT / kWave];
     sq = wave_sum(sq);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     if (lane == 0) red[wave] = sq;
     __syncthreads();
     if (threadIdx.x == 0) {
-      float s = 0.f;
-      for (int w = 0; w < int(blockDim.x >> 6); ++w) s += red[w];
-      frob[(b * chunks + chunk) * gridDim.x + blockIdx.x] = s;
+      float t = 0.f;
+      for (int w = 0; w < int(blockDim.x >> 6); ++w) t += red[w];
+      frob[(b * chunks + chunk) * gridDim.x + blockIdx.x] = t;
     }
   }
 }
 
-// ============================================================ per-stream reduce
-// grid (ceil(H/NT), S): column h of stream s is summed over the chunk partials
-// in chunk order (loads unrolled for memory-level parallelism, additions kept
-// in order) into sums[s, h]; each block also writes the sum of squares of its
-// columns to sq_part[s, block] for the ||S_s|| norm.
-__global__ __launch_bounds__(NT) void chunk_reduce_kernel(const float* partials, int64_t H,
-                                                          int chunks, float* sums, float* sq_part) {
-  __shared__ float red[NT / kWave];
+// ====================================================== per-sample reductions
+// Items: 4 consecutive columns (V4, H % 4 == 0) or one column.  A workgroup
+// takes 64 items of one stream; its four waves each sum one contiguous quarter
+// of the chunks (loads in flight together, additions in chunk order) and the
+// quarters are added in order through LDS: fixed order, no atomics.
+template <bool V4>
+struct Item {
+  static constexpr int W = V4 ? 4 : 1;
+  f32x4 v;
+  __device__ void zero() { v = f32x4{0.f, 0.f, 0.f, 0.f}; }
+  __device__ void load(const float* p) {
+    if constexpr (V4) v = *reinterpret_cast<const f32x4*>(p);
+    else v = f32x4{p[0], 0.f, 0.f, 0.f};
+  }
+  __device__ void store(float* p) const {
+    if constexpr (V4) *reinterpret_cast<f32x4*>(p) = v;
+    else p[0] = v[0];
+  }
+  __device__ float sq() const {
+    return (v[0] * v[0] + v[1] * v[1]) + (v[2] * v[2] + v[3] * v[3]);
+  }
+};
+
+constexpr int kItemsPerBlock = 64;
+
+// grid (item_blocks, S): sums[s][h] = sum_c partials[s][c][h];
+// sq_part[s][item_block] = sum of squares of this block's sums.
+template <bool V4>
+__global__ __launch_bounds__(NT) void chunk_sum_kernel(const float* partials, int64_t H,
+                                                       int chunks, float* sums, float* sq_part) {
+  __shared__ f32x4 grp[NT / kWave][kItemsPerBlock];
   const int64_t s = blockIdx.y;
-  const int64_t h = int64_t(blockIdx.x) * NT + threadIdx.x;
-  float acc = 0.f;
-  if (h < H) {
-    const float* src = partials + s * chunks * H + h;
-    int c = 0;
-    for (; c + 8 <= chunks; c += 8) {
-      float v[8];
+  const int lane = threadIdx.x & 63, g = threadIdx.x >> 6;
+  const int64_t items = (H + Item<V4>::W - 1) / Item<V4>::W;
+  const int64_t it = int64_t(blockIdx.x) * kItemsPerBlock + lane;
+  const int per = (chunks + NT / kWave - 1) / (NT / kWave);
+  const int c0 = g * per < chunks ? g * per : chunks;
+  const int c1 = c0 + per < chunks ? c0 + per : chunks;
+  Item<V4> acc;
+  acc.zero();
+  if (it < items) {
+    const float* src = partials + s * chunks * H + it * Item<V4>::W;
+    int c = c0;
+    for (; c + 8 <= c1; c += 8) {
+      Item<V4> x[8];
 #pragma unroll
-      for (int q = 0; q < 8; ++q) v[q] = src[int64_t(c + q) * H];
+      for (int q = 0; q < 8; ++q) x[q].load(src + int64_t(c + q) * H);
 #pragma unroll
-      for (int q = 0; q < 8; ++q) acc += v[q];
+      for (int q = 0; q < 8; ++q) acc.v += x[q].v;
     }
-    for (; c < chunks; ++c) acc += src[int64_t(c) * H];
-    sums[s * H + h] = acc;
+    for (; c < c1; ++c) {
+      Item<V4> x;
+      x.load(src + int64_t(c) * H);
+      acc.v += x.v;
+    }
   }
-  const float sq = wave_sum(acc * acc);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = sq;
+  grp[g][lane] = acc.v;
   __syncthreads();
-  if (threadIdx.x == 0) sq_part[s * gridDim.x + blockIdx.x] = (red[0] + red[1]) + (red[2] + red[3]);
+  if (g == 0) {
+    Item<V4> tot;
+    tot.v = ((grp[0][lane] + grp[1][lane]) + grp[2][lane]) + grp[3][lane];
+    float q = 0.f;
+    if (it < items) {
+      tot.store(sums + s * H + it * Item<V4>::W);
+      q = tot.sq();
+    }
+    q = wave_sum(q);
+    if (lane == 0) sq_part[s * gridDim.x + blockIdx.x] = q;
+  }
 }
 
-// One wavefront per stream: n_s = sqrt(sum of its squared-norm parts), c_s.
-// The parts are the per-block sums of squares of S_s (FDP_NORM_SUM) or the
-// per-(chunk, column block) sums of u^2 (FDP_NORM_FROB), nparts per stream.
-__global__ __launch_bounds__(NT) void stream_factor_kernel(const float* parts, int64_t S,
-                                                           int nparts, float C, float clamp,
-                                                           const float* clip_args_dev, float* fac,
-                                                           float* norms, float* factors) {
+constexpr int kFacChunk = 1024;  // clip factors staged in LDS per pass
+
+// grid (item_blocks, nstreams): stream k's clip factors c_{k,b} from the norm
+// parts (nparts per sample, summed in order), then
+//   out_k[h] = out_scale * sum_b c_{k,b} sums[k*B+b][h] + noise_scale * noise_k[h]
+// with the four waves each taking a contiguous quarter of the samples, added
+// in order.  Workgroup 0 of each stream also writes norms / factors.
+template <bool V4>
+__global__ __launch_bounds__(NT) void combine_kernel(
+    const float* sums, const float* parts, int nparts, int64_t B, int64_t H, float C,
+    float clamp, const float* clip_args_dev, float out_scale, const void* noise0,
+    const void* noise1, float noise_scale, void* out0, void* out1, int out_dtype, float* norms,
+    float* factors) {
+  __shared__ float fac[kFacChunk];
+  __shared__ f32x4 grp[NT / kWave][kItemsPerBlock];
   if (clip_args_dev != nullptr) {
     C = clip_args_dev[0];
     clamp = clip_args_dev[1];
   }
-  const int lane = threadIdx.x & 63;
-  const int64_t s = int64_t(blockIdx.x) * (NT / kWave) + (threadIdx.x >> 6);
-  if (s >= S) return;
-  float q = 0.f;
-  for (int i = lane; i < nparts; i += kWave) q += parts[s * nparts + i];
-  const float n = sqrtf(wave_sum(q));
-  if (lane == 0) {
-    const float c = clip_factor(n, C, clamp);
-    fac[s] = c;
-    if (norms) norms[s] = n;
-    if (factors) factors[s] = c;
-  }
-}
-
-// out_k[h] = out_scale * sum_b fac[kB+b] * sums[kB+b, h] + noise_scale * noise_k[h]
-// for k = 0 (out0) and, when out1 != NULL, k = 1.
-__global__ __launch_bounds__(NT) void combine_kernel(const float* sums, const float* fac,
-                                                     int64_t B, int64_t H, float out_scale,
-                                                     const void* noise0, const void* noise1,
-                                                     float noise_scale, void* out0, void* out1,
-                                                     int out_dtype) {
-  const int64_t h = int64_t(blockIdx.x) * NT + threadIdx.x;
-  if (h >= H) return;
-  for (int k = 0; k < 2; ++k) {
-    void* out = k == 0 ? out0 : out1;
-    if (out == nullptr) continue;
-    const void* noise = k == 0 ? noise0 : noise1;
-    float acc = 0.f;
-    for (int64_t b = 0; b < B; ++b) acc += fac[k * B + b] * sums[(k * B + b) * H + h];
-    float v = acc * out_scale;
-    if (noise) v += noise_scale * load_as_f32(noise, h, out_dtype);
-    store_from_f32(out, h, out_dtype, v);
-  }
-}
-
-// Zero-fill used instead of hipMemsetAsync so that callers may capture the
-// entry points in a HIP graph.
-__global__ __launch_bounds__(NT) void fill_zero_kernel(float* p, int64_t n) {
-  for (int64_t i = int64_t(blockIdx.x) * NT + threadIdx.x; i < n; i += int64_t(gridDim.x) * NT)
-    p[i] = 0.f;
-}
-
-// ================================================================= LayerNorm
-// One wavefront per row; 4 rows in flight per workgroup.
-template <class DT, int EPL, int VEC>
-__global__ __launch_bounds__(NT) void ln_fwd_kernel(const typename DT::storage* x, const void* w,
-                                                    const void* bias, int w_dtype, int64_t rows,
-                                                    int64_t H, float eps,
-                                                    typename DT::storage* y, float* mean,
-                                                    float* rstd) {
-  const int lane = threadIdx.x & 63;
-  const int64_t wid = int64_t(blockIdx.x) * (NT / kWave) + (threadIdx.x >> 6);
-  const int64_t nw = int64_t(gridDim.x) * (NT / kWave);
-  float wv[EPL], bv[EPL];
-  load_param<EPL, VEC>(w, w_dtype, H, lane, 1.f, wv);
-  load_param<EPL, VEC>(bias, w_dtype, H, lane, 0.f, bv);
-  const float inv_h = 1.f / static_cast<float>(H);
-  for (int64_t r = wid; r < rows; r += nw) {
-    float xv[EPL];
-    load_row<DT, EPL, VEC>(x + r * H, H, lane, xv);
-    float s = 0.f;
-#pragma unroll
-    for (int i = 0; i < EPL; ++i) s += xv[i];
-    const float mu = wave_sum(s) * inv_h;
-    float q = 0.f;
-#pragma unroll
-    for (int i = 0; i < EPL / VEC; ++i)
-#pragma unroll
-      for (int j = 0; j < VEC; ++j) {
-        const float d = wave_elem<EPL, VEC>(lane, i) + j < H ? xv[i * VEC + j] - mu : 0.f;
-        q += d * d;
+  const int k = blockIdx.y;
+  void* out = k == 0 ? out0 : out1;
+  const void* noise = k == 0 ? noise0 : noise1;
+  const bool write_stats = blockIdx.x == 0;
+  const int lane = threadIdx.x & 63, g = threadIdx.x >> 6;
+  const int64_t items = (H + Item<V4>::W - 1) / Item<V4>::W;
+  const int64_t it = int64_t(blockIdx.x) * kItemsPerBlock + lane;
+  const int64_t per = (B + NT / kWave - 1) / (NT / kWave);
+  const int64_t g0 = g * per < B ? g * per : B;
+  const int64_t g1 = g0 + per < B ? g0 + per : B;
+  Item<V4> acc;
+  acc.zero();
+  for (int64_t bc = 0; bc < B; bc += kFacChunk) {
+    const int64_t nb = B - bc < kFacChunk ? B - bc : kFacChunk;
+    __syncthreads();
+    for (int64_t i = threadIdx.x; i < nb; i += NT) {
+      const int64_t s = k * B + bc + i;
+      const float* src = parts + s * nparts;
+      float q = 0.f;
+      int j = 0;
+      for (; j + 4 <= nparts; j += 4) {
+        const float a0 = src[j], a1 = src[j + 1], a2 = src[j + 2], a3 = src[j + 3];
+        q = (((q + a0) + a1) + a2) + a3;
       }
-    const float var = wave_sum(q) * inv_h;
-    const float rs = 1.f / sqrtf(var + eps);
-    float yv[EPL];
+      for (; j < nparts; ++j) q += src[j];
+      const float n = sqrtf(q);
+      const float c = clip_factor(n, C, clamp);
+      fac[i] = c;
+      if (write_stats) {
+        if (norms) norms[s] = n;
+        if (factors) factors[s] = c;
+      }
+    }
+    __syncthreads();
+    if (out != nullptr && it < items) {
+      const int64_t lo = g0 > bc ? g0 : bc;
+      const int64_t hi = g1 < bc + nb ? g1 : bc + nb;
+      const float* src = sums + (k * B) * H + it * Item<V4>::W;
+      int64_t b = lo;
+      for (; b + 8 <= hi; b += 8) {
+        Item<V4> x[8];
 #pragma unroll
-    for (int i = 0; i < EPL; ++i) yv[i] = (xv[i] - mu) * rs * wv[i] + bv[i];
-    store_row<DT, EPL, VEC>(y + r * H, H, lane, yv);
-    if (lane == 0) {
-      if (mean) mean[r] = mu;
-      if (rstd) rstd[r] = rs;
+        for (int q = 0; q < 8; ++q) x[q].load(src + (b + q) * H);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) acc.v += fac[b + q - bc] * x[q].v;
+      }
+      for (; b < hi; ++b) {
+        Item<V4> x;
+        x.load(src + b * H);
+        acc.v += fac[b - bc] * x.v;
+      }
+    }
+  }
+  if (out == nullptr) return;
+  grp[g][lane] = acc.v;
+  __syncthreads();
+  if (g == 0 && it < items) {
+    const f32x4 tot = ((grp[0][lane] + grp[1][lane]) + grp[2][lane]) + grp[3][lane];
+    for (int e = 0; e < Item<V4>::W; ++e) {
+      const int64_t h = it * Item<V4>::W + e;
+      float o = tot[e] * out_scale;
+      if (noise) o += noise_scale * load_as_f32(noise, h, out_dtype);
+      store_from_f32(out, h, out_dtype, o);
     }
   }
 }
+
+// ================================================================= LayerNorm
+constexpr int kLnThreads = 512;  // forward: 8 wavefronts, one row each at a time
 
 // Raw (undecoded) row fragment of one lane: lets the next row's loads be in
 // flight while the current row is processed.
@@ -367,18 +405,67 @@ struct RawRow<DT, EPL, 1> {  // any dtype, element loads (unaligned rows)
   }
 };
 
-// grid (chunks, B).  Each wave handles rows t = chunk*rows + wave, +4, ...
-// with the next row's x / dy loads issued before the current row is used:
-// writes dx and accumulates P = sum dy*x_hat, Q = sum dy in registers; the four
-// waves are then folded in wave order through LDS into one partial per chunk.
+// One wavefront per row, rows dealt grid-stride to the wavefronts, the next
+// row's loads issued before the current row is normalised.
 template <class DT, int EPL, int VEC>
-__global__ __launch_bounds__(NT) void ln_bwd_kernel(const typename DT::storage* dy,
+__global__ __launch_bounds__(kLnThreads) void ln_fwd_kernel(const typename DT::storage* x,
+                                                            const void* w, const void* bias,
+                                                            int w_dtype, int64_t rows, int64_t H,
+                                                            float eps, typename DT::storage* y,
+                                                            float* mean, float* rstd) {
+  constexpr int W = kLnThreads / kWave;
+  const int lane = threadIdx.x & 63;
+  const int64_t wid = int64_t(blockIdx.x) * W + (threadIdx.x >> 6);
+  const int64_t nw = int64_t(gridDim.x) * W;
+  float wv[EPL], bv[EPL];
+  load_param<EPL, VEC>(w, w_dtype, H, lane, 1.f, wv);
+  load_param<EPL, VEC>(bias, w_dtype, H, lane, 0.f, bv);
+  const float inv_h = 1.f / static_cast<float>(H);
+  RawRow<DT, EPL, VEC> rx;
+  if (wid < rows) rx.load(x + wid * H, H, lane);
+  for (int64_t r = wid; r < rows; r += nw) {
+    float xv[EPL];
+    rx.decode(xv);
+    if (r + nw < rows) rx.load(x + (r + nw) * H, H, lane);
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) s += xv[i];
+    const float mu = wave_sum(s) * inv_h;
+    float q = 0.f;
+#pragma unroll
+    for (int i = 0; i < EPL / VEC; ++i)
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) {
+        const float d = wave_elem<EPL, VEC>(lane, i) + j < H ? xv[i * VEC + j] - mu : 0.f;
+        q += d * d;
+      }
+    const float var = wave_sum(q) * inv_h;
+    const float rs = 1.f / sqrtf(var + eps);
+    float yv[EPL];
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) yv[i] = (xv[i] - mu) * rs * wv[i] + bv[i];
+    store_row<DT, EPL, VEC>(y + r * H, H, lane, yv);
+    if (lane == 0) {
+      if (mean) mean[r] = mu;
+      if (rstd) rstd[r] = rs;
+    }
+  }
+}
+
+// grid (chunks, B).  Wave w handles rows t = chunk*rows + w, +W, ... with the
+// next row's x / dy / mean / rstd loads in flight while the current row is
+// processed: writes dx and accumulates P = sum dy*x_hat, Q = sum dy in
+// registers; the W = NTH/64 waves are folded in wave order through LDS into
+// the chunk's partials (stream b: P, stream B+b: Q).
+template <class DT, int EPL, int VEC, int NTH>
+__global__ __launch_bounds__(NTH) void ln_bwd_kernel(const typename DT::storage* dy,
                                                     const typename DT::storage* x, const void* w,
                                                     int w_dtype, const float* mean,
                                                     const float* rstd, int64_t T, int64_t H,
                                                     int64_t rows, int chunks,
                                                     typename DT::storage* dx, float* partials,
                                                     int64_t B) {
+  constexpr int W = NTH / kWave;
   extern __shared__ __attribute__((aligned(16))) char smem_raw[];
   float* lds = reinterpret_cast<float*>(smem_raw);  // [2][H]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -396,21 +483,26 @@ __global__ __launch_bounds__(NT) void ln_bwd_kernel(const typename DT::storage* 
   }
   const float inv_h = 1.f / static_cast<float>(H);
   RawRow<DT, EPL, VEC> rx, rg;
+  float mu_n = 0.f, rs_n = 0.f;
   int64_t t = t0 + wave;
   if (t < t1) {
     rx.load(x + (b * T + t) * H, H, lane);
     rg.load(dy + (b * T + t) * H, H, lane);
+    mu_n = mean[b * T + t];
+    rs_n = rstd[b * T + t];
   }
-  for (; t < t1; t += NT / kWave) {
+  for (; t < t1; t += W) {
     const int64_t r = b * T + t;
     float xv[EPL], gv[EPL];
     rx.decode(xv);
     rg.decode(gv);
-    const float mu = mean[r], rs = rstd[r];
-    const int64_t tn = t + NT / kWave;
-    if (tn < t1) {  // next row in flight while this one is processed
+    const float mu = mu_n, rs = rs_n;
+    const int64_t tn = t + W;
+    if (tn < t1) {
       rx.load(x + (b * T + tn) * H, H, lane);
       rg.load(dy + (b * T + tn) * H, H, lane);
+      mu_n = mean[b * T + tn];
+      rs_n = rstd[b * T + tn];
     }
     float s1 = 0.f, s2 = 0.f;
 #pragma unroll
@@ -428,13 +520,12 @@ __global__ __launch_bounds__(NT) void ln_bwd_kernel(const typename DT::storage* 
       }
     const float c1 = wave_sum(s1) * inv_h;
     const float c2 = wave_sum(s2) * inv_h;
-    float dv[EPL];
 #pragma unroll
-    for (int k = 0; k < EPL; ++k) dv[k] = (wv[k] * gv[k] - (xv[k] * c1 + c2)) * rs;
-    store_row<DT, EPL, VEC>(dx + r * H, H, lane, dv);
+    for (int k = 0; k < EPL; ++k) gv[k] = (wv[k] * gv[k] - (xv[k] * c1 + c2)) * rs;
+    store_row<DT, EPL, VEC>(dx + r * H, H, lane, gv);
   }
-  // Fold the four waves in order 0,1,2,3.
-  for (int wsel = 0; wsel < NT / kWave; ++wsel) {
+  // Fold the waves in order 0..W-1.
+  for (int wsel = 0; wsel < W; ++wsel) {
     if (wave == wsel) {
 #pragma unroll
       for (int i = 0; i < EPL / VEC; ++i)
@@ -452,7 +543,7 @@ __global__ __launch_bounds__(NT) void ln_bwd_kernel(const typename DT::storage* 
   }
   float* pP = partials + (b * chunks + chunk) * H;
   float* pQ = partials + ((B + b) * chunks + chunk) * H;
-  for (int64_t e = threadIdx.x; e < H; e += NT) {
+  for (int64_t e = threadIdx.x; e < H; e += NTH) {
     pP[e] = lds[e];
     pQ[e] = lds[H + e];
   }
@@ -482,58 +573,56 @@ int num_cus() {
   return cus;
 }
 
-// ---------------------------------------------------------- column sums
-struct ColPlan {
-  int vec, bs, cblocks, chunks, nblk;
+// Workspace of both reductions (offsets in bytes), S = streams * B:
+//   off_part   partials [S][chunks][H] (fp32)
+//   off_frob   per-(sample, workgroup) sums of u^2 [B][parts] (FDP_NORM_FROB)
+//   off_sums   per-sample sums [S][H] (fp32)
+//   off_sq     per-(stream, item block) sums of squares [S][item_blocks]
+struct RedPlan {
+  int vec, bs, cblocks, chunks, parts, iblocks;
+  bool v4;
   int64_t rows;
-  size_t off_part, off_frob, off_sums, off_fac, off_sq, total;
+  size_t off_part, off_frob, off_sums, off_sq, total;
 };
 
-ColPlan col_plan(int64_t B, int64_t T, int64_t H, int dtype, int cus, bool aligned) {
-  ColPlan p{};
+void finish_plan(RedPlan& p, int64_t B, int64_t H, int streams) {
+  const size_t S = size_t(streams) * B;
+  p.parts = p.chunks * p.cblocks;
+  p.v4 = H % 4 == 0;
+  const int64_t items = p.v4 ? H / 4 : H;
+  p.iblocks = static_cast<int>((items + kItemsPerBlock - 1) / kItemsPerBlock);
+  p.off_part = 0;
+  p.off_frob = align_up(sizeof(float) * S * p.chunks * H);
+  p.off_sums = p.off_frob + align_up(sizeof(float) * size_t(B) * p.parts);
+  p.off_sq = p.off_sums + align_up(sizeof(float) * S * H);
+  p.total = p.off_sq + align_up(sizeof(float) * S * p.iblocks);
+}
+
+// Rows per chunk so that there are about `per_cu` workgroups per CU, with at
+// least `min_rows` rows per chunk.
+void split_rows(RedPlan& p, int64_t B, int64_t T, int cus, int per_cu, int64_t min_rows) {
+  int64_t want = (per_cu * int64_t(cus) + B * p.cblocks - 1) / (B * p.cblocks);
+  int64_t max_chunks = (T + min_rows - 1) / min_rows;
+  if (max_chunks < 1) max_chunks = 1;
+  if (want > max_chunks) want = max_chunks;
+  if (want < 1) want = 1;
+  p.rows = T > 0 ? (T + want - 1) / want : 1;
+  p.chunks = static_cast<int>(T > 0 ? (T + p.rows - 1) / p.rows : 1);
+}
+
+RedPlan col_plan(int64_t B, int64_t T, int64_t H, int dtype, int cus, bool aligned) {
+  RedPlan p{};
   p.vec = aligned ? 16 / esize(dtype) : 1;
   const int64_t nvec = (H + p.vec - 1) / p.vec;
   int64_t bs = ((nvec + 63) / 64) * 64;
   if (bs > NT) bs = NT;
   p.bs = static_cast<int>(bs);
   p.cblocks = static_cast<int>((nvec + bs - 1) / bs);
-  // Aim for ~4 workgroups per CU, at least 8 rows per chunk.
-  int64_t want = (4 * int64_t(cus) + B * p.cblocks - 1) / (B * p.cblocks);
-  int64_t max_chunks = (T + 7) / 8;
-  if (max_chunks < 1) max_chunks = 1;
-  if (want > max_chunks) want = max_chunks;
-  if (want < 1) want = 1;
-  p.rows = (T + want - 1) / want;
-  if (p.rows < 1) p.rows = 1;
-  p.chunks = static_cast<int>(T > 0 ? (T + p.rows - 1) / p.rows : 1);
-  p.off_part = 0;
-  p.off_frob = align_up(sizeof(float) * size_t(B) * p.chunks * H);
-  p.off_sums = p.off_frob + align_up(sizeof(float) * size_t(B) * p.chunks * p.cblocks);
-  p.off_fac = p.off_sums + align_up(sizeof(float) * size_t(B) * H);
-  p.nblk = static_cast<int>((H + NT - 1) / NT);
-  p.off_sq = p.off_fac + align_up(sizeof(float) * size_t(B));
-  p.total = p.off_sq + align_up(sizeof(float) * size_t(B) * p.nblk);
+  split_rows(p, B, T, cus, 4, 8);
+  finish_plan(p, B, H, 1);
   return p;
 }
 
-template <class DT, int VEC>
-void launch_colsum(const ColPlan& p, const void* u, const void* v, int64_t B, int64_t T,
-                   int64_t H, float* part, float* frob, hipStream_t s) {
-  using S = typename DT::storage;
-  hipLaunchKernelGGL((colsum_partials_kernel<DT, VEC>), dim3(p.cblocks, p.chunks, B), dim3(p.bs),
-                     0, s, static_cast<const S*>(u), static_cast<const S*>(v), T, H, p.rows,
-                     p.chunks, part, frob);
-}
-
-template <class DT>
-void launch_colsum_dt(const ColPlan& p, const void* u, const void* v, int64_t B, int64_t T,
-                      int64_t H, float* part, float* frob, hipStream_t s) {
-  if (p.vec == 1) launch_colsum<DT, 1>(p, u, v, B, T, H, part, frob, s);
-  else if constexpr (DT::code == FDP_F32) launch_colsum<DT, 4>(p, u, v, B, T, H, part, frob, s);
-  else launch_colsum<DT, 8>(p, u, v, B, T, H, part, frob, s);
-}
-
-// ------------------------------------------------------------ LayerNorm
 constexpr int64_t kMaxLnH = 4096;  // 64 elements per lane, one wave per row
 
 // Elements per lane for a row of H (EPL in {8,16,32,64}).
@@ -543,17 +632,88 @@ int ln_epl(int64_t H) {
   return epl;
 }
 
+
+// LayerNorm backward workgroup: 4 waves; rows of up to 1024 elements need
+// ~150 VGPRs, so three workgroups share a CU (measured faster than one
+// 12-wave workgroup per CU, whose fold and partial stores are not overlapped).
+constexpr int ln_bwd_threads(int) { return 256; }
+
+RedPlan ln_plan(int64_t B, int64_t T, int64_t H, int cus) {
+  RedPlan p{};
+  p.cblocks = 1;
+  split_rows(p, B, T, cus, 3, 16);
+  finish_plan(p, B, H, 2);
+  return p;
+}
+
+// chunk sums -> per-sample norms, clip factors and the clipped, scaled sum.
+struct Epilogue {
+  float C, clamp;
+  const float* clip_args_dev;
+  float out_scale, noise_scale;
+  const void* noise0;
+  const void* noise1;
+  void* out0;
+  void* out1;
+  int out_dtype;
+  float* norms;
+  float* factors;
+};
+
+void launch_reduce(const RedPlan& p, char* ws, int64_t B, int64_t H, int streams, bool frob,
+                   const Epilogue& e, hipStream_t s) {
+  const float* part = reinterpret_cast<const float*>(ws + p.off_part);
+  float* sums = reinterpret_cast<float*>(ws + p.off_sums);
+  float* sq = reinterpret_cast<float*>(ws + p.off_sq);
+  const float* nparts = frob ? reinterpret_cast<const float*>(ws + p.off_frob) : sq;
+  const int np = frob ? p.parts : p.iblocks;
+  const dim3 rgrid(static_cast<unsigned>(p.iblocks), static_cast<unsigned>(streams * B));
+  const dim3 cgrid(static_cast<unsigned>(p.iblocks), static_cast<unsigned>(streams));
+  if (p.v4) {
+    hipLaunchKernelGGL(chunk_sum_kernel<true>, rgrid, dim3(NT), 0, s, part, H, p.chunks, sums, sq);
+    hipLaunchKernelGGL(combine_kernel<true>, cgrid, dim3(NT), 0, s, sums, nparts, np, B, H, e.C,
+                       e.clamp, e.clip_args_dev, e.out_scale, e.noise0, e.noise1, e.noise_scale,
+                       e.out0, e.out1, e.out_dtype, e.norms, e.factors);
+  } else {
+    hipLaunchKernelGGL(chunk_sum_kernel<false>, rgrid, dim3(NT), 0, s, part, H, p.chunks, sums,
+                       sq);
+    hipLaunchKernelGGL(combine_kernel<false>, cgrid, dim3(NT), 0, s, sums, nparts, np, B, H, e.C,
+                       e.clamp, e.clip_args_dev, e.out_scale, e.noise0, e.noise1, e.noise_scale,
+                       e.out0, e.out1, e.out_dtype, e.norms, e.factors);
+  }
+}
+
+template <class DT, int VEC>
+void launch_colsum(const RedPlan& p, const void* u, const void* v, int64_t B, int64_t T,
+                   int64_t H, char* ws, bool frob, hipStream_t s) {
+  using S = typename DT::storage;
+  hipLaunchKernelGGL((colsum_kernel<DT, VEC>), dim3(p.cblocks, p.chunks, B), dim3(p.bs), 0, s,
+                     static_cast<const S*>(u), static_cast<const S*>(v), T, H, p.rows, p.chunks,
+                     reinterpret_cast<float*>(ws + p.off_part),
+                     frob ? reinterpret_cast<float*>(ws + p.off_frob) : nullptr);
+}
+
+template <class DT>
+void launch_colsum_dt(const RedPlan& p, const void* u, const void* v, int64_t B, int64_t T,
+                      int64_t H, char* ws, bool frob, hipStream_t s) {
+  if (p.vec == 1) launch_colsum<DT, 1>(p, u, v, B, T, H, ws, frob, s);
+  else if constexpr (DT::code == FDP_F32) launch_colsum<DT, 4>(p, u, v, B, T, H, ws, frob, s);
+  else launch_colsum<DT, 8>(p, u, v, B, T, H, ws, frob, s);
+}
+
 template <class DT, int EPL, int VEC>
 void launch_ln_fwd_t(const void* x, const void* w, const void* b, int w_dtype, int64_t rows,
                      int64_t H, float eps, void* y, float* mean, float* rstd, int cus,
                      hipStream_t s) {
   using S = typename DT::storage;
-  int64_t grid = (rows + 3) / 4;
-  const int64_t cap = int64_t(cus) * 8;
+  constexpr int W = kLnThreads / kWave;
+  // enough wavefronts for ~4 rows each, at most 2 workgroups per CU
+  int64_t grid = (rows + 4 * W - 1) / (4 * W);
+  const int64_t cap = int64_t(cus) * 2;
   if (grid > cap) grid = cap;
   if (grid < 1) grid = 1;
-  hipLaunchKernelGGL((ln_fwd_kernel<DT, EPL, VEC>), dim3(static_cast<unsigned>(grid)), dim3(NT),
-                     0, s, static_cast<const S*>(x), w, b, w_dtype, rows, H, eps,
+  hipLaunchKernelGGL((ln_fwd_kernel<DT, EPL, VEC>), dim3(static_cast<unsigned>(grid)),
+                     dim3(kLnThreads), 0, s, static_cast<const S*>(x), w, b, w_dtype, rows, H, eps,
                      static_cast<S*>(y), mean, rstd);
 }
 
@@ -579,72 +739,46 @@ void launch_ln_fwd(bool vec, int epl, const void* x, const void* w, const void* 
   else launch_ln_fwd_v<DT, 8>(epl, x, w, b, w_dtype, rows, H, eps, y, mean, rstd, cus, s);
 }
 
-struct LnPlan {
-  int chunks, nblk;
-  int64_t rows;
-  size_t off_part, off_sums, off_fac, off_sq, total;
+struct LnBwdIo {
+  const void* dy;
+  const void* x;
+  const void* w;
+  int w_dtype;
+  const float* mean;
+  const float* rstd;
+  int64_t B, T, H;
+  void* dx;
 };
 
-LnPlan ln_plan(int64_t B, int64_t T, int64_t H, int cus) {
-  LnPlan p{};
-  // ~2 workgroups per CU, >= 16 rows (4 per wave) per chunk.
-  int64_t want = (2 * int64_t(cus) + B - 1) / B;
-  int64_t max_chunks = (T + 15) / 16;
-  if (max_chunks < 1) max_chunks = 1;
-  if (want > max_chunks) want = max_chunks;
-  if (want < 1) want = 1;
-  p.rows = T > 0 ? (T + want - 1) / want : 1;
-  p.chunks = static_cast<int>(T > 0 ? (T + p.rows - 1) / p.rows : 1);
-  p.off_part = 0;
-  p.off_sums = align_up(sizeof(float) * size_t(2 * B) * p.chunks * H);
-  p.off_fac = p.off_sums + align_up(sizeof(float) * size_t(2 * B) * H);
-  p.nblk = static_cast<int>((H + NT - 1) / NT);
-  p.off_sq = p.off_fac + align_up(sizeof(float) * size_t(2 * B));
-  p.total = p.off_sq + align_up(sizeof(float) * size_t(2 * B) * p.nblk);
-  return p;
-}
-
 template <class DT, int EPL, int VEC>
-void launch_ln_bwd_t(const LnPlan& p, const void* dy, const void* x, const void* w, int w_dtype,
-                     const float* mean, const float* rstd, int64_t B, int64_t T, int64_t H,
-                     void* dx, float* part, hipStream_t s) {
+void launch_ln_bwd_t(const RedPlan& p, const LnBwdIo& io, float* part, hipStream_t s) {
   using S = typename DT::storage;
-  hipLaunchKernelGGL((ln_bwd_kernel<DT, EPL, VEC>), dim3(p.chunks, B), dim3(NT),
-                     sizeof(float) * 2 * H, s, static_cast<const S*>(dy),
-                     static_cast<const S*>(x), w, w_dtype, mean, rstd, T, H, p.rows, p.chunks,
-                     static_cast<S*>(dx), part, B);
+  constexpr int NTH = ln_bwd_threads(EPL);
+  hipLaunchKernelGGL((ln_bwd_kernel<DT, EPL, VEC, NTH>), dim3(p.chunks, io.B), dim3(NTH),
+                     sizeof(float) * 2 * io.H, s, static_cast<const S*>(io.dy),
+                     static_cast<const S*>(io.x), io.w, io.w_dtype, io.mean, io.rstd, io.T, io.H,
+                     p.rows, p.chunks, static_cast<S*>(io.dx), part, io.B);
 }
 
 template <class DT, int VEC>
-void launch_ln_bwd_v(int epl, const LnPlan& p, const void* dy, const void* x, const void* w,
-                     int w_dtype, const float* mean, const float* rstd, int64_t B, int64_t T,
-                     int64_t H, void* dx, float* part, hipStream_t s) {
+void launch_ln_bwd_v(int epl, const RedPlan& p, const LnBwdIo& io, float* part, hipStream_t s) {
   switch (epl) {
-    case 8: launch_ln_bwd_t<DT, 8, VEC>(p, dy, x, w, w_dtype, mean, rstd, B, T, H, dx, part, s); break;
-    case 16: launch_ln_bwd_t<DT, 16, VEC>(p, dy, x, w, w_dtype, mean, rstd, B, T, H, dx, part, s); break;
-    case 32: launch_ln_bwd_t<DT, 32, VEC>(p, dy, x, w, w_dtype, mean, rstd, B, T, H, dx, part, s); break;
-    default: launch_ln_bwd_t<DT, 64, VEC>(p, dy, x, w, w_dtype, mean, rstd, B, T, H, dx, part, s); break;
+    case 8: launch_ln_bwd_t<DT, 8, VEC>(p, io, part, s); break;
+    case 16: launch_ln_bwd_t<DT, 16, VEC>(p, io, part, s); break;
+    case 32: launch_ln_bwd_t<DT, 32, VEC>(p, io, part, s); break;
+    default: launch_ln_bwd_t<DT, 64, VEC>(p, io, part, s); break;
   }
 }
 
 template <class DT>
-void launch_ln_bwd(bool vec, int epl, const LnPlan& p, const void* dy, const void* x,
-                   const void* w, int w_dtype, const float* mean, const float* rstd, int64_t B,
-                   int64_t T, int64_t H, void* dx, float* part, hipStream_t s) {
-  if (!vec) launch_ln_bwd_v<DT, 1>(epl, p, dy, x, w, w_dtype, mean, rstd, B, T, H, dx, part, s);
-  else if constexpr (DT::code == FDP_F32)
-    launch_ln_bwd_v<DT, 4>(epl, p, dy, x, w, w_dtype, mean, rstd, B, T, H, dx, part, s);
-  else launch_ln_bwd_v<DT, 8>(epl, p, dy, x, w, w_dtype, mean, rstd, B, T, H, dx, part, s);
+void launch_ln_bwd(bool vec, int epl, const RedPlan& p, const LnBwdIo& io, float* part,
+                   hipStream_t s) {
+  if (!vec) launch_ln_bwd_v<DT, 1>(epl, p, io, part, s);
+  else if constexpr (DT::code == FDP_F32) launch_ln_bwd_v<DT, 4>(epl, p, io, part, s);
+  else launch_ln_bwd_v<DT, 8>(epl, p, io, part, s);
 }
 
 bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
-
-void zero_fill(float* p, int64_t n, hipStream_t s) {
-  int64_t g = (n + NT - 1) / NT;
-  if (g > 1024) g = 1024;
-  if (g < 1) g = 1;
-  hipLaunchKernelGGL(fill_zero_kernel, dim3(static_cast<unsigned>(g)), dim3(NT), 0, s, p, n);
-}
 
 }  // namespace
 
@@ -655,8 +789,8 @@ extern "C" int fdp_colsum_clip_workspace_size(int64_t B, int64_t T, int64_t H, i
   if (!valid_dtype(dtype)) return FDP_ERR_DTYPE;
   if (B < 1 || T < 0 || H < 1) return FDP_ERR_SHAPE;
   // The aligned plan has the most chunk partials; size for the larger of both.
-  const ColPlan a = col_plan(B, T, H, dtype, num_cus(), true);
-  const ColPlan u = col_plan(B, T, H, dtype, num_cus(), false);
+  const RedPlan a = col_plan(B, T, H, dtype, num_cus(), true);
+  const RedPlan u = col_plan(B, T, H, dtype, num_cus(), false);
   *bytes = a.total > u.total ? a.total : u.total;
   return FDP_OK;
 }
@@ -671,38 +805,23 @@ extern "C" int fdp_colsum_clip(const void* u, const void* v, int64_t B, int64_t 
   if (norm_kind != FDP_NORM_SUM && norm_kind != FDP_NORM_FROB) return FDP_ERR_ARG;
   if (B < 1 || T < 0 || H < 1) return FDP_ERR_SHAPE;
   // samples index grid.y / grid.z (at most 65535)
-  if (B > 32767 || H > (int64_t(1) << 31)) return FDP_ERR_SHAPE;
+  if (B > 65535 || H > (int64_t(1) << 31)) return FDP_ERR_SHAPE;
   if ((T > 0 && u == nullptr) || out == nullptr) return FDP_ERR_ARG;
   const bool aligned = aligned16(u) && (v == nullptr || aligned16(v)) &&
                        (H * esize(dtype)) % 16 == 0;
   const int cus = num_cus();
-  const ColPlan p = col_plan(B, T, H, dtype, cus, aligned);
+  const RedPlan p = col_plan(B, T, H, dtype, cus, aligned);
   if (workspace == nullptr || workspace_bytes < p.total) return FDP_ERR_WORKSPACE;
   if (!aligned16(workspace)) return FDP_ERR_ALIGN;
   char* ws = static_cast<char*>(workspace);
-  float* part = reinterpret_cast<float*>(ws + p.off_part);
-  float* frob = norm_kind == FDP_NORM_FROB ? reinterpret_cast<float*>(ws + p.off_frob) : nullptr;
-  float* sums = reinterpret_cast<float*>(ws + p.off_sums);
-  float* fac = reinterpret_cast<float*>(ws + p.off_fac);
+  const bool frob = norm_kind == FDP_NORM_FROB;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (T > 0) {
-    if (dtype == FDP_BF16) launch_colsum_dt<BF16>(p, u, v, B, T, H, part, frob, s);
-    else if (dtype == FDP_F16) launch_colsum_dt<F16>(p, u, v, B, T, H, part, frob, s);
-    else launch_colsum_dt<F32>(p, u, v, B, T, H, part, frob, s);
-  } else {
-    zero_fill(part, int64_t(B) * p.chunks * H, s);
-    if (frob) zero_fill(frob, int64_t(B) * p.chunks * p.cblocks, s);
-  }
-  float* sq = reinterpret_cast<float*>(ws + p.off_sq);
-  hipLaunchKernelGGL(chunk_reduce_kernel, dim3(static_cast<unsigned>(p.nblk), static_cast<unsigned>(B)),
-                     dim3(NT), 0, s, part, H, p.chunks, sums, sq);
-  hipLaunchKernelGGL(stream_factor_kernel, dim3(static_cast<unsigned>((B + 3) / 4)), dim3(NT), 0, s,
-                     frob ? static_cast<const float*>(frob) : static_cast<const float*>(sq), B,
-                     frob ? p.chunks * p.cblocks : p.nblk, C, clamp, clip_args_dev, fac, norms,
-                     factors);
-  hipLaunchKernelGGL(combine_kernel, dim3(static_cast<unsigned>((H + NT - 1) / NT)), dim3(NT), 0,
-                     s, sums, fac, B, H, out_scale, noise, static_cast<const void*>(nullptr),
-                     noise_scale, out, static_cast<void*>(nullptr), out_dtype);
+  if (dtype == FDP_BF16) launch_colsum_dt<BF16>(p, u, v, B, T, H, ws, frob, s);
+  else if (dtype == FDP_F16) launch_colsum_dt<F16>(p, u, v, B, T, H, ws, frob, s);
+  else launch_colsum_dt<F32>(p, u, v, B, T, H, ws, frob, s);
+  const Epilogue e{C, clamp, clip_args_dev, out_scale, noise_scale, noise, nullptr, out, nullptr,
+                   out_dtype, norms, factors};
+  launch_reduce(p, ws, B, H, 1, frob, e, s);
   return hipGetLastError() == hipSuccess ? FDP_OK : FDP_ERR_HIP;
 }
 
@@ -742,41 +861,26 @@ extern "C" int fdp_layernorm_bwd_clip(const void* dy, const void* x, const void*
                                       size_t workspace_bytes, void* stream) {
   if (!valid_dtype(dtype) || !valid_dtype(w_dtype)) return FDP_ERR_DTYPE;
   if (B < 1 || T < 0 || H < 1 || H > kMaxLnH) return FDP_ERR_SHAPE;
-  if (B > 32767) return FDP_ERR_SHAPE;  // 2B streams index grid.y
+  if (B > 32767) return FDP_ERR_SHAPE;  // the 2B streams index grid.y
   if (T > 0 && (dy == nullptr || x == nullptr || dx == nullptr || mean == nullptr ||
                 rstd == nullptr))
     return FDP_ERR_ARG;
   const int cus = num_cus();
-  const LnPlan p = ln_plan(B, T, H, cus);
+  const RedPlan p = ln_plan(B, T, H, cus);
   if (workspace == nullptr || workspace_bytes < p.total) return FDP_ERR_WORKSPACE;
   if (!aligned16(workspace)) return FDP_ERR_ALIGN;
   char* ws = static_cast<char*>(workspace);
-  float* part = reinterpret_cast<float*>(ws + p.off_part);
-  float* sums = reinterpret_cast<float*>(ws + p.off_sums);
-  float* fac = reinterpret_cast<float*>(ws + p.off_fac);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool vec = aligned16(dy) && aligned16(x) && aligned16(dx) && (H * esize(dtype)) % 16 == 0;
   const int epl = ln_epl(H);
-  if (T > 0) {
-    if (dtype == FDP_BF16) launch_ln_bwd<BF16>(vec, epl, p, dy, x, w, w_dtype, mean, rstd, B, T, H, dx, part, s);
-    else if (dtype == FDP_F16) launch_ln_bwd<F16>(vec, epl, p, dy, x, w, w_dtype, mean, rstd, B, T, H, dx, part, s);
-    else launch_ln_bwd<F32>(vec, epl, p, dy, x, w, w_dtype, mean, rstd, B, T, H, dx, part, s);
-  } else {
-    zero_fill(part, int64_t(2 * B) * p.chunks * H, s);
-  }
-  float* sq = reinterpret_cast<float*>(ws + p.off_sq);
-  hipLaunchKernelGGL(chunk_reduce_kernel,
-                     dim3(static_cast<unsigned>(p.nblk), static_cast<unsigned>(2 * B)), dim3(NT), 0,
-                     s, part, H, p.chunks, sums, sq);
-  hipLaunchKernelGGL(stream_factor_kernel, dim3(static_cast<unsigned>((2 * B + 3) / 4)), dim3(NT),
-                     0, s, static_cast<const float*>(sq), 2 * B, p.nblk, C, clamp, clip_args_dev,
-                     fac, norms, factors);
-  if (dw != nullptr || db != nullptr) {
-    // combine_kernel writes out0 from streams [0,B) and out1 from [B,2B).
-    hipLaunchKernelGGL(combine_kernel, dim3(static_cast<unsigned>((H + NT - 1) / NT)), dim3(NT),
-                       0, s, sums, fac, B, H, out_scale, noise_w, noise_b, noise_scale, dw, db,
-                       w_dtype);
-  }
+  const LnBwdIo io{dy, x, w, w_dtype, mean, rstd, B, T, H, dx};
+  float* part = reinterpret_cast<float*>(ws + p.off_part);
+  if (dtype == FDP_BF16) launch_ln_bwd<BF16>(vec, epl, p, io, part, s);
+  else if (dtype == FDP_F16) launch_ln_bwd<F16>(vec, epl, p, io, part, s);
+  else launch_ln_bwd<F32>(vec, epl, p, io, part, s);
+  const Epilogue e{C, clamp, clip_args_dev, out_scale, noise_scale, noise_w, noise_b, dw, db,
+                   w_dtype, norms, factors};
+  launch_reduce(p, ws, B, H, 2, false, e, s);
   return hipGetLastError() == hipSuccess ? FDP_OK : FDP_ERR_HIP;
 }
 

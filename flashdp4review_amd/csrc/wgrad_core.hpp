@@ -380,15 +380,6 @@ __device__ __forceinline__ void tile_coords(const Args& p, int tile, int64_t& m0
 constexpr unsigned kSpinLimit = 1u << 22;
 constexpr int kXcds = 8;
 
-__device__ __forceinline__ void st_coherent(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ld_coherent(const float* p) {
-  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void wait_stores() {
-  __builtin_amdgcn_s_waitcnt((0 & 0xf) | (0x7 << 4) | (0xf << 8));  // vmcnt(0)
-}
 
 // All workgroups of the (co-resident) grid arrive before any leaves.
 __device__ inline void grid_barrier(unsigned* bar, unsigned n, int* err) {
@@ -521,8 +512,6 @@ extern __device__ unsigned long long fdp_phase_ts[1024 * 16];
 // is one 128x128 fp32 tile kept in "thread-major" order: float4 q (0..15) of
 // thread t sits at byte (q*256 + t)*16, which makes every wave instruction one
 // contiguous 1 KB access.
-typedef __attribute__((__vector_size__(4 * sizeof(unsigned)))) unsigned u32x4;
-constexpr int kCoherent = 0x10;  // buffer cache policy bit: sc1
 
 __device__ inline void slot_store(float* slot, const f32x16 (&v)[2][2]) {
   const __amdgpu_buffer_rsrc_t r =

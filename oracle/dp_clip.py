@@ -26,7 +26,7 @@ repository liangyuwang/FlashDP4Review) on float64 copies of its inputs:
 Deliberate deviations from the reference (each pinned by a test):
   - grad_output is never modified in place (reference: linear_clip.py:118-121);
   - Conv1D uses the intended x^T g orientation (transformers_conv1d_clip.py:22-28;
-    the reference layer routes through the Linear helper, transformers_conv1d.py:186-188);
+    the reference layer routes through the Linear helper, layers/transformers_conv1d.py:80-95);
   - LayerNorm clips per sample with one noise draw each for dgamma and dbeta
     (reference fused path clamps lock-group partials elementwise,
     layernorm_clip.py:118-127; non-fused path adds both draws to dgamma,
