@@ -8,7 +8,7 @@
 // v_mfma_f32_32x32x16_{bf16,f16} accumulators.
 //
 //  * Global -> LDS: buffer_load_dwordx4 ... lds (16 bytes per lane straight into
-//    LDS, no VGPR staging).  A 64(k) x R tile of 16-bit values is rows of R/8
+//    LDS, no VGPR staging).  A BK(k) x R tile of 16-bit values is rows of R/8
 //    chunks of 16 bytes; lane l of a wave's load j fills the next 64 slots in
 //    order, i.e. slot -> row k = slot / (R/8), physical chunk slot % (R/8), and
 //    the lane loads logical chunk (physical ^ swz(k)) of that row: every row is
@@ -43,37 +43,45 @@ constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, 32-bit records
 
 __device__ __forceinline__ int swz(int k) { return (k & 3) << 2; }
 
-// Tile geometry: BM x BN outputs, 4 waves in 2 x 2, each (BM/2) x (BN/2).
-template <int BM_, int BN_>
+// Tile geometry: BM x BN outputs, 4 waves in 2 x 2, each (BM/2) x (BN/2);
+// k-tiles of BK rows (a multiple of 16) per LDS stage.
+template <int BM_, int BN_, int BK_ = kBK>
 struct Geom {
   static constexpr int BM = BM_;
   static constexpr int BN = BN_;
+  static constexpr int BK = BK_;
+  static constexpr int KS = BK / 16;      // 16-deep MFMA k-steps per k-tile
   static constexpr int WM = BM / 2;       // wave tile rows
   static constexpr int WN = BN / 2;       // wave tile columns
   static constexpr int FI = WM / 32;      // 32-row MFMA blocks per wave
   static constexpr int FJ = WN / 32;      // 32-column MFMA blocks per wave
-  static constexpr int TILE_A = kBK * BM * 2;
-  static constexpr int TILE_B = kBK * BN * 2;
+  static constexpr int TILE_A = BK * BM * 2;
+  static constexpr int TILE_B = BK * BN * 2;
   static constexpr int STAGE = TILE_A + TILE_B;
   static constexpr int LOADS_A = TILE_A / (4 * 64 * 16);  // per wave per k-tile
   static constexpr int LOADS_B = TILE_B / (4 * 64 * 16);
   static constexpr int LOADS = LOADS_A + LOADS_B;
 };
 
-// One operand's per-thread load state: L buffer loads per k-tile.
-template <int L>
+// One operand's per-thread load state: L buffer loads per k-tile of BK rows.
+//
+// The loads are issued with inline asm rather than the LDS-DMA builtin: the
+// compiler cannot always tell the stage being filled from the one being read
+// and then inserts a full vmcnt(0) drain before the reads.  Outside the
+// compiler's view, every wait on these loads is the explicit wait_tiles()
+// below (its own vmcnt waits stay correct: they only become stronger).
+template <int L, int BK = kBK>
 struct Operand {
-  __amdgpu_buffer_rsrc_t rsrc;
+  u32x4 rsrc;        // raw buffer descriptor of the sample's operand
   uint32_t voff[L];  // byte offsets of this thread's loads for k-tile 0
-  uint32_t step;     // bytes per k-tile (64 rows)
+  uint32_t step;     // bytes per k-tile (BK rows)
 
   // base: the sample's operand [K, ld] (16-bit); R: tile width; r0: first column.
   template <int R>
   __device__ inline void init(const uint16_t* base, int64_t ld, int64_t K, int64_t r0) {
     constexpr int CPR = R / 8;  // 16-byte chunks per row
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), static_cast<short>(0),
-                                             static_cast<int>(K * ld * 2), kRsrcWord3);
+    retarget(base, ld, K);
 #pragma unroll
     for (int j = 0; j < L; ++j) {
       const int slot = (wave * L + j) * 64 + lane;
@@ -81,17 +89,38 @@ struct Operand {
       const int c = (slot % CPR) ^ swz(k);
       voff[j] = static_cast<uint32_t>((int64_t(k) * ld + r0 + 8 * c) * 2);
     }
-    step = static_cast<uint32_t>(kBK * ld * 2);
+    step = static_cast<uint32_t>(BK * ld * 2);
+  }
+  // The same tile of another sample (same ld, K and columns).  Records past
+  // K*ld*2 bytes read as zero.
+  __device__ __forceinline__ void retarget(const uint16_t* base, int64_t ld, int64_t K) {
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    rsrc = u32x4{static_cast<uint32_t>(a), static_cast<uint32_t>(a >> 32) & 0xffffu,
+                 static_cast<uint32_t>(K * ld * 2), kRsrcWord3};
   }
 
+  // buffer_load_dwordx4 ... lds: lane l of load j writes 16 bytes to
+  // tile + (wave*L + j)*1024 + 16*l; M0 holds the wave's LDS address for the
+  // load and is restored afterwards (the compiler may keep a value in it).
   __device__ __forceinline__ void issue(FDP_LDS char* tile, int kt) const {
-    const int wave = threadIdx.x >> 6;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(tile)) + wave * L * 1024;
     const uint32_t add = step * static_cast<uint32_t>(kt);
+    u32x4 r;
 #pragma unroll
-    for (int j = 0; j < L; ++j)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rsrc, reinterpret_cast<FDP_LDS void*>(tile + (wave * L + j) * 1024), 16, voff[j] + add,
-          0, 0, 0);
+    for (int w = 0; w < 4; ++w) r[w] = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(rsrc[w]));
+#pragma unroll
+    for (int j = 0; j < L; ++j) {
+      uint32_t saved;
+      asm volatile(
+          "s_mov_b32 %0, m0\n\t"
+          "s_mov_b32 m0, %1\n\t"
+          "buffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
+          "s_mov_b32 m0, %0"
+          : "=&s"(saved)
+          : "s"(lds + j * 1024), "v"(voff[j] + add), "s"(r)
+          : "memory");
+    }
   }
 };
 
@@ -159,12 +188,12 @@ struct Frags {
   }
 };
 
-// One 64-deep k-tile of the wave's sub-tile from LDS stage `st`.
+// One BK-deep k-tile of the wave's sub-tile from LDS stage `st`.
 template <class DT, class G>
 __device__ __forceinline__ void compute_stage(const FDP_LDS char* st, const FragOffsets<G>& fo,
                                               f32x16 (&acc)[G::FI][G::FJ]) {
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
+  for (int ks = 0; ks < G::KS; ++ks) {
     Frags<G> f;
     f.load(st, fo, ks);
 #pragma unroll
@@ -180,13 +209,15 @@ __device__ __forceinline__ void wait_vm() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
   __builtin_amdgcn_s_waitcnt((N & 0xf) | (0x7 << 4) | (0xf << 8) | ((N >> 4) << 14));
 }
-// Wait until at most `tiles` k-tiles (L loads each) of this thread's loads are outstanding.
+// Wait until at most `tiles` k-tiles (L loads each) of this thread's loads are
+// outstanding (stores issued in between only make the wait stronger).
 template <int L>
 __device__ __forceinline__ void wait_tiles(int tiles) {
   switch (tiles) {
     case 0: wait_vm<0>(); break;
     case 1: wait_vm<L>(); break;
-    default: wait_vm<2 * L>(); break;
+    case 2: wait_vm<2 * L>(); break;
+    default: wait_vm<3 * L>(); break;
   }
 }
 
@@ -213,12 +244,17 @@ struct Stages {
 // Per-thread state of one (tile, sample) product.
 template <class G>
 struct Job {
-  Operand<G::LOADS_A> a;
-  Operand<G::LOADS_B> b;
+  Operand<G::LOADS_A, G::BK> a;
+  Operand<G::LOADS_B, G::BK> b;
   __device__ __forceinline__ void init(const uint16_t* pa, int64_t lda, const uint16_t* pb,
                                        int64_t ldb, int64_t K, int64_t m0, int64_t n0) {
     a.template init<G::BM>(pa, lda, K, m0);
     b.template init<G::BN>(pb, ldb, K, n0);
+  }
+  __device__ __forceinline__ void retarget(const uint16_t* pa, int64_t lda, const uint16_t* pb,
+                                           int64_t ldb, int64_t K) {
+    a.retarget(pa, lda, K);
+    b.retarget(pb, ldb, K);
   }
   __device__ __forceinline__ void issue(FDP_LDS char* stage, int kt) const {
     a.issue(stage, kt);

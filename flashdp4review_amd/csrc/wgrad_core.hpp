@@ -547,23 +547,33 @@ __device__ inline void slot_add(const float* slot, f32x16 (&v)[2][2]) {
 }
 
 // out[m, n] = out_scale * tot + noise_scale * noise for one 128x128 tile, staged
-// through LDS (rows 0..63 in lo, 64..127 in hi, 32 KB each, fp32) so that the
+// through LDS (rows 32q .. 32q+31 in quarter q, 16 KB each, fp32) so that the
 // global stores and noise loads are 16-byte row chunks.
+__device__ __forceinline__ float* quarter(float* const (&q)[4], int i) {
+  switch (i) {
+    case 0: return q[0];
+    case 1: return q[1];
+    case 2: return q[2];
+    default: return q[3];
+  }
+}
+
 template <class OT>
 __device__ inline void store_tile_staged(const Args& p, int64_t m0, int64_t n0,
-                                         const f32x16 (&tot)[2][2], float* lo, float* hi) {
+                                         const f32x16 (&tot)[2][2], float* const (&q4)[4]) {
   using S = typename OT::storage;
   constexpr int E = 16 / sizeof(S);  // elements per 16-byte chunk
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
-  float* half = wm == 0 ? lo : hi;
 #pragma unroll
-  for (int a = 0; a < 2; ++a)
+  for (int a = 0; a < 2; ++a) {
+    float* qd = quarter(q4, wm / 32 + a);
 #pragma unroll
     for (int c = 0; c < 2; ++c)
 #pragma unroll
       for (int r = 0; r < 16; ++r)
-        half[(acc_row(0, a, lane, r)) * BN + acc_col(wn, c, lane)] = tot[a][c][r];
+        qd[(acc_row(0, 0, lane, r)) * BN + acc_col(wn, c, lane)] = tot[a][c][r];
+  }
   __syncthreads();
   S* out = static_cast<S*>(p.out);
   const S* noise = static_cast<const S*>(p.noise);
@@ -574,7 +584,7 @@ __device__ inline void store_tile_staged(const Args& p, int64_t m0, int64_t n0,
     const int row = q / CPR, col = (q % CPR) * E;
     const int64_t m = m0 + row, n = n0 + col;
     if (m >= p.M || n >= p.N) continue;
-    const float* src = (row < 64 ? lo : hi) + (row & 63) * BN + col;
+    const float* src = quarter(q4, row >> 5) + (row & 31) * BN + col;
     float v[E];
 #pragma unroll
     for (int e = 0; e < E; ++e) v[e] = src[e] * p.out_scale;
@@ -610,9 +620,12 @@ __device__ inline void store_tile_staged(const Args& p, int64_t m0, int64_t n0,
 // sum_b c_b G_b for its tile in sample order and leaves it in its group's
 // slot.  The last group to arrive at a tile sums the slots in group order
 // (deterministic) and writes the output (or the running chunk sum).
+constexpr int kStages = 2;  // LDS ring depth of the single-pass kernel (64-deep k-tiles)
+
 template <class DT, int U>
 __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
-  using G = dma::Geom<BM, BN>;
+  using G = dma::Geom<BM, BN, 64>;
+  static_assert(kStages * G::STAGE == BM * BN * 4, "the output staging reuses the ring");
   __shared__ __attribute__((aligned(16))) char st0[G::STAGE];
   __shared__ __attribute__((aligned(16))) char st1[G::STAGE];
   __shared__ float red[NT / kWave];
@@ -630,44 +643,79 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
   const int nb = static_cast<int>((b0 + p.spg < bend ? b0 + p.spg : bend) - b0);
   int64_t m0, n0;
   tile_coords(p, tile, m0, n0);
-  const int nk = static_cast<int>((p.K + dma::kBK - 1) / dma::kBK);
+  const int nk = static_cast<int>((p.K + G::BK - 1) / G::BK);
   dma::FragOffsets<G> fo;
   fo.init(wm, wn);
   FDP_TS(0);
 
-  // ---- phase 1
+  // ---- phase 1: the nb per-sample products run as one stream of nb*nk
+  // k-tiles through the LDS ring, so that the next sample's first k-tiles
+  // load while this sample's last ones multiply and its norm is taken.
+  const uint16_t* pa = static_cast<const uint16_t*>(p.a);
+  const uint16_t* pb = static_cast<const uint16_t*>(p.b);
   Held<true> held[U > 1 ? U - 1 : 1];
   f32x16 acc[2][2];
-  for (int i = 0; i < nb; ++i) {
-    const int64_t bidx = b0 + i;
-    dma::Job<G> job;
-    job.init(static_cast<const uint16_t*>(p.a) + bidx * p.sab, p.lda,
-             static_cast<const uint16_t*>(p.b) + bidx * p.sbb, p.ldb, p.K, m0, n0);
+  zero(acc);
+  const int nq = nb * nk;
+  dma::Job<G> job;  // loads of k-tile ik of unit iu, the next one to issue
+  int iu = 0, ik = 0;
+  if (nq > 0) job.init(pa + b0 * p.sab, p.lda, pb + b0 * p.sbb, p.ldb, p.K, m0, n0);
+  auto issue_next = [&](FDP_LDS char* stage) {
+    job.issue(stage, ik);
+    if (++ik == nk) {
+      ik = 0;
+      if (++iu < nb) job.retarget(pa + (b0 + iu) * p.sab, p.lda, pb + (b0 + iu) * p.sbb, p.ldb, p.K);
+    }
+  };
+  dma::wait_vm<0>();
 #pragma unroll
-    for (int j = 0; j < U - 1; ++j)
-      if (j == i - 1) held[j].put(acc);  // park the previous product
-    zero(acc);
-    dma::gemm<DT, G, 2>(job, nk, fo, stages, acc);
-    // Rows/columns past M/N may hold the next row's values: leave them out.
-    float s = 0.f;
+  for (int s = 0; s < kStages - 1; ++s)
+    if (s < nq) issue_next(stages.get(s));
+  int cu = 0, ck = 0;  // unit / k-tile being multiplied
+  for (int base = 0; base < nq; base += kStages) {
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+    for (int s = 0; s < kStages; ++s) {
+      const int q = base + s;
+      if (q < nq) {
+        const int ahead = nq - 1 - q;
+        dma::wait_tiles<G::LOADS>(ahead < kStages - 2 ? ahead : kStages - 2);
+        dma::barrier();
+        if (q + kStages - 1 < nq) issue_next(stages.get((s + kStages - 1) % kStages));
+        dma::compute_stage<DT, G>(stages.get(s), fo, acc);
+        if (++ck == nk) {
+          // product of sample b0+cu done.  Rows/columns past M/N may hold the
+          // next row's values: leave them out of the norm.
+          float sq = 0.f;
 #pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        const bool ncol = n0 + acc_col(wn, c, lane) < p.N;
+          for (int a = 0; a < 2; ++a)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const bool in = ncol && (m0 + acc_row(wm, a, lane, r) < p.M);
-          s += in ? acc[a][c][r] * acc[a][c][r] : 0.f;
+            for (int c = 0; c < 2; ++c) {
+              const bool ncol = n0 + acc_col(wn, c, lane) < p.N;
+#pragma unroll
+              for (int r = 0; r < 16; ++r) {
+                const bool in = ncol && (m0 + acc_row(wm, a, lane, r) < p.M);
+                sq += in ? acc[a][c][r] * acc[a][c][r] : 0.f;
+              }
+            }
+          sq = wave_sum(sq);
+          if (lane == 0) red[wave] = sq;
+          __syncthreads();
+          if (threadIdx.x == 0)
+            st_coherent(p.partials + (b0 + cu) * tiles + tile, (red[0] + red[1]) + (red[2] + red[3]));
+          FDP_TS(1 + cu);
+          if (cu + 1 < nb) {  // park it and start the next product
+#pragma unroll
+            for (int j = 0; j < U - 1; ++j)
+              if (j == cu) held[j].put(acc);
+            zero(acc);
+          }
+          ck = 0;
+          ++cu;
         }
       }
-    s = wave_sum(s);
-    if (lane == 0) red[wave] = s;
-    __syncthreads();
-    if (threadIdx.x == 0)
-      st_coherent(p.partials + bidx * tiles + tile, (red[0] + red[1]) + (red[2] + red[3]));
-    FDP_TS(1 + i);
+    }
   }
+  dma::barrier();  // every wave is done reading the ring
 
   grid_barrier(p.bar, unsigned(p.nwg), p.err);
   FDP_TS(9);
@@ -763,11 +811,11 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
         }
     }
     if (p.chunk_last) {
-      float* lo = reinterpret_cast<float*>(st0);
-      float* hi = reinterpret_cast<float*>(st1);
-      if (p.out_dtype == FDP_BF16) store_tile_staged<BF16>(p, m0, n0, acc, lo, hi);
-      else if (p.out_dtype == FDP_F16) store_tile_staged<F16>(p, m0, n0, acc, lo, hi);
-      else store_tile_staged<F32>(p, m0, n0, acc, lo, hi);
+      float* const q4[4] = {reinterpret_cast<float*>(st0), reinterpret_cast<float*>(st0) + 4096,
+                            reinterpret_cast<float*>(st1), reinterpret_cast<float*>(st1) + 4096};
+      if (p.out_dtype == FDP_BF16) store_tile_staged<BF16>(p, m0, n0, acc, q4);
+      else if (p.out_dtype == FDP_F16) store_tile_staged<F16>(p, m0, n0, acc, q4);
+      else store_tile_staged<F32>(p, m0, n0, acc, q4);
       FDP_TS(12);
     }
   }
