@@ -6,15 +6,15 @@ grad_out [8,1024,3072] ~ N(0,0.02^2), C = 1, sigma = 1:
     dW = (1/B) sum_b clip(||g_b^T x_b||) g_b^T x_b + (sigma/sqrt(B)) z
 One step = one noise draw + one fdp_wgrad_clip call (single-pass kernel:
 per-sample products, norms, factors, clipped sum, 1/B and the noise add in
-its epilogue), inputs resident in HBM, default (cooperative) launch.
+its epilogue), inputs resident in HBM, default (ordinary-dispatch) launch.
 
 value = algorithmic TFLOP/s = 2*B*T*M*N / step time (norm, scale and recompute
 flops are not credited).  The JSON line also carries the roofline of the
 dominant kernel (wgrad_group_kernel: HIP events on the launch stream around
 back-to-back calls in ordinary-dispatch mode, where one call is exactly one
 launch of that kernel), the reference's torch op sequence timed on the host CPU
-(cpu_baseline), and extra measurements: the same step with the ordinary
-dispatch, the DP Linear layer fwd+bwd vs a plain nn.Linear, the Conv1D (cfg3)
+(cpu_baseline), and extra measurements: the same step with the cooperative
+launch, the DP Linear layer fwd+bwd vs a plain nn.Linear, the Conv1D (cfg3)
 and LayerNorm (cfg4) paths.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload cfg2|cfg3|cfg4]
@@ -217,15 +217,16 @@ def main():
         x, go, _ = cfg2_inputs(dev)
         B, T, I, O = 8, 1024, 768, 3072
         step, _ = run_wgrad(x, go, torch.bfloat16)
-        step_plain, kernel_call = run_wgrad(x, go, torch.bfloat16, launch="plain")
+        step_coop, _ = run_wgrad(x, go, torch.bfloat16, launch="cooperative")
+        _, kernel_call = run_wgrad(x, go, torch.bfloat16, launch="plain")
         workload = ("cfg2: DP Linear 768->3072 clipped per-sample weight grad, B=8 T=1024, "
                     "C=1, sigma=1")
     elif args.workload == "cfg3":
         x, go = cfg3_inputs(dev)
         B, T, I, O = 16, 1024, 768, 2304
         step, _ = run_wgrad(x, go, torch.bfloat16, transpose=True)
-        step_plain, kernel_call = run_wgrad(x, go, torch.bfloat16, transpose=True,
-                                            launch="plain")
+        step_coop, _ = run_wgrad(x, go, torch.bfloat16, transpose=True, launch="cooperative")
+        _, kernel_call = run_wgrad(x, go, torch.bfloat16, transpose=True, launch="plain")
         workload = "cfg3: DP Conv1D 768->2304 clipped per-sample weight grad, B=16 T=1024"
     else:
         from flashdp4review_amd.core import layernorm_bwd_clip, layernorm_fwd
@@ -241,7 +242,7 @@ def main():
             return layernorm_bwd_clip(gl, xl, w, mean, rstd, 1.0, 1.0, out_scale=1.0 / 16,
                                       noise_w=zw, noise_b=zb, noise_scale=0.25)
 
-        step_plain = None
+        step_coop = None
         kernel_call = lambda: layernorm_bwd_clip(gl, xl, w, mean, rstd, 1.0, 1.0)  # noqa: E731
 
     # ---- timed region: K steps bracketed by synchronisation
@@ -292,10 +293,10 @@ def main():
         out["cpu_baseline"] = cpu_baseline_cfg2()
     if not args.no_extra and args.workload == "cfg2":
         extra = {}
-        t_plain = median_cuda_time(step_plain, args.steps, 3, reps=3)
+        t_coop = median_cuda_time(step_coop, args.steps, 3, reps=3)
         F = 2.0 * B * T * I * O
-        extra["cfg2_step_plain_dispatch"] = {"ms": round(t_plain, 4),
-                                             "tflops": round(F / t_plain / 1e9, 2)}
+        extra["cfg2_step_cooperative_launch"] = {"ms": round(t_coop, 4),
+                                                 "tflops": round(F / t_coop / 1e9, 2)}
         extra.update(extra_measurements(dev, max(5, args.steps // 5), 3))
         out["extra"] = extra
     out["device"] = torch.cuda.get_device_name(dev)

@@ -20,7 +20,7 @@ from .utils import RuntimeAutoTuner
 
 
 _LAUNCH_MODES = ("cooperative", "plain")
-_launch_mode = os.environ.get("FDP_WGRAD_LAUNCH", "cooperative")
+_launch_mode = os.environ.get("FDP_WGRAD_LAUNCH", "plain")
 if _launch_mode not in _LAUNCH_MODES:
     raise ValueError(f"FDP_WGRAD_LAUNCH must be one of {_LAUNCH_MODES}, got {_launch_mode!r}")
 _ws_sizes: dict = {}
@@ -52,12 +52,16 @@ def release_workspaces() -> None:
 def set_wgrad_launch(mode: str) -> str:
     """Default launch of the single-pass kernel; returns the previous mode.
 
-    "cooperative" (default) is safe whatever else runs on the device.  "plain"
-    dispatches it as an ordinary kernel, which saves the runtime's
-    cooperative-launch synchronisation (about 15 us per call) but requires
-    that nothing else occupies the device during the call (no concurrent
-    streams, e.g. collectives); a violated guarantee is reported through the
-    workspace status word (``check=True``), never a hang.
+    "plain" (default): an ordinary dispatch.  The grid is sized to the
+    kernel's occupancy, so on a device with nothing else resident every
+    workgroup runs at once; work on other streams only delays workgroups
+    until it finishes.  If a grid wait nevertheless expires (seconds), the
+    affected outputs are NaN and the workspace status word is set
+    (``check=True`` raises): results are never silently wrong.
+    "cooperative": hipLaunchCooperativeKernel, which guarantees co-residency
+    at the cost of the runtime's synchronisation around each launch (about
+    25 us per call on MI355X); use it when another kernel running at the
+    same time may wait on this one.
     """
     global _launch_mode
     if mode not in _LAUNCH_MODES:

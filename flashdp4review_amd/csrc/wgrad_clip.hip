@@ -32,6 +32,8 @@
 // in 16-byte chunks to spread both the transposing writes and the fragment
 // reads over the banks.  LDS is double-buffered: the next k-tile's global loads
 // are issued before the current tile's MFMAs.
+#include <cstdlib>
+
 #include "wgrad_core.hpp"
 
 namespace fdp {
@@ -200,6 +202,15 @@ struct Plan {
   size_t total_two_pass, total_fused, total;
 };
 
+// Polls before a grid wait of the single-pass kernel gives up (seconds of
+// waiting).  FDP_WGRAD_SPIN_LIMIT overrides it so that tests can exercise the
+// expiry path with every kernel still running to completion.
+unsigned spin_limit() {
+  const char* e = getenv("FDP_WGRAD_SPIN_LIMIT");
+  if (e != nullptr && *e != '\0') return static_cast<unsigned>(strtoul(e, nullptr, 10));
+  return kSpinLimit;
+}
+
 int num_cus() {
   int dev = 0, cus = 256;
   if (hipGetDevice(&dev) == hipSuccess) {
@@ -354,6 +365,7 @@ extern "C" int fdp_wgrad_clip(const void* a, const void* b, int64_t B, int64_t K
   args.err = reinterpret_cast<int*>(ws);
   args.bar = reinterpret_cast<unsigned*>(ws) + 1;
   args.done = reinterpret_cast<unsigned*>(ws) + 2;
+  args.spin_limit = spin_limit();
   args.tile_turn = reinterpret_cast<unsigned*>(ws + pl.off_turn);
   args.tile_acc = reinterpret_cast<float*>(ws + pl.off_slots);
   args.chunk_acc = reinterpret_cast<float*>(ws + pl.off_chunk);

@@ -39,6 +39,7 @@ struct Args {
   unsigned* tile_turn;    // [tiles] hand-over tickets for tiles shared by workgroups
   float* tile_acc;        // [tiles, BM*BN] fp32 running sums of shared tiles
   int* err;               // set when a bounded wait gives up
+  unsigned spin_limit;    // polls before a grid wait gives up
   float C, clamp;
   const float* clip_args_dev;
   float* norms_out;       // optional [B]
@@ -381,22 +382,31 @@ constexpr unsigned kSpinLimit = 1u << 22;
 constexpr int kXcds = 8;
 
 
-// All workgroups of the (co-resident) grid arrive before any leaves.
-__device__ inline void grid_barrier(unsigned* bar, unsigned n, int* err) {
+// All workgroups of the (co-resident) grid arrive before any leaves.  Returns
+// (in every thread) whether this workgroup's results must be poisoned: its own
+// wait expired, or an earlier workgroup's did (that one set *err before this
+// one could arrive).
+__device__ inline bool grid_barrier(unsigned* bar, unsigned n, int* err, unsigned limit,
+                                    int* flag) {
   wait_stores();
   __syncthreads();
   if (threadIdx.x == 0) {
     __hip_atomic_fetch_add(bar, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     unsigned spins = 0;
+    int bad = 0;
     while (__hip_atomic_load(bar, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < n) {
       __builtin_amdgcn_s_sleep(1);
-      if (++spins > kSpinLimit) {
+      if (++spins > limit) {
         atomicOr(err, 1);
+        bad = 1;
         break;
       }
     }
+    if (!bad) bad = __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+    *flag = bad;
   }
   __syncthreads();
+  return *flag != 0;
 }
 
 // Workgroups are dealt round-robin to the 8 XCDs; give each XCD a contiguous
@@ -717,7 +727,10 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
   }
   dma::barrier();  // every wave is done reading the ring
 
-  grid_barrier(p.bar, unsigned(p.nwg), p.err);
+  // A wait that expired (only possible when the grid was not resident at once)
+  // poisons this workgroup's results with NaN rather than leave them silently
+  // wrong; the status word reports it.
+  const bool poisoned = grid_barrier(p.bar, unsigned(p.nwg), p.err, p.spin_limit, &is_last);
   FDP_TS(9);
 
   // ---- clip factors of this group's samples: all partials in one sweep
@@ -739,8 +752,8 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
     if (lane == 0) red[wave] = s;
     __syncthreads();
     if (threadIdx.x == 0 && i < nb) {
-      const float n = sqrtf((red[0] + red[1]) + (red[2] + red[3]));
-      const float cf = clip_factor(n, C, clamp);
+      const float n = poisoned ? __builtin_nanf("") : sqrtf((red[0] + red[1]) + (red[2] + red[3]));
+      const float cf = poisoned ? n : clip_factor(n, C, clamp);
       fac[i] = cf;
       if (tile == 0) {
         if (p.norms_out) p.norms_out[b0 + i] = n;

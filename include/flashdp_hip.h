@@ -102,11 +102,13 @@ int fdp_version(void);
  *            cooperative kernel the library uses whenever the problem fits it;
  *            bit 2 (FDP_WGRAD_PLAIN_LAUNCH) dispatches the single-pass kernel
  *            as an ordinary launch instead of a cooperative one, saving the
- *            runtime's cooperative-launch synchronisation (about 15 us per
- *            call on MI355X).  The caller then guarantees that nothing else
- *            occupies the device during the call, so that the grid (sized to
- *            the kernel's occupancy) is resident at once; if that fails, a
- *            bounded wait expires and the status word below is set;
+ *            runtime's cooperative-launch synchronisation (about 25 us per
+ *            call on MI355X).  The grid is sized to the kernel's occupancy,
+ *            so it is resident at once when nothing else occupies the device;
+ *            work on other streams only delays it.  The caller must not run
+ *            concurrently a kernel that waits on this one.  Should a bounded
+ *            grid wait (seconds) still expire, the affected outputs (and
+ *            norms/factors) are NaN and the status word below is set;
  *            bit 3 (FDP_WGRAD_CLEAN_WORKSPACE) states that the workspace's
  *            control words (its first 256 bytes and the per-tile tickets after
  *            them) are zero -- a zero-filled buffer, or one whose last use was

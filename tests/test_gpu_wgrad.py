@@ -139,6 +139,29 @@ def test_wgrad_reused_workspace_stays_clean(shape):
     assert_close(ref, exp, torch.bfloat16, "clipped sum")
 
 
+def test_wgrad_expired_grid_wait_is_loud(monkeypatch):
+    """Force the single-pass kernel's bounded grid wait to expire at its first poll
+    (FDP_WGRAD_SPIN_LIMIT=0; every kernel still runs to completion): the affected
+    outputs are NaN, the status word is set and check=True raises.  The next call
+    on the same workspace is clean again."""
+    from flashdp4review_amd import _lib
+    a, b = make(8, 1024, 512, 384, torch.bfloat16, "tn", seed=13)
+    monkeypatch.setenv("FDP_WGRAD_SPIN_LIMIT", "0")
+    for launch in ("plain", "cooperative"):
+        with pytest.raises(_lib.FlashDPError):
+            out = core.wgrad_clip(a, b, 0.5, 1.0, launch=launch, out_dtype=torch.float32,
+                                  check=True)
+        out = core.wgrad_clip(a, b, 0.5, 1.0, launch=launch, out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        assert torch.isnan(out).any()
+        with pytest.raises(_lib.FlashDPError):  # the status word is sticky until checked
+            core.wgrad_clip(a, b, 0.5, 1.0, launch=launch, out_dtype=torch.float32, check=True)
+    monkeypatch.delenv("FDP_WGRAD_SPIN_LIMIT")
+    ref, _, _ = O.wgrad_clip(a, b, 0.5, 1.0, "tn")
+    out = core.wgrad_clip(a, b, 0.5, 1.0, out_dtype=torch.float32, check=True)
+    assert_close(out, ref, torch.bfloat16, "after expiry")
+
+
 def test_wgrad_does_not_modify_inputs():
     a, b = make(4, 64, 128, 128, torch.bfloat16, "tn", seed=8)
     a0, b0 = a.clone(), b.clone()
