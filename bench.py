@@ -138,6 +138,131 @@ def cpu_baseline_cfg2():
             "cpu_model": platform.processor() or platform.machine()}
 
 
+# ------------------------------------------------------------------------ cfg5
+def _attention(q, k, v):
+    """Causal attention on a fused backend (flash / memory-efficient); the plain
+    math backend is excluded because its bf16 batched products with transposed
+    operands are avoided on these GPUs.  Falls back to fp32 products."""
+    import torch.nn.functional as F
+    try:
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+            return F.scaled_dot_product_attention(q, k, v, is_causal=True)
+    except (RuntimeError, ImportError):
+        T = q.shape[-2]
+        qf, kf, vf = q.float(), k.float().transpose(-1, -2).contiguous(), v.float().contiguous()
+        att = torch.matmul(qf, kf) / math.sqrt(q.shape[-1])
+        mask = torch.ones(T, T, device=q.device, dtype=torch.bool).tril()
+        att = att.masked_fill(~mask, float("-inf")).softmax(-1)
+        return torch.matmul(att, vf).to(q.dtype)
+
+
+def gpt_model(n_layer=24, d=2048, n_head=16, ffn=8192, vocab=50257, ctx=1024):
+    """GPT-2-style decoder (pre-LN, no Linear bias, GELU MLP), random init."""
+    import torch.nn as nn
+    import torch.nn.functional as F
+
+    class Block(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.ln_1 = nn.LayerNorm(d)
+            self.c_attn = nn.Linear(d, 3 * d, bias=False)
+            self.c_proj = nn.Linear(d, d, bias=False)
+            self.ln_2 = nn.LayerNorm(d)
+            self.c_fc = nn.Linear(d, ffn, bias=False)
+            self.mlp_proj = nn.Linear(ffn, d, bias=False)
+
+        def forward(self, x):
+            B, T, C = x.shape
+            q, k, v = self.c_attn(self.ln_1(x)).split(C, dim=2)
+            q, k, v = (t.view(B, T, n_head, C // n_head).transpose(1, 2) for t in (q, k, v))
+            y = _attention(q, k, v).transpose(1, 2).reshape(B, T, C)
+            x = x + self.c_proj(y)
+            return x + self.mlp_proj(F.gelu(self.c_fc(self.ln_2(x))))
+
+    class GPT(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.wte = nn.Embedding(vocab, d)
+            self.wpe = nn.Embedding(ctx, d)
+            self.h = nn.ModuleList(Block() for _ in range(n_layer))
+            self.ln_f = nn.LayerNorm(d)
+            self.lm_head = nn.Linear(d, vocab, bias=False)
+            for m in self.modules():
+                if isinstance(m, (nn.Linear, nn.Embedding)):
+                    nn.init.normal_(m.weight, std=0.02)
+
+        def forward(self, idx):
+            pos = torch.arange(idx.shape[1], device=idx.device)
+            x = self.wte(idx) + self.wpe(pos)
+            for blk in self.h:
+                x = blk(x)
+            return self.lm_head(self.ln_f(x))
+
+    return GPT()
+
+
+def cfg5_training(dev, steps=5, warmup=2, n_layer=24):
+    """Tokens/s of full training steps (fwd, bwd, Adam) of the cfg5 decoder, plain and
+    with every Linear/LayerNorm except lm_head wrapped by wrap_with_flashdp_layers
+    (C=1, sigma=1), bf16 weights, B=8, T=1024, uniform random token ids."""
+    import contextlib
+    import copy
+    import torch.nn as nn
+    import torch.nn.functional as F
+    from flashdp4review_amd import wrap_with_flashdp_layers
+    B, T, V = 8, 1024, 50257
+    torch.manual_seed(0)
+    base = gpt_model(n_layer=n_layer).to(dev, torch.bfloat16)
+    g = torch.Generator(device=dev).manual_seed(0)
+    idx = torch.randint(0, V, (B, T + 1), device=dev, generator=g)
+    x, y = idx[:, :-1].contiguous(), idx[:, 1:].contiguous()
+
+    def run(model):
+        opt = torch.optim.Adam(model.parameters(), lr=1e-5, foreach=True)
+
+        def step():
+            logits = model(x)
+            loss = F.cross_entropy(logits.view(-1, V).float(), y.view(-1))
+            loss.backward()
+            opt.step()
+            opt.zero_grad(set_to_none=True)
+            return loss
+
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(steps):
+            loss = step()
+        e.record()
+        torch.cuda.synchronize()
+        ms = s.elapsed_time(e) / steps
+        return ms, float(loss.item())
+
+    ms_plain, loss_plain = run(base)
+    dp = copy.deepcopy(base)
+    with contextlib.redirect_stdout(sys.stderr):
+        wrap_with_flashdp_layers(dp, target_modules=[nn.Linear, nn.LayerNorm],
+                                 skip_layers=["lm_head"], C=1.0, noise_multiplier=1.0,
+                                 feedback=False)
+    del base
+    torch.cuda.empty_cache()
+    ms_dp, loss_dp = run(dp)
+    del dp
+    torch.cuda.empty_cache()
+    tok = B * T
+    return {"workload": f"cfg5: GPT-2-style decoder {n_layer}L d=2048 h=16 ffn=8192 V=50257, "
+                        "B=8 T=1024 bf16, Adam, C=1 sigma=1",
+            "dp_tokens_per_s": round(tok / ms_dp * 1e3, 1),
+            "non_dp_tokens_per_s": round(tok / ms_plain * 1e3, 1),
+            "dp_over_non_dp_throughput": round(ms_plain / ms_dp, 4),
+            "ms_per_step": {"dp": round(ms_dp, 2), "non_dp": round(ms_plain, 2)},
+            "final_loss": {"dp": round(loss_dp, 4), "non_dp": round(loss_plain, 4)},
+            "steps": steps, "warmup": warmup}
+
+
 # ---------------------------------------------------------------------- extras
 def extra_measurements(dev, steps, warmup):
     import torch.nn as nn
@@ -187,7 +312,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="cfg2", choices=["cfg2", "cfg3", "cfg4"])
+    ap.add_argument("--workload", default="cfg2", choices=["cfg2", "cfg3", "cfg4", "cfg5"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MiB",
@@ -204,6 +329,18 @@ def main():
     torch.cuda.set_device(dev)
     from flashdp4review_amd import _lib
     _lib.lib()  # fail loudly if the HIP library is missing
+
+    if args.workload == "cfg5":
+        r = cfg5_training(dev, steps=args.steps, warmup=args.warmup)
+        out = {"metric": "DP-SGD train tokens/s", "value": r["dp_tokens_per_s"],
+               "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+               "ms_per_step": r["ms_per_step"]["dp"], "higher_is_better": True,
+               "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+               "data": "synthetic (uniform random token ids, random-init weights)",
+               "config": {"workload": r["workload"]}, "extra": r,
+               "device": torch.cuda.get_device_name(dev)}
+        print(json.dumps(out), flush=True)
+        return
 
     if args.copy_calibration > 0:
         n = args.copy_calibration * (1 << 20) // 4

@@ -73,7 +73,8 @@ struct Geom {
 template <int L, int BK = kBK>
 struct Operand {
   u32x4 rsrc;        // raw buffer descriptor of the sample's operand
-  uint32_t voff[L];  // byte offsets of this thread's loads for k-tile 0
+  uint32_t voff[L];  // byte offsets of this thread's loads for k-tile 0, column 0
+  uint32_t col;      // byte offset of the tile's first column (uniform)
   uint32_t step;     // bytes per k-tile (BK rows)
 
   // base: the sample's operand [K, ld] (16-bit); R: tile width; r0: first column.
@@ -87,8 +88,9 @@ struct Operand {
       const int slot = (wave * L + j) * 64 + lane;
       const int k = slot / CPR;
       const int c = (slot % CPR) ^ swz(k);
-      voff[j] = static_cast<uint32_t>((int64_t(k) * ld + r0 + 8 * c) * 2);
+      voff[j] = static_cast<uint32_t>((int64_t(k) * ld + 8 * c) * 2);
     }
+    retile(r0);
     step = static_cast<uint32_t>(BK * ld * 2);
   }
   // The same tile of another sample (same ld, K and columns).  Records past
@@ -98,6 +100,8 @@ struct Operand {
     rsrc = u32x4{static_cast<uint32_t>(a), static_cast<uint32_t>(a >> 32) & 0xffffu,
                  static_cast<uint32_t>(K * ld * 2), kRsrcWord3};
   }
+  // Another tile (first column r0) of the same operand.
+  __device__ __forceinline__ void retile(int64_t r0) { col = static_cast<uint32_t>(r0 * 2); }
 
   // buffer_load_dwordx4 ... lds: lane l of load j writes 16 bytes to
   // tile + (wave*L + j)*1024 + 16*l; M0 holds the wave's LDS address for the
@@ -105,7 +109,7 @@ struct Operand {
   __device__ __forceinline__ void issue(FDP_LDS char* tile, int kt) const {
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(tile)) + wave * L * 1024;
-    const uint32_t add = step * static_cast<uint32_t>(kt);
+    const uint32_t add = step * static_cast<uint32_t>(kt) + col;
     u32x4 r;
 #pragma unroll
     for (int w = 0; w < 4; ++w) r[w] = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(rsrc[w]));
@@ -255,6 +259,10 @@ struct Job {
                                            int64_t ldb, int64_t K) {
     a.retarget(pa, lda, K);
     b.retarget(pb, ldb, K);
+  }
+  __device__ __forceinline__ void retile(int64_t m0, int64_t n0) {
+    a.retile(m0);
+    b.retile(n0);
   }
   __device__ __forceinline__ void issue(FDP_LDS char* stage, int kt) const {
     a.issue(stage, kt);

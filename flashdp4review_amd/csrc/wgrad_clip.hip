@@ -188,7 +188,8 @@ inline size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 // Workspace layout (both schedules):
 //   [0, 256)            status word (int), barrier and finished-workgroup
 //                       counters (uint); zero between calls, except a status set
-//                       by an expired wait
+//                       by an expired wait (the only words a reused workspace
+//                       must carry over: everything after them is rewritten)
 //   off_turn            per-tile counters [tiles] (uint)
 //   off_partials        partials [B, tiles] (fp32)
 //   two-pass:  off_factors [B], off_group [groups, M, N] (fp32)

@@ -110,10 +110,10 @@ int fdp_version(void);
  *            grid wait (seconds) still expire, the affected outputs (and
  *            norms/factors) are NaN and the status word below is set;
  *            bit 3 (FDP_WGRAD_CLEAN_WORKSPACE) states that the workspace's
- *            control words (its first 256 bytes and the per-tile tickets after
- *            them) are zero -- a zero-filled buffer, or one whose last use was
- *            a completed fdp_wgrad_clip call, which always leaves them zero
- *            (the status word excepted) -- so the library skips clearing them.
+ *            control words (its first 256 bytes) are zero -- a zero-filled
+ *            buffer, or one whose last use was a completed fdp_wgrad_clip call
+ *            (of any shape), which always leaves them zero (the status word
+ *            excepted) -- so the library skips clearing them.
  * workspace: device buffer of at least fdp_wgrad_clip_workspace_size() bytes,
  *            16-byte aligned.  Its first int is a status word: nonzero after
  *            the call completes means a bounded inter-workgroup wait of the

@@ -162,6 +162,38 @@ def test_wgrad_expired_grid_wait_is_loud(monkeypatch):
     assert_close(out, ref, torch.bfloat16, "after expiry")
 
 
+@pytest.mark.parametrize("shape", [(5, 96, 4000, 2300), (2, 64, 8192, 2048), (3, 33, 6000, 3000)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_wgrad_tile_major(shape):
+    """Layers with more 128x128 tiles than resident workgroups (two or three tiles
+    per workgroup, one sample per launch, running sum carried between launches)."""
+    B, K, M, N = shape
+    a, b = make(B, K, M, N, torch.bfloat16, "tn", seed=14)
+    _, norms_ref, _ = O.wgrad_clip(a, b, 1.0, 1.0, "tn")
+    C = float(np.median(norms_ref))
+    ref, norms_ref, fac_ref = O.wgrad_clip(a, b, C, 1.0, "tn")
+    out, norms, fac = core.wgrad_clip(a, b, C, 1.0, out_dtype=torch.float32, return_stats=True,
+                                      check=True)
+    assert_close(out, ref, torch.bfloat16, "out")
+    assert_elementwise(norms, norms_ref, torch.bfloat16, "norms")
+    assert_elementwise(fac, fac_ref, torch.bfloat16, "factors")
+    out2 = core.wgrad_clip(a, b, C, 1.0, out_dtype=torch.float32, check=True)
+    assert torch.equal(out, out2)
+
+
+def test_wgrad_workspace_reused_across_shapes():
+    """Consecutive calls of different shapes share the cached per-stream workspace;
+    each shape lays it out differently (one call's partial norms sit where the
+    next one's tile tickets go), and every result must still be exact."""
+    for i, (B, K, M, N) in enumerate([(8, 64, 1536, 768), (2, 64, 3072, 768), (4, 64, 128, 128),
+                                      (3, 64, 3072, 768), (2, 64, 3072, 768)]):
+        a, b = make(B, K, M, N, torch.bfloat16, "tn", seed=20 + i)
+        ref, _, _ = O.wgrad_clip(a, b, 0.5, 1.0, "tn")
+        for tp in (True, False):
+            out = core.wgrad_clip(a, b, 0.5, 1.0, out_dtype=torch.float32, two_pass=tp, check=True)
+            assert_close(out, ref, torch.bfloat16, f"{(B, K, M, N)} two_pass={tp}")
+
+
 def test_wgrad_does_not_modify_inputs():
     a, b = make(4, 64, 128, 128, torch.bfloat16, "tn", seed=8)
     a0, b0 = a.clone(), b.clone()
