@@ -9,7 +9,14 @@
 // materialises every G_b in HBM and scales it in a second kernel; here no
 // per-sample gradient ever leaves the register file.
 //
-// Two passes over the operands:
+// Three schedules, chosen per call:
+//   single pass (wgrad_core.hpp): 16-bit TN operands whose 128x128 output tiles
+//     fit the co-resident grid: every per-sample tile product stays in the
+//     register file across one grid barrier.
+//   streamed two-pass (wgrad_stream.hpp): the other 16-bit TN problems with
+//     aligned rows (layers larger than the resident grid): Gram-form or direct
+//     per-sample norms, then one clipped-sum contraction per output tile.
+//   generic two-pass (below): fp32 inputs, NN layout, unaligned rows --
 //   pass A (wgrad_norm_kernel): one workgroup per (output tile, sample) runs the
 //     tile product on MFMA, squares and sums its fp32 accumulators and writes
 //     one partial per (sample, tile) -- a deterministic [B, tiles] buffer.
@@ -22,7 +29,7 @@
 //     out_scale and the noise (single group) or writes an fp32 group partial that
 //     wgrad_finalize_kernel sums in fixed group order.
 //
-// Tiles: 128x128 outputs per 256-thread workgroup (4 waves, 64x64 each as 2x2
+// Generic tiles: 128x128 outputs per 256-thread workgroup (4 waves, 64x64 each as 2x2
 // blocks of 32x32 MFMA).  16-bit inputs use v_mfma_f32_32x32x16_{bf16,f16} with
 // BK=64; fp32 inputs use v_mfma_f32_32x32x2_f32 with BK=16.  Global loads are
 // 16-byte and coalesced along the contiguous dimension; for operands whose
@@ -34,7 +41,7 @@
 // are issued before the current tile's MFMAs.
 #include <cstdlib>
 
-#include "wgrad_core.hpp"
+#include "wgrad_stream.hpp"
 
 namespace fdp {
 namespace wg {
@@ -191,7 +198,7 @@ inline size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 //                       by an expired wait (the only words a reused workspace
 //                       must carry over: everything after them is rewritten)
 //   off_turn            per-tile counters [tiles] (uint)
-//   off_partials        partials [B, tiles] (fp32)
+//   off_partials        partials [B, max(tiles, Gram items per sample)] (fp32)
 //   two-pass:  off_factors [B], off_group [groups, M, N] (fp32)
 //   one-pass:  off_slots [groups, tiles, BM*BN] (fp32) per-group tile sums,
 //              off_chunk [M, N] (fp32) running sum when the batch needs
@@ -199,6 +206,7 @@ inline size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 struct Plan {
   int tiles_m, tiles_n, tiles;
   int spg, groups;
+  StreamPlan sp;  // streamed two-pass schedule (16-bit TN operands)
   size_t off_turn, off_partials, off_factors, off_group, off_slots, off_chunk;
   size_t total_two_pass, total_fused, total;
 };
@@ -222,7 +230,7 @@ int num_cus() {
   return cus;
 }
 
-Plan make_plan(int64_t B, int64_t M, int64_t N, int cus) {
+Plan make_plan(int64_t B, int64_t K, int64_t M, int64_t N, int cus) {
   Plan pl{};
   pl.tiles_m = static_cast<int>((M + BM - 1) / BM);
   pl.tiles_n = static_cast<int>((N + BN - 1) / BN);
@@ -236,13 +244,17 @@ Plan make_plan(int64_t B, int64_t M, int64_t N, int cus) {
   if (want < 1) want = 1;
   pl.spg = static_cast<int>((B + want - 1) / want);
   pl.groups = static_cast<int>((B + pl.spg - 1) / pl.spg);
+  pl.sp = stream_plan(B, K, M, N, cus);
   pl.off_turn = kWsHead;
   pl.off_partials = pl.off_turn + align_up(sizeof(unsigned) * size_t(pl.tiles));
-  const size_t after_partials = pl.off_partials + align_up(sizeof(float) * size_t(B) * pl.tiles);
+  const size_t per_sample =
+      size_t(pl.tiles > pl.sp.gram_per_sample ? pl.tiles : pl.sp.gram_per_sample);
+  const size_t after_partials = pl.off_partials + align_up(sizeof(float) * size_t(B) * per_sample);
   pl.off_factors = after_partials;
   pl.off_group = pl.off_factors + align_up(sizeof(float) * size_t(B));
+  const int max_groups = pl.groups > pl.sp.sum_groups ? pl.groups : pl.sp.sum_groups;
   pl.total_two_pass =
-      pl.off_group + (pl.groups > 1 ? align_up(sizeof(float) * size_t(pl.groups) * M * N) : 0);
+      pl.off_group + (max_groups > 1 ? align_up(sizeof(float) * size_t(max_groups) * M * N) : 0);
   const GroupPlan gp = group_plan(B, pl.tiles, 2 * cus);
   pl.off_slots = after_partials;
   pl.off_chunk = pl.off_slots;
@@ -297,16 +309,64 @@ hipError_t dispatch_layout(int layout, bool vec, const Args& a, const Plan& pl, 
                                                          factors, fac_ws, s);
 }
 
+// Streamed two-pass schedule for 16-bit TN operands with aligned rows: Gram
+// (or direct) norms, factors, then one clipped-sum contraction per output tile.
+template <class DT>
+hipError_t launch_stream(Args a, const Plan& pl, bool noclip, float C, float clamp,
+                         const float* clip_args_dev, float* norms, float* factors, float* fac_ws,
+                         hipStream_t s) {
+  const dim3 block(NT);
+  int per_sample = pl.tiles;
+  if (!noclip) {
+    if (pl.sp.gram) {
+      GramArgs g{};
+      g.a = static_cast<const uint16_t*>(a.a);
+      g.b = static_cast<const uint16_t*>(a.b);
+      g.B = a.B;
+      g.T = a.K;
+      g.M = a.M;
+      g.N = a.N;
+      g.sab = a.sab;
+      g.lda = a.lda;
+      g.sbb = a.sbb;
+      g.ldb = a.ldb;
+      g.nt = pl.sp.gram_nt;
+      g.per_sample = pl.sp.gram_per_sample;
+      g.items = a.B * g.per_sample;
+      g.partials = a.partials;
+      per_sample = g.per_sample;
+      const hipError_t e = DT::code == FDP_BF16 ? launch_gram_norm_bf16(g, s) : launch_gram_norm_f16(g, s);
+      if (e != hipSuccess) return e;
+    } else {
+      hipLaunchKernelGGL((wgrad_norm_kernel<Core16<DT>, FDP_LAYOUT_TN, true>), dim3(pl.tiles, a.B),
+                         block, Core16<DT>::SMEM, s, a);
+    }
+  }
+  const unsigned fb = static_cast<unsigned>((a.B + (NT / kWave) - 1) / (NT / kWave));
+  hipLaunchKernelGGL(wgrad_factor_kernel, dim3(fb < 1024 ? fb : 1024), block, 0, s, a.partials,
+                     a.B, per_sample, C, clamp, clip_args_dev, noclip ? 1 : 0, fac_ws, norms,
+                     factors, a.err);
+  const hipError_t e = DT::code == FDP_BF16 ? launch_clipsum_bf16(a, pl.sp, s) : launch_clipsum_f16(a, pl.sp, s);
+  if (e != hipSuccess) return e;
+  if (pl.sp.sum_groups > 1) {
+    a.groups = pl.sp.sum_groups;
+    const int64_t MN = a.M * a.N;
+    int64_t nb = (MN + NT - 1) / NT;
+    if (nb > 4096) nb = 4096;
+    hipLaunchKernelGGL(wgrad_finalize_kernel, dim3(static_cast<unsigned>(nb)), block, 0, s, a);
+  }
+  return hipGetLastError();
+}
+
 }  // namespace
 
 extern "C" int fdp_wgrad_clip_workspace_size(int64_t B, int64_t K, int64_t M, int64_t N,
                                              int dtype, int flags, size_t* bytes) {
-  (void)K;
   (void)flags;
   if (bytes == nullptr) return FDP_ERR_ARG;
   if (!valid_dtype(dtype)) return FDP_ERR_DTYPE;
   if (B < 1 || M < 1 || N < 1 || K < 0) return FDP_ERR_SHAPE;
-  *bytes = make_plan(B, M, N, num_cus()).total;
+  *bytes = make_plan(B, K, M, N, num_cus()).total;
   return FDP_OK;
 }
 
@@ -332,7 +392,7 @@ extern "C" int fdp_wgrad_clip(const void* a, const void* b, int64_t B, int64_t K
   if (noclip && norms != nullptr) return FDP_ERR_ARG;
 
   const int cus = num_cus();
-  const Plan pl = make_plan(B, M, N, cus);
+  const Plan pl = make_plan(B, K, M, N, cus);
   if (workspace == nullptr || workspace_bytes < pl.total) return FDP_ERR_WORKSPACE;
   if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0) return FDP_ERR_ALIGN;
 
@@ -400,6 +460,14 @@ extern "C" int fdp_wgrad_clip(const void* a, const void* b, int64_t B, int64_t K
   }
 
   hipError_t e;
+  if (layout == FDP_LAYOUT_TN && vec && dtype != FDP_F32 && K > 0) {
+    args.group_out = pl.sp.sum_groups > 1 ? reinterpret_cast<float*>(ws + pl.off_group) : nullptr;
+    e = dtype == FDP_BF16 ? launch_stream<BF16>(args, pl, noclip, C, clamp, clip_args_dev, norms,
+                                                factors, fac_ws, s)
+                          : launch_stream<F16>(args, pl, noclip, C, clamp, clip_args_dev, norms,
+                                               factors, fac_ws, s);
+    return e == hipSuccess ? FDP_OK : FDP_ERR_HIP;
+  }
   if (dtype == FDP_BF16) {
     e = dispatch_layout<Core16<BF16>>(layout, vec, args, pl, noclip, C, clamp, clip_args_dev,
                                       norms, factors, fac_ws, s);

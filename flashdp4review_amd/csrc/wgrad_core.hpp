@@ -44,9 +44,7 @@ struct Args {
   const float* clip_args_dev;
   float* norms_out;       // optional [B]
   float* factors_out;     // optional [B]
-  // single-pass kernel: this launch covers samples [chunk_b0, chunk_b0+chunk_nb);
-  // tpw > 1 selects the tile-major unit map (tpw tiles per workgroup, groups 1)
-  int tpw;
+  // single-pass kernel: this launch covers samples [chunk_b0, chunk_b0+chunk_nb)
   int64_t chunk_b0, chunk_nb;
   int chunk_first, chunk_last;
   float* chunk_acc;       // [M, N] fp32 running sum carried between chunks
@@ -366,9 +364,17 @@ __device__ __forceinline__ int acc_row(int wm, int i, int lane, int r) {
 }
 __device__ __forceinline__ int acc_col(int wn, int j, int lane) { return wn + 32 * j + (lane & 31); }
 
+// Tile id -> output tile, in bands of kBandRows tile rows walked column by
+// column: consecutive ids (which the XCD-aware workgroup numbering keeps on
+// one XCD) form compact blocks that share A and B panels in that XCD's L2.
+constexpr int kBandRows = 8;
 __device__ __forceinline__ void tile_coords(const Args& p, int tile, int64_t& m0, int64_t& n0) {
-  m0 = int64_t(tile / p.tiles_n) * BM;
-  n0 = int64_t(tile % p.tiles_n) * BN;
+  const int per_band = kBandRows * p.tiles_n;
+  const int band = tile / per_band, in_band = tile % per_band;
+  const int rows_left = p.tiles_m - band * kBandRows;
+  const int band_rows = rows_left < kBandRows ? rows_left : kBandRows;
+  m0 = int64_t(band * kBandRows + in_band % band_rows) * BM;
+  n0 = int64_t(in_band / band_rows) * BN;
 }
 
 // ============================================================ single pass
@@ -624,54 +630,22 @@ __device__ inline void store_tile_staged(const Args& p, int64_t m0, int64_t n0,
 
 // ------------------------------------------------------ single pass
 // Work units of one workgroup: unit j is the 128x128 product of one tile and
-// one sample.  Two maps:
-//  * grouped (tpw == 1): grid = groups x tiles; workgroup (g, tile) holds the
-//    tile's products of samples chunk_b0 + g*spg + j.  Groups of one tile are
-//    combined through slots after the grid barrier.
-//  * tile-major (tpw > 1, groups == 1): for layers with more tiles than
-//    resident workgroups; workgroup w holds tiles w, w + nwg, ... (up to tpw)
-//    of every sample of the launch's chunk, unit j = t * nsamp + s.  Each tile
-//    has a single owner: no slots.
-template <bool TM>
+// one sample.  The grid is groups x tiles; workgroup (g, tile) holds the tile's
+// products of samples chunk_b0 + g*spg + j.  Groups of one tile are combined
+// through slots after the grid barrier.
 struct UnitMap {
-  int lw, tiles, nwg, nsamp, nb, nt;
+  int tile, nb;
   int64_t b0;
-  __device__ __forceinline__ int tile_of(int j) const {
-    if constexpr (TM) return lw + (j / nsamp) * nwg;
-    else return lw % tiles;
-  }
-  __device__ __forceinline__ int sidx(int j) const {
-    if constexpr (TM) return j % nsamp;
-    else return j;
-  }
-  __device__ __forceinline__ int64_t sample_of(int j) const { return b0 + sidx(j); }
-  __device__ __forceinline__ int tslot(int j) const {
-    if constexpr (TM) return j / nsamp;
-    else return 0;
-  }
+  __device__ __forceinline__ int64_t sample_of(int j) const { return b0 + j; }
 };
 
-template <bool TM>
-__device__ inline UnitMap<TM> unit_map(const Args& p, int lw, int tiles) {
-  UnitMap<TM> u{};
-  u.lw = lw;
-  u.tiles = tiles;
-  u.nwg = p.nwg;
+__device__ inline UnitMap unit_map(const Args& p, int lw, int tiles) {
+  UnitMap u{};
+  u.tile = lw % tiles;
   const int64_t bend = p.chunk_b0 + p.chunk_nb;
-  if constexpr (!TM) {
-    const int g = lw / tiles;
-    u.b0 = p.chunk_b0 + int64_t(g) * p.spg;
-    u.nb = static_cast<int>((u.b0 + p.spg < bend ? u.b0 + p.spg : bend) - u.b0);
-    u.nsamp = u.nb;
-    u.nt = 1;
-  } else {
-    u.b0 = p.chunk_b0;
-    u.nsamp = static_cast<int>(p.chunk_nb);
-    u.nt = 0;
-    for (int t = 0; t < p.tpw; ++t)
-      if (lw + t * p.nwg < tiles) u.nt = t + 1;
-    u.nb = u.nt * u.nsamp;
-  }
+  u.b0 = p.chunk_b0 + int64_t(lw / tiles) * p.spg;
+  u.nb = static_cast<int>((u.b0 + p.spg < bend ? u.b0 + p.spg : bend) - u.b0);
+  if (u.nb < 0) u.nb = 0;
   return u;
 }
 
@@ -687,21 +661,51 @@ __device__ inline void finish_tile(const Args& p, int64_t m0, int64_t n0, f32x16
     // per-lane offset, so that no 64-bit address is kept per element.
     const int hi = 4 * (lane >> 5);
     const uint32_t loff = static_cast<uint32_t>(hi * p.N + (lane & 31));
+    if (m0 + BM <= p.M && n0 + BN <= p.N) {
+      // interior tile: straight-line code, every load in flight at once
+      if (!p.chunk_first) {
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+        for (int a = 0; a < 2; ++a) {
+          float v[2][16];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t mrow = m0 + wm + 32 * a + 8 * (r >> 2) + (r & 3);
-        if (mrow + hi >= p.M) continue;
-        float* rp = p.chunk_acc + (mrow * p.N + n0 + wn);
+          for (int r = 0; r < 16; ++r) {
+            const float* rp = p.chunk_acc + ((m0 + wm + 32 * a + 8 * (r >> 2) + (r & 3)) * p.N + n0 + wn) + loff;
 #pragma unroll
-        for (int c = 0; c < 2; ++c) {
-          if (n0 + wn + 32 * c + (lane & 31) >= p.N) continue;
-          float* e = rp + loff + 32 * c;
-          if (!p.chunk_first) acc[a][c][r] += *e;
-          if (!p.chunk_last) *e = acc[a][c][r];
+            for (int c = 0; c < 2; ++c) v[c][r] = rp[32 * c];
+          }
+#pragma unroll
+          for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[a][c][r] += v[c][r];
         }
       }
+      if (!p.chunk_last) {
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            float* rp = p.chunk_acc + ((m0 + wm + 32 * a + 8 * (r >> 2) + (r & 3)) * p.N + n0 + wn) + loff;
+#pragma unroll
+            for (int c = 0; c < 2; ++c) rp[32 * c] = acc[a][c][r];
+          }
+      }
+    } else {
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t mrow = m0 + wm + 32 * a + 8 * (r >> 2) + (r & 3);
+          if (mrow + hi >= p.M) continue;
+          float* rp = p.chunk_acc + (mrow * p.N + n0 + wn);
+#pragma unroll
+          for (int c = 0; c < 2; ++c) {
+            if (n0 + wn + 32 * c + (lane & 31) >= p.N) continue;
+            float* e = rp + loff + 32 * c;
+            if (!p.chunk_first) acc[a][c][r] += *e;
+            if (!p.chunk_last) *e = acc[a][c][r];
+          }
+        }
+    }
   }
   if (p.chunk_last) {
     __syncthreads();  // the staging area may still be read for a previous tile
@@ -717,13 +721,13 @@ __device__ inline void finish_tile(const Args& p, int64_t m0, int64_t n0, f32x16
 // Workgroups of the grid run their nb products, keeping the finished ones
 // packed in AGPRs and the last one live in its accumulators; each product's
 // sum of squares goes to partials[sample, tile].  After the grid barrier every
-// workgroup knows the norms of its samples and forms sum_b c_b G_b per owned
-// tile (fixed order: deterministic); grouped tiles are then combined in group
-// order by the last group to arrive, and the result is written (or carried
-// to the next launch in chunk_acc).
+// workgroup knows the norms of its samples and forms sum_b c_b G_b for its
+// tile (fixed order: deterministic); the groups of a tile are then combined in
+// group order by the last group to arrive, and the result is written (or
+// carried to the next launch in chunk_acc).
 constexpr int kStages = 2;  // LDS ring depth of the single-pass kernel (64-deep k-tiles)
 
-template <class DT, int U, bool TM>
+template <class DT, int U>
 __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
   using G = dma::Geom<BM, BN, 64>;
   static_assert(kStages * G::STAGE == BM * BN * 4, "the output staging reuses the ring");
@@ -738,7 +742,7 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
   const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
   const int tiles = p.tiles_m * p.tiles_n;
   const int lw = logical_wg(blockIdx.x, p.nwg);
-  const UnitMap<TM> um = unit_map<TM>(p, lw, tiles);
+  const UnitMap um = unit_map(p, lw, tiles);
   const int nb = um.nb;
   const int nk = static_cast<int>((p.K + G::BK - 1) / G::BK);
   dma::FragOffsets<G> fo;
@@ -756,11 +760,9 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
   const int nq = nb * nk;
   dma::Job<G> job;  // loads of k-tile ik of unit iu, the next one to issue
   int iu = 0, ik = 0;
-  if (nq > 0) {
-    int64_t m0, n0;
-    tile_coords(p, um.tile_of(0), m0, n0);
-    job.init(pa + um.b0 * p.sab, p.lda, pb + um.b0 * p.sbb, p.ldb, p.K, m0, n0);
-  }
+  int64_t m0, n0;
+  tile_coords(p, um.tile, m0, n0);
+  if (nq > 0) job.init(pa + um.b0 * p.sab, p.lda, pb + um.b0 * p.sbb, p.ldb, p.K, m0, n0);
   auto issue_next = [&](FDP_LDS char* stage) {
     job.issue(stage, ik);
     if (++ik == nk) {
@@ -768,11 +770,6 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
       if (++iu < nb) {
         const int64_t b = um.sample_of(iu);
         job.retarget(pa + b * p.sab, p.lda, pb + b * p.sbb, p.ldb, p.K);
-        if constexpr (TM) {
-          int64_t m0, n0;
-          tile_coords(p, um.tile_of(iu), m0, n0);
-          job.retile(m0, n0);
-        }
       }
     }
   };
@@ -794,9 +791,6 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
         if (++ck == nk) {
           // unit cu done.  Rows/columns past M/N may hold the next row's
           // values: leave them out of the norm.
-          const int tl = um.tile_of(cu);
-          int64_t m0, n0;
-          tile_coords(p, tl, m0, n0);
           float sq = 0.f;
 #pragma unroll
           for (int a = 0; a < 2; ++a)
@@ -813,7 +807,7 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
           if (lane == 0) red[wave] = sq;
           __syncthreads();
           if (threadIdx.x == 0)
-            st_coherent(p.partials + um.sample_of(cu) * tiles + tl,
+            st_coherent(p.partials + um.sample_of(cu) * tiles + um.tile,
                         (red[0] + red[1]) + (red[2] + red[3]));
           FDP_TS(1 + cu);
           if (cu + 1 < nb) {  // park it and start the next product
@@ -833,10 +827,8 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
   // The tile's hand-over ticket starts at zero in every launch: group 0 clears
   // it before the grid barrier, every ticket is taken after it.  (A ticket
   // word may hold another problem's data: workspace layouts differ by shape.)
-  if constexpr (!TM) {
-    if (threadIdx.x == 0 && p.groups > 1 && lw / tiles == 0)
-      __hip_atomic_store(p.tile_turn + lw % tiles, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+  if (threadIdx.x == 0 && p.groups > 1 && lw / tiles == 0)
+    __hip_atomic_store(p.tile_turn + um.tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
   // A wait that expired (only possible when the grid was not resident at once)
   // poisons this workgroup's results with NaN rather than leave them silently
@@ -854,17 +846,17 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
 #pragma unroll
   for (int i = 0; i < U; ++i) {
     ps[i] = 0.f;
-    if (i < um.nsamp)
+    if (i < nb)
       for (int t = threadIdx.x; t < tiles; t += NT)
         ps[i] += ld_coherent(p.partials + (um.b0 + i) * tiles + t);
   }
-  const bool stats_owner = nb > 0 && um.tile_of(0) == 0;  // one writer per sample
+  const bool stats_owner = nb > 0 && um.tile == 0;  // one writer per sample
 #pragma unroll
   for (int i = 0; i < U; ++i) {
     const float s = wave_sum(ps[i]);
     if (lane == 0) red[wave] = s;
     __syncthreads();
-    if (threadIdx.x == 0 && i < um.nsamp) {
+    if (threadIdx.x == 0 && i < nb) {
       const float n = poisoned ? __builtin_nanf("") : sqrtf((red[0] + red[1]) + (red[2] + red[3]));
       const float cf = poisoned ? n : clip_factor(n, C, clamp);
       fac[i] = cf;
@@ -875,81 +867,52 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
     }
     __syncthreads();
   }
+  FDP_TS(14);
 
-  // ---- phase 2.  Tile-major: one sample per launch, so each owned tile is one
-  // unit: c * G_t, written (or carried in chunk_acc) tile by tile.
-  if constexpr (TM) {
-    const float cf = fac[0];
+  // ---- phase 2: sum_b c_b G_b formed in place in the accumulators as
+  // c_last G_last + c_0 G_0 + c_1 G_1 + ... (a fixed order: deterministic)
+  if (nb > 0) {
+    const float cl = fac[nb - 1];
 #pragma unroll
-    for (int t = U - 1; t >= 0; --t) {
-      if (t < um.nt) {
-        if (t == um.nt - 1) {  // the live unit
+    for (int a = 0; a < 2; ++a)
 #pragma unroll
-          for (int a = 0; a < 2; ++a)
+      for (int c = 0; c < 2; ++c)
 #pragma unroll
-            for (int c = 0; c < 2; ++c)
-#pragma unroll
-              for (int r = 0; r < 16; ++r) acc[a][c][r] *= cf;
-        } else {
-          zero(acc);
-#pragma unroll
-          for (int j = 0; j < U - 1; ++j)
-            if (j == t) held[j].add_to(acc, cf);
-        }
-        int64_t m0, n0;
-        tile_coords(p, lw + t * p.nwg, m0, n0);
-        finish_tile(p, m0, n0, acc, st0, st1);
-      }
-    }
+        for (int r = 0; r < 16; ++r) acc[a][c][r] *= cl;
   } else {
-    // Grouped: sum_b c_b G_b formed in place in the accumulators as
-    // c_last G_last + c_0 G_0 + c_1 G_1 + ... (a fixed order: deterministic)
-    if (nb > 0) {
-      const float cl = fac[nb - 1];
-#pragma unroll
-      for (int a = 0; a < 2; ++a)
-#pragma unroll
-        for (int c = 0; c < 2; ++c)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) acc[a][c][r] *= cl;
-    } else {
-      zero(acc);
-    }
-#pragma unroll
-    for (int j = 0; j < U - 1; ++j)
-      if (j < nb - 1) held[j].add_to(acc, fac[j]);
-    const int tile = lw % tiles;
-    int64_t m0, n0;
-    tile_coords(p, tile, m0, n0);
-
-    // combine the groups of this tile: the last to arrive sums the slots
-    const int ngroups = p.groups;
-    bool owner = true;
-    if (ngroups > 1) {
-      const int g = lw / tiles;
-      slot_store(p.tile_acc + (int64_t(g) * tiles + tile) * (BM * BN), acc);
-      wait_stores();
-      __syncthreads();
-      if (threadIdx.x == 0) {
-        const unsigned old = __hip_atomic_fetch_add(p.tile_turn + tile, 1u, __ATOMIC_RELAXED,
-                                                    __HIP_MEMORY_SCOPE_AGENT);
-        is_last = old == unsigned(ngroups - 1);
-        // every group has taken its ticket: leave the counter zeroed
-        if (is_last)
-          __hip_atomic_store(p.tile_turn + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-      __syncthreads();
-      FDP_TS(10);
-      owner = is_last != 0;
-      if (owner) {
-        zero(acc);
-        for (int gg = 0; gg < ngroups; ++gg)
-          slot_add(p.tile_acc + (int64_t(gg) * tiles + tile) * (BM * BN), acc);
-      }
-    }
-    FDP_TS(11);
-    if (owner) finish_tile(p, m0, n0, acc, st0, st1);
+    zero(acc);
   }
+#pragma unroll
+  for (int j = 0; j < U - 1; ++j)
+    if (j < nb - 1) held[j].add_to(acc, fac[j]);
+
+  // combine the groups of this tile: the last to arrive sums the slots
+  const int ngroups = p.groups;
+  bool owner = true;
+  if (ngroups > 1) {
+    const int g = lw / tiles;
+    slot_store(p.tile_acc + (int64_t(g) * tiles + um.tile) * (BM * BN), acc);
+    wait_stores();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const unsigned old = __hip_atomic_fetch_add(p.tile_turn + um.tile, 1u, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT);
+      is_last = old == unsigned(ngroups - 1);
+      // every group has taken its ticket: leave the counter zeroed
+      if (is_last)
+        __hip_atomic_store(p.tile_turn + um.tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    FDP_TS(10);
+    owner = is_last != 0;
+    if (owner) {
+      zero(acc);
+      for (int gg = 0; gg < ngroups; ++gg)
+        slot_add(p.tile_acc + (int64_t(gg) * tiles + um.tile) * (BM * BN), acc);
+    }
+  }
+  FDP_TS(11);
+  if (owner) finish_tile(p, m0, n0, acc, st0, st1);
   // ---- leave the control words zeroed for the next launch on this
   // workspace: every workgroup has passed the barrier once `done` reaches nwg.
   if (threadIdx.x == 0) {
@@ -975,38 +938,25 @@ constexpr size_t kWsHead = 256;   // err / barrier words at the head of the work
 constexpr int kGroupUnits = 3;    // samples per group held by one workgroup
 
 // Single-pass geometry for B samples over `tiles` 128x128 tiles on `slots`
-// co-resident workgroups.  tiles <= slots: grouped map, `groups` groups of
-// `spg` samples per launch.  tiles > slots: tile-major map, `tpw` tiles per
-// workgroup and one sample per launch.  units = products
-// held by one workgroup (the kernel instance); groups == 0: no single pass.
+// co-resident workgroups: `groups` groups of `spg` samples per launch, units =
+// products held by one workgroup (the kernel instance).  groups == 0: more
+// tiles than slots, no single pass (the streamed two-pass schedule is used).
 struct GroupPlan {
-  int groups, spg, tpw, units, nwg;
+  int groups, spg, units, nwg;
   int64_t chunk;  // samples per launch
 };
 inline GroupPlan group_plan(int64_t B, int tiles, int slots) {
   GroupPlan g{};
-  if (tiles <= slots) {
-    int64_t G = slots / tiles;
-    if (G > B) G = B;
-    const int64_t per = (B + G - 1) / G;
-    g.spg = static_cast<int>(per < kGroupUnits ? per : kGroupUnits);
-    // fewest groups that still cover the chunk with spg samples each
-    g.chunk = G * g.spg < B ? G * g.spg : B;
-    g.groups = static_cast<int>((g.chunk + g.spg - 1) / g.spg);
-    g.tpw = 1;
-    g.units = g.spg;
-    g.nwg = g.groups * tiles;
-  } else {
-    // one sample per launch (two or three units per workgroup)
-    const int tpw = (tiles + slots - 1) / slots;
-    if (tpw > kGroupUnits) return g;  // groups == 0
-    g.groups = 1;
-    g.tpw = tpw;
-    g.spg = 1;
-    g.chunk = 1;
-    g.units = tpw;
-    g.nwg = (tiles + tpw - 1) / tpw;
-  }
+  if (tiles > slots) return g;  // groups == 0
+  int64_t G = slots / tiles;
+  if (G > B) G = B;
+  const int64_t per = (B + G - 1) / G;
+  g.spg = static_cast<int>(per < kGroupUnits ? per : kGroupUnits);
+  // fewest groups that still cover the chunk with spg samples each
+  g.chunk = G * g.spg < B ? G * g.spg : B;
+  g.groups = static_cast<int>((g.chunk + g.spg - 1) / g.spg);
+  g.units = g.spg;
+  g.nwg = g.groups * tiles;
   return g;
 }
 
@@ -1022,32 +972,22 @@ hipError_t try_grouped(Args a, int cus, bool plain, bool clean, hipStream_t s) {
     return hipErrorNotSupported;
   const GroupPlan gp = group_plan(a.B, tiles, 2 * cus);
   if (gp.groups == 0) return hipErrorNotSupported;
-  KernelFn grouped[kGroupUnits] = {&wgrad_group_kernel<DT, 1, false>,
-                                   &wgrad_group_kernel<DT, 2, false>,
-                                   &wgrad_group_kernel<DT, 3, false>};
-  KernelFn tile_major[kGroupUnits] = {&wgrad_group_kernel<DT, 2, true>,  // tpw >= 2
-                                      &wgrad_group_kernel<DT, 2, true>,
-                                      &wgrad_group_kernel<DT, 3, true>};
-  KernelFn fn = gp.tpw == 1 ? grouped[gp.units - 1] : tile_major[gp.units - 1];
+  KernelFn grouped[kGroupUnits] = {&wgrad_group_kernel<DT, 1>, &wgrad_group_kernel<DT, 2>,
+                                   &wgrad_group_kernel<DT, 3>};
+  KernelFn fn = grouped[gp.units - 1];
   int occ = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void*>(fn), NT,
                                                    0) != hipSuccess ||
       occ < 2)
     return hipErrorNotSupported;
   a.spg = gp.spg;
-  a.tpw = gp.tpw;
   const int64_t words = int64_t(kWsHead / sizeof(unsigned));
   for (int64_t b0 = 0; b0 < a.B; b0 += gp.chunk) {
     Args c = a;
     c.chunk_b0 = b0;
     c.chunk_nb = a.B - b0 < gp.chunk ? a.B - b0 : gp.chunk;
-    if (gp.tpw == 1) {
-      c.groups = static_cast<int>((c.chunk_nb + gp.spg - 1) / gp.spg);
-      c.nwg = c.groups * tiles;
-    } else {
-      c.groups = 1;
-      c.nwg = gp.nwg;
-    }
+    c.groups = static_cast<int>((c.chunk_nb + gp.spg - 1) / gp.spg);
+    c.nwg = c.groups * tiles;
     c.chunk_first = b0 == 0;
     c.chunk_last = b0 + c.chunk_nb >= a.B;
     if (b0 == 0 && !clean)

@@ -98,8 +98,11 @@ int fdp_version(void);
  * flags    : bit 0 (FDP_WGRAD_NOCLIP) skips the norm pass and uses c_b = clamp
  *            (a plain batched product sum; `norms` must then be NULL);
  *            bit 1 (FDP_WGRAD_TWO_PASS) forces the two-pass schedule (norm
- *            pass, then clipped-sum pass) instead of the single-pass
- *            cooperative kernel the library uses whenever the problem fits it;
+ *            pass, then clipped-sum pass) instead of the single-pass kernel
+ *            the library uses whenever the problem fits it (16-bit TN
+ *            operands, aligned rows, at most two 128x128 output tiles per
+ *            CU); larger layers always take the two-pass schedule, whose norm
+ *            pass uses the per-sample Gram matrices when that is cheaper;
  *            bit 2 (FDP_WGRAD_PLAIN_LAUNCH) dispatches the single-pass kernel
  *            as an ordinary launch instead of a cooperative one, saving the
  *            runtime's cooperative-launch synchronisation (about 25 us per

@@ -164,9 +164,10 @@ def test_wgrad_expired_grid_wait_is_loud(monkeypatch):
 
 @pytest.mark.parametrize("shape", [(5, 96, 4000, 2300), (2, 64, 8192, 2048), (3, 33, 6000, 3000)],
                          ids=lambda s: "x".join(map(str, s)))
-def test_wgrad_tile_major(shape):
-    """Layers with more 128x128 tiles than resident workgroups (two or three tiles
-    per workgroup, one sample per launch, running sum carried between launches)."""
+def test_wgrad_more_tiles_than_workgroups(shape):
+    """Layers with more 128x128 output tiles than resident workgroups take the
+    streamed two-pass schedule by default (Gram-form norms for 2x64x8192x2048,
+    direct norms where M or N is not a multiple of 64)."""
     B, K, M, N = shape
     a, b = make(B, K, M, N, torch.bfloat16, "tn", seed=14)
     _, norms_ref, _ = O.wgrad_clip(a, b, 1.0, 1.0, "tn")
@@ -179,6 +180,33 @@ def test_wgrad_tile_major(shape):
     assert_elementwise(fac, fac_ref, torch.bfloat16, "factors")
     out2 = core.wgrad_clip(a, b, C, 1.0, out_dtype=torch.float32, check=True)
     assert torch.equal(out, out2)
+
+
+@pytest.mark.parametrize("shape", [(3, 300, 2048, 1024), (2, 256, 4096, 1536), (16, 64, 512, 512),
+                                   (4, 128, 640, 1088), (3, 130, 1024, 3000)],
+                         ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=str)
+def test_wgrad_stream_two_pass(shape, dtype):
+    """The streamed two-pass schedule: per-sample norms from the Gram matrices
+    (sum over t, s of (g_t . g_s)(x_t . x_s)) where that is cheaper and M, N are
+    multiples of 64, else from the per-tile products; then one clipped-sum
+    contraction per 128x256 output tile, split over sample groups when there
+    are few tiles (16x64x512x512)."""
+    B, K, M, N = shape
+    a, b = make(B, K, M, N, dtype, "tn", seed=31)
+    _, norms_ref, _ = O.wgrad_clip(a, b, 1.0, 1.0, "tn")
+    C = float(np.median(norms_ref))
+    ref, norms_ref, fac_ref = O.wgrad_clip(a, b, C, 1.0, "tn")
+    out, norms, fac = core.wgrad_clip(a, b, C, 1.0, out_dtype=torch.float32, return_stats=True,
+                                      two_pass=True, check=True)
+    assert_close(out, ref, dtype, "out")
+    assert_elementwise(norms, norms_ref, dtype, "norms")
+    assert_elementwise(fac, fac_ref, dtype, "factors")
+    noise = torch.randn(M, N, generator=torch.Generator().manual_seed(5)).to(dtype).to(DEV)
+    out2 = core.wgrad_clip(a, b, C, 1.0, out_scale=0.25, noise=noise, noise_scale=0.5,
+                           two_pass=True, check=True)
+    ref2 = 0.25 * ref + 0.5 * noise.double().cpu().numpy()
+    assert_close(out2, ref2, dtype, "out (scale, noise)")
 
 
 def test_wgrad_workspace_reused_across_shapes():
