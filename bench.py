@@ -4,9 +4,10 @@ Default workload ("cfg2"): the clipped per-sample weight
 gradient of a DP Linear 768 -> 3072 in bf16 with x [8,1024,768] ~ N(0,1),
 grad_out [8,1024,3072] ~ N(0,0.02^2), C = 1, sigma = 1:
     dW = (1/B) sum_b clip(||g_b^T x_b||) g_b^T x_b + (sigma/sqrt(B)) z
-One step = one noise draw + one fdp_wgrad_clip call (single-pass kernel:
-per-sample products, norms, factors, clipped sum, 1/B and the noise add in
-its epilogue), inputs resident in HBM, default (ordinary-dispatch) launch.
+One step = one fdp_wgrad_clip call, which is one launch of the single-pass
+kernel: per-sample products, norms, factors, clipped sum, 1/B, and the
+Gaussian noise drawn (Philox4x32-10) and added in its epilogue; inputs
+resident in HBM, default (ordinary-dispatch) launch.
 
 value = algorithmic TFLOP/s = 2*B*T*M*N / step time (norm, scale and recompute
 flops are not credited).  The JSON line also carries the roofline of the
@@ -92,23 +93,21 @@ def cfg3_inputs(dev):
 
 
 def run_wgrad(x, go, out_dtype, sigma=1.0, transpose=False, launch=None):
-    """One DP weight-gradient step: noise draw + fused clipped product sum."""
+    """One DP weight-gradient step: the fused clipped product sum with its noise
+    drawn in the epilogue (a fresh Philox counter range every step)."""
     from flashdp4review_amd.core import wgrad_clip
+    from flashdp4review_amd.layers.utils import NoiseStream
     B = x.shape[0]
     a, b = (x, go) if transpose else (go, x)
     M, N = a.shape[2], b.shape[2]
     std = sigma / math.sqrt(B)
+    keys = NoiseStream()
 
     def step():
-        z = torch.randn(M, N, device=x.device, dtype=out_dtype)
-        return wgrad_clip(a, b, 1.0, 1.0, layout="tn", out_scale=1.0 / B, noise=z,
-                          noise_scale=std, out_dtype=out_dtype, launch=launch)
+        return wgrad_clip(a, b, 1.0, 1.0, layout="tn", out_scale=1.0 / B, noise_scale=std,
+                          noise_key=keys.next(M * N), out_dtype=out_dtype, launch=launch)
 
-    def gemm_only():
-        return wgrad_clip(a, b, 1.0, 1.0, layout="tn", out_scale=1.0 / B, out_dtype=out_dtype,
-                          launch=launch)
-
-    return step, gemm_only
+    return step, step
 
 
 # --------------------------------------------------------------- cpu baseline
@@ -373,14 +372,15 @@ def main():
         w = torch.ones(1024, device=dev, dtype=torch.bfloat16)
         _, mean, rstd = layernorm_fwd(xl, w, torch.zeros_like(w), 1e-5)
 
+        from flashdp4review_amd.layers.utils import NoiseStream
+        keys = NoiseStream()
+
         def step():
-            zw = torch.randn(1024, device=dev, dtype=torch.bfloat16)
-            zb = torch.randn(1024, device=dev, dtype=torch.bfloat16)
             return layernorm_bwd_clip(gl, xl, w, mean, rstd, 1.0, 1.0, out_scale=1.0 / 16,
-                                      noise_w=zw, noise_b=zb, noise_scale=0.25)
+                                      noise_scale=0.25, noise_key=keys.next(1024))
 
         step_coop = None
-        kernel_call = lambda: layernorm_bwd_clip(gl, xl, w, mean, rstd, 1.0, 1.0)  # noqa: E731
+        kernel_call = step
 
     # ---- timed region: K steps bracketed by synchronisation
     for _ in range(args.warmup):

@@ -33,6 +33,23 @@ _c_f = ctypes.c_float
 _c_p = ctypes.c_void_p
 _c_sz_p = ctypes.POINTER(ctypes.c_size_t)
 
+
+class NoiseKey(ctypes.Structure):
+    """fdp_noise_key: the Philox4x32-10 key (seed) and first counter block of an
+    in-kernel Gaussian draw (include/flashdp_hip.h)."""
+    _fields_ = [("seed", ctypes.c_uint64), ("offset", ctypes.c_uint64)]
+
+
+_c_key = ctypes.POINTER(NoiseKey)
+
+
+def noise_key(key) -> "ctypes._Pointer | None":
+    """(seed, offset) -> a fdp_noise_key pointer for the call (None -> NULL)."""
+    if key is None:
+        return None
+    seed, offset = key
+    return ctypes.pointer(NoiseKey(int(seed) & (2**64 - 1), int(offset) & (2**64 - 1)))
+
 # Every exported symbol with its (restype, argtypes); tests check this list
 # against include/flashdp_hip.h.
 SIGNATURES = {
@@ -42,19 +59,19 @@ SIGNATURES = {
                                                _c_sz_p]),
     "fdp_wgrad_clip": (_c_int, [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                 _c_i64, _c_i64, _c_int, _c_int, _c_f, _c_f, _c_p, _c_f, _c_p,
-                                _c_f, _c_p, _c_i64, _c_int, _c_p, _c_p, _c_int, _c_p,
+                                _c_f, _c_key, _c_p, _c_i64, _c_int, _c_p, _c_p, _c_int, _c_p,
                                 ctypes.c_size_t, _c_p]),
     "fdp_colsum_clip_workspace_size": (_c_int, [_c_i64, _c_i64, _c_i64, _c_int, _c_sz_p]),
     "fdp_colsum_clip": (_c_int, [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_f, _c_f,
-                                 _c_p, _c_f, _c_p, _c_f, _c_p, _c_int, _c_p, _c_p, _c_p,
+                                 _c_p, _c_f, _c_p, _c_f, _c_key, _c_p, _c_int, _c_p, _c_p, _c_p,
                                  ctypes.c_size_t, _c_p]),
     "fdp_layernorm_fwd": (_c_int, [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_f, _c_int, _c_int, _c_p,
                                    _c_p, _c_p, _c_p]),
     "fdp_layernorm_bwd_clip_workspace_size": (_c_int, [_c_i64, _c_i64, _c_i64, _c_int, _c_sz_p]),
     "fdp_layernorm_bwd_clip": (_c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64,
                                         _c_int, _c_int, _c_f, _c_f, _c_p, _c_f, _c_p, _c_p, _c_f,
-                                        _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, ctypes.c_size_t,
-                                        _c_p]),
+                                        _c_key, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p,
+                                        ctypes.c_size_t, _c_p]),
 }
 
 _lock = threading.Lock()

@@ -28,10 +28,11 @@ def _as_bth(t: torch.Tensor) -> torch.Tensor:
 def colsum_clip(u: torch.Tensor, v: torch.Tensor | None = None, C: float = 1.0,
                 clamp_value: float = 1.0, *, norm: str = "sum", clip_args=None,
                 out_scale: float = 1.0, noise: torch.Tensor | None = None,
-                noise_scale: float = 1.0, out_dtype: torch.dtype | None = None,
-                return_stats: bool = False):
-    """out[h] = out_scale * sum_b c_b S_b[h] + noise_scale * noise[h],
-    S_b = sum_t u_bt (* v_bt), c_b from ||S_b|| (norm="sum") or ||u_b||_F (norm="frob")."""
+                noise_scale: float = 1.0, noise_key: tuple[int, int] | None = None,
+                out_dtype: torch.dtype | None = None, return_stats: bool = False):
+    """out[h] = out_scale * sum_b c_b S_b[h] + noise_scale * z[h],
+    S_b = sum_t u_bt (* v_bt), c_b from ||S_b|| (norm="sum") or ||u_b||_F (norm="frob");
+    z is ``noise`` or the in-kernel draw of ``noise_key = (seed, offset)``."""
     dev = _lib.require_hip(u, v, noise)
     u3 = _as_bth(u)
     v3 = None
@@ -62,7 +63,8 @@ def colsum_clip(u: torch.Tensor, v: torch.Tensor | None = None, C: float = 1.0,
     st = L.fdp_colsum_clip(
         _lib.ptr(u3), _lib.ptr(v3), B, T, H, dt, kind, ctypes.c_float(C_),
         ctypes.c_float(clamp_), _lib.ptr(cad), ctypes.c_float(out_scale), _lib.ptr(noise),
-        ctypes.c_float(noise_scale), out.data_ptr(), odt, _lib.ptr(norms), _lib.ptr(factors),
+        ctypes.c_float(noise_scale), _lib.noise_key(noise_key), out.data_ptr(), odt,
+        _lib.ptr(norms), _lib.ptr(factors),
         ws.data_ptr(), ws.numel(), _lib.stream_handle(dev))
     _lib.check(st, "fdp_colsum_clip")
     if return_stats:

@@ -56,13 +56,15 @@ def layernorm_bwd_clip(grad_output: torch.Tensor, x: torch.Tensor, weight: torch
                        mean: torch.Tensor, rstd: torch.Tensor, C: float = 1.0,
                        clamp_value: float = 1.0, *, clip_args=None, out_scale: float | None = None,
                        noise_w: torch.Tensor | None = None, noise_b: torch.Tensor | None = None,
-                       noise_scale: float = 1.0, need_dw: bool = True, need_db: bool = True,
+                       noise_scale: float = 1.0, noise_key: tuple[int, int] | None = None,
+                       need_dw: bool = True, need_db: bool = True,
                        param_dtype: torch.dtype | None = None, return_stats: bool = False):
     """dx, dw, db of LayerNorm over the last axis with per-sample clipped dw/db.
 
     x, grad_output [B, ..., H]; samples are the leading axis.  dw / db are
-    out_scale * sum_b clip(||.||) (.) + noise_scale * noise with out_scale = 1/B by
-    default.  With ``return_stats`` also returns norms [2B] and factors [2B]
+    out_scale * sum_b clip(||.||) (.) + noise_scale * z with out_scale = 1/B by
+    default, z the noise_w / noise_b tensors or, for one without a tensor, the
+    in-kernel draw of ``noise_key = (seed, offset)`` (dw stream 0, db stream 1).  With ``return_stats`` also returns norms [2B] and factors [2B]
     (dgamma's per-sample values first, then dbeta's)."""
     dev = _lib.require_hip(grad_output, x, weight, mean, rstd, noise_w, noise_b)
     H = x.shape[-1]
@@ -102,7 +104,8 @@ def layernorm_bwd_clip(grad_output: torch.Tensor, x: torch.Tensor, weight: torch
         dy.data_ptr(), x.data_ptr(), _lib.ptr(weight), mean.data_ptr(), rstd.data_ptr(), B, T, H,
         dt, wdt, ctypes.c_float(C_), ctypes.c_float(clamp_), _lib.ptr(cad),
         ctypes.c_float(out_scale), _lib.ptr(noise_w), _lib.ptr(noise_b),
-        ctypes.c_float(noise_scale), dx.data_ptr(), _lib.ptr(dw), _lib.ptr(db), _lib.ptr(norms),
+        ctypes.c_float(noise_scale), _lib.noise_key(noise_key), dx.data_ptr(), _lib.ptr(dw),
+        _lib.ptr(db), _lib.ptr(norms),
         _lib.ptr(factors), ws.data_ptr(), ws.numel(), _lib.stream_handle(dev))
     _lib.check(st, "fdp_layernorm_bwd_clip")
     if return_stats:

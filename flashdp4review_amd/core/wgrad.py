@@ -81,14 +81,18 @@ def _inner_contig(t: torch.Tensor) -> torch.Tensor:
 def wgrad_clip(a: torch.Tensor, b: torch.Tensor, C: float = 1.0, clamp_value: float = 1.0, *,
                layout: str = "tn", clip_args=None, out_scale: float = 1.0,
                noise: torch.Tensor | None = None, noise_scale: float = 1.0,
+               noise_key: tuple[int, int] | None = None,
                out_dtype: torch.dtype | None = None, out: torch.Tensor | None = None,
                return_stats: bool = False, noclip: bool = False, two_pass: bool = False,
                launch: str | None = None, check: bool = False):
-    """out = out_scale * sum_b c_b G_b + noise_scale * noise, c_b = clip(||G_b||_F).
+    """out = out_scale * sum_b c_b G_b + noise_scale * z, c_b = clip(||G_b||_F).
 
     layout "tn": a [B,K,M], b [B,K,N], G_b = a_b^T b_b;
     layout "nn": a [B,M,K], b [B,K,N], G_b = a_b b_b.
     ``clip_args`` (tensor [C, clamp] or pair) overrides C / clamp_value.
+    z is the ``noise`` tensor, or, without one, the in-kernel Philox draw of
+    ``noise_key = (seed, offset)`` (fdp_noise_key in include/flashdp_hip.h);
+    neither: no noise.
     With ``return_stats`` also returns the fp32 per-sample norms and factors.
     ``two_pass`` forces the norm-pass + clipped-sum-pass schedule instead of the
     single-pass kernel; ``launch`` ("cooperative" / "plain", default: the
@@ -148,7 +152,8 @@ def wgrad_clip(a: torch.Tensor, b: torch.Tensor, C: float = 1.0, clamp_value: fl
     st = L.fdp_wgrad_clip(
         _lib.ptr(a), _lib.ptr(b), Bn, K, M, N, a.stride(0), a.stride(1), b.stride(0), b.stride(1),
         lay, dt, ctypes.c_float(C_), ctypes.c_float(clamp_), _lib.ptr(cad),
-        ctypes.c_float(out_scale), _lib.ptr(noise), ctypes.c_float(noise_scale), out.data_ptr(),
+        ctypes.c_float(out_scale), _lib.ptr(noise), ctypes.c_float(noise_scale),
+        _lib.noise_key(noise_key), out.data_ptr(),
         out.stride(0), odt, _lib.ptr(norms), _lib.ptr(factors), flags, ws.data_ptr(), ws.numel(),
         stream)
     _lib.check(st, "fdp_wgrad_clip")

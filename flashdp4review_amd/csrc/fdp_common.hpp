@@ -62,6 +62,160 @@ __device__ inline void store_from_f32(void* p, int64_t i, int dtype, float v) {
   }
 }
 
+// ------------------------------------------------------------ Gaussian noise
+// Philox4x32-10 (Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as easy
+// as 1, 2, 3", SC 2011): ten rounds, each multiplying counter words 0 and 2 by
+// the round constants (32x32 -> 64 bits) and mixing the halves with the other
+// words and the key; the key is bumped by the Weyl constants between rounds.
+struct U32x4 {
+  uint32_t w[4];
+};
+__device__ __forceinline__ U32x4 philox4x32_10(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3,
+                                               uint32_t k0, uint32_t k1) {
+  constexpr uint32_t kM0 = 0xD2511F53u, kM1 = 0xCD9E8D57u;
+  constexpr uint32_t kW0 = 0x9E3779B9u, kW1 = 0xBB67AE85u;
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    if (r > 0) {
+      k0 += kW0;
+      k1 += kW1;
+    }
+    // one v_mad_u64_u32 per product (both halves at once)
+    const uint64_t p0 = static_cast<uint64_t>(kM0) * c0, p1 = static_cast<uint64_t>(kM1) * c2;
+    const uint32_t lo0 = static_cast<uint32_t>(p0), hi0 = static_cast<uint32_t>(p0 >> 32);
+    const uint32_t lo1 = static_cast<uint32_t>(p1), hi1 = static_cast<uint32_t>(p1 >> 32);
+    const uint32_t n0 = hi1 ^ c1 ^ k0, n2 = hi0 ^ c3 ^ k1;
+    c0 = n0;
+    c1 = lo1;
+    c2 = n2;
+    c3 = lo0;
+  }
+  return U32x4{{c0, c1, c2, c3}};
+}
+
+// Box-Muller on two 24-bit uniforms in (0, 1): r = sqrt(-2 ln u_a),
+// (r cos 2 pi u_b, r sin 2 pi u_b).  v_log_f32 is log2; v_sin/v_cos_f32 take
+// their argument in revolutions.
+__device__ __forceinline__ void box_muller(uint32_t a, uint32_t b, float& z0, float& z1) {
+  constexpr float kInv24 = 5.9604644775390625e-08f;  // 2^-24
+  const float ua = (static_cast<float>(a >> 8) + 0.5f) * kInv24;
+  const float ub = (static_cast<float>(b >> 8) + 0.5f) * kInv24;
+  const float r = __builtin_sqrtf(-1.3862943611198906f * __builtin_amdgcn_logf(ua));  // -2 ln 2 log2
+  z0 = r * __builtin_amdgcn_cosf(ub);
+  z1 = r * __builtin_amdgcn_sinf(ub);
+}
+
+// Noise of one output: an injected tensor z (row-major, dtype `dtype`) or, when
+// `draw`, the Philox stream of fdp_noise_key (counter block offset + e/4,
+// counter word 2 = stream).
+struct NoiseSrc {
+  const void* z;
+  int dtype;
+  bool draw;
+  uint32_t k0, k1, stream;
+  uint64_t offset;
+  __device__ __forceinline__ bool on() const { return z != nullptr || draw; }
+  __device__ __forceinline__ void block(int64_t q, float (&o)[4]) const {
+    const uint64_t c = offset + static_cast<uint64_t>(q);
+    const U32x4 r = philox4x32_10(static_cast<uint32_t>(c), static_cast<uint32_t>(c >> 32), stream,
+                                  0u, k0, k1);
+    box_muller(r.w[0], r.w[1], o[0], o[1]);
+    box_muller(r.w[2], r.w[3], o[2], o[3]);
+  }
+  // z[e] (a single element)
+  __device__ __forceinline__ float at(int64_t e) const;
+  // z[e .. e+n-1] for any e: whole blocks around the window, then a select
+  // network on e mod 4 (no dynamically indexed register arrays)
+  template <int n>
+  __device__ __forceinline__ void window(int64_t e, float (&o)[n]) const {
+    static_assert(n % 4 == 0, "whole Philox blocks");
+    float w[n + 4];
+#pragma unroll
+    for (int i = 0; i <= n / 4; ++i) {
+      float b[4];
+      block(e / 4 + i, b);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) w[4 * i + j] = b[j];
+    }
+    const int sh = static_cast<int>(e & 3);
+#pragma unroll
+    for (int j = 0; j < n; ++j)
+      o[j] = sh == 0 ? w[j] : sh == 1 ? w[j + 1] : sh == 2 ? w[j + 2] : w[j + 3];
+  }
+  // z[e .. e+n-1] for n a multiple of 4 and e a multiple of 4
+  template <int n>
+  __device__ __forceinline__ void run(int64_t e, float (&o)[n]) const {
+    static_assert(n % 4 == 0, "whole Philox blocks");
+#pragma unroll
+    for (int i = 0; i < n / 4; ++i) {
+      float b[4];
+      block(e / 4 + i, b);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[4 * i + j] = b[j];
+    }
+  }
+};
+
+__device__ __forceinline__ float NoiseSrc::at(int64_t e) const {
+  if (z != nullptr) return load_as_f32(z, e, dtype);
+  float b[4];
+  block(e / 4, b);
+  const int j = static_cast<int>(e & 3);
+  return j == 0 ? b[0] : j == 1 ? b[1] : j == 2 ? b[2] : b[3];
+}
+
+// How the E-element chunk at row-major index e (e % E == 0, whole chunk inside
+// a row of length N) can be read: 2 = one 16-byte load of the injected
+// tensor, 1 = whole Philox blocks, 0 = element by element, -1 = no noise.
+template <int E>
+__device__ __forceinline__ int noise_chunks(const NoiseSrc& nz, int64_t N) {
+  if (!nz.on()) return -1;
+  if (nz.z != nullptr)
+    return (reinterpret_cast<uintptr_t>(nz.z) % 16 == 0 && N % (16 / (nz.dtype == FDP_F32 ? 4 : 2)) == 0 &&
+            E == 16 / (nz.dtype == FDP_F32 ? 4 : 2))
+               ? 2
+               : 0;
+  return N % 4 == 0 ? 1 : 0;
+}
+// v[j] += scale * z[e + j], j < E, read as noise_chunks() allows; the injected
+// tensor has the output's storage type OT.
+template <class OT, int E>
+__device__ __forceinline__ void add_noise_chunk(const NoiseSrc& nz, int how, int64_t e, float scale,
+                                                float (&v)[E]) {
+  static_assert(E % 4 == 0, "16-byte chunks of 16- or 32-bit values");
+  if (how < 0) return;
+  if (how == 2) {
+    using S = typename OT::storage;
+    const uint4 raw = *reinterpret_cast<const uint4*>(static_cast<const S*>(nz.z) + e);
+    const S* zs = reinterpret_cast<const S*>(&raw);
+#pragma unroll
+    for (int j = 0; j < E; ++j) v[j] += scale * OT::to_f32(zs[j]);
+  } else if (how == 1) {
+    float z[E];
+    nz.run(e, z);
+#pragma unroll
+    for (int j = 0; j < E; ++j) v[j] += scale * z[j];
+  } else {
+#pragma unroll
+    for (int j = 0; j < E; ++j) v[j] += scale * nz.at(e + j);
+  }
+}
+
+// Host side: the noise of output `stream` of a call.
+inline NoiseSrc make_noise(const void* z, int dtype, const fdp_noise_key* key, uint32_t stream) {
+  NoiseSrc n{};
+  n.z = z;
+  n.dtype = dtype;
+  n.draw = z == nullptr && key != nullptr;
+  n.stream = stream;
+  if (key != nullptr) {
+    n.k0 = static_cast<uint32_t>(key->seed);
+    n.k1 = static_cast<uint32_t>(key->seed >> 32);
+    n.offset = key->offset;
+  }
+  return n;
+}
+
 // ------------------------------------------------------------ reductions
 __device__ inline float wave_sum(float v) {
 #pragma unroll

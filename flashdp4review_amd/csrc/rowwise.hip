@@ -264,9 +264,8 @@ constexpr int kFacChunk = 1024;  // clip factors staged in LDS per pass
 template <bool V4>
 __global__ __launch_bounds__(NT) void combine_kernel(
     const float* sums, const float* parts, int nparts, int64_t B, int64_t H, float C,
-    float clamp, const float* clip_args_dev, float out_scale, const void* noise0,
-    const void* noise1, float noise_scale, void* out0, void* out1, int out_dtype, float* norms,
-    float* factors) {
+    float clamp, const float* clip_args_dev, float out_scale, NoiseSrc noise0, NoiseSrc noise1,
+    float noise_scale, void* out0, void* out1, int out_dtype, float* norms, float* factors) {
   __shared__ float fac[kFacChunk];
   __shared__ f32x4 grp[NT / kWave][kItemsPerBlock];
   if (clip_args_dev != nullptr) {
@@ -275,7 +274,7 @@ __global__ __launch_bounds__(NT) void combine_kernel(
   }
   const int k = blockIdx.y;
   void* out = k == 0 ? out0 : out1;
-  const void* noise = k == 0 ? noise0 : noise1;
+  const NoiseSrc noise = k == 0 ? noise0 : noise1;
   const bool write_stats = blockIdx.x == 0;
   const int lane = threadIdx.x & 63, g = threadIdx.x >> 6;
   const int64_t items = (H + Item<V4>::W - 1) / Item<V4>::W;
@@ -331,11 +330,19 @@ __global__ __launch_bounds__(NT) void combine_kernel(
   __syncthreads();
   if (g == 0 && it < items) {
     const f32x4 tot = ((grp[0][lane] + grp[1][lane]) + grp[2][lane]) + grp[3][lane];
-    for (int e = 0; e < Item<V4>::W; ++e) {
-      const int64_t h = it * Item<V4>::W + e;
-      float o = tot[e] * out_scale;
-      if (noise) o += noise_scale * load_as_f32(noise, h, out_dtype);
-      store_from_f32(out, h, out_dtype, o);
+    constexpr int W = Item<V4>::W;
+    float z[4] = {0.f, 0.f, 0.f, 0.f};
+    if (noise.z != nullptr) {
+#pragma unroll
+      for (int e = 0; e < W; ++e)
+        if (it * W + e < H) z[e] = noise.at(it * W + e);
+    } else if (noise.draw) {
+      noise.window(it * W, z);
+    }
+#pragma unroll
+    for (int e = 0; e < W; ++e) {
+      const int64_t h = it * W + e;
+      if (h < H) store_from_f32(out, h, out_dtype, tot[e] * out_scale + noise_scale * z[e]);
     }
   }
 }
@@ -651,8 +658,7 @@ struct Epilogue {
   float C, clamp;
   const float* clip_args_dev;
   float out_scale, noise_scale;
-  const void* noise0;
-  const void* noise1;
+  NoiseSrc noise0, noise1;
   void* out0;
   void* out1;
   int out_dtype;
@@ -798,9 +804,9 @@ extern "C" int fdp_colsum_clip_workspace_size(int64_t B, int64_t T, int64_t H, i
 extern "C" int fdp_colsum_clip(const void* u, const void* v, int64_t B, int64_t T, int64_t H,
                                int dtype, int norm_kind, float C, float clamp,
                                const float* clip_args_dev, float out_scale, const void* noise,
-                               float noise_scale, void* out, int out_dtype, float* norms,
-                               float* factors, void* workspace, size_t workspace_bytes,
-                               void* stream) {
+                               float noise_scale, const fdp_noise_key* noise_key, void* out,
+                               int out_dtype, float* norms, float* factors, void* workspace,
+                               size_t workspace_bytes, void* stream) {
   if (!valid_dtype(dtype) || !valid_dtype(out_dtype)) return FDP_ERR_DTYPE;
   if (norm_kind != FDP_NORM_SUM && norm_kind != FDP_NORM_FROB) return FDP_ERR_ARG;
   if (B < 1 || T < 0 || H < 1) return FDP_ERR_SHAPE;
@@ -819,8 +825,15 @@ extern "C" int fdp_colsum_clip(const void* u, const void* v, int64_t B, int64_t 
   if (dtype == FDP_BF16) launch_colsum_dt<BF16>(p, u, v, B, T, H, ws, frob, s);
   else if (dtype == FDP_F16) launch_colsum_dt<F16>(p, u, v, B, T, H, ws, frob, s);
   else launch_colsum_dt<F32>(p, u, v, B, T, H, ws, frob, s);
-  const Epilogue e{C, clamp, clip_args_dev, out_scale, noise_scale, noise, nullptr, out, nullptr,
-                   out_dtype, norms, factors};
+  const fdp_noise_key* key = noise_scale != 0.f ? noise_key : nullptr;
+  const Epilogue e{C,         clamp,
+                   clip_args_dev,
+                   out_scale, noise_scale,
+                   make_noise(noise, out_dtype, key, 0),
+                   make_noise(nullptr, out_dtype, nullptr, 1),
+                   out,       nullptr,
+                   out_dtype, norms,
+                   factors};
   launch_reduce(p, ws, B, H, 1, frob, e, s);
   return hipGetLastError() == hipSuccess ? FDP_OK : FDP_ERR_HIP;
 }
@@ -856,9 +869,9 @@ extern "C" int fdp_layernorm_bwd_clip(const void* dy, const void* x, const void*
                                       int64_t H, int dtype, int w_dtype, float C, float clamp,
                                       const float* clip_args_dev, float out_scale,
                                       const void* noise_w, const void* noise_b,
-                                      float noise_scale, void* dx, void* dw, void* db,
-                                      float* norms, float* factors, void* workspace,
-                                      size_t workspace_bytes, void* stream) {
+                                      float noise_scale, const fdp_noise_key* noise_key,
+                                      void* dx, void* dw, void* db, float* norms, float* factors,
+                                      void* workspace, size_t workspace_bytes, void* stream) {
   if (!valid_dtype(dtype) || !valid_dtype(w_dtype)) return FDP_ERR_DTYPE;
   if (B < 1 || T < 0 || H < 1 || H > kMaxLnH) return FDP_ERR_SHAPE;
   if (B > 32767) return FDP_ERR_SHAPE;  // the 2B streams index grid.y
@@ -878,8 +891,15 @@ extern "C" int fdp_layernorm_bwd_clip(const void* dy, const void* x, const void*
   if (dtype == FDP_BF16) launch_ln_bwd<BF16>(vec, epl, p, io, part, s);
   else if (dtype == FDP_F16) launch_ln_bwd<F16>(vec, epl, p, io, part, s);
   else launch_ln_bwd<F32>(vec, epl, p, io, part, s);
-  const Epilogue e{C, clamp, clip_args_dev, out_scale, noise_scale, noise_w, noise_b, dw, db,
-                   w_dtype, norms, factors};
+  const fdp_noise_key* key = noise_scale != 0.f ? noise_key : nullptr;
+  const Epilogue e{C,        clamp,
+                   clip_args_dev,
+                   out_scale, noise_scale,
+                   make_noise(noise_w, w_dtype, key, 0),
+                   make_noise(noise_b, w_dtype, key, 1),
+                   dw,       db,
+                   w_dtype,  norms,
+                   factors};
   launch_reduce(p, ws, B, H, 2, false, e, s);
   return hipGetLastError() == hipSuccess ? FDP_OK : FDP_ERR_HIP;
 }

@@ -143,6 +143,7 @@ __global__ __launch_bounds__(NT) void wgrad_sum_kernel(Args p) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
   const bool single = p.groups == 1;
+  const NoiseSrc nz = p.noise;
   const float scale = any ? c_prev * (single ? p.out_scale : 1.f) : 0.f;
 #pragma unroll
   for (int i = 0; i < 2; ++i)
@@ -156,7 +157,7 @@ __global__ __launch_bounds__(NT) void wgrad_sum_kernel(Args p) {
         if (m >= p.M) continue;
         float v = acc[i][j][r] * scale;
         if (single) {
-          if (p.noise) v += p.noise_scale * load_as_f32(p.noise, m * p.N + n, p.out_dtype);
+          if (nz.on()) v += p.noise_scale * nz.at(m * p.N + n);
           store_from_f32(p.out, m * p.ldo + n, p.out_dtype, v);
         } else {
           p.group_out[(int64_t(g) * p.M + m) * p.N + n] = v;
@@ -168,11 +169,12 @@ __global__ __launch_bounds__(NT) void wgrad_sum_kernel(Args p) {
 // out = out_scale * sum_g group_out[g] + noise_scale * noise, fixed order in g.
 __global__ __launch_bounds__(NT) void wgrad_finalize_kernel(Args p) {
   const int64_t MN = p.M * p.N;
+  const NoiseSrc nz = p.noise;
   for (int64_t e = int64_t(blockIdx.x) * NT + threadIdx.x; e < MN; e += int64_t(gridDim.x) * NT) {
     float s = 0.f;
     for (int g = 0; g < p.groups; ++g) s += p.group_out[int64_t(g) * MN + e];
     float v = s * p.out_scale;
-    if (p.noise) v += p.noise_scale * load_as_f32(p.noise, e, p.out_dtype);
+    if (nz.on()) v += p.noise_scale * nz.at(e);
     const int64_t m = e / p.N, n = e - m * p.N;
     store_from_f32(p.out, m * p.ldo + n, p.out_dtype, v);
   }
@@ -374,7 +376,8 @@ extern "C" int fdp_wgrad_clip(const void* a, const void* b, int64_t B, int64_t K
                               int64_t N, int64_t stride_ab, int64_t lda, int64_t stride_bb,
                               int64_t ldb, int layout, int dtype, float C, float clamp,
                               const float* clip_args_dev, float out_scale, const void* noise,
-                              float noise_scale, void* out, int64_t ldo, int out_dtype,
+                              float noise_scale, const fdp_noise_key* noise_key, void* out,
+                              int64_t ldo, int out_dtype,
                               float* norms, float* factors, int flags, void* workspace,
                               size_t workspace_bytes, void* stream) {
   if (!valid_dtype(dtype) || !valid_dtype(out_dtype)) return FDP_ERR_DTYPE;
@@ -420,7 +423,7 @@ extern "C" int fdp_wgrad_clip(const void* a, const void* b, int64_t B, int64_t K
   args.ldo = ldo;
   args.out_dtype = out_dtype;
   args.out_scale = out_scale;
-  args.noise = noise;
+  args.noise = make_noise(noise, out_dtype, noise_scale != 0.f ? noise_key : nullptr, 0);
   args.noise_scale = noise_scale;
   args.units = int64_t(pl.tiles) * B;
   args.err = reinterpret_cast<int*>(ws);

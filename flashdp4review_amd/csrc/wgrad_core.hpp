@@ -29,7 +29,7 @@ struct Args {
   int64_t ldo;
   int out_dtype;
   float out_scale;
-  const void* noise;
+  NoiseSrc noise;          // injected or drawn z (row-major [M, N])
   float noise_scale;
   // single-pass (fused) kernel
   int64_t units;          // tiles * B work units, unit u = (tile u/B, sample u%B)
@@ -474,39 +474,6 @@ struct Held<false> {
   }
 };
 
-// out[m, n] = out_scale * tot + noise_scale * noise for the in-range part of a tile.
-template <class OT>
-__device__ inline void store_tile_t(const Args& p, int64_t m0, int64_t n0,
-                                    const f32x16 (&tot)[2][2]) {
-  using S = typename OT::storage;
-  S* out = static_cast<S*>(p.out);
-  const S* noise = static_cast<const S*>(p.noise);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int64_t n = n0 + acc_col(wn, j, lane);
-      if (n >= p.N) continue;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t m = m0 + acc_row(wm, i, lane, r);
-        if (m >= p.M) continue;
-        float v = tot[i][j][r] * p.out_scale;
-        if (noise) v += p.noise_scale * OT::to_f32(noise[m * p.N + n]);
-        out[m * p.ldo + n] = OT::from_f32(v);
-      }
-    }
-}
-__device__ inline void store_tile(const Args& p, int tile, const f32x16 (&tot)[2][2]) {
-  int64_t m0, n0;
-  tile_coords(p, tile, m0, n0);
-  if (p.out_dtype == FDP_BF16) store_tile_t<BF16>(p, m0, n0, tot);
-  else if (p.out_dtype == FDP_F16) store_tile_t<F16>(p, m0, n0, tot);
-  else store_tile_t<F32>(p, m0, n0, tot);
-}
-
 // Tile-local fp32 buffer access in the accumulator layout (coalesced along n).
 __device__ __forceinline__ int tl_index(int wm, int wn, int i, int j, int lane, int r) {
   return acc_row(wm, i, lane, r) * BN + acc_col(wn, j, lane);
@@ -594,10 +561,11 @@ __device__ inline void store_tile_staged(const Args& p, int64_t m0, int64_t n0,
   }
   __syncthreads();
   S* out = static_cast<S*>(p.out);
-  const S* noise = static_cast<const S*>(p.noise);
-  const bool vec = (reinterpret_cast<uintptr_t>(out) % 16 == 0) && (p.ldo % E == 0) &&
-                   (noise == nullptr || (reinterpret_cast<uintptr_t>(noise) % 16 == 0 && p.N % E == 0));
+  const bool vec = (reinterpret_cast<uintptr_t>(out) % 16 == 0) && (p.ldo % E == 0);
+  const NoiseSrc nz = p.noise;  // a value copy: no address of the kernel argument is taken
+  const int zvec = noise_chunks<E>(nz, p.N);
   constexpr int CPR = BN / E;  // chunks per tile row
+#pragma unroll 1
   for (int q = threadIdx.x; q < BM * CPR; q += NT) {
     const int row = q / CPR, col = (q % CPR) * E;
     const int64_t m = m0 + row, n = n0 + col;
@@ -607,23 +575,27 @@ __device__ inline void store_tile_staged(const Args& p, int64_t m0, int64_t n0,
 #pragma unroll
     for (int e = 0; e < E; ++e) v[e] = src[e] * p.out_scale;
     if (vec && n + E <= p.N) {
-      if (noise) {
-        const uint4 nz = *reinterpret_cast<const uint4*>(noise + m * p.N + n);
-        const S* ns = reinterpret_cast<const S*>(&nz);
-#pragma unroll
-        for (int e = 0; e < E; ++e) v[e] += p.noise_scale * OT::to_f32(ns[e]);
-      }
+      add_noise_chunk<OT, E>(nz, zvec, m * p.N + n, p.noise_scale, v);
       uint4 o;
       S* os = reinterpret_cast<S*>(&o);
 #pragma unroll
       for (int e = 0; e < E; ++e) os[e] = OT::from_f32(v[e]);
       *reinterpret_cast<uint4*>(out + m * p.ldo + n) = o;
     } else {
-      for (int e = 0; e < E && n + e < p.N; ++e) {
-        float x = v[e];
-        if (noise) x += p.noise_scale * OT::to_f32(noise[m * p.N + n + e]);
-        out[m * p.ldo + n + e] = OT::from_f32(x);
+      // right edge or unaligned rows: element stores, noise from whole blocks
+      if (nz.z != nullptr) {
+      #pragma unroll
+        for (int e = 0; e < E; ++e)
+          if (n + e < p.N) v[e] += p.noise_scale * nz.at(m * p.N + n + e);
+      } else if (nz.draw) {
+        float z[E];
+        nz.window(m * p.N + n, z);
+      #pragma unroll
+        for (int e = 0; e < E; ++e) v[e] += p.noise_scale * z[e];
       }
+      #pragma unroll
+      for (int e = 0; e < E; ++e)
+        if (n + e < p.N) out[m * p.ldo + n + e] = OT::from_f32(v[e]);
     }
   }
 }

@@ -264,9 +264,10 @@ __device__ inline void store_half(const Args& p, int64_t m0, int64_t n0, int h,
     constexpr int E = 16 / sizeof(S);
     constexpr int CPR = G::BN / E;
     S* out = static_cast<S*>(p.out);
-    const S* noise = static_cast<const S*>(p.noise);
-    const bool vec = (reinterpret_cast<uintptr_t>(out) % 16 == 0) && (p.ldo % E == 0) &&
-                     (noise == nullptr || (reinterpret_cast<uintptr_t>(noise) % 16 == 0 && p.N % E == 0));
+    const bool vec = (reinterpret_cast<uintptr_t>(out) % 16 == 0) && (p.ldo % E == 0);
+    const NoiseSrc nz = p.noise;  // a value copy: no address of the kernel argument is taken
+  const int zvec = noise_chunks<E>(nz, p.N);
+#pragma unroll 1
     for (int q = threadIdx.x; q < G::WM * CPR; q += NT) {
       const int row = q / CPR, col = (q % CPR) * E;
       const int64_t m = mh + row, n = n0 + col;
@@ -276,23 +277,27 @@ __device__ inline void store_half(const Args& p, int64_t m0, int64_t n0, int h,
 #pragma unroll
       for (int e = 0; e < E; ++e) v[e] = src[e];
       if (vec && n + E <= p.N) {
-        if (noise) {
-          const uint4 nz = *reinterpret_cast<const uint4*>(noise + m * p.N + n);
-          const S* ns = reinterpret_cast<const S*>(&nz);
-#pragma unroll
-          for (int e = 0; e < E; ++e) v[e] += p.noise_scale * OT::to_f32(ns[e]);
-        }
+        add_noise_chunk<OT, E>(nz, zvec, m * p.N + n, p.noise_scale, v);
         uint4 o;
         S* os = reinterpret_cast<S*>(&o);
 #pragma unroll
         for (int e = 0; e < E; ++e) os[e] = OT::from_f32(v[e]);
         *reinterpret_cast<uint4*>(out + m * p.ldo + n) = o;
       } else {
-        for (int e = 0; e < E && n + e < p.N; ++e) {
-          float x = v[e];
-          if (noise) x += p.noise_scale * OT::to_f32(noise[m * p.N + n + e]);
-          out[m * p.ldo + n + e] = OT::from_f32(x);
+        // right edge or unaligned rows: element stores, noise from whole blocks
+        if (nz.z != nullptr) {
+        #pragma unroll
+          for (int e = 0; e < E; ++e)
+            if (n + e < p.N) v[e] += p.noise_scale * nz.at(m * p.N + n + e);
+        } else if (nz.draw) {
+          float z[E];
+          nz.window(m * p.N + n, z);
+        #pragma unroll
+          for (int e = 0; e < E; ++e) v[e] += p.noise_scale * z[e];
         }
+        #pragma unroll
+        for (int e = 0; e < E; ++e)
+          if (n + e < p.N) out[m * p.ldo + n + e] = OT::from_f32(v[e]);
       }
     }
   }

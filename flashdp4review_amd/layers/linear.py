@@ -18,7 +18,7 @@ from torch.autograd.function import Function
 from ..core import colsum_clip, wgrad_clip
 from ..core.utils import RuntimeAutoTuner
 from .utils import DPParameter as Parameter
-from .utils import as_btf, draw_noise, noise_std
+from .utils import NoiseStream, as_btf, noise_args, noise_std
 
 
 class DPLinear(nn.Linear):
@@ -41,8 +41,10 @@ class DPLinear(nn.Linear):
         else:
             self.register_parameter("bias", None)
         self.reset_parameters()
-        # Optional torch.Generator for the noise draws (z_W first, then z_b).
+        # Noise: drawn inside the kernels from noise_stream, or, when a
+        # torch.Generator is set here, drawn with it (z_W first, then z_b).
         self.noise_generator = None
+        self.noise_stream = NoiseStream()
         # When True, backward stores per-sample norms / clip factors in last_stats.
         self.record_stats = False
         self.last_stats = None
@@ -59,7 +61,7 @@ class _DPLinearFunction(Function):
         ctx.has_bias = bias is not None
         ctx.bias_dtype = bias.dtype if bias is not None else None
         ctx.cfg = (float(module.C), float(module.clamp_value), float(module.noise_multiplier),
-                   module.noise_generator)
+                   module.noise_generator, module.noise_stream)
         ctx.module = module if module.record_stats else None
         w = weight if weight.dtype == input.dtype else weight.to(input.dtype)
         b = None if bias is None else (bias if bias.dtype == input.dtype else bias.to(input.dtype))
@@ -68,7 +70,7 @@ class _DPLinearFunction(Function):
     @staticmethod
     def backward(ctx, grad_output):
         input, weight = ctx.saved_tensors
-        C, clamp_value, sigma, gen = ctx.cfg
+        C, clamp_value, sigma, gen, nstream = ctx.cfg
         x3, g3 = as_btf(input), as_btf(grad_output)
         B, T = x3.shape[0], x3.shape[1]
         std = noise_std(sigma, B)
@@ -78,9 +80,9 @@ class _DPLinearFunction(Function):
             w = weight if weight.dtype == g3.dtype else weight.to(g3.dtype)
             grad_input = (g3 @ w).reshape(input.shape)
         if ctx.needs_input_grad[1]:
-            z = draw_noise(weight.shape, weight.dtype, weight.device, gen) if std > 0 else None
+            z, key = noise_args(std, gen, nstream, weight.shape, weight.dtype, weight.device)
             r = wgrad_clip(g3, x3.to(g3.dtype), C, clamp_value, layout="tn", out_scale=1.0 / B,
-                           noise=z, noise_scale=std, out_dtype=weight.dtype,
+                           noise=z, noise_scale=std, noise_key=key, out_dtype=weight.dtype,
                            return_stats=stats is not None)
             if stats is not None:
                 grad_weight, stats["norms_w"], stats["fac_w"] = r
@@ -88,9 +90,9 @@ class _DPLinearFunction(Function):
                 grad_weight = r
         if ctx.has_bias and ctx.needs_input_grad[2]:
             O = g3.shape[-1]
-            z = draw_noise((O,), ctx.bias_dtype, g3.device, gen) if std > 0 else None
+            z, key = noise_args(std, gen, nstream, (O,), ctx.bias_dtype, g3.device)
             r = colsum_clip(g3, None, C, clamp_value, norm="frob", out_scale=1.0 / (B * T),
-                            noise=z, noise_scale=std, out_dtype=ctx.bias_dtype,
+                            noise=z, noise_scale=std, noise_key=key, out_dtype=ctx.bias_dtype,
                             return_stats=stats is not None)
             if stats is not None:
                 grad_bias, stats["norms_b"], stats["fac_b"] = r

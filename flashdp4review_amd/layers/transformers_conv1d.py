@@ -19,7 +19,7 @@ from torch.autograd.function import Function
 from ..core import colsum_clip, wgrad_clip
 from ..core.utils import RuntimeAutoTuner
 from .utils import DPParameter as Parameter
-from .utils import as_btf, draw_noise, noise_std
+from .utils import NoiseStream, as_btf, noise_args, noise_std
 
 try:  # the HF module type is what wrap_with_flashdp_layers replaces
     from transformers.pytorch_utils import Conv1D as _HFConv1D
@@ -57,6 +57,7 @@ class DPConv1D(_Base):
         self.bias = Parameter(torch.zeros(nf))
         nn.init.normal_(self.weight, std=0.02)
         self.noise_generator = None
+        self.noise_stream = NoiseStream()
         self.record_stats = False
         self.last_stats = None
 
@@ -73,7 +74,7 @@ class _DPConv1DFunction(Function):
         ctx.save_for_backward(input, weight)
         ctx.bias_dtype = bias.dtype
         ctx.cfg = (float(module.C), float(module.clamp_value), float(module.noise_multiplier),
-                   module.noise_generator)
+                   module.noise_generator, module.noise_stream)
         ctx.module = module if module.record_stats else None
         w = weight if weight.dtype == input.dtype else weight.to(input.dtype)
         b = bias if bias.dtype == input.dtype else bias.to(input.dtype)
@@ -83,7 +84,7 @@ class _DPConv1DFunction(Function):
     @staticmethod
     def backward(ctx, grad_output):
         input, weight = ctx.saved_tensors
-        C, clamp_value, sigma, gen = ctx.cfg
+        C, clamp_value, sigma, gen, nstream = ctx.cfg
         x3, g3 = as_btf(input), as_btf(grad_output)
         B, T = x3.shape[0], x3.shape[1]
         std = noise_std(sigma, B)
@@ -93,18 +94,18 @@ class _DPConv1DFunction(Function):
             w = weight if weight.dtype == g3.dtype else weight.to(g3.dtype)
             grad_input = (g3 @ w.t()).reshape(input.shape)
         if ctx.needs_input_grad[1]:
-            z = draw_noise(weight.shape, weight.dtype, weight.device, gen) if std > 0 else None
+            z, key = noise_args(std, gen, nstream, weight.shape, weight.dtype, weight.device)
             r = wgrad_clip(x3.to(g3.dtype), g3, C, clamp_value, layout="tn", out_scale=1.0 / B,
-                           noise=z, noise_scale=std, out_dtype=weight.dtype,
+                           noise=z, noise_scale=std, noise_key=key, out_dtype=weight.dtype,
                            return_stats=stats is not None)
             if stats is not None:
                 grad_weight, stats["norms_w"], stats["fac_w"] = r
             else:
                 grad_weight = r
         if ctx.needs_input_grad[2]:
-            z = draw_noise((g3.shape[-1],), ctx.bias_dtype, g3.device, gen) if std > 0 else None
+            z, key = noise_args(std, gen, nstream, (g3.shape[-1],), ctx.bias_dtype, g3.device)
             r = colsum_clip(g3, None, C, clamp_value, norm="frob", out_scale=1.0 / (B * T),
-                            noise=z, noise_scale=std, out_dtype=ctx.bias_dtype,
+                            noise=z, noise_scale=std, noise_key=key, out_dtype=ctx.bias_dtype,
                             return_stats=stats is not None)
             if stats is not None:
                 grad_bias, stats["norms_b"], stats["fac_b"] = r

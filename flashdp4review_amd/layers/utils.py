@@ -44,3 +44,34 @@ def noise_std(noise_multiplier: float, batch: int) -> float:
 def draw_noise(shape, dtype, device, generator) -> torch.Tensor:
     """Standard-normal draw on the device; scaled by noise_std inside the kernels."""
     return torch.randn(shape, dtype=dtype, device=device, generator=generator)
+
+
+class NoiseStream:
+    """Keys of one DP module's in-kernel Gaussian draws (fdp_noise_key): a 64-bit
+    Philox seed taken from torch's default CPU generator at the first draw (so
+    torch.manual_seed makes a run reproducible) and a counter offset advanced
+    past every draw (an output of n elements uses ceil(n / 4) counter blocks).
+    The reference draws the same N(0, 1) noise with torch.normal
+    (flashdp/layers/linear.py:74-80); drawing it in the output epilogue saves
+    writing and re-reading a noise tensor per parameter."""
+
+    def __init__(self):
+        self.seed = None
+        self.offset = 0
+
+    def next(self, numel: int) -> tuple[int, int]:
+        if self.seed is None:
+            self.seed = int(torch.randint(0, 2**62, (1,), dtype=torch.int64).item())
+        key = (self.seed, self.offset)
+        self.offset += (int(numel) + 3) // 4
+        return key
+
+
+def noise_args(std: float, generator, stream: NoiseStream, shape, dtype, device):
+    """(z, key) for one noisy output: nothing at std == 0; an explicit torch draw
+    when the module has a noise_generator; else the next in-kernel key."""
+    if std <= 0:
+        return None, None
+    if generator is not None:
+        return draw_noise(shape, dtype, device, generator), None
+    return None, stream.next(math.prod(shape))

@@ -21,6 +21,10 @@
  *     {C, clamp} and overrides the scalar C/clamp arguments, the same device
  *     layout the reference's Triton kernels read (clip_fn.py:21-25).
  *   - Optional outputs (norms, factors, noise) may be NULL.
+ *   - Noise (the layers' torch.normal draw + add_, flashdp/layers/linear.py:74-92):
+ *     out += noise_scale * z with z either an injected tensor (`noise`), or,
+ *     when `noise` is NULL and `noise_key` is not, standard normals drawn in
+ *     the kernels (fdp_noise_key below); neither: no noise.
  */
 #ifndef FLASHDP_HIP_H
 #define FLASHDP_HIP_H
@@ -59,6 +63,21 @@ typedef enum fdp_layout {
   FDP_LAYOUT_NN = 1
 } fdp_layout;
 
+/* In-kernel Gaussian noise.  Output k of a call (k = 0; the LayerNorm entry
+ * point's db is k = 1) gets, at its row-major element e, the (e mod 4)-th of
+ * four normals made from the Philox4x32-10 block (Salmon et al., SC'11)
+ *   counter {lo32(offset + e/4), hi32(offset + e/4), k, 0}, key {lo32(seed), hi32(seed)}
+ * whose words (w0, w1) and (w2, w3) each give two normals by Box-Muller on
+ * 24-bit uniforms u = ((w >> 8) + 0.5) / 2^24:
+ *   r = sqrt(-2 ln u_first), z = (r cos 2 pi u_second, r sin 2 pi u_second).
+ * A call uses counter blocks [offset, offset + ceil(numel / 4)) of each output;
+ * callers advance `offset` (or change `seed`) between calls.  The struct is
+ * read on the host during the call. */
+typedef struct fdp_noise_key {
+  uint64_t seed;
+  uint64_t offset;
+} fdp_noise_key;
+
 /* Which per-sample norm drives the clip of a column-sum reduction.
  *   FDP_NORM_SUM:  || sum_t u_bt (.* v_bt) ||_2       (LayerNorm dgamma/dbeta,
  *                  flashdp/core/layernorm_clip.py:163-198)
@@ -93,6 +112,7 @@ int fdp_version(void);
  *            contiguous.
  * out      : [M, N] row-major with row stride ldo, dtype `out_dtype`.
  * noise    : NULL or [M, N] contiguous, dtype `out_dtype`.
+ * noise_key: NULL, or the in-kernel draw used when `noise` is NULL.
  * norms    : NULL or [B] fp32, ||G_b||_F.
  * factors  : NULL or [B] fp32, c_b.
  * flags    : bit 0 (FDP_WGRAD_NOCLIP) skips the norm pass and uses c_b = clamp
@@ -136,9 +156,9 @@ int fdp_wgrad_clip(const void* a, const void* b, int64_t B, int64_t K, int64_t M
                    int64_t N, int64_t stride_ab, int64_t lda, int64_t stride_bb,
                    int64_t ldb, int layout, int dtype, float C, float clamp,
                    const float* clip_args_dev, float out_scale, const void* noise,
-                   float noise_scale, void* out, int64_t ldo, int out_dtype,
-                   float* norms, float* factors, int flags, void* workspace,
-                   size_t workspace_bytes, void* stream);
+                   float noise_scale, const fdp_noise_key* noise_key, void* out,
+                   int64_t ldo, int out_dtype, float* norms, float* factors, int flags,
+                   void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
  * Clipped per-sample column sums over the middle axis:
@@ -155,7 +175,8 @@ int fdp_wgrad_clip(const void* a, const void* b, int64_t B, int64_t K, int64_t M
  *           noise add_ of the layers (flashdp/layers/linear.py:84-92,
  *           flashdp/layers/layernorm.py:139-155).
  * u, v     : [B, T, H] contiguous, dtype `dtype`; v may be NULL.
- * out      : [H], dtype `out_dtype`; noise NULL or [H] of `out_dtype`.
+ * out      : [H], dtype `out_dtype`; noise NULL or [H] of `out_dtype`;
+ *            noise_key as for fdp_wgrad_clip.
  * ---------------------------------------------------------------------- */
 int fdp_colsum_clip_workspace_size(int64_t B, int64_t T, int64_t H, int dtype,
                                    size_t* bytes);
@@ -163,9 +184,9 @@ int fdp_colsum_clip_workspace_size(int64_t B, int64_t T, int64_t H, int dtype,
 int fdp_colsum_clip(const void* u, const void* v, int64_t B, int64_t T, int64_t H,
                     int dtype, int norm_kind, float C, float clamp,
                     const float* clip_args_dev, float out_scale, const void* noise,
-                    float noise_scale, void* out, int out_dtype, float* norms,
-                    float* factors, void* workspace, size_t workspace_bytes,
-                    void* stream);
+                    float noise_scale, const fdp_noise_key* noise_key, void* out,
+                    int out_dtype, float* norms, float* factors, void* workspace,
+                    size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
  * LayerNorm forward over the last axis, fp32 statistics:
@@ -198,6 +219,7 @@ int fdp_layernorm_fwd(const void* x, const void* w, const void* b, int64_t rows,
  * mean,rstd: [B*T] fp32 from fdp_layernorm_fwd.
  * dw, db   : [H] of `w_dtype`; either may be NULL to skip it.
  * norms    : NULL or [2*B] fp32 (||P_b|| then ||Q_b||); factors likewise.
+ * noise_key: as for fdp_wgrad_clip; dw draws stream k = 0, db k = 1.
  * ---------------------------------------------------------------------- */
 int fdp_layernorm_bwd_clip_workspace_size(int64_t B, int64_t T, int64_t H,
                                           int dtype, size_t* bytes);
@@ -207,9 +229,10 @@ int fdp_layernorm_bwd_clip(const void* dy, const void* x, const void* w,
                            int64_t T, int64_t H, int dtype, int w_dtype, float C,
                            float clamp, const float* clip_args_dev,
                            float out_scale, const void* noise_w,
-                           const void* noise_b, float noise_scale, void* dx,
-                           void* dw, void* db, float* norms, float* factors,
-                           void* workspace, size_t workspace_bytes, void* stream);
+                           const void* noise_b, float noise_scale,
+                           const fdp_noise_key* noise_key, void* dx, void* dw, void* db,
+                           float* norms, float* factors, void* workspace,
+                           size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

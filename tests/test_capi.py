@@ -44,7 +44,8 @@ def test_header_matches_exports_and_binding():
 
 def _wgrad(**kw):
     args = dict(a=1, b=1, B=2, K=4, M=8, N=8, sab=32, lda=8, sbb=32, ldb=8, layout=0, dtype=2,
-                C=1.0, clamp=1.0, cad=None, out_scale=1.0, noise=None, noise_scale=0.0, out=1,
+                C=1.0, clamp=1.0, cad=None, out_scale=1.0, noise=None, noise_scale=0.0, key=None,
+                out=1,
                 ldo=8, odt=2, norms=None, factors=None, flags=0, ws=None, wsb=0, stream=None)
     args.update(kw)
     return _lib.lib().fdp_wgrad_clip(*args.values())
@@ -77,15 +78,15 @@ def test_workspace_queries():
 
 def test_other_validation_codes():
     L = _lib.lib()
-    st = L.fdp_colsum_clip(1, None, 2, 3, 4, 2, 9, 1.0, 1.0, None, 1.0, None, 0.0, 1, 2, None,
-                           None, None, 0, None)
+    st = L.fdp_colsum_clip(1, None, 2, 3, 4, 2, 9, 1.0, 1.0, None, 1.0, None, 0.0, None, 1, 2,
+                           None, None, None, 0, None)
     assert st == 3  # bad norm kind
     st = L.fdp_layernorm_fwd(1, None, None, 4, 8192, 1e-5, 2, 2, 1, None, None, None)
     assert st == 2
     st = L.fdp_layernorm_fwd(1, None, None, 4, 64, 1e-5, 5, 2, 1, None, None, None)
     assert st == 1
     st = L.fdp_layernorm_bwd_clip(1, 1, None, 1, 1, 2, 4, 64, 2, 2, 1.0, 1.0, None, 0.5, None,
-                                  None, 0.0, 1, None, None, None, None, None, 0, None)
+                                  None, 0.0, None, 1, None, None, None, None, None, 0, None)
     assert st == 4
 
 

@@ -138,3 +138,41 @@ def test_wrapped_mlp_trains():
         opt.step()
         losses.append(loss.item())
     assert losses[-1] < 0.8 * losses[0]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=str)
+def test_layers_in_kernel_noise(dtype):
+    """Without a noise_generator the layers draw their noise inside the kernels:
+    dW gets counter blocks [0, O*I/4) of the module's Philox key, db the next
+    ones; LayerNorm's dgamma / dbeta share one key (streams 0 and 1).  The
+    oracle's Philox stream (oracle/philox.py) reproduces every draw."""
+    from oracle import philox as PX
+    torch.manual_seed(3)
+    lin = DPLinear(96, 64, bias=True, C=1.0, noise_multiplier=1.0).to(DEV, dtype)
+    x = torch.randn(4, 16, 96, device=DEV).to(dtype).requires_grad_(True)
+    g = (torch.randn(4, 16, 64, device=DEV) * 0.01).to(dtype)
+    lin(x).backward(g)
+    seed = lin.noise_stream.seed
+    assert seed is not None and lin.noise_stream.offset == (64 * 96) // 4 + 64 // 4
+    zw = torch.tensor(PX.normals(64 * 96, seed, 0).reshape(64, 96))
+    zb = torch.tensor(PX.normals(64, seed, (64 * 96) // 4))
+    ref = O.linear_backward(x.detach(), g, lin.weight.detach(), 1.0, 1.0, 1.0, zw, zb)
+    assert_close(lin.weight.grad, ref["dw"], dtype, "dW")
+    assert_close(lin.bias.grad, ref["db"], dtype, "db")
+
+    ln = DPLayerNorm(256, C=1.0, noise_multiplier=1.0).to(DEV, dtype)
+    xl = torch.randn(4, 8, 256, device=DEV).to(dtype).requires_grad_(True)
+    gl = (torch.randn(4, 8, 256, device=DEV) * 0.01).to(dtype)
+    ln(xl).backward(gl)
+    s2 = ln.noise_stream.seed
+    zgw = torch.tensor(PX.normals(256, s2, 0, stream=0))
+    zgb = torch.tensor(PX.normals(256, s2, 0, stream=1))
+    refl = O.layernorm_bwd_clip(gl, xl.detach(), ln.weight.detach(), ln.eps, C=1.0,
+                                noise_multiplier=1.0, z_w=zgw, z_b=zgb)
+    assert_close(ln.weight.grad, refl["dw"], dtype, "dgamma")
+    assert_close(ln.bias.grad, refl["db"], dtype, "dbeta")
+    # a second step continues the stream instead of repeating it
+    w1 = lin.weight.grad.clone()
+    lin.weight.grad = None
+    lin(x).backward(g)
+    assert not torch.equal(w1, lin.weight.grad)

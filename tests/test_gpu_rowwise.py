@@ -154,3 +154,28 @@ def test_layernorm_bwd_deterministic():
     b = core.layernorm_bwd_clip(g, x, None, mean, rstd, 1.0, 1.0)
     for u, v in zip(a, b):
         assert torch.equal(u, v)
+
+
+def test_colsum_and_layernorm_in_kernel_noise():
+    """Bias / LayerNorm grads with the in-kernel draw: colsum output stream 0,
+    LayerNorm dgamma stream 0 and dbeta stream 1 of the same key."""
+    from oracle import philox as PX
+    key = (0x0123456789ABCDEF, 99)
+    g = randn((4, 33, 770), torch.bfloat16, 30, 0.01)
+    o0 = core.colsum_clip(g, None, 0.5, 1.0, norm="frob", out_scale=0.1, noise_scale=0.5,
+                          out_dtype=torch.float32)
+    o1 = core.colsum_clip(g, None, 0.5, 1.0, norm="frob", out_scale=0.1, noise_scale=0.5,
+                          noise_key=key, out_dtype=torch.float32)
+    z = PX.normals(770, *key)
+    assert np.max(np.abs((o1 - o0).double().cpu().numpy() / 0.5 - z)) < 1e-4
+    x = randn((3, 40, 1024), torch.bfloat16, 31)
+    dy = randn((3, 40, 1024), torch.bfloat16, 32, 0.01)
+    _, mean, rstd = core.layernorm_fwd(x, None, None, 1e-5)
+    _, w0, b0 = core.layernorm_bwd_clip(dy, x, None, mean, rstd, 1.0, 1.0, noise_scale=0.3,
+                                        param_dtype=torch.float32)
+    _, w1, b1 = core.layernorm_bwd_clip(dy, x, None, mean, rstd, 1.0, 1.0, noise_scale=0.3,
+                                        noise_key=key, param_dtype=torch.float32)
+    zw = PX.normals(1024, *key, stream=0)
+    zb = PX.normals(1024, *key, stream=1)
+    assert np.max(np.abs((w1 - w0).double().cpu().numpy() / 0.3 - zw)) < 1e-4
+    assert np.max(np.abs((b1 - b0).double().cpu().numpy() / 0.3 - zb)) < 1e-4

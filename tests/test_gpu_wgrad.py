@@ -120,7 +120,7 @@ def test_wgrad_reused_workspace_stays_clean(shape):
         st = L.fdp_wgrad_clip(a.data_ptr(), b.data_ptr(), B, K, M, N, a.stride(0), a.stride(1),
                               b.stride(0), b.stride(1), _lib.LAYOUT_TN, _lib.FDP_BF16,
                               ctypes.c_float(0.05), ctypes.c_float(1.0), None, ctypes.c_float(1.0),
-                              None, ctypes.c_float(1.0), out.data_ptr(), N, _lib.FDP_F32, None,
+                              None, ctypes.c_float(1.0), None, out.data_ptr(), N, _lib.FDP_F32, None,
                               None, flags, ws.data_ptr(), ws.numel(),
                               _lib.stream_handle(torch.device(DEV)))
         assert st == 0
@@ -290,3 +290,50 @@ def test_wgrad_memory_no_per_sample_materialisation():
     extra = torch.cuda.max_memory_allocated() - base
     assert extra < B * M * N * 2, extra
     del out
+
+
+# ------------------------------------------------------------ in-kernel noise
+from oracle import philox as PX  # noqa: E402
+
+NOISE_KEY = (0x9E3779B97F4A7C15, 12345)
+
+
+@pytest.mark.parametrize("shape,layout,dtype,two_pass", [
+    ((8, 64, 392, 520), "tn", torch.bfloat16, False),    # single pass, ragged tiles
+    ((4, 128, 768, 768), "tn", torch.bfloat16, False),   # single pass, 4 groups
+    ((3, 37, 104, 72), "tn", torch.float16, False),
+    ((3, 300, 2048, 1024), "tn", torch.bfloat16, True),  # streamed two-pass (Gram norms)
+    ((2, 64, 130, 257), "tn", torch.bfloat16, False),    # unaligned rows: generic two-pass
+    ((3, 37, 100, 70), "nn", torch.float32, False),      # generic two-pass, odd N
+    ((16, 16, 256, 256), "tn", torch.float32, True),     # generic, several groups (finalize)
+], ids=lambda v: "x".join(map(str, v)) if isinstance(v, tuple) else str(v))
+def test_wgrad_in_kernel_noise(shape, layout, dtype, two_pass):
+    """z drawn inside the output epilogue equals the oracle's Philox4x32-10 /
+    Box-Muller stream element for element (row-major over [M, N])."""
+    B, K, M, N = shape
+    a, b = make(B, K, M, N, dtype, layout, seed=40)
+    ref, _, _ = O.wgrad_clip(a, b, 0.5, 1.0, layout)
+    kw = dict(layout=layout, out_scale=0.5, out_dtype=torch.float32, two_pass=two_pass, check=True)
+    out0 = core.wgrad_clip(a, b, 0.5, 1.0, noise_scale=0.25, **kw)  # no z: no noise
+    out = core.wgrad_clip(a, b, 0.5, 1.0, noise_scale=0.25, noise_key=NOISE_KEY, **kw)
+    z = PX.normals(M * N, *NOISE_KEY).reshape(M, N)
+    assert_close(out0, 0.5 * ref, dtype, "no noise")
+    got = (out.double() - out0.double()).cpu().numpy() / 0.25
+    assert np.max(np.abs(got - z)) < 1e-4, np.max(np.abs(got - z))
+    # bf16 output: the same draw, rounded once with the clipped sum
+    out16 = core.wgrad_clip(a, b, 0.5, 1.0, noise_scale=0.25, noise_key=NOISE_KEY,
+                            **{**kw, "out_dtype": torch.bfloat16})
+    assert_close(out16, 0.5 * ref + 0.25 * z, torch.bfloat16, "bf16 out with noise")
+
+
+def test_wgrad_noise_key_advances():
+    """Disjoint offsets give independent draws; the same key repeats exactly."""
+    a, b = make(2, 32, 256, 128, torch.bfloat16, "tn", seed=41)
+    f = lambda key: core.wgrad_clip(a, b, 1.0, 1.0, noise_scale=1.0, noise_key=key,
+                                    out_dtype=torch.float32)
+    base = core.wgrad_clip(a, b, 1.0, 1.0, noise_scale=1.0, out_dtype=torch.float32)
+    z1 = (f((7, 0)) - base).cpu().numpy()
+    z2 = (f((7, 256 * 128 // 4)) - base).cpu().numpy()
+    assert torch.equal(f((7, 0)), f((7, 0)))
+    assert abs(np.corrcoef(z1.ravel(), z2.ravel())[0, 1]) < 0.05
+    assert abs(z1.std() - 1) < 0.05

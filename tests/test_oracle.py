@@ -269,3 +269,40 @@ def test_reference_bias_clip_mutates_input():
     g0 = g.clone()
     R.linear_bias_grad_clip(g, 1.0, 1.0)
     assert not torch.equal(g, g0)
+
+
+# ---------------------------------------------------------------- noise stream
+from oracle import philox as PX  # noqa: E402
+
+
+@pytest.mark.parametrize("ctr,key,expect", [
+    ((0, 0, 0, 0), (0, 0), (0x6627e8d5, 0xe169c58d, 0xbc57ac4c, 0x9b00dbd8)),
+    ((0xffffffff,) * 4, (0xffffffff,) * 2, (0x408f276d, 0x41c83b0e, 0xa20bc7c6, 0x6d5451fd)),
+    ((0x243f6a88, 0x85a308d3, 0x13198a2e, 0x03707344), (0xa4093822, 0x299f31d0),
+     (0xd16cfe09, 0x94fdcceb, 0x5001e420, 0x24126ea1)),
+])
+def test_philox_known_answers(ctr, key, expect):
+    """Philox4x32-10 against the Random123 known-answer vectors."""
+    got = PX.philox4x32_10(np.array([ctr], dtype=np.uint32), np.array(key, dtype=np.uint32))
+    assert tuple(int(v) for v in got[0]) == expect
+
+
+def test_noise_stream_statistics():
+    """Moments and tails of N(0,1), no correlation between neighbours or streams,
+    and a different seed / offset / stream gives a different draw."""
+    n = 1 << 18
+    z = PX.normals(n, seed=0x123456789ABCDEF, offset=7)
+    se = 1 / np.sqrt(n)
+    assert abs(z.mean()) < 5 * se
+    assert abs(z.std() - 1) < 5 * se
+    assert abs(np.mean(z ** 3)) < 5 * np.sqrt(15 / n)      # skew 0
+    assert abs(np.mean(z ** 4) - 3) < 5 * np.sqrt(96 / n)  # kurtosis 3
+    assert abs(np.mean(np.abs(z) > 3) - 0.0026998) < 5 * np.sqrt(0.0027 / n)
+    for lag in (1, 2, 3, 4):
+        assert abs(np.corrcoef(z[:-lag], z[lag:])[0, 1]) < 5 * se
+    z1 = PX.normals(n, seed=0x123456789ABCDEF, offset=7, stream=1)
+    assert abs(np.corrcoef(z, z1)[0, 1]) < 5 * se
+    # the same key reproduces; offsets address the stream block-wise
+    assert np.array_equal(z, PX.normals(n, seed=0x123456789ABCDEF, offset=7))
+    assert np.array_equal(z[8:16], PX.normals(8, seed=0x123456789ABCDEF, offset=9))
+    assert not np.allclose(z[:64], PX.normals(64, seed=0x123456789ABCDEE, offset=7))
