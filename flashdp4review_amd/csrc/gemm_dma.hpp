@@ -43,24 +43,29 @@ constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, 32-bit records
 
 __device__ __forceinline__ int swz(int k) { return (k & 3) << 2; }
 
-// Tile geometry: BM x BN outputs, 4 waves in 2 x 2, each (BM/2) x (BN/2);
-// k-tiles of BK rows (a multiple of 16) per LDS stage.
-template <int BM_, int BN_, int BK_ = kBK>
+// Tile geometry: BM x BN outputs, WGM x WGN waves (default 2 x 2), each
+// (BM/WGM) x (BN/WGN); k-tiles of BK rows (a multiple of 16) per LDS stage.
+template <int BM_, int BN_, int BK_ = kBK, int WGM_ = 2, int WGN_ = 2>
 struct Geom {
   static constexpr int BM = BM_;
   static constexpr int BN = BN_;
   static constexpr int BK = BK_;
+  static constexpr int WGM = WGM_;
+  static constexpr int WGN = WGN_;
+  static constexpr int NW = WGM * WGN;    // waves per workgroup
   static constexpr int KS = BK / 16;      // 16-deep MFMA k-steps per k-tile
-  static constexpr int WM = BM / 2;       // wave tile rows
-  static constexpr int WN = BN / 2;       // wave tile columns
+  static constexpr int WM = BM / WGM;     // wave tile rows
+  static constexpr int WN = BN / WGN;     // wave tile columns
   static constexpr int FI = WM / 32;      // 32-row MFMA blocks per wave
   static constexpr int FJ = WN / 32;      // 32-column MFMA blocks per wave
   static constexpr int TILE_A = BK * BM * 2;
   static constexpr int TILE_B = BK * BN * 2;
   static constexpr int STAGE = TILE_A + TILE_B;
-  static constexpr int LOADS_A = TILE_A / (4 * 64 * 16);  // per wave per k-tile
-  static constexpr int LOADS_B = TILE_B / (4 * 64 * 16);
+  static constexpr int LOADS_A = TILE_A / (NW * 64 * 16);  // per wave per k-tile
+  static constexpr int LOADS_B = TILE_B / (NW * 64 * 16);
   static constexpr int LOADS = LOADS_A + LOADS_B;
+  static_assert(LOADS_A * NW * 64 * 16 == TILE_A && LOADS_B * NW * 64 * 16 == TILE_B,
+                "each wave issues whole 1 KB loads");
 };
 
 // One operand's per-thread load state: L buffer loads per k-tile of BK rows.
@@ -215,13 +220,15 @@ __device__ __forceinline__ void wait_vm() {
 }
 // Wait until at most `tiles` k-tiles (L loads each) of this thread's loads are
 // outstanding (stores issued in between only make the wait stronger).
+// (Counts above the 6-bit vmcnt field are clamped: a smaller count only makes
+// the wait stronger.)
 template <int L>
 __device__ __forceinline__ void wait_tiles(int tiles) {
   switch (tiles) {
     case 0: wait_vm<0>(); break;
-    case 1: wait_vm<L>(); break;
-    case 2: wait_vm<2 * L>(); break;
-    default: wait_vm<3 * L>(); break;
+    case 1: wait_vm<(L < 63 ? L : 63)>(); break;
+    case 2: wait_vm<(2 * L < 63 ? 2 * L : 63)>(); break;
+    default: wait_vm<(3 * L < 63 ? 3 * L : 63)>(); break;
   }
 }
 

@@ -261,8 +261,8 @@ Plan make_plan(int64_t B, int64_t K, int64_t M, int64_t N, int cus) {
   pl.off_slots = after_partials;
   pl.off_chunk = pl.off_slots;
   pl.total_fused = 0;
-  if (gp.groups > 0) {
-    pl.off_chunk += gp.groups > 1 ? sizeof(float) * size_t(gp.groups) * pl.tiles * BM * BN : 0;
+  if (gp.chunk > 0) {
+    pl.off_chunk += align_up(sizeof(uint16_t) * size_t(gp.max_nwg) * BM * BN);
     pl.total_fused = pl.off_chunk + (gp.chunk < B ? sizeof(float) * size_t(M) * N : 0);
   }
   pl.total = pl.total_two_pass > pl.total_fused ? pl.total_two_pass : pl.total_fused;

@@ -14,6 +14,8 @@ constexpr int BM = 128;
 constexpr int BN = 128;
 constexpr int NT = 256;
 
+constexpr int kPermMax = 1024;  // workgroups whose order the single-pass launch sets
+
 struct Args {
   const void* a;
   const void* b;
@@ -37,7 +39,7 @@ struct Args {
   unsigned* bar;          // grid barrier arrivals
   unsigned* done;         // workgroups finished (the last one re-zeroes bar / done)
   unsigned* tile_turn;    // [tiles] hand-over tickets for tiles shared by workgroups
-  float* tile_acc;        // [tiles, BM*BN] fp32 running sums of shared tiles
+  float* tile_acc;        // [nwg, BM*BN] bf16 per-group tile sums (row-major)
   int* err;               // set when a bounded wait gives up
   unsigned spin_limit;    // polls before a grid wait gives up
   float C, clamp;
@@ -48,6 +50,8 @@ struct Args {
   int64_t chunk_b0, chunk_nb;
   int chunk_first, chunk_last;
   float* chunk_acc;       // [M, N] fp32 running sum carried between chunks
+  int gq, gr;             // groups per tile (gr tiles have gq + 1)
+  uint16_t perm[kPermMax];  // hardware workgroup -> work list index
 };
 
 // ------------------------------------------------------------------ 16-bit
@@ -387,6 +391,10 @@ __device__ __forceinline__ void tile_coords(const Args& p, int tile, int64_t& m0
 // (kSpinLimit polls); on expiry err is set and the kernel runs to completion,
 // so no wave is ever left spinning.
 constexpr unsigned kSpinLimit = 1u << 22;
+// Poll interval of every inter-workgroup wait: s_sleep 16 (about 1000 clocks).
+// All waiting workgroups poll one word; polling it faster congests the L2
+// channel that holds it and slows the workgroups still computing.
+constexpr int kPollSleep = 16;
 constexpr int kXcds = 8;
 
 
@@ -394,16 +402,23 @@ constexpr int kXcds = 8;
 // (in every thread) whether this workgroup's results must be poisoned: its own
 // wait expired, or an earlier workgroup's did (that one set *err before this
 // one could arrive).
+//
+// quiet_until (a wall_clock64() value, 0 = none): before the first poll the
+// waiting wave sleeps without touching memory until then.  Coherent polling
+// loads stall the vector memory pipeline of their CU, so a workgroup that
+// arrives early would otherwise slow the other workgroup still computing on
+// its CU; callers pass an estimate of when the slowest workgroup arrives.
 __device__ inline bool grid_barrier(unsigned* bar, unsigned n, int* err, unsigned limit,
-                                    int* flag) {
+                                    int* flag, uint64_t quiet_until = 0) {
   wait_stores();
   __syncthreads();
   if (threadIdx.x == 0) {
     __hip_atomic_fetch_add(bar, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    while (wall_clock64() < quiet_until) __builtin_amdgcn_s_sleep(32);
     unsigned spins = 0;
     int bad = 0;
     while (__hip_atomic_load(bar, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < n) {
-      __builtin_amdgcn_s_sleep(1);
+      __builtin_amdgcn_s_sleep(kPollSleep);
       if (++spins > limit) {
         atomicOr(err, 1);
         bad = 1;
@@ -427,7 +442,7 @@ __device__ __forceinline__ int logical_wg(int hw, int nwg) {
 template <bool PACK>
 struct Held;
 template <>
-struct Held<true> {  // 64 fp32 accumulators -> 32 bf16 pairs parked in AGPRs
+struct Held<true> {  // 64 fp32 accumulators -> 32 bf16 pairs (RNE)
   uint32_t v[2][2][8];
   __device__ __forceinline__ void put(const f32x16 (&acc)[2][2]) {
 #pragma unroll
@@ -435,11 +450,9 @@ struct Held<true> {  // 64 fp32 accumulators -> 32 bf16 pairs parked in AGPRs
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          const uint32_t w = uint32_t(BF16::from_f32(acc[i][j][2 * q])) |
-                             (uint32_t(BF16::from_f32(acc[i][j][2 * q + 1])) << 16);
-          asm volatile("v_accvgpr_write_b32 %0, %1" : "=a"(v[i][j][q]) : "v"(w));
-        }
+        for (int q = 0; q < 8; ++q)
+          v[i][j][q] = uint32_t(BF16::from_f32(acc[i][j][2 * q])) |
+                       (uint32_t(BF16::from_f32(acc[i][j][2 * q + 1])) << 16);
   }
   __device__ __forceinline__ void add_to(f32x16 (&tot)[2][2], float c) const {
 #pragma unroll
@@ -448,8 +461,7 @@ struct Held<true> {  // 64 fp32 accumulators -> 32 bf16 pairs parked in AGPRs
       for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
-          uint32_t w;
-          asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(w) : "a"(v[i][j][q]));
+          const uint32_t w = v[i][j][q];
           tot[i][j][2 * q] += c * __uint_as_float(w << 16);
           tot[i][j][2 * q + 1] += c * __uint_as_float(w & 0xffff0000u);
         }
@@ -474,11 +486,6 @@ struct Held<false> {
   }
 };
 
-// Tile-local fp32 buffer access in the accumulator layout (coalesced along n).
-__device__ __forceinline__ int tl_index(int wm, int wn, int i, int j, int lane, int r) {
-  return acc_row(wm, i, lane, r) * BN + acc_col(wn, j, lane);
-}
-
 #ifdef FDP_PHASE_TIMING
 extern __device__ unsigned long long fdp_phase_ts[1024 * 16];
 #define FDP_TS(slot)                                                  \
@@ -492,48 +499,48 @@ extern __device__ unsigned long long fdp_phase_ts[1024 * 16];
   } while (0)
 #endif
 
+// ------------------------------------------------------ single-pass work map
+// A launch covers samples [chunk_b0, chunk_b0 + chunk_nb) with W workgroups.
+// The workgroups form a tile-major list: tiles [0, gr) have gq + 1 groups,
+// tiles [gr, tiles) have gq groups, and group g of a tile with ng groups holds
+// samples chunk_b0 + [g*nb/ng, (g+1)*nb/ng) (nb = chunk_nb): contiguous ranges
+// whose sizes differ by at most one.
+struct Assign {
+  int tile, g, ng;  // tile, group index, groups of the tile
+  int first;        // list index of the tile's group 0 (its slots are first .. first+ng-1)
+  int b0, nb;       // first sample, number of samples
+};
 
-// 16-byte coherent (sc1) stores/loads for the per-group slot exchange.  A slot
-// is one 128x128 fp32 tile kept in "thread-major" order: float4 q (0..15) of
-// thread t sits at byte (q*256 + t)*16, which makes every wave instruction one
-// contiguous 1 KB access.
-
-__device__ inline void slot_store(float* slot, const f32x16 (&v)[2][2]) {
-  const __amdgpu_buffer_rsrc_t r =
-      __builtin_amdgcn_make_buffer_rsrc(slot, static_cast<short>(0), BM * BN * 4, dma::kRsrcWord3);
-#pragma unroll
-  for (int a = 0; a < 2; ++a)
-#pragma unroll
-    for (int c = 0; c < 2; ++c)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int idx = (a * 2 + c) * 4 + q;
-        const f32x4 x = {v[a][c][4 * q], v[a][c][4 * q + 1], v[a][c][4 * q + 2], v[a][c][4 * q + 3]};
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), r,
-                                               (idx * NT + threadIdx.x) * 16, 0, kCoherent);
-      }
-}
-__device__ inline void slot_add(const float* slot, f32x16 (&v)[2][2]) {
-  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<float*>(slot), static_cast<short>(0), BM * BN * 4, dma::kRsrcWord3);
-#pragma unroll
-  for (int a = 0; a < 2; ++a)
-#pragma unroll
-    for (int c = 0; c < 2; ++c)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int idx = (a * 2 + c) * 4 + q;
-        const f32x4 x = __builtin_bit_cast(
-            f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (idx * NT + threadIdx.x) * 16, 0,
-                                                         kCoherent));
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[a][c][4 * q + e] += x[e];
-      }
+__device__ __forceinline__ Assign assign_of(const Args& p, int j) {
+  Assign a;
+  const int q = p.gq, big = p.gr * (q + 1);
+  if (j < big) {
+    a.tile = j / (q + 1);
+    a.g = j - a.tile * (q + 1);
+    a.ng = q + 1;
+    a.first = a.tile * (q + 1);
+  } else {
+    const int jj = j - big;
+    a.tile = p.gr + jj / q;
+    a.g = jj - (a.tile - p.gr) * q;
+    a.ng = q;
+    a.first = big + (a.tile - p.gr) * q;
+  }
+  const int nb = static_cast<int>(p.chunk_nb);
+  const int lo = (a.g * nb) / a.ng, hi = ((a.g + 1) * nb) / a.ng;
+  a.b0 = static_cast<int>(p.chunk_b0) + lo;
+  a.nb = hi - lo;
+  return a;
 }
 
-// out[m, n] = out_scale * tot + noise_scale * noise for one 128x128 tile, staged
-// through LDS (rows 32q .. 32q+31 in quarter q, 16 KB each, fp32) so that the
-// global stores and noise loads are 16-byte row chunks.
+// Hardware workgroup -> list index: perm[] (host-made, see order_workgroups)
+// when the grid has at most kPermMax workgroups, else the identity.
+__device__ __forceinline__ int list_index(const Args& p, int hw) {
+  return p.nwg <= kPermMax ? static_cast<int>(p.perm[hw]) : hw;
+}
+
+// out rows of a 128x128 tile staged in LDS as four 32-row quarters (fp32,
+// row-major, 16 KB each): row r, column c at quarter r/32, (r%32)*128 + c.
 __device__ __forceinline__ float* quarter(float* const (&q)[4], int i) {
   switch (i) {
     case 0: return q[0];
@@ -542,183 +549,153 @@ __device__ __forceinline__ float* quarter(float* const (&q)[4], int i) {
     default: return q[3];
   }
 }
+__device__ __forceinline__ float* staged_row(float* const (&q)[4], int r) {
+  return quarter(q, r >> 5) + (r & 31) * BN;
+}
 
+// Final values of 8 consecutive outputs (row m, columns n .. n+7 of the
+// problem): the chunk carried from earlier launches is added; the result is
+// carried on (not the last launch) or written as out_scale * v + noise.
 template <class OT>
-__device__ inline void store_tile_staged(const Args& p, int64_t m0, int64_t n0,
-                                         const f32x16 (&tot)[2][2], float* const (&q4)[4]) {
+__device__ inline void finish_chunk(const Args& p, int64_t m, int64_t n, float (&v)[8]) {
   using S = typename OT::storage;
-  constexpr int E = 16 / sizeof(S);  // elements per 16-byte chunk
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+  const bool whole = n + 8 <= p.N;
+  const bool cvec = whole && (p.N % 4 == 0);
+  if (!p.chunk_first) {
+    const float* src = p.chunk_acc + m * p.N + n;
+    if (cvec) {
+      const float4 c0 = reinterpret_cast<const float4*>(src)[0];
+      const float4 c1 = reinterpret_cast<const float4*>(src)[1];
+      v[0] += c0.x; v[1] += c0.y; v[2] += c0.z; v[3] += c0.w;
+      v[4] += c1.x; v[5] += c1.y; v[6] += c1.z; v[7] += c1.w;
+    } else {
 #pragma unroll
-  for (int a = 0; a < 2; ++a) {
-    float* qd = quarter(q4, wm / 32 + a);
-#pragma unroll
-    for (int c = 0; c < 2; ++c)
-#pragma unroll
-      for (int r = 0; r < 16; ++r)
-        qd[(acc_row(0, 0, lane, r)) * BN + acc_col(wn, c, lane)] = tot[a][c][r];
+      for (int e = 0; e < 8; ++e)
+        if (n + e < p.N) v[e] += src[e];
+    }
   }
-  __syncthreads();
-  S* out = static_cast<S*>(p.out);
-  const bool vec = (reinterpret_cast<uintptr_t>(out) % 16 == 0) && (p.ldo % E == 0);
-  const NoiseSrc nz = p.noise;  // a value copy: no address of the kernel argument is taken
-  const int zvec = noise_chunks<E>(nz, p.N);
-  constexpr int CPR = BN / E;  // chunks per tile row
-#pragma unroll 1
-  for (int q = threadIdx.x; q < BM * CPR; q += NT) {
-    const int row = q / CPR, col = (q % CPR) * E;
-    const int64_t m = m0 + row, n = n0 + col;
-    if (m >= p.M || n >= p.N) continue;
-    const float* src = quarter(q4, row >> 5) + (row & 31) * BN + col;
-    float v[E];
+  if (!p.chunk_last) {
+    float* dst = p.chunk_acc + m * p.N + n;
+    if (cvec) {
+      reinterpret_cast<float4*>(dst)[0] = make_float4(v[0], v[1], v[2], v[3]);
+      reinterpret_cast<float4*>(dst)[1] = make_float4(v[4], v[5], v[6], v[7]);
+    } else {
 #pragma unroll
-    for (int e = 0; e < E; ++e) v[e] = src[e] * p.out_scale;
-    if (vec && n + E <= p.N) {
-      add_noise_chunk<OT, E>(nz, zvec, m * p.N + n, p.noise_scale, v);
+      for (int e = 0; e < 8; ++e)
+        if (n + e < p.N) dst[e] = v[e];
+    }
+    return;
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] *= p.out_scale;
+  const NoiseSrc nz = p.noise;  // a value copy: no address of the kernel argument is taken
+  if (nz.on()) {
+    if (whole && nz.z == nullptr && p.N % 4 == 0) {
+      float z[8];
+      nz.run(m * p.N + n, z);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] += p.noise_scale * z[e];
+    } else if (whole && nz.z == nullptr) {
+      float z[8];
+      nz.window(m * p.N + n, z);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] += p.noise_scale * z[e];
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (n + e < p.N) v[e] += p.noise_scale * nz.at(m * p.N + n + e);
+    }
+  }
+  S* out = static_cast<S*>(p.out) + m * p.ldo + n;
+  constexpr int E = 16 / sizeof(S);  // elements per 16-byte store
+  const bool ovec = whole && reinterpret_cast<uintptr_t>(out) % 16 == 0;
+  if (ovec) {
+#pragma unroll
+    for (int k = 0; k < 8 / E; ++k) {
       uint4 o;
       S* os = reinterpret_cast<S*>(&o);
 #pragma unroll
-      for (int e = 0; e < E; ++e) os[e] = OT::from_f32(v[e]);
-      *reinterpret_cast<uint4*>(out + m * p.ldo + n) = o;
-    } else {
-      // right edge or unaligned rows: element stores, noise from whole blocks
-      if (nz.z != nullptr) {
-      #pragma unroll
-        for (int e = 0; e < E; ++e)
-          if (n + e < p.N) v[e] += p.noise_scale * nz.at(m * p.N + n + e);
-      } else if (nz.draw) {
-        float z[E];
-        nz.window(m * p.N + n, z);
-      #pragma unroll
-        for (int e = 0; e < E; ++e) v[e] += p.noise_scale * z[e];
-      }
-      #pragma unroll
-      for (int e = 0; e < E; ++e)
-        if (n + e < p.N) out[m * p.ldo + n + e] = OT::from_f32(v[e]);
+      for (int e = 0; e < E; ++e) os[e] = OT::from_f32(v[k * E + e]);
+      reinterpret_cast<uint4*>(out)[k] = o;
     }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (n + e < p.N) out[e] = OT::from_f32(v[e]);
   }
 }
 
-// ------------------------------------------------------ single pass
-// Work units of one workgroup: unit j is the 128x128 product of one tile and
-// one sample.  The grid is groups x tiles; workgroup (g, tile) holds the tile's
-// products of samples chunk_b0 + g*spg + j.  Groups of one tile are combined
-// through slots after the grid barrier.
-struct UnitMap {
-  int tile, nb;
-  int64_t b0;
-  __device__ __forceinline__ int64_t sample_of(int j) const { return b0 + j; }
-};
-
-__device__ inline UnitMap unit_map(const Args& p, int lw, int tiles) {
-  UnitMap u{};
-  u.tile = lw % tiles;
-  const int64_t bend = p.chunk_b0 + p.chunk_nb;
-  u.b0 = p.chunk_b0 + int64_t(lw / tiles) * p.spg;
-  u.nb = static_cast<int>((u.b0 + p.spg < bend ? u.b0 + p.spg : bend) - u.b0);
-  if (u.nb < 0) u.nb = 0;
-  return u;
+// Exchange slot of list entry j: a 128x128 bf16 tile, row-major (the
+// group's clipped sum, rounded once to bf16 for the exchange).
+__device__ __forceinline__ const float* slot_of(const Args& p, int j) {
+  return reinterpret_cast<const float*>(reinterpret_cast<const uint16_t*>(p.tile_acc) +
+                                        int64_t(j) * (BM * BN));
 }
 
-// The tile's sum for this launch: added to the running sum of earlier launches
-// and kept for later ones (chunk_acc), or written out on the last launch.
-__device__ inline void finish_tile(const Args& p, int64_t m0, int64_t n0, f32x16 (&acc)[2][2],
-                                   char* st0, char* st1) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
-  if (!p.chunk_first || !p.chunk_last) {
-    // element (a, c, r) sits at row m0 + wm + 32a + 8(r/4) + r%4 + 4(lane/32)
-    // and column n0 + wn + 32c + lane%32: a uniform row base plus a 32-bit
-    // per-lane offset, so that no 64-bit address is kept per element.
-    const int hi = 4 * (lane >> 5);
-    const uint32_t loff = static_cast<uint32_t>(hi * p.N + (lane & 31));
-    if (m0 + BM <= p.M && n0 + BN <= p.N) {
-      // interior tile: straight-line code, every load in flight at once
-      if (!p.chunk_first) {
+// Rows [r0, r1) of the tile: the staged sum of this group plus the slots of
+// the tile's other groups (in group order; a fixed order per row), finished.
+template <class OT>
+__device__ inline void finish_rows(const Args& p, const Assign& as, int64_t m0, int64_t n0, int r0,
+                                   int r1, float* const (&q4)[4], bool poisoned) {
+  const int nchunks = (r1 - r0) * (BN / 8);
+  for (int c = threadIdx.x; c < nchunks; c += NT) {
+    const int r = r0 + c / (BN / 8), col = (c % (BN / 8)) * 8;
+    const int64_t m = m0 + r, n = n0 + col;
+    if (m >= p.M || n >= p.N) continue;
+    const float* own = staged_row(q4, r) + col;
+    float v[8];
 #pragma unroll
-        for (int a = 0; a < 2; ++a) {
-          float v[2][16];
+    for (int e = 0; e < 8; ++e) v[e] = own[e];
+    for (int gg = 0; gg < as.ng; ++gg) {
+      if (gg == as.g) continue;
+      const CoherentSpan sl(slot_of(p, as.first + gg), BM * BN * 2);
+      const u32x4 w = __builtin_bit_cast(u32x4, sl.load4(static_cast<uint32_t>((r * BN + col) * 2)));
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const float* rp = p.chunk_acc + ((m0 + wm + 32 * a + 8 * (r >> 2) + (r & 3)) * p.N + n0 + wn) + loff;
-#pragma unroll
-            for (int c = 0; c < 2; ++c) v[c][r] = rp[32 * c];
-          }
-#pragma unroll
-          for (int c = 0; c < 2; ++c)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[a][c][r] += v[c][r];
-        }
+      for (int e = 0; e < 4; ++e) {
+        v[2 * e] += __uint_as_float(w[e] << 16);
+        v[2 * e + 1] += __uint_as_float(w[e] & 0xffff0000u);
       }
-      if (!p.chunk_last) {
-#pragma unroll
-        for (int a = 0; a < 2; ++a)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            float* rp = p.chunk_acc + ((m0 + wm + 32 * a + 8 * (r >> 2) + (r & 3)) * p.N + n0 + wn) + loff;
-#pragma unroll
-            for (int c = 0; c < 2; ++c) rp[32 * c] = acc[a][c][r];
-          }
-      }
-    } else {
-#pragma unroll
-      for (int a = 0; a < 2; ++a)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int64_t mrow = m0 + wm + 32 * a + 8 * (r >> 2) + (r & 3);
-          if (mrow + hi >= p.M) continue;
-          float* rp = p.chunk_acc + (mrow * p.N + n0 + wn);
-#pragma unroll
-          for (int c = 0; c < 2; ++c) {
-            if (n0 + wn + 32 * c + (lane & 31) >= p.N) continue;
-            float* e = rp + loff + 32 * c;
-            if (!p.chunk_first) acc[a][c][r] += *e;
-            if (!p.chunk_last) *e = acc[a][c][r];
-          }
-        }
     }
-  }
-  if (p.chunk_last) {
-    __syncthreads();  // the staging area may still be read for a previous tile
-    float* const q4[4] = {reinterpret_cast<float*>(st0), reinterpret_cast<float*>(st0) + 4096,
-                          reinterpret_cast<float*>(st1), reinterpret_cast<float*>(st1) + 4096};
-    if (p.out_dtype == FDP_BF16) store_tile_staged<BF16>(p, m0, n0, acc, q4);
-    else if (p.out_dtype == FDP_F16) store_tile_staged<F16>(p, m0, n0, acc, q4);
-    else store_tile_staged<F32>(p, m0, n0, acc, q4);
-    FDP_TS(12);
+    if (poisoned) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = __builtin_nanf("");
+    }
+    finish_chunk<OT>(p, m, n, v);
   }
 }
 
 // Workgroups of the grid run their nb products, keeping the finished ones
-// packed in AGPRs and the last one live in its accumulators; each product's
-// sum of squares goes to partials[sample, tile].  After the grid barrier every
-// workgroup knows the norms of its samples and forms sum_b c_b G_b for its
-// tile (fixed order: deterministic); the groups of a tile are then combined in
-// group order by the last group to arrive, and the result is written (or
-// carried to the next launch in chunk_acc).
+// packed in registers and the last one live in its accumulators; each
+// product's sum of squares goes to partials[sample, tile].  After the grid
+// barrier every workgroup knows the norms of its samples and forms
+// sum_b c_b G_b for its tile (fixed order: deterministic).  The groups of a
+// tile then exchange their sums: group g publishes the rows the other groups
+// finish, waits for the tile's other groups, and finishes rows
+// [g*128/ng, (g+1)*128/ng) itself (output, or the running sum carried to the
+// next launch in chunk_acc).
 constexpr int kStages = 2;  // LDS ring depth of the single-pass kernel (64-deep k-tiles)
 
 template <class DT, int U>
 __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
   using G = dma::Geom<BM, BN, 64>;
   static_assert(kStages * G::STAGE == BM * BN * 4, "the output staging reuses the ring");
+  static_assert(U <= NT / kWave, "one wavefront per held sample forms its factor");
   __shared__ __attribute__((aligned(16))) char st0[G::STAGE];
   __shared__ __attribute__((aligned(16))) char st1[G::STAGE];
   __shared__ float red[NT / kWave];
   __shared__ float fac[U];
-  __shared__ int is_last;
+  __shared__ int flag;
   const dma::Stages stages{{(FDP_LDS char*)(st0), (FDP_LDS char*)(st1),
                             (FDP_LDS char*)(st0), (FDP_LDS char*)(st1)}};
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
   const int tiles = p.tiles_m * p.tiles_n;
-  const int lw = logical_wg(blockIdx.x, p.nwg);
-  const UnitMap um = unit_map(p, lw, tiles);
-  const int nb = um.nb;
+  const Assign as = assign_of(p, list_index(p, blockIdx.x));
+  const int nb = as.nb;
   const int nk = static_cast<int>((p.K + G::BK - 1) / G::BK);
   dma::FragOffsets<G> fo;
   fo.init(wm, wn);
+  const uint64_t t_begin = wall_clock64();
   FDP_TS(0);
 
   // ---- phase 1: the nb products run as one stream of nb*nk k-tiles through
@@ -733,14 +710,14 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
   dma::Job<G> job;  // loads of k-tile ik of unit iu, the next one to issue
   int iu = 0, ik = 0;
   int64_t m0, n0;
-  tile_coords(p, um.tile, m0, n0);
-  if (nq > 0) job.init(pa + um.b0 * p.sab, p.lda, pb + um.b0 * p.sbb, p.ldb, p.K, m0, n0);
+  tile_coords(p, as.tile, m0, n0);
+  if (nq > 0) job.init(pa + as.b0 * p.sab, p.lda, pb + as.b0 * p.sbb, p.ldb, p.K, m0, n0);
   auto issue_next = [&](FDP_LDS char* stage) {
     job.issue(stage, ik);
     if (++ik == nk) {
       ik = 0;
       if (++iu < nb) {
-        const int64_t b = um.sample_of(iu);
+        const int64_t b = as.b0 + iu;
         job.retarget(pa + b * p.sab, p.lda, pb + b * p.sbb, p.ldb, p.K);
       }
     }
@@ -779,7 +756,7 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
           if (lane == 0) red[wave] = sq;
           __syncthreads();
           if (threadIdx.x == 0)
-            st_coherent(p.partials + um.sample_of(cu) * tiles + um.tile,
+            st_coherent(p.partials + (as.b0 + cu) * tiles + as.tile,
                         (red[0] + red[1]) + (red[2] + red[3]));
           FDP_TS(1 + cu);
           if (cu + 1 < nb) {  // park it and start the next product
@@ -796,45 +773,48 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
   }
   dma::barrier();  // every wave is done reading the ring
 
-  // The tile's hand-over ticket starts at zero in every launch: group 0 clears
+  // The tile's exchange ticket starts at zero in every launch: group 0 clears
   // it before the grid barrier, every ticket is taken after it.  (A ticket
   // word may hold another problem's data: workspace layouts differ by shape.)
-  if (threadIdx.x == 0 && p.groups > 1 && lw / tiles == 0)
-    __hip_atomic_store(p.tile_turn + um.tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x == 0 && as.ng > 1 && as.g == 0)
+    __hip_atomic_store(p.tile_turn + as.tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
   // A wait that expired (only possible when the grid was not resident at once)
   // poisons this workgroup's results with NaN rather than leave them silently
   // wrong; the status word reports it.
-  const bool poisoned = grid_barrier(p.bar, unsigned(p.nwg), p.err, p.spin_limit, &is_last);
+  // Workgroups with fewer products than the launch's most loaded ones wait
+  // quietly for about half of the time those need for the rest of theirs
+  // (measured on this workgroup's own products; a lone workgroup runs faster
+  // than two sharing a CU).
+  uint64_t quiet = 0;
+  if (nb > 0 && nb < U) {
+    const uint64_t now = wall_clock64();
+    quiet = now + (now - t_begin) * uint64_t(U - nb) / uint64_t(2 * nb);
+  }
+  bool poisoned = grid_barrier(p.bar, unsigned(p.nwg), p.err, p.spin_limit, &flag, quiet);
   FDP_TS(9);
 
-  // ---- clip factors of this workgroup's samples: all partials in one sweep
-  float C = p.C, clamp = p.clamp;
-  if (p.clip_args_dev != nullptr) {
-    C = p.clip_args_dev[0];
-    clamp = p.clip_args_dev[1];
-  }
-  float ps[U];
-#pragma unroll
-  for (int i = 0; i < U; ++i) {
-    ps[i] = 0.f;
-    if (i < nb)
-      for (int t = threadIdx.x; t < tiles; t += NT)
-        ps[i] += ld_coherent(p.partials + (um.b0 + i) * tiles + t);
-  }
-  const bool stats_owner = nb > 0 && um.tile == 0;  // one writer per sample
-#pragma unroll
-  for (int i = 0; i < U; ++i) {
-    const float s = wave_sum(ps[i]);
-    if (lane == 0) red[wave] = s;
-    __syncthreads();
-    if (threadIdx.x == 0 && i < nb) {
-      const float n = poisoned ? __builtin_nanf("") : sqrtf((red[0] + red[1]) + (red[2] + red[3]));
-      const float cf = poisoned ? n : clip_factor(n, C, clamp);
-      fac[i] = cf;
-      if (stats_owner) {
-        if (p.norms_out) p.norms_out[um.b0 + i] = n;
-        if (p.factors_out) p.factors_out[um.b0 + i] = cf;
+  // ---- clip factors of this workgroup's samples: wavefront i sums the
+  // partials of sample b0 + i in a fixed order
+  {
+    float C = p.C, clamp = p.clamp;
+    if (p.clip_args_dev != nullptr) {
+      C = p.clip_args_dev[0];
+      clamp = p.clip_args_dev[1];
+    }
+    if (wave < nb) {
+      const float* part = p.partials + int64_t(as.b0 + wave) * tiles;
+      float s = 0.f;
+      for (int t = lane; t < tiles; t += kWave) s += ld_coherent(part + t);
+      s = wave_sum(s);
+      if (lane == 0) {
+        const float n = poisoned ? __builtin_nanf("") : sqrtf(s);
+        const float cf = poisoned ? n : clip_factor(n, C, clamp);
+        fac[wave] = cf;
+        if (as.tile == 0) {  // one writer per sample
+          if (p.norms_out) p.norms_out[as.b0 + wave] = n;
+          if (p.factors_out) p.factors_out[as.b0 + wave] = cf;
+        }
       }
     }
     __syncthreads();
@@ -857,40 +837,77 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
 #pragma unroll
   for (int j = 0; j < U - 1; ++j)
     if (j < nb - 1) held[j].add_to(acc, fac[j]);
+  FDP_TS(4);
 
-  // combine the groups of this tile: the last to arrive sums the slots
-  const int ngroups = p.groups;
-  bool owner = true;
-  if (ngroups > 1) {
-    const int g = lw / tiles;
-    slot_store(p.tile_acc + (int64_t(g) * tiles + um.tile) * (BM * BN), acc);
+  // stage the group's sum in LDS, row-major (the ring is free)
+  float* const q4[4] = {reinterpret_cast<float*>(st0), reinterpret_cast<float*>(st0) + 4096,
+                        reinterpret_cast<float*>(st1), reinterpret_cast<float*>(st1) + 4096};
+#pragma unroll
+  for (int a = 0; a < 2; ++a) {
+    float* qd = quarter(q4, wm / 32 + a);
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) qd[acc_row(0, 0, lane, r) * BN + acc_col(wn, c, lane)] = acc[a][c][r];
+  }
+  __syncthreads();
+  FDP_TS(5);
+  const int r0 = (as.g * BM) / as.ng, r1 = ((as.g + 1) * BM) / as.ng;
+  if (as.ng > 1) {
+    // publish the rows the other groups finish (row-major slot), then wait
+    // until every group of the tile has published
+    const uint64_t t_pub = wall_clock64();
+    const CoherentSpan mine(slot_of(p, as.first + as.g), BM * BN * 2);
+    for (int c = threadIdx.x; c < BM * (BN / 8); c += NT) {
+      const int r = c / (BN / 8), col = (c % (BN / 8)) * 8;
+      if (r >= r0 && r < r1) continue;
+      const float* src = staged_row(q4, r) + col;
+      u32x4 w;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        w[e] = uint32_t(BF16::from_f32(src[2 * e])) | (uint32_t(BF16::from_f32(src[2 * e + 1])) << 16);
+      mine.store4(static_cast<uint32_t>((r * BN + col) * 2), __builtin_bit_cast(f32x4, w));
+    }
     wait_stores();
     __syncthreads();
+    FDP_TS(6);
     if (threadIdx.x == 0) {
-      const unsigned old = __hip_atomic_fetch_add(p.tile_turn + um.tile, 1u, __ATOMIC_RELAXED,
-                                                  __HIP_MEMORY_SCOPE_AGENT);
-      is_last = old == unsigned(ngroups - 1);
-      // every group has taken its ticket: leave the counter zeroed
-      if (is_last)
-        __hip_atomic_store(p.tile_turn + um.tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_fetch_add(p.tile_turn + as.tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      // the tile's other groups started publishing together with this one:
+      // stay off the memory pipeline for a fraction of this group's own time
+      const uint64_t now = wall_clock64();
+      const uint64_t quiet_until = now + (now - t_pub) / 2;
+      while (wall_clock64() < quiet_until) __builtin_amdgcn_s_sleep(8);
+      unsigned spins = 0;
+      int bad = 0;
+      while (__hip_atomic_load(p.tile_turn + as.tile, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
+             unsigned(as.ng)) {
+        __builtin_amdgcn_s_sleep(kPollSleep);
+        if (++spins > p.spin_limit) {
+          atomicOr(p.err, 1);
+          bad = 1;
+          break;
+        }
+      }
+      flag = bad;
     }
     __syncthreads();
-    FDP_TS(10);
-    owner = is_last != 0;
-    if (owner) {
-      zero(acc);
-      for (int gg = 0; gg < ngroups; ++gg)
-        slot_add(p.tile_acc + (int64_t(gg) * tiles + um.tile) * (BM * BN), acc);
-    }
+    poisoned = poisoned || flag != 0;
   }
-  FDP_TS(11);
-  if (owner) finish_tile(p, m0, n0, acc, st0, st1);
+  FDP_TS(10);
+  if (p.out_dtype == FDP_BF16) finish_rows<BF16>(p, as, m0, n0, r0, r1, q4, poisoned);
+  else if (p.out_dtype == FDP_F16) finish_rows<F16>(p, as, m0, n0, r0, r1, q4, poisoned);
+  else finish_rows<F32>(p, as, m0, n0, r0, r1, q4, poisoned);
+  FDP_TS(12);
   // ---- leave the control words zeroed for the next launch on this
   // workspace: every workgroup has passed the barrier once `done` reaches nwg.
   if (threadIdx.x == 0) {
     const unsigned old =
         __hip_atomic_fetch_add(p.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (old == unsigned(p.nwg - 1)) {
+      // every workgroup is past its ticket wait: zero the tickets too
+      for (int t = 0; t < tiles; ++t)
+        __hip_atomic_store(p.tile_turn + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(p.bar, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(p.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -907,29 +924,91 @@ __global__ __launch_bounds__(NT) void clear_words_kernel(unsigned* p, int64_t n)
 // ---------------------------------------------------------- single-pass launch
 using KernelFn = void (*)(Args);
 constexpr size_t kWsHead = 256;   // err / barrier words at the head of the workspace
-constexpr int kGroupUnits = 3;    // samples per group held by one workgroup
+constexpr int kGroupUnits = 4;    // samples held by one workgroup at most
 
-// Single-pass geometry for B samples over `tiles` 128x128 tiles on `slots`
-// co-resident workgroups: `groups` groups of `spg` samples per launch, units =
-// products held by one workgroup (the kernel instance).  groups == 0: more
-// tiles than slots, no single pass (the streamed two-pass schedule is used).
+// Single-pass schedule for B samples over `tiles` 128x128 tiles on `slots`
+// co-resident workgroups (2 per CU).  A launch covers `chunk` samples (the
+// last one fewer) with at most kGroupUnits samples per workgroup; its grid has
+// min(slots, tiles * chunk) workgroups.  chunk == 0: more tiles than slots,
+// no single pass (the streamed two-pass schedule is used).
 struct GroupPlan {
-  int groups, spg, units, nwg;
   int64_t chunk;  // samples per launch
+  int max_nwg;    // workgroups of the largest launch
 };
 inline GroupPlan group_plan(int64_t B, int tiles, int slots) {
   GroupPlan g{};
-  if (tiles > slots) return g;  // groups == 0
-  int64_t G = slots / tiles;
-  if (G > B) G = B;
-  const int64_t per = (B + G - 1) / G;
-  g.spg = static_cast<int>(per < kGroupUnits ? per : kGroupUnits);
-  // fewest groups that still cover the chunk with spg samples each
-  g.chunk = G * g.spg < B ? G * g.spg : B;
-  g.groups = static_cast<int>((g.chunk + g.spg - 1) / g.spg);
-  g.units = g.spg;
-  g.nwg = g.groups * tiles;
+  if (tiles > slots) return g;
+  const int64_t gcap = slots / tiles;  // groups per tile that fit the grid
+  g.chunk = gcap * kGroupUnits < B ? gcap * kGroupUnits : B;
+  const int64_t w = int64_t(tiles) * g.chunk;
+  g.max_nwg = static_cast<int>(w < slots ? w : slots);
   return g;
+}
+
+// Grid of one launch over nb samples: W workgroups, gq groups per tile (gr
+// tiles have one more), at most `units` samples per workgroup.
+struct LaunchShape {
+  int nwg, gq, gr, units;
+};
+inline LaunchShape launch_shape(int64_t nb, int tiles, int slots) {
+  LaunchShape l{};
+  const int64_t w = int64_t(tiles) * nb < slots ? int64_t(tiles) * nb : slots;
+  l.nwg = static_cast<int>(w);
+  l.gq = static_cast<int>(w / tiles);
+  l.gr = static_cast<int>(w % tiles);
+  l.units = static_cast<int>((nb + l.gq - 1) / l.gq);
+  return l;
+}
+
+// Hardware workgroup -> work list index.  Workgroups are dealt round-robin
+// to the 8 XCDs, and on an otherwise idle device workgroups w and w + CUs
+// share a CU.  The list entries are sorted by (first sample, tile) and cut
+// into 8 contiguous ranges, one per XCD: the workgroups of one XCD then step
+// through the same samples over neighbouring (band-ordered) tiles at the same
+// time and share their operand tiles in that XCD's L2.  Within an XCD the
+// entries go heaviest first, so that the heavy ones (k < CUs/8) share their
+// CUs with the lightest ones.  The order only affects speed.
+inline void order_workgroups(const Args& c, int cus, uint16_t* perm) {
+  const int W = c.nwg;
+  for (int i = 0; i < W && i < kPermMax; ++i) perm[i] = static_cast<uint16_t>(i);
+  if (W > kPermMax || W % kXcds != 0 || cus % kXcds != 0) return;
+  const int n = W / kXcds;
+  const int nb = static_cast<int>(c.chunk_nb), q = c.gq, big = c.gr * (q + 1);
+  int key[kPermMax], units[kPermMax], order[kPermMax];
+  for (int j = 0; j < W; ++j) {
+    int tile, g, ng;
+    if (j < big) {
+      ng = q + 1;
+      tile = j / ng;
+      g = j % ng;
+    } else {
+      ng = q;
+      tile = c.gr + (j - big) / q;
+      g = (j - big) % q;
+    }
+    const int lo = (g * nb) / ng;
+    units[j] = ((g + 1) * nb) / ng - lo;
+    key[j] = lo * (c.tiles_m * c.tiles_n) + tile;
+    order[j] = j;
+  }
+  // insertion sort by key (W <= kPermMax; runs on the host once per launch)
+  for (int i = 1; i < W; ++i) {
+    const int v = order[i];
+    int k = i - 1;
+    while (k >= 0 && key[order[k]] > key[v]) {
+      order[k + 1] = order[k];
+      --k;
+    }
+    order[k + 1] = v;
+  }
+  for (int x = 0; x < kXcds; ++x) {
+    int k = 0;
+    for (int u = kGroupUnits; u >= 0; --u)
+      for (int i = 0; i < n; ++i) {
+        const int j = order[x * n + i];
+        if (units[j] == u) perm[x + kXcds * k++] = static_cast<uint16_t>(j);
+      }
+  }
 }
 
 // `plain`: ordinary dispatch instead of a cooperative launch (the caller
@@ -943,25 +1022,27 @@ hipError_t try_grouped(Args a, int cus, bool plain, bool clean, hipStream_t s) {
   if (a.K * a.lda * 2 >= (int64_t(1) << 31) || a.K * a.ldb * 2 >= (int64_t(1) << 31))
     return hipErrorNotSupported;
   const GroupPlan gp = group_plan(a.B, tiles, 2 * cus);
-  if (gp.groups == 0) return hipErrorNotSupported;
+  if (gp.chunk == 0) return hipErrorNotSupported;
   KernelFn grouped[kGroupUnits] = {&wgrad_group_kernel<DT, 1>, &wgrad_group_kernel<DT, 2>,
-                                   &wgrad_group_kernel<DT, 3>};
-  KernelFn fn = grouped[gp.units - 1];
-  int occ = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void*>(fn), NT,
-                                                   0) != hipSuccess ||
-      occ < 2)
-    return hipErrorNotSupported;
-  a.spg = gp.spg;
+                                   &wgrad_group_kernel<DT, 3>, &wgrad_group_kernel<DT, 4>};
   const int64_t words = int64_t(kWsHead / sizeof(unsigned));
   for (int64_t b0 = 0; b0 < a.B; b0 += gp.chunk) {
     Args c = a;
     c.chunk_b0 = b0;
     c.chunk_nb = a.B - b0 < gp.chunk ? a.B - b0 : gp.chunk;
-    c.groups = static_cast<int>((c.chunk_nb + gp.spg - 1) / gp.spg);
-    c.nwg = c.groups * tiles;
+    const LaunchShape ls = launch_shape(c.chunk_nb, tiles, 2 * cus);
+    c.nwg = ls.nwg;
+    c.gq = ls.gq;
+    c.gr = ls.gr;
     c.chunk_first = b0 == 0;
     c.chunk_last = b0 + c.chunk_nb >= a.B;
+    order_workgroups(c, cus, c.perm);
+    KernelFn fn = grouped[ls.units - 1];
+    int occ = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void*>(fn), NT,
+                                                     0) != hipSuccess ||
+        occ < 2)
+      return hipErrorNotSupported;
     if (b0 == 0 && !clean)
       hipLaunchKernelGGL(clear_words_kernel<0>,
                          dim3(static_cast<unsigned>((words + NT - 1) / NT)), dim3(NT), 0, s,
