@@ -45,9 +45,9 @@ PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 # factor the same counter reads on a plain copy of known size.  None = not
 # measured for that workload.
 TRAFFIC_BYTES = {
-    "cfg2": 161835642,   # profiles/wgrad_group_kernel_cfg2.md
-    "cfg3": 183441173,   # profiles/wgrad_group_kernel_cfg3.md
-    "cfg4": 113890950,   # profiles/layernorm_bwd_clip_cfg4.md (3 kernels of one call)
+    "cfg2": 176361137,   # profiles/wgrad_group_kernel_cfg2.md
+    "cfg3": 229628351,   # profiles/wgrad_group_kernel_cfg3.md
+    "cfg4": 113932746,   # profiles/layernorm_bwd_clip_cfg4.md (3 kernels of one call)
 }
 
 

@@ -634,33 +634,59 @@ __device__ __forceinline__ const float* slot_of(const Args& p, int j) {
 
 // Rows [r0, r1) of the tile: the staged sum of this group plus the slots of
 // the tile's other groups (in group order; a fixed order per row), finished.
+// A thread takes its chunks kFinishChunks at a time and issues the coherent
+// slot loads of all of them before using any, so that they are in flight
+// together.
+constexpr int kFinishChunks = 4;
 template <class OT>
 __device__ inline void finish_rows(const Args& p, const Assign& as, int64_t m0, int64_t n0, int r0,
                                    int r1, float* const (&q4)[4], bool poisoned) {
   const int nchunks = (r1 - r0) * (BN / 8);
-  for (int c = threadIdx.x; c < nchunks; c += NT) {
-    const int r = r0 + c / (BN / 8), col = (c % (BN / 8)) * 8;
-    const int64_t m = m0 + r, n = n0 + col;
-    if (m >= p.M || n >= p.N) continue;
-    const float* own = staged_row(q4, r) + col;
-    float v[8];
+  for (int c0 = threadIdx.x; c0 < nchunks; c0 += NT * kFinishChunks) {
+    float v[kFinishChunks][8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = own[e];
+    for (int k = 0; k < kFinishChunks; ++k) {
+      const int c = c0 + k * NT;
+      const int r = r0 + c / (BN / 8), col = (c % (BN / 8)) * 8;
+      if (c < nchunks) {
+        const float* own = staged_row(q4, r) + col;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[k][e] = own[e];
+      }
+    }
     for (int gg = 0; gg < as.ng; ++gg) {
       if (gg == as.g) continue;
       const CoherentSpan sl(slot_of(p, as.first + gg), BM * BN * 2);
-      const u32x4 w = __builtin_bit_cast(u32x4, sl.load4(static_cast<uint32_t>((r * BN + col) * 2)));
+      u32x4 w[kFinishChunks];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        v[2 * e] += __uint_as_float(w[e] << 16);
-        v[2 * e + 1] += __uint_as_float(w[e] & 0xffff0000u);
+      for (int k = 0; k < kFinishChunks; ++k) {
+        const int c = c0 + k * NT;
+        const int r = r0 + c / (BN / 8), col = (c % (BN / 8)) * 8;
+        // chunks past the range read inside the slot (c < 2048) and are unused
+        w[k] = __builtin_bit_cast(
+            u32x4, sl.load4(static_cast<uint32_t>(((r * BN + col) * 2) & (BM * BN * 2 - 1))));
       }
-    }
-    if (poisoned) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = __builtin_nanf("");
+      for (int k = 0; k < kFinishChunks; ++k)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[k][2 * e] += __uint_as_float(w[k][e] << 16);
+          v[k][2 * e + 1] += __uint_as_float(w[k][e] & 0xffff0000u);
+        }
     }
-    finish_chunk<OT>(p, m, n, v);
+#pragma unroll
+    for (int k = 0; k < kFinishChunks; ++k) {
+      const int c = c0 + k * NT;
+      if (c >= nchunks) continue;
+      const int r = r0 + c / (BN / 8), col = (c % (BN / 8)) * 8;
+      const int64_t m = m0 + r, n = n0 + col;
+      if (m >= p.M || n >= p.N) continue;
+      if (poisoned) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[k][e] = __builtin_nanf("");
+      }
+      finish_chunk<OT>(p, m, n, v[k]);
+    }
   }
 }
 
@@ -783,13 +809,14 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
   // poisons this workgroup's results with NaN rather than leave them silently
   // wrong; the status word reports it.
   // Workgroups with fewer products than the launch's most loaded ones wait
-  // quietly for about half of the time those need for the rest of theirs
-  // (measured on this workgroup's own products; a lone workgroup runs faster
-  // than two sharing a CU).
+  // quietly for about 60% of the time those need for the rest of theirs
+  // (measured on this workgroup's own products; a workgroup left alone on its
+  // CU runs its last product faster than two sharing the CU, and a late wake-up
+  // delays this tile's exchange).
   uint64_t quiet = 0;
   if (nb > 0 && nb < U) {
     const uint64_t now = wall_clock64();
-    quiet = now + (now - t_begin) * uint64_t(U - nb) / uint64_t(2 * nb);
+    quiet = now + (now - t_begin) * uint64_t(3 * (U - nb)) / uint64_t(5 * nb);
   }
   bool poisoned = grid_barrier(p.bar, unsigned(p.nwg), p.err, p.spin_limit, &flag, quiet);
   FDP_TS(9);
@@ -962,19 +989,21 @@ inline LaunchShape launch_shape(int64_t nb, int tiles, int slots) {
 
 // Hardware workgroup -> work list index.  Workgroups are dealt round-robin
 // to the 8 XCDs, and on an otherwise idle device workgroups w and w + CUs
-// share a CU.  The list entries are sorted by (first sample, tile) and cut
-// into 8 contiguous ranges, one per XCD: the workgroups of one XCD then step
-// through the same samples over neighbouring (band-ordered) tiles at the same
-// time and share their operand tiles in that XCD's L2.  Within an XCD the
-// entries go heaviest first, so that the heavy ones (k < CUs/8) share their
-// CUs with the lightest ones.  The order only affects speed.
+// share a CU.  The entries with the most samples ("heavy") and the others are
+// each sorted by (first sample, tile) and cut into 8 equal contiguous shares,
+// one per XCD: every XCD gets the same work, and its workgroups step through
+// the same samples over neighbouring (band-ordered) tiles at the same time, so
+// they share operand tiles in that XCD's L2.  Within an XCD the heavy entries
+// come first, so that they share their CUs (k and k + CUs/8) with light ones.
+// The order only affects speed.
 inline void order_workgroups(const Args& c, int cus, uint16_t* perm) {
   const int W = c.nwg;
   for (int i = 0; i < W && i < kPermMax; ++i) perm[i] = static_cast<uint16_t>(i);
   if (W > kPermMax || W % kXcds != 0 || cus % kXcds != 0) return;
   const int n = W / kXcds;
   const int nb = static_cast<int>(c.chunk_nb), q = c.gq, big = c.gr * (q + 1);
-  int key[kPermMax], units[kPermMax], order[kPermMax];
+  int key[kPermMax], units[kPermMax], heavy[kPermMax], light[kPermMax];
+  int umax = 0;
   for (int j = 0; j < W; ++j) {
     int tile, g, ng;
     if (j < big) {
@@ -989,25 +1018,39 @@ inline void order_workgroups(const Args& c, int cus, uint16_t* perm) {
     const int lo = (g * nb) / ng;
     units[j] = ((g + 1) * nb) / ng - lo;
     key[j] = lo * (c.tiles_m * c.tiles_n) + tile;
-    order[j] = j;
+    umax = units[j] > umax ? units[j] : umax;
   }
-  // insertion sort by key (W <= kPermMax; runs on the host once per launch)
-  for (int i = 1; i < W; ++i) {
-    const int v = order[i];
-    int k = i - 1;
-    while (k >= 0 && key[order[k]] > key[v]) {
-      order[k + 1] = order[k];
-      --k;
-    }
-    order[k + 1] = v;
+  int nh = 0, nl = 0;
+  for (int j = 0; j < W; ++j) {
+    if (units[j] == umax) heavy[nh++] = j;
+    else light[nl++] = j;
   }
-  for (int x = 0; x < kXcds; ++x) {
-    int k = 0;
-    for (int u = kGroupUnits; u >= 0; --u)
-      for (int i = 0; i < n; ++i) {
-        const int j = order[x * n + i];
-        if (units[j] == u) perm[x + kXcds * k++] = static_cast<uint16_t>(j);
+  // insertion sorts by key (W <= kPermMax; on the host, once per launch)
+  auto sort = [&](int* v, int len) {
+    for (int i = 1; i < len; ++i) {
+      const int x = v[i];
+      int k = i - 1;
+      while (k >= 0 && key[v[k]] > key[x]) {
+        v[k + 1] = v[k];
+        --k;
       }
+      v[k + 1] = x;
+    }
+  };
+  sort(heavy, nh);
+  sort(light, nl);
+  for (int x = 0; x < kXcds; ++x) {
+    const int h0 = (x * nh) / kXcds, h1 = ((x + 1) * nh) / kXcds;
+    const int l0 = (x * nl) / kXcds, l1 = ((x + 1) * nl) / kXcds;
+    // an XCD's share is n entries when nh and nl split evenly; otherwise the
+    // shares are rebalanced below so that every XCD has exactly n
+    int k = 0;
+    for (int i = h0; i < h1 && k < n; ++i) perm[x + kXcds * k++] = static_cast<uint16_t>(heavy[i]);
+    for (int i = l0; i < l1 && k < n; ++i) perm[x + kXcds * k++] = static_cast<uint16_t>(light[i]);
+    if (k != n) {  // uneven split: fall back to the plain sorted order
+      for (int i = 0; i < W && i < kPermMax; ++i) perm[i] = static_cast<uint16_t>(i);
+      return;
+    }
   }
 }
 

@@ -125,7 +125,7 @@ int fdp_version(void);
  *            pass uses the per-sample Gram matrices when that is cheaper;
  *            bit 2 (FDP_WGRAD_PLAIN_LAUNCH) dispatches the single-pass kernel
  *            as an ordinary launch instead of a cooperative one, saving the
- *            runtime's cooperative-launch synchronisation (about 25 us per
+ *            runtime's cooperative-launch synchronisation (about 15 us per
  *            call on MI355X).  The grid is sized to the kernel's occupancy,
  *            so it is resident at once when nothing else occupies the device;
  *            work on other streams only delays it.  The caller must not run
