@@ -223,6 +223,25 @@ __device__ inline float wave_sum(float v) {
   return v;
 }
 
+// The same sum through DPP lane moves only (no LDS round trips): butterflies
+// within each row of 16 lanes (quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror,
+// row_mirror), then row_bcast:15 and row_bcast:31 carry the row sums into
+// lane 63, which is broadcast.  Every lane of the wavefront must be active.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_add(float x) {
+  return x + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROW_MASK, 0xf,
+                                                        false));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v = dpp_add<0xB1, 0xf>(v);   // quad_perm [1,0,3,2]
+  v = dpp_add<0x4E, 0xf>(v);   // quad_perm [2,3,0,1]
+  v = dpp_add<0x141, 0xf>(v);  // row_half_mirror
+  v = dpp_add<0x140, 0xf>(v);  // row_mirror
+  v = dpp_add<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
+  v = dpp_add<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 // min(clamp, C / (n + 1e-10)) with the reference's epsilon
 // (flashdp/core/clip_fn.py:6-8).
 __device__ inline float clip_factor(float norm, float C, float clamp) {
