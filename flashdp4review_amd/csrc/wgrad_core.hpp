@@ -37,7 +37,6 @@ struct Args {
   int64_t units;          // tiles * B work units, unit u = (tile u/B, sample u%B)
   int nwg;                // workgroups of the cooperative grid
   unsigned* bar;          // grid barrier arrivals
-  unsigned* done;         // workgroups finished (the last one re-zeroes bar / done)
   unsigned* tile_turn;    // [tiles] hand-over tickets for tiles shared by workgroups
   float* tile_acc;        // [nwg, BM*BN] bf16 per-group tile sums (row-major)
   int* err;               // set when a bounded wait gives up
@@ -403,6 +402,12 @@ constexpr int kXcds = 8;
 // wait expired, or an earlier workgroup's did (that one set *err before this
 // one could arrive).
 //
+// The counter resets itself: the last arriver (arrival index n-1) stores 0 and
+// leaves at once.  A waiter with arrival index i sees the counter in
+// [i+1, n-1] until everyone has arrived, then n or (after the reset) 0, which
+// is <= i: either ends its wait.  So the counter is zero again when the
+// barrier is over, with no second counter to reset.
+//
 // quiet_until (a wall_clock64() value, 0 = none): before the first poll the
 // waiting wave sleeps without touching memory until then.  Coherent polling
 // loads stall the vector memory pipeline of their CU, so a workgroup that
@@ -413,16 +418,23 @@ __device__ inline bool grid_barrier(unsigned* bar, unsigned n, int* err, unsigne
   wait_stores();
   __syncthreads();
   if (threadIdx.x == 0) {
-    __hip_atomic_fetch_add(bar, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    while (wall_clock64() < quiet_until) __builtin_amdgcn_s_sleep(32);
-    unsigned spins = 0;
+    const unsigned i =
+        __hip_atomic_fetch_add(bar, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     int bad = 0;
-    while (__hip_atomic_load(bar, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < n) {
-      __builtin_amdgcn_s_sleep(kPollSleep);
-      if (++spins > limit) {
-        atomicOr(err, 1);
-        bad = 1;
-        break;
+    if (i + 1 == n) {
+      __hip_atomic_store(bar, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+      while (wall_clock64() < quiet_until) __builtin_amdgcn_s_sleep(32);
+      unsigned spins = 0;
+      for (;;) {
+        const unsigned v = __hip_atomic_load(bar, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (v >= n || v <= i) break;
+        __builtin_amdgcn_s_sleep(kPollSleep);
+        if (++spins > limit) {
+          atomicOr(err, 1);
+          bad = 1;
+          break;
+        }
       }
     }
     if (!bad) bad = __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
@@ -553,11 +565,29 @@ __device__ __forceinline__ float* staged_row(float* const (&q)[4], int r) {
   return quarter(q, r >> 5) + (r & 31) * BN;
 }
 
+// Noise for the 8 outputs (row m, columns n .. n+7 of the problem), unscaled;
+// entries past N are left alone.  Only the last launch of a batch adds noise.
+__device__ inline void noise8(const Args& p, int64_t m, int64_t n, float (&z)[8]) {
+  const NoiseSrc nz = p.noise;  // a value copy: no address of the kernel argument is taken
+  if (!p.chunk_last || !nz.on()) return;
+  const bool whole = n + 8 <= p.N;
+  if (whole && nz.z == nullptr && p.N % 4 == 0) {
+    nz.run(m * p.N + n, z);
+  } else if (whole && nz.z == nullptr) {
+    nz.window(m * p.N + n, z);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (n + e < p.N) z[e] = nz.at(m * p.N + n + e);
+  }
+}
+
 // Final values of 8 consecutive outputs (row m, columns n .. n+7 of the
 // problem): the chunk carried from earlier launches is added; the result is
-// carried on (not the last launch) or written as out_scale * v + noise.
+// carried on (not the last launch) or written as out_scale * v + noise_scale * z.
 template <class OT>
-__device__ inline void finish_chunk(const Args& p, int64_t m, int64_t n, float (&v)[8]) {
+__device__ inline void finish_chunk(const Args& p, int64_t m, int64_t n, float (&v)[8],
+                                    const float (&z)[8]) {
   using S = typename OT::storage;
   const bool whole = n + 8 <= p.N;
   const bool cvec = whole && (p.N % 4 == 0);
@@ -588,23 +618,9 @@ __device__ inline void finish_chunk(const Args& p, int64_t m, int64_t n, float (
   }
 #pragma unroll
   for (int e = 0; e < 8; ++e) v[e] *= p.out_scale;
-  const NoiseSrc nz = p.noise;  // a value copy: no address of the kernel argument is taken
-  if (nz.on()) {
-    if (whole && nz.z == nullptr && p.N % 4 == 0) {
-      float z[8];
-      nz.run(m * p.N + n, z);
+  if (p.noise.on()) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] += p.noise_scale * z[e];
-    } else if (whole && nz.z == nullptr) {
-      float z[8];
-      nz.window(m * p.N + n, z);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] += p.noise_scale * z[e];
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        if (n + e < p.N) v[e] += p.noise_scale * nz.at(m * p.N + n + e);
-    }
+    for (int e = 0; e < 8; ++e) v[e] += p.noise_scale * z[e];
   }
   S* out = static_cast<S*>(p.out) + m * p.ldo + n;
   constexpr int E = 16 / sizeof(S);  // elements per 16-byte store
@@ -632,15 +648,33 @@ __device__ __forceinline__ const float* slot_of(const Args& p, int j) {
                                         int64_t(j) * (BM * BN));
 }
 
+// Rows [r0, r1) of the tile are taken as chunks of 8 outputs; a thread takes
+// chunks c0, c0 + NT, ... kFinishChunks at a time.
+constexpr int kFinishChunks = 4;
+constexpr int kSlotBatch = 3;  // other groups' slots loaded together
+
+// The noise of this thread's first kFinishChunks chunks (drawn while the tile's
+// other groups publish).
+__device__ inline void noise_rows(const Args& p, int64_t m0, int64_t n0, int r0, int r1,
+                                  float (&z)[kFinishChunks][8]) {
+  const int nchunks = (r1 - r0) * (BN / 8);
+#pragma unroll
+  for (int k = 0; k < kFinishChunks; ++k) {
+    const int c = threadIdx.x + k * NT;
+    const int r = r0 + c / (BN / 8), col = (c % (BN / 8)) * 8;
+    if (c < nchunks && m0 + r < p.M && n0 + col < p.N) noise8(p, m0 + r, n0 + col, z[k]);
+  }
+}
+
 // Rows [r0, r1) of the tile: the staged sum of this group plus the slots of
 // the tile's other groups (in group order; a fixed order per row), finished.
-// A thread takes its chunks kFinishChunks at a time and issues the coherent
-// slot loads of all of them before using any, so that they are in flight
-// together.
-constexpr int kFinishChunks = 4;
+// The coherent slot loads of kSlotBatch groups and all kFinishChunks chunks
+// are issued before any is used, so that they are in flight together.  zpre
+// holds the noise of the first kFinishChunks chunks when `pre` is set.
 template <class OT>
 __device__ inline void finish_rows(const Args& p, const Assign& as, int64_t m0, int64_t n0, int r0,
-                                   int r1, float* const (&q4)[4], bool poisoned) {
+                                   int r1, float* const (&q4)[4], bool poisoned,
+                                   const float (&zpre)[kFinishChunks][8], bool pre) {
   const int nchunks = (r1 - r0) * (BN / 8);
   for (int c0 = threadIdx.x; c0 < nchunks; c0 += NT * kFinishChunks) {
     float v[kFinishChunks][8];
@@ -654,26 +688,37 @@ __device__ inline void finish_rows(const Args& p, const Assign& as, int64_t m0, 
         for (int e = 0; e < 8; ++e) v[k][e] = own[e];
       }
     }
-    for (int gg = 0; gg < as.ng; ++gg) {
-      if (gg == as.g) continue;
-      const CoherentSpan sl(slot_of(p, as.first + gg), BM * BN * 2);
-      u32x4 w[kFinishChunks];
+    for (int gb = 0; gb < as.ng; gb += kSlotBatch + 1) {
+      // groups gb .. gb + kSlotBatch, this one's own left out
+      u32x4 w[kSlotBatch + 1][kFinishChunks];
 #pragma unroll
-      for (int k = 0; k < kFinishChunks; ++k) {
-        const int c = c0 + k * NT;
-        const int r = r0 + c / (BN / 8), col = (c % (BN / 8)) * 8;
-        // chunks past the range read inside the slot (c < 2048) and are unused
-        w[k] = __builtin_bit_cast(
-            u32x4, sl.load4(static_cast<uint32_t>(((r * BN + col) * 2) & (BM * BN * 2 - 1))));
+      for (int s = 0; s <= kSlotBatch; ++s) {
+        const int gg = gb + s;
+        if (gg >= as.ng || gg == as.g) continue;
+        const CoherentSpan sl(slot_of(p, as.first + gg), BM * BN * 2);
+#pragma unroll
+        for (int k = 0; k < kFinishChunks; ++k) {
+          const int c = c0 + k * NT;
+          const int r = r0 + c / (BN / 8), col = (c % (BN / 8)) * 8;
+          // chunks past the range read inside the slot (c < 2048) and are unused
+          w[s][k] = __builtin_bit_cast(
+              u32x4, sl.load4(static_cast<uint32_t>(((r * BN + col) * 2) & (BM * BN * 2 - 1))));
+        }
       }
 #pragma unroll
-      for (int k = 0; k < kFinishChunks; ++k)
+      for (int s = 0; s <= kSlotBatch; ++s) {
+        const int gg = gb + s;
+        if (gg >= as.ng || gg == as.g) continue;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          v[k][2 * e] += __uint_as_float(w[k][e] << 16);
-          v[k][2 * e + 1] += __uint_as_float(w[k][e] & 0xffff0000u);
-        }
+        for (int k = 0; k < kFinishChunks; ++k)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            v[k][2 * e] += __uint_as_float(w[s][k][e] << 16);
+            v[k][2 * e + 1] += __uint_as_float(w[s][k][e] & 0xffff0000u);
+          }
+      }
     }
+    const bool first = pre && c0 == static_cast<int>(threadIdx.x);
 #pragma unroll
     for (int k = 0; k < kFinishChunks; ++k) {
       const int c = c0 + k * NT;
@@ -685,7 +730,14 @@ __device__ inline void finish_rows(const Args& p, const Assign& as, int64_t m0, 
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[k][e] = __builtin_nanf("");
       }
-      finish_chunk<OT>(p, m, n, v[k]);
+      float z[8] = {};
+      if (first) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) z[e] = zpre[k][e];
+      } else {
+        noise8(p, m, n, z);
+      }
+      finish_chunk<OT>(p, m, n, v[k], z);
     }
   }
 }
@@ -880,6 +932,8 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
   __syncthreads();
   FDP_TS(5);
   const int r0 = (as.g * BM) / as.ng, r1 = ((as.g + 1) * BM) / as.ng;
+  float zpre[kFinishChunks][8] = {};
+  const bool pre = as.ng > 1;
   if (as.ng > 1) {
     // publish the rows the other groups finish (row-major slot), then wait
     // until every group of the tile has published
@@ -898,12 +952,18 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
     wait_stores();
     __syncthreads();
     FDP_TS(6);
+    uint64_t quiet_until = 0;
     if (threadIdx.x == 0) {
       __hip_atomic_fetch_add(p.tile_turn + as.tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       // the tile's other groups started publishing together with this one:
       // stay off the memory pipeline for a fraction of this group's own time
       const uint64_t now = wall_clock64();
-      const uint64_t quiet_until = now + (now - t_pub) / 2;
+      quiet_until = now + (now - t_pub) / 2;
+    }
+    // this group's noise does not depend on the exchange: draw it meanwhile
+    noise_rows(p, m0, n0, r0, r1, zpre);
+    FDP_TS(7);
+    if (threadIdx.x == 0) {
       while (wall_clock64() < quiet_until) __builtin_amdgcn_s_sleep(8);
       unsigned spins = 0;
       int bad = 0;
@@ -922,23 +982,12 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
     poisoned = poisoned || flag != 0;
   }
   FDP_TS(10);
-  if (p.out_dtype == FDP_BF16) finish_rows<BF16>(p, as, m0, n0, r0, r1, q4, poisoned);
-  else if (p.out_dtype == FDP_F16) finish_rows<F16>(p, as, m0, n0, r0, r1, q4, poisoned);
-  else finish_rows<F32>(p, as, m0, n0, r0, r1, q4, poisoned);
+  // The control words are zero again: the grid barrier resets its counter, and
+  // group 0 of each tile clears the tile's ticket before that barrier.
+  if (p.out_dtype == FDP_BF16) finish_rows<BF16>(p, as, m0, n0, r0, r1, q4, poisoned, zpre, pre);
+  else if (p.out_dtype == FDP_F16) finish_rows<F16>(p, as, m0, n0, r0, r1, q4, poisoned, zpre, pre);
+  else finish_rows<F32>(p, as, m0, n0, r0, r1, q4, poisoned, zpre, pre);
   FDP_TS(12);
-  // ---- leave the control words zeroed for the next launch on this
-  // workspace: every workgroup has passed the barrier once `done` reaches nwg.
-  if (threadIdx.x == 0) {
-    const unsigned old =
-        __hip_atomic_fetch_add(p.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (old == unsigned(p.nwg - 1)) {
-      // every workgroup is past its ticket wait: zero the tickets too
-      for (int t = 0; t < tiles; ++t)
-        __hip_atomic_store(p.tile_turn + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(p.bar, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(p.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
 }
 
 // Clears the barrier / ticket words at the head of the workspace.

@@ -106,14 +106,15 @@ def test_wgrad_deterministic(two_pass):
 def test_wgrad_reused_workspace_stays_clean(shape):
     """Calls that reuse one workspace without clearing it (FDP_WGRAD_CLEAN_WORKSPACE)
     match a call on a garbage-filled workspace that the library clears, and leave
-    the control words zero (tiles shared by groups; several launches per call)."""
+    the control words (the first 256 bytes) zero.  Tiles are shared by groups and a
+    call makes several launches; the tile tickets after the head are cleared by the
+    kernel itself, so the dirty workspace's tickets start as garbage."""
     import ctypes
     from flashdp4review_amd import _lib
     B, K, M, N = shape
     a, b = make(B, K, M, N, torch.bfloat16, "tn", seed=12)
     L = _lib.lib()
     nb = _lib.size_query(L.fdp_wgrad_clip_workspace_size, B, K, M, N, _lib.FDP_BF16, 0)
-    tiles = ((M + 127) // 128) * ((N + 127) // 128)
 
     def call(ws, flags):
         out = torch.empty(M, N, dtype=torch.float32, device=DEV)
@@ -134,7 +135,6 @@ def test_wgrad_reused_workspace_stays_clean(shape):
         torch.cuda.synchronize()
         assert torch.equal(out, ref)
         assert torch.count_nonzero(clean[:256]) == 0
-        assert torch.count_nonzero(clean[256:256 + 4 * tiles]) == 0
     exp, _, _ = O.wgrad_clip(a, b, 0.05, 1.0, "tn")
     assert_close(ref, exp, torch.bfloat16, "clipped sum")
 
