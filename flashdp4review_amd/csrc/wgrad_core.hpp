@@ -397,8 +397,8 @@ constexpr int kPollSleep = 16;
 constexpr int kXcds = 8;
 
 
-// All workgroups of the (co-resident) grid arrive before any leaves.  Returns
-// (in every thread) whether this workgroup's results must be poisoned: its own
+// All workgroups of the (co-resident) grid arrive before any leaves.
+// grid_wait returns (in every thread) whether this workgroup's results must be poisoned: its own
 // wait expired, or an earlier workgroup's did (that one set *err before this
 // one could arrive).
 //
@@ -413,13 +413,20 @@ constexpr int kXcds = 8;
 // loads stall the vector memory pipeline of their CU, so a workgroup that
 // arrives early would otherwise slow the other workgroup still computing on
 // its CU; callers pass an estimate of when the slowest workgroup arrives.
-__device__ inline bool grid_barrier(unsigned* bar, unsigned n, int* err, unsigned limit,
-                                    int* flag, uint64_t quiet_until = 0) {
+//
+// Split in two: grid_arrive() (every thread; thread 0 gets the arrival index)
+// and grid_wait(); a workgroup may do work of its own in between.
+__device__ inline unsigned grid_arrive(unsigned* bar) {
   wait_stores();
   __syncthreads();
+  unsigned i = 0;
+  if (threadIdx.x == 0)
+    i = __hip_atomic_fetch_add(bar, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return i;
+}
+__device__ inline bool grid_wait(unsigned* bar, unsigned n, unsigned i, int* err, unsigned limit,
+                                 int* flag, uint64_t quiet_until = 0) {
   if (threadIdx.x == 0) {
-    const unsigned i =
-        __hip_atomic_fetch_add(bar, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     int bad = 0;
     if (i + 1 == n) {
       __hip_atomic_store(bar, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -653,8 +660,7 @@ __device__ __forceinline__ const float* slot_of(const Args& p, int j) {
 constexpr int kFinishChunks = 4;
 constexpr int kSlotBatch = 3;  // other groups' slots loaded together
 
-// The noise of this thread's first kFinishChunks chunks (drawn while the tile's
-// other groups publish).
+// The noise of this thread's first kFinishChunks chunks of rows [r0, r1).
 __device__ inline void noise_rows(const Args& p, int64_t m0, int64_t n0, int r0, int r1,
                                   float (&z)[kFinishChunks][8]) {
   const int nchunks = (r1 - r0) * (BN / 8);
@@ -670,11 +676,11 @@ __device__ inline void noise_rows(const Args& p, int64_t m0, int64_t n0, int r0,
 // the tile's other groups (in group order; a fixed order per row), finished.
 // The coherent slot loads of kSlotBatch groups and all kFinishChunks chunks
 // are issued before any is used, so that they are in flight together.  zpre
-// holds the noise of the first kFinishChunks chunks when `pre` is set.
+// holds the noise of the first kFinishChunks chunks.
 template <class OT>
 __device__ inline void finish_rows(const Args& p, const Assign& as, int64_t m0, int64_t n0, int r0,
                                    int r1, float* const (&q4)[4], bool poisoned,
-                                   const float (&zpre)[kFinishChunks][8], bool pre) {
+                                   const float (&zpre)[kFinishChunks][8]) {
   const int nchunks = (r1 - r0) * (BN / 8);
   for (int c0 = threadIdx.x; c0 < nchunks; c0 += NT * kFinishChunks) {
     float v[kFinishChunks][8];
@@ -718,7 +724,7 @@ __device__ inline void finish_rows(const Args& p, const Assign& as, int64_t m0, 
           }
       }
     }
-    const bool first = pre && c0 == static_cast<int>(threadIdx.x);
+    const bool first = c0 == static_cast<int>(threadIdx.x);
 #pragma unroll
     for (int k = 0; k < kFinishChunks; ++k) {
       const int c = c0 + k * NT;
@@ -789,6 +795,13 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
   int iu = 0, ik = 0;
   int64_t m0, n0;
   tile_coords(p, as.tile, m0, n0);
+  // rows [r0, r1) of the tile are finished by this group; their noise (VALU
+  // work independent of the data) is drawn ahead into zpre: by workgroups with
+  // fewer products than the most loaded ones while they wait at the grid
+  // barrier, by the others while the tile's groups publish
+  const int r0 = (as.g * BM) / as.ng, r1 = ((as.g + 1) * BM) / as.ng;
+  float zpre[kFinishChunks][8] = {};
+  const bool early = nb < U;
   if (nq > 0) job.init(pa + as.b0 * p.sab, p.lda, pb + as.b0 * p.sbb, p.ldb, p.K, m0, n0);
   auto issue_next = [&](FDP_LDS char* stage) {
     job.issue(stage, ik);
@@ -870,7 +883,9 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
     const uint64_t now = wall_clock64();
     quiet = now + (now - t_begin) * uint64_t(3 * (U - nb)) / uint64_t(5 * nb);
   }
-  bool poisoned = grid_barrier(p.bar, unsigned(p.nwg), p.err, p.spin_limit, &flag, quiet);
+  const unsigned arrival = grid_arrive(p.bar);
+  if (early) noise_rows(p, m0, n0, r0, r1, zpre);
+  bool poisoned = grid_wait(p.bar, unsigned(p.nwg), arrival, p.err, p.spin_limit, &flag, quiet);
   FDP_TS(9);
 
   // ---- clip factors of this workgroup's samples: wavefront i sums the
@@ -931,9 +946,6 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
   }
   __syncthreads();
   FDP_TS(5);
-  const int r0 = (as.g * BM) / as.ng, r1 = ((as.g + 1) * BM) / as.ng;
-  float zpre[kFinishChunks][8] = {};
-  const bool pre = as.ng > 1;
   if (as.ng > 1) {
     // publish the rows the other groups finish (row-major slot), then wait
     // until every group of the tile has published
@@ -960,8 +972,7 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
       const uint64_t now = wall_clock64();
       quiet_until = now + (now - t_pub) / 2;
     }
-    // this group's noise does not depend on the exchange: draw it meanwhile
-    noise_rows(p, m0, n0, r0, r1, zpre);
+    if (!early) noise_rows(p, m0, n0, r0, r1, zpre);
     FDP_TS(7);
     if (threadIdx.x == 0) {
       while (wall_clock64() < quiet_until) __builtin_amdgcn_s_sleep(8);
@@ -982,11 +993,12 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
     poisoned = poisoned || flag != 0;
   }
   FDP_TS(10);
+  if (!early && as.ng == 1) noise_rows(p, m0, n0, r0, r1, zpre);
   // The control words are zero again: the grid barrier resets its counter, and
   // group 0 of each tile clears the tile's ticket before that barrier.
-  if (p.out_dtype == FDP_BF16) finish_rows<BF16>(p, as, m0, n0, r0, r1, q4, poisoned, zpre, pre);
-  else if (p.out_dtype == FDP_F16) finish_rows<F16>(p, as, m0, n0, r0, r1, q4, poisoned, zpre, pre);
-  else finish_rows<F32>(p, as, m0, n0, r0, r1, q4, poisoned, zpre, pre);
+  if (p.out_dtype == FDP_BF16) finish_rows<BF16>(p, as, m0, n0, r0, r1, q4, poisoned, zpre);
+  else if (p.out_dtype == FDP_F16) finish_rows<F16>(p, as, m0, n0, r0, r1, q4, poisoned, zpre);
+  else finish_rows<F32>(p, as, m0, n0, r0, r1, q4, poisoned, zpre);
   FDP_TS(12);
 }
 
