@@ -41,13 +41,13 @@ PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 
 # HBM bytes per launch of the dominant kernel, from rocprofv3 --pmc FETCH_SIZE
-# and WRITE_SIZE runs of this script (profiles/*_traffic.md), each scaled by the
+# and WRITE_SIZE runs of this script (the HBM traffic sections of profiles/*.md), each scaled by the
 # factor the same counter reads on a plain copy of known size.  None = not
 # measured for that workload.
 TRAFFIC_BYTES = {
-    "cfg2": 176361137,   # profiles/wgrad_group_kernel_cfg2.md
-    "cfg3": 229628351,   # profiles/wgrad_group_kernel_cfg3.md
-    "cfg4": 113932746,   # profiles/layernorm_bwd_clip_cfg4.md (3 kernels of one call)
+    "cfg2": 176559938,   # profiles/wgrad_group_kernel_cfg2.md
+    "cfg3": 229808557,   # profiles/wgrad_group_kernel_cfg3.md
+    "cfg4": 105519248,   # profiles/layernorm_bwd_clip_cfg4.md (3 kernels of one call)
 }
 
 
