@@ -11,10 +11,12 @@
 //   LN dx:     flashdp/core/layernorm_clip.py:98-107
 //
 // All reductions are fixed-order (no float atomics): the row kernel writes
-// per-(sample, row-chunk) partial vectors to the workspace, chunk_sum_kernel
+// per-(sample, row-chunk) partial vectors to the workspace, chunk_sum_block
 // adds each sample's chunks in chunk order (and the squares for the norm), and
-// combine_kernel derives the clip factors and adds the clipped samples in
-// sample order into the output.  Rows are read with 16-byte loads, one
+// combine_block derives the clip factors and adds the clipped samples in
+// sample order into the output -- in two launches (chunk_sum_kernel,
+// combine_kernel), or in one (reduce_kernel) when the per-stream sums are
+// small.  Rows are read with 16-byte loads, one
 // wavefront per row for the LayerNorm kernels (row statistics are wavefront
 // shuffles, no LDS), 64..256 threads across the columns for the column sums.
 #include "fdp_common.hpp"
@@ -116,12 +118,16 @@ __device__ inline void load_param(const void* p, int dtype, int64_t H, int lane,
 // 16-byte vector and walks `rows` rows of one sample.  Writes the chunk's
 // partial column sums partials[b][chunk][h] and, for FDP_NORM_FROB, the
 // workgroup's sum of u^2 to frob[b][chunk * col_blocks + col_block].
+// Workgroup (0,0,0) zeroes the reduction's ticket.
 template <class DT, int VEC>
 __global__ __launch_bounds__(NT) void colsum_kernel(const typename DT::storage* u,
                                                     const typename DT::storage* v, int64_t T,
                                                     int64_t H, int64_t rows, int chunks,
-                                                    float* partials, float* frob) {
+                                                    float* partials, float* frob,
+                                                    unsigned* tickets) {
   __shared__ float red[NT / kWave];
+  if (blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0 && threadIdx.x == 0)
+    __hip_atomic_store(tickets, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const int64_t b = blockIdx.z;
   const int chunk = blockIdx.y;
   const int64_t vi = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -208,16 +214,46 @@ struct Item {
 
 constexpr int kItemsPerBlock = 64;
 
-// grid (item_blocks, S): sums[s][h] = sum_c partials[s][c][h];
-// sq_part[s][item_block] = sum of squares of this block's sums.
-template <bool V4>
-__global__ __launch_bounds__(NT) void chunk_sum_kernel(const float* partials, int64_t H,
-                                                       int chunks, float* sums, float* sq_part) {
+// Loads and stores of the per-sample sums: element `off` of the region at
+// `base` (uniform across the workgroup; `bytes` long, < 2^32).  COH:
+// agent-coherent (sc1) accesses, for values exchanged between workgroups of
+// one launch that may sit on different XCDs; otherwise plain ones (values from
+// an earlier launch).
+template <bool V4, bool COH>
+__device__ __forceinline__ f32x4 ld_item(const float* base, int64_t off, uint32_t bytes) {
+  if constexpr (COH) {
+    if constexpr (V4) return CoherentSpan(base, bytes).load4(static_cast<uint32_t>(off * 4));
+    else return f32x4{ld_coherent(base + off), 0.f, 0.f, 0.f};
+  } else {
+    if constexpr (V4) return *reinterpret_cast<const f32x4*>(base + off);
+    else return f32x4{base[off], 0.f, 0.f, 0.f};
+  }
+}
+template <bool V4, bool COH>
+__device__ __forceinline__ void st_item(float* base, int64_t off, uint32_t bytes, f32x4 v) {
+  if constexpr (COH) {
+    if constexpr (V4) CoherentSpan(base, bytes).store4(static_cast<uint32_t>(off * 4), v);
+    else st_coherent(base + off, v[0]);
+  } else {
+    if constexpr (V4) *reinterpret_cast<f32x4*>(base + off) = v;
+    else base[off] = v[0];
+  }
+}
+template <bool COH>
+__device__ __forceinline__ float ld_word(const float* p) {
+  if constexpr (COH) return ld_coherent(p);
+  else return *p;
+}
+
+// Item block ib of stream s: sums[s][h] = sum_c partials[s][c][h];
+// sq_part[s][ib] = sum of squares of this block's sums.
+template <bool V4, bool COH>
+__device__ inline void chunk_sum_block(const float* partials, int64_t H, int chunks, float* sums,
+                                       float* sq_part, int64_t s, int ib, int nib) {
   __shared__ f32x4 grp[NT / kWave][kItemsPerBlock];
-  const int64_t s = blockIdx.y;
   const int lane = threadIdx.x & 63, g = threadIdx.x >> 6;
   const int64_t items = (H + Item<V4>::W - 1) / Item<V4>::W;
-  const int64_t it = int64_t(blockIdx.x) * kItemsPerBlock + lane;
+  const int64_t it = int64_t(ib) * kItemsPerBlock + lane;
   const int per = (chunks + NT / kWave - 1) / (NT / kWave);
   const int c0 = g * per < chunks ? g * per : chunks;
   const int c1 = c0 + per < chunks ? c0 + per : chunks;
@@ -225,18 +261,17 @@ __global__ __launch_bounds__(NT) void chunk_sum_kernel(const float* partials, in
   acc.zero();
   if (it < items) {
     const float* src = partials + s * chunks * H + it * Item<V4>::W;
-    int c = c0;
-    for (; c + 8 <= c1; c += 8) {
+    // batches of 8 chunks, the last one masked: its loads are in flight together
+    for (int c = c0; c < c1; c += 8) {
       Item<V4> x[8];
 #pragma unroll
-      for (int q = 0; q < 8; ++q) x[q].load(src + int64_t(c + q) * H);
+      for (int q = 0; q < 8; ++q) {
+        if (c + q < c1) x[q].load(src + int64_t(c + q) * H);
+        else x[q].zero();
+      }
 #pragma unroll
-      for (int q = 0; q < 8; ++q) acc.v += x[q].v;
-    }
-    for (; c < c1; ++c) {
-      Item<V4> x;
-      x.load(src + int64_t(c) * H);
-      acc.v += x.v;
+      for (int q = 0; q < 8; ++q)
+        if (c + q < c1) acc.v += x[q].v;
     }
   }
   grp[g][lane] = acc.v;
@@ -246,39 +281,65 @@ __global__ __launch_bounds__(NT) void chunk_sum_kernel(const float* partials, in
     tot.v = ((grp[0][lane] + grp[1][lane]) + grp[2][lane]) + grp[3][lane];
     float q = 0.f;
     if (it < items) {
-      tot.store(sums + s * H + it * Item<V4>::W);
+      st_item<V4, COH>(sums + s * H, it * Item<V4>::W, static_cast<uint32_t>(H * 4), tot.v);
       q = tot.sq();
     }
     q = wave_sum(q);
-    if (lane == 0) sq_part[s * gridDim.x + blockIdx.x] = q;
+    if (lane == 0) {
+      if constexpr (COH) st_coherent(sq_part + s * nib + ib, q);
+      else sq_part[s * nib + ib] = q;
+    }
   }
+}
+
+// grid (item_blocks, S): chunk_sum_block of every (stream, item block).
+template <bool V4>
+__global__ __launch_bounds__(NT) void chunk_sum_kernel(const float* partials, int64_t H,
+                                                       int chunks, float* sums, float* sq_part) {
+  chunk_sum_block<V4, false>(partials, H, chunks, sums, sq_part, blockIdx.y, blockIdx.x,
+                             gridDim.x);
 }
 
 constexpr int kFacChunk = 1024;  // clip factors staged in LDS per pass
 
-// grid (item_blocks, nstreams): stream k's clip factors c_{k,b} from the norm
-// parts (nparts per sample, summed in order), then
+// What the clipped sum of stream k needs besides the sums.
+struct CombineArgs {
+  const float* parts;  // per-sample norm parts [S][nparts]
+  int nparts;
+  int64_t B, H;
+  float C, clamp;
+  const float* clip_args_dev;
+  float out_scale;
+  NoiseSrc noise0, noise1;
+  float noise_scale;
+  void* out0;
+  void* out1;
+  int out_dtype;
+  float* norms;
+  float* factors;
+};
+
+// Item block ib of stream k: the clip factors c_{k,b} from the norm parts
+// (nparts per sample, summed in order), then
 //   out_k[h] = out_scale * sum_b c_{k,b} sums[k*B+b][h] + noise_scale * noise_k[h]
 // with the four waves each taking a contiguous quarter of the samples, added
-// in order.  Workgroup 0 of each stream also writes norms / factors.
-template <bool V4>
-__global__ __launch_bounds__(NT) void combine_kernel(
-    const float* sums, const float* parts, int nparts, int64_t B, int64_t H, float C,
-    float clamp, const float* clip_args_dev, float out_scale, NoiseSrc noise0, NoiseSrc noise1,
-    float noise_scale, void* out0, void* out1, int out_dtype, float* norms, float* factors) {
+// in order.  write_stats: also write norms / factors.
+template <bool V4, bool COH>
+__device__ inline void combine_block(const float* sums, const CombineArgs& a, int k, int ib,
+                                     bool write_stats) {
   __shared__ float fac[kFacChunk];
   __shared__ f32x4 grp[NT / kWave][kItemsPerBlock];
-  if (clip_args_dev != nullptr) {
-    C = clip_args_dev[0];
-    clamp = clip_args_dev[1];
+  float C = a.C, clamp = a.clamp;
+  if (a.clip_args_dev != nullptr) {
+    C = a.clip_args_dev[0];
+    clamp = a.clip_args_dev[1];
   }
-  const int k = blockIdx.y;
-  void* out = k == 0 ? out0 : out1;
-  const NoiseSrc noise = k == 0 ? noise0 : noise1;
-  const bool write_stats = blockIdx.x == 0;
+  const int64_t B = a.B, H = a.H;
+  void* out = k == 0 ? a.out0 : a.out1;
+  const NoiseSrc noise = k == 0 ? a.noise0 : a.noise1;
   const int lane = threadIdx.x & 63, g = threadIdx.x >> 6;
   const int64_t items = (H + Item<V4>::W - 1) / Item<V4>::W;
-  const int64_t it = int64_t(blockIdx.x) * kItemsPerBlock + lane;
+  const int64_t it = int64_t(ib) * kItemsPerBlock + lane;
   const int64_t per = (B + NT / kWave - 1) / (NT / kWave);
   const int64_t g0 = g * per < B ? g * per : B;
   const int64_t g1 = g0 + per < B ? g0 + per : B;
@@ -289,40 +350,40 @@ __global__ __launch_bounds__(NT) void combine_kernel(
     __syncthreads();
     for (int64_t i = threadIdx.x; i < nb; i += NT) {
       const int64_t s = k * B + bc + i;
-      const float* src = parts + s * nparts;
+      const float* src = a.parts + s * a.nparts;
       float q = 0.f;
       int j = 0;
-      for (; j + 4 <= nparts; j += 4) {
-        const float a0 = src[j], a1 = src[j + 1], a2 = src[j + 2], a3 = src[j + 3];
+      for (; j + 4 <= a.nparts; j += 4) {
+        const float a0 = ld_word<COH>(src + j), a1 = ld_word<COH>(src + j + 1);
+        const float a2 = ld_word<COH>(src + j + 2), a3 = ld_word<COH>(src + j + 3);
         q = (((q + a0) + a1) + a2) + a3;
       }
-      for (; j < nparts; ++j) q += src[j];
+      for (; j < a.nparts; ++j) q += ld_word<COH>(src + j);
       const float n = sqrtf(q);
       const float c = clip_factor(n, C, clamp);
       fac[i] = c;
       if (write_stats) {
-        if (norms) norms[s] = n;
-        if (factors) factors[s] = c;
+        if (a.norms) a.norms[s] = n;
+        if (a.factors) a.factors[s] = c;
       }
     }
     __syncthreads();
     if (out != nullptr && it < items) {
       const int64_t lo = g0 > bc ? g0 : bc;
       const int64_t hi = g1 < bc + nb ? g1 : bc + nb;
-      const float* src = sums + (k * B) * H + it * Item<V4>::W;
+      // the stream's sums: [B][H] at base (B * H * 4 bytes < 2^32 where COH)
+      const float* base = sums + (k * B) * H;
+      const uint32_t bytes = static_cast<uint32_t>(COH ? B * H * 4 : 0);
+      const int64_t col = it * Item<V4>::W;
       int64_t b = lo;
       for (; b + 8 <= hi; b += 8) {
-        Item<V4> x[8];
+        f32x4 x[8];
 #pragma unroll
-        for (int q = 0; q < 8; ++q) x[q].load(src + (b + q) * H);
+        for (int q = 0; q < 8; ++q) x[q] = ld_item<V4, COH>(base, (b + q) * H + col, bytes);
 #pragma unroll
-        for (int q = 0; q < 8; ++q) acc.v += fac[b + q - bc] * x[q].v;
+        for (int q = 0; q < 8; ++q) acc.v += fac[b + q - bc] * x[q];
       }
-      for (; b < hi; ++b) {
-        Item<V4> x;
-        x.load(src + b * H);
-        acc.v += fac[b - bc] * x.v;
-      }
+      for (; b < hi; ++b) acc.v += fac[b - bc] * ld_item<V4, COH>(base, b * H + col, bytes);
     }
   }
   if (out == nullptr) return;
@@ -342,9 +403,118 @@ __global__ __launch_bounds__(NT) void combine_kernel(
 #pragma unroll
     for (int e = 0; e < W; ++e) {
       const int64_t h = it * W + e;
-      if (h < H) store_from_f32(out, h, out_dtype, tot[e] * out_scale + noise_scale * z[e]);
+      if (h < H) store_from_f32(out, h, a.out_dtype, tot[e] * a.out_scale + a.noise_scale * z[e]);
     }
   }
+}
+
+// grid (item_blocks, nstreams): combine_block of every (stream, item block);
+// workgroup 0 of each stream writes norms / factors.
+template <bool V4>
+__global__ __launch_bounds__(NT) void combine_kernel(const float* sums, CombineArgs a) {
+  combine_block<V4, false>(sums, a, blockIdx.y, blockIdx.x, blockIdx.x == 0);
+}
+
+// The clipped sum of stream k by one workgroup: every thread takes whole items
+// and adds the samples in sample order, 16 loads in flight at a time (a fixed
+// order, not combine_block's quarters).  B <= kFacChunk.  Reads agent-coherent
+// sums and parts.
+template <bool V4>
+__device__ inline void combine_stream(const float* sums, const CombineArgs& a, int k) {
+  __shared__ float fac[kFacChunk];
+  float C = a.C, clamp = a.clamp;
+  if (a.clip_args_dev != nullptr) {
+    C = a.clip_args_dev[0];
+    clamp = a.clip_args_dev[1];
+  }
+  const int64_t B = a.B, H = a.H;
+  void* out = k == 0 ? a.out0 : a.out1;
+  constexpr int W = Item<V4>::W;
+  const int64_t items = (H + W - 1) / W;
+  const float* base = sums + (k * B) * H;
+  const uint32_t bytes = static_cast<uint32_t>(B * H * 4);
+  // the first batch of this thread's first item is loaded before the factors
+  // are formed: the two round trips overlap
+  f32x4 x[16];
+  const bool pre = out != nullptr && static_cast<int64_t>(threadIdx.x) < items;
+  if (pre) {
+#pragma unroll
+    for (int q = 0; q < 16; ++q)
+      x[q] = q < B ? ld_item<V4, true>(base, q * H + int64_t(threadIdx.x) * W, bytes)
+                   : f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  for (int64_t i = threadIdx.x; i < B; i += NT) {
+    const int64_t s = k * B + i;
+    const float* src = a.parts + s * a.nparts;
+    float q = 0.f;
+    int j = 0;
+    for (; j + 4 <= a.nparts; j += 4) {
+      const float a0 = ld_coherent(src + j), a1 = ld_coherent(src + j + 1);
+      const float a2 = ld_coherent(src + j + 2), a3 = ld_coherent(src + j + 3);
+      q = (((q + a0) + a1) + a2) + a3;
+    }
+    for (; j < a.nparts; ++j) q += ld_coherent(src + j);
+    const float n = sqrtf(q);
+    const float c = clip_factor(n, C, clamp);
+    fac[i] = c;
+    if (a.norms) a.norms[s] = n;
+    if (a.factors) a.factors[s] = c;
+  }
+  __syncthreads();
+  if (out == nullptr) return;
+  const NoiseSrc noise = k == 0 ? a.noise0 : a.noise1;
+  for (int64_t it = threadIdx.x; it < items; it += NT) {
+    const int64_t col = it * W;
+    f32x4 tot = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int64_t b = 0; b < B; b += 16) {
+      if (b > 0 || it != static_cast<int64_t>(threadIdx.x)) {
+#pragma unroll
+        for (int q = 0; q < 16; ++q)
+          x[q] = b + q < B ? ld_item<V4, true>(base, (b + q) * H + col, bytes)
+                           : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int q = 0; q < 16; ++q)
+        if (b + q < B) tot += fac[b + q] * x[q];
+    }
+    float z[4] = {0.f, 0.f, 0.f, 0.f};
+    if (noise.z != nullptr) {
+#pragma unroll
+      for (int e = 0; e < W; ++e)
+        if (col + e < H) z[e] = noise.at(col + e);
+    } else if (noise.draw) {
+      noise.window(col, z);
+    }
+#pragma unroll
+    for (int e = 0; e < W; ++e)
+      if (col + e < H)
+        store_from_f32(out, col + e, a.out_dtype, tot[e] * a.out_scale + a.noise_scale * z[e]);
+  }
+}
+
+// Both steps in one launch, for small per-stream sums: grid (item_blocks, S)
+// runs chunk_sum_block, and the last workgroup of stream k to finish (a ticket
+// per stream, zeroed by the row kernel that wrote the partials) runs
+// combine_stream.  The sums and squares it reads are agent-coherent; every
+// workgroup's stores have completed before it takes its ticket.
+template <bool V4>
+__global__ __launch_bounds__(NT) void reduce_kernel(const float* partials, int chunks,
+                                                    float* sums, float* sq_part,
+                                                    unsigned* tickets, CombineArgs a) {
+  __shared__ int last;
+  const int64_t s = blockIdx.y;
+  const int k = static_cast<int>(s / a.B);
+  chunk_sum_block<V4, true>(partials, a.H, chunks, sums, sq_part, s, blockIdx.x, gridDim.x);
+  wait_stores();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned n = static_cast<unsigned>(a.B) * gridDim.x;
+    const unsigned old =
+        __hip_atomic_fetch_add(tickets + k, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last = old + 1 == n;
+  }
+  __syncthreads();
+  if (last) combine_stream<V4>(sums, a, k);
 }
 
 // ================================================================= LayerNorm
@@ -463,7 +633,8 @@ __global__ __launch_bounds__(kLnThreads) void ln_fwd_kernel(const typename DT::s
 // next row's x / dy / mean / rstd loads in flight while the current row is
 // processed: writes dx and accumulates P = sum dy*x_hat, Q = sum dy in
 // registers; the W = NTH/64 waves are folded in wave order through LDS into
-// the chunk's partials (stream b: P, stream B+b: Q).
+// the chunk's partials (stream b: P, stream B+b: Q).  Workgroup (0,0) zeroes
+// the reduction's two tickets.
 template <class DT, int EPL, int VEC, int NTH>
 __global__ __launch_bounds__(NTH) void ln_bwd_kernel(const typename DT::storage* dy,
                                                     const typename DT::storage* x, const void* w,
@@ -471,8 +642,10 @@ __global__ __launch_bounds__(NTH) void ln_bwd_kernel(const typename DT::storage*
                                                     const float* rstd, int64_t T, int64_t H,
                                                     int64_t rows, int chunks,
                                                     typename DT::storage* dx, float* partials,
-                                                    int64_t B) {
+                                                    int64_t B, unsigned* tickets) {
   constexpr int W = NTH / kWave;
+  if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x < 2)
+    __hip_atomic_store(tickets + threadIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   extern __shared__ __attribute__((aligned(16))) char smem_raw[];
   float* lds = reinterpret_cast<float*>(smem_raw);  // [W][H]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -586,12 +759,19 @@ int num_cus() {
 //   off_frob   per-(sample, workgroup) sums of u^2 [B][parts] (FDP_NORM_FROB)
 //   off_sums   per-sample sums [S][H] (fp32)
 //   off_sq     per-(stream, item block) sums of squares [S][item_blocks]
+//   off_ticket one arrival ticket per stream (reduce_kernel; zeroed by the row
+//              kernel of the same call)
 struct RedPlan {
   int vec, bs, cblocks, chunks, parts, iblocks;
   bool v4;
+  bool one_launch;  // reduce_kernel instead of chunk_sum_kernel + combine_kernel
   int64_t rows;
-  size_t off_part, off_frob, off_sums, off_sq, total;
+  size_t off_part, off_frob, off_sums, off_sq, off_ticket, total;
 };
+
+// Per-stream sums of at most this many elements are combined by one workgroup
+// (reduce_kernel): there the saved launch outweighs the serial combine.
+constexpr int64_t kOneLaunchElems = 65536;
 
 void finish_plan(RedPlan& p, int64_t B, int64_t H, int streams) {
   const size_t S = size_t(streams) * B;
@@ -603,7 +783,9 @@ void finish_plan(RedPlan& p, int64_t B, int64_t H, int streams) {
   p.off_frob = align_up(sizeof(float) * S * p.chunks * H);
   p.off_sums = p.off_frob + align_up(sizeof(float) * size_t(B) * p.parts);
   p.off_sq = p.off_sums + align_up(sizeof(float) * S * H);
-  p.total = p.off_sq + align_up(sizeof(float) * S * p.iblocks);
+  p.off_ticket = p.off_sq + align_up(sizeof(float) * S * p.iblocks);
+  p.total = p.off_ticket + align_up(sizeof(unsigned) * streams);
+  p.one_launch = B * H <= kOneLaunchElems && B <= kFacChunk;
 }
 
 // Rows per chunk so that there are about `per_cu` workgroups per CU, with at
@@ -673,21 +855,27 @@ void launch_reduce(const RedPlan& p, char* ws, int64_t B, int64_t H, int streams
   const float* part = reinterpret_cast<const float*>(ws + p.off_part);
   float* sums = reinterpret_cast<float*>(ws + p.off_sums);
   float* sq = reinterpret_cast<float*>(ws + p.off_sq);
-  const float* nparts = frob ? reinterpret_cast<const float*>(ws + p.off_frob) : sq;
-  const int np = frob ? p.parts : p.iblocks;
+  unsigned* tickets = reinterpret_cast<unsigned*>(ws + p.off_ticket);
+  const CombineArgs a{frob ? reinterpret_cast<const float*>(ws + p.off_frob) : sq,
+                      frob ? p.parts : p.iblocks,
+                      B, H, e.C, e.clamp, e.clip_args_dev, e.out_scale, e.noise0, e.noise1,
+                      e.noise_scale, e.out0, e.out1, e.out_dtype, e.norms, e.factors};
   const dim3 rgrid(static_cast<unsigned>(p.iblocks), static_cast<unsigned>(streams * B));
   const dim3 cgrid(static_cast<unsigned>(p.iblocks), static_cast<unsigned>(streams));
-  if (p.v4) {
+  if (p.one_launch) {
+    if (p.v4)
+      hipLaunchKernelGGL(reduce_kernel<true>, rgrid, dim3(NT), 0, s, part, p.chunks, sums, sq,
+                         tickets, a);
+    else
+      hipLaunchKernelGGL(reduce_kernel<false>, rgrid, dim3(NT), 0, s, part, p.chunks, sums, sq,
+                         tickets, a);
+  } else if (p.v4) {
     hipLaunchKernelGGL(chunk_sum_kernel<true>, rgrid, dim3(NT), 0, s, part, H, p.chunks, sums, sq);
-    hipLaunchKernelGGL(combine_kernel<true>, cgrid, dim3(NT), 0, s, sums, nparts, np, B, H, e.C,
-                       e.clamp, e.clip_args_dev, e.out_scale, e.noise0, e.noise1, e.noise_scale,
-                       e.out0, e.out1, e.out_dtype, e.norms, e.factors);
+    hipLaunchKernelGGL(combine_kernel<true>, cgrid, dim3(NT), 0, s, sums, a);
   } else {
     hipLaunchKernelGGL(chunk_sum_kernel<false>, rgrid, dim3(NT), 0, s, part, H, p.chunks, sums,
                        sq);
-    hipLaunchKernelGGL(combine_kernel<false>, cgrid, dim3(NT), 0, s, sums, nparts, np, B, H, e.C,
-                       e.clamp, e.clip_args_dev, e.out_scale, e.noise0, e.noise1, e.noise_scale,
-                       e.out0, e.out1, e.out_dtype, e.norms, e.factors);
+    hipLaunchKernelGGL(combine_kernel<false>, cgrid, dim3(NT), 0, s, sums, a);
   }
 }
 
@@ -698,7 +886,8 @@ void launch_colsum(const RedPlan& p, const void* u, const void* v, int64_t B, in
   hipLaunchKernelGGL((colsum_kernel<DT, VEC>), dim3(p.cblocks, p.chunks, B), dim3(p.bs), 0, s,
                      static_cast<const S*>(u), static_cast<const S*>(v), T, H, p.rows, p.chunks,
                      reinterpret_cast<float*>(ws + p.off_part),
-                     frob ? reinterpret_cast<float*>(ws + p.off_frob) : nullptr);
+                     frob ? reinterpret_cast<float*>(ws + p.off_frob) : nullptr,
+                     reinterpret_cast<unsigned*>(ws + p.off_ticket));
 }
 
 template <class DT>
@@ -759,31 +948,33 @@ struct LnBwdIo {
 };
 
 template <class DT, int EPL, int VEC>
-void launch_ln_bwd_t(const RedPlan& p, const LnBwdIo& io, float* part, hipStream_t s) {
+void launch_ln_bwd_t(const RedPlan& p, const LnBwdIo& io, float* part, unsigned* tickets,
+                     hipStream_t s) {
   using S = typename DT::storage;
   constexpr int NTH = ln_bwd_threads(EPL);
   hipLaunchKernelGGL((ln_bwd_kernel<DT, EPL, VEC, NTH>), dim3(p.chunks, io.B), dim3(NTH),
                      sizeof(float) * (NTH / kWave) * io.H, s, static_cast<const S*>(io.dy),
                      static_cast<const S*>(io.x), io.w, io.w_dtype, io.mean, io.rstd, io.T, io.H,
-                     p.rows, p.chunks, static_cast<S*>(io.dx), part, io.B);
+                     p.rows, p.chunks, static_cast<S*>(io.dx), part, io.B, tickets);
 }
 
 template <class DT, int VEC>
-void launch_ln_bwd_v(int epl, const RedPlan& p, const LnBwdIo& io, float* part, hipStream_t s) {
+void launch_ln_bwd_v(int epl, const RedPlan& p, const LnBwdIo& io, float* part,
+                     unsigned* tickets, hipStream_t s) {
   switch (epl) {
-    case 8: launch_ln_bwd_t<DT, 8, VEC>(p, io, part, s); break;
-    case 16: launch_ln_bwd_t<DT, 16, VEC>(p, io, part, s); break;
-    case 32: launch_ln_bwd_t<DT, 32, VEC>(p, io, part, s); break;
-    default: launch_ln_bwd_t<DT, 64, VEC>(p, io, part, s); break;
+    case 8: launch_ln_bwd_t<DT, 8, VEC>(p, io, part, tickets, s); break;
+    case 16: launch_ln_bwd_t<DT, 16, VEC>(p, io, part, tickets, s); break;
+    case 32: launch_ln_bwd_t<DT, 32, VEC>(p, io, part, tickets, s); break;
+    default: launch_ln_bwd_t<DT, 64, VEC>(p, io, part, tickets, s); break;
   }
 }
 
 template <class DT>
 void launch_ln_bwd(bool vec, int epl, const RedPlan& p, const LnBwdIo& io, float* part,
-                   hipStream_t s) {
-  if (!vec) launch_ln_bwd_v<DT, 1>(epl, p, io, part, s);
-  else if constexpr (DT::code == FDP_F32) launch_ln_bwd_v<DT, 4>(epl, p, io, part, s);
-  else launch_ln_bwd_v<DT, 8>(epl, p, io, part, s);
+                   unsigned* tickets, hipStream_t s) {
+  if (!vec) launch_ln_bwd_v<DT, 1>(epl, p, io, part, tickets, s);
+  else if constexpr (DT::code == FDP_F32) launch_ln_bwd_v<DT, 4>(epl, p, io, part, tickets, s);
+  else launch_ln_bwd_v<DT, 8>(epl, p, io, part, tickets, s);
 }
 
 bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
@@ -890,9 +1081,10 @@ extern "C" int fdp_layernorm_bwd_clip(const void* dy, const void* x, const void*
   const int epl = ln_epl(H);
   const LnBwdIo io{dy, x, w, w_dtype, mean, rstd, B, T, H, dx};
   float* part = reinterpret_cast<float*>(ws + p.off_part);
-  if (dtype == FDP_BF16) launch_ln_bwd<BF16>(vec, epl, p, io, part, s);
-  else if (dtype == FDP_F16) launch_ln_bwd<F16>(vec, epl, p, io, part, s);
-  else launch_ln_bwd<F32>(vec, epl, p, io, part, s);
+  unsigned* tickets = reinterpret_cast<unsigned*>(ws + p.off_ticket);
+  if (dtype == FDP_BF16) launch_ln_bwd<BF16>(vec, epl, p, io, part, tickets, s);
+  else if (dtype == FDP_F16) launch_ln_bwd<F16>(vec, epl, p, io, part, tickets, s);
+  else launch_ln_bwd<F32>(vec, epl, p, io, part, tickets, s);
   const fdp_noise_key* key = noise_scale != 0.f ? noise_key : nullptr;
   const Epilogue e{C,        clamp,
                    clip_args_dev,

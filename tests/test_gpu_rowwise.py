@@ -22,9 +22,12 @@ def randn(shape, dtype, seed, scale=1.0):
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=str)
 @pytest.mark.parametrize("shape", [(8, 1024, 768), (3, 7, 100), (2, 33, 2304), (5, 1, 9),
-                                   (16, 64, 3072)], ids=lambda s: "x".join(map(str, s)))
+                                   (16, 64, 3072), (24, 16, 3000), (40, 8, 2050)],
+                         ids=lambda s: "x".join(map(str, s)))
 @pytest.mark.parametrize("norm", ["frob", "sum"])
 def test_colsum_parity(shape, norm, dtype):
+    """B*H up to 65536 takes the one-launch reduction, larger the two-launch one
+    (the last two shapes; 2050 columns are not a multiple of 4)."""
     B, T, H = shape
     u = randn(shape, dtype, 1, 0.02)
     v = randn(shape, dtype, 2) if norm == "sum" else None
@@ -71,8 +74,11 @@ def test_layernorm_fwd_parity(H, dtype):
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=str)
 @pytest.mark.parametrize("shape", [(16, 1024, 1024), (4, 33, 768), (2, 5, 100), (3, 64, 4096),
-                                   (1, 1, 64)], ids=lambda s: "x".join(map(str, s)))
+                                   (1, 1, 64), (20, 8, 4096), (70, 3, 1000)],
+                         ids=lambda s: "x".join(map(str, s)))
 def test_layernorm_bwd_parity(shape, dtype):
+    """B*H up to 65536 takes the one-launch reduction, larger the two-launch one
+    (the last two shapes)."""
     B, T, H = shape
     x = randn(shape, dtype, 8)
     w = randn((H,), dtype, 9)
