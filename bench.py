@@ -47,7 +47,7 @@ PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 TRAFFIC_BYTES = {
     "cfg2": 176559938,   # profiles/wgrad_group_kernel_cfg2.md
     "cfg3": 229808557,   # profiles/wgrad_group_kernel_cfg3.md
-    "cfg4": 105519248,   # profiles/layernorm_bwd_clip_cfg4.md (3 kernels of one call)
+    "cfg4": 105494739,   # profiles/layernorm_bwd_clip_cfg4.md (2 kernels of one call)
 }
 
 
