@@ -309,14 +309,21 @@ def extra_measurements(dev, steps, warmup):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=None,
+                    help="timed steps (default 200; cfg5: 5)")
+    ap.add_argument("--warmup", type=int, default=None,
+                    help="untimed warm-up steps (default 100, enough for the clocks to settle; "
+                         "cfg5: 2)")
     ap.add_argument("--workload", default="cfg2", choices=["cfg2", "cfg3", "cfg4", "cfg5"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MiB",
                     help="also run one plain device copy of this size (for PMC byte calibration)")
     args = ap.parse_args()
+    if args.steps is None:
+        args.steps = 5 if args.workload == "cfg5" else 200
+    if args.warmup is None:
+        args.warmup = 2 if args.workload == "cfg5" else 100
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the DP hot path here is single-GPU "
               "(multi-GPU sharding is a design note, not part of this build).", file=sys.stderr)
