@@ -160,7 +160,9 @@ def wgrad_clip(a: torch.Tensor, b: torch.Tensor, C: float = 1.0, clamp_value: fl
     if check:
         status = ws[:4].view(torch.int32)
         if int(status.item()) != 0:
-            status.zero_()  # the status word is sticky on a reused workspace
+            # the status word is sticky on a reused workspace, and an expired
+            # wait can leave other control words set: clear them all
+            ws[:_lib.WGRAD_CONTROL_BYTES].zero_()
             raise _lib.FlashDPError("fdp_wgrad_clip: an inter-workgroup wait timed out")
     if return_stats:
         return out, norms, factors

@@ -428,6 +428,7 @@ extern "C" int fdp_wgrad_clip(const void* a, const void* b, int64_t B, int64_t K
   args.units = int64_t(pl.tiles) * B;
   args.err = reinterpret_cast<int*>(ws);
   args.bar = reinterpret_cast<unsigned*>(ws) + 1;
+  args.pair_flag = reinterpret_cast<unsigned*>(ws) + kPairFlag0;
   args.spin_limit = spin_limit();
   args.tile_turn = reinterpret_cast<unsigned*>(ws + pl.off_turn);
   args.tile_acc = reinterpret_cast<float*>(ws + pl.off_slots);

@@ -15,6 +15,7 @@ constexpr int BN = 128;
 constexpr int NT = 256;
 
 constexpr int kPermMax = 1024;  // workgroups whose order the single-pass launch sets
+constexpr int kPairMax = 256;   // split products per single-pass launch
 
 struct Args {
   const void* a;
@@ -51,6 +52,14 @@ struct Args {
   float* chunk_acc;       // [M, N] fp32 running sum carried between chunks
   int gq, gr;             // groups per tile (gr tiles have gq + 1)
   uint16_t perm[kPermMax];  // hardware workgroup -> work list index
+  // Split products (single pass): the last product of each "owner" list entry
+  // is contracted over its first split_k1 k-tiles by the owner and over the
+  // rest by a "helper" entry of another CU; the r-th owner (in list order)
+  // pairs with the r-th helper.  split_k1 == 0: no split products.
+  uint32_t owner_mask[kPermMax / 32];
+  uint32_t helper_mask[kPermMax / 32];
+  unsigned* pair_flag;    // [kPairMax] helper -> owner hand-over flags
+  int split_k1;
 };
 
 // ------------------------------------------------------------------ 16-bit
@@ -748,6 +757,73 @@ __device__ inline void finish_rows(const Args& p, const Assign& as, int64_t m0, 
   }
 }
 
+// List-index bit sets of the split products (Args::owner_mask / helper_mask).
+__device__ __forceinline__ bool mask_has(const uint32_t* m, int j) {
+  return (m[j >> 5] >> (j & 31)) & 1u;
+}
+// Entries of the set below j.
+__device__ inline int mask_rank(const uint32_t* m, int j) {
+  int r = 0;
+  for (int w = 0; w < (j >> 5); ++w) r += __builtin_popcount(m[w]);
+  return r + __builtin_popcount(m[j >> 5] & ((1u << (j & 31)) - 1u));
+}
+// The r-th entry of the set, or -1.
+__device__ inline int mask_select(const uint32_t* m, int r) {
+  for (int w = 0; w < kPermMax / 32; ++w) {
+    uint32_t x = m[w];
+    const int c = __builtin_popcount(x);
+    if (r < c) {
+      for (; r > 0; --r) x &= x - 1u;  // drop the r lowest set bits
+      return w * 32 + __builtin_ctz(x);
+    }
+    r -= c;
+  }
+  return -1;
+}
+
+// Hand-over of a split product through an exchange slot: each thread's 64
+// accumulators as 32 bf16 pairs (RNE), in 16-byte chunks q at byte
+// (q * NT + thread) * 16, agent-coherent.
+__device__ inline void hand_over(const float* slot, const f32x16 (&acc)[2][2]) {
+  const CoherentSpan sp(slot, BM * BN * 2);
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const int q = (i * 2 + j) * 2 + half;
+        u32x4 w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 8 * half + 2 * e;
+          w[e] = uint32_t(BF16::from_f32(acc[i][j][r])) |
+                 (uint32_t(BF16::from_f32(acc[i][j][r + 1])) << 16);
+        }
+        sp.store4(static_cast<uint32_t>((q * NT + threadIdx.x) * 16), __builtin_bit_cast(f32x4, w));
+      }
+}
+// acc += the product handed over in the slot.
+__device__ inline void take_over(const float* slot, f32x16 (&acc)[2][2]) {
+  const CoherentSpan sp(slot, BM * BN * 2);
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const int q = (i * 2 + j) * 2 + half;
+        const u32x4 w = __builtin_bit_cast(
+            u32x4, sp.load4(static_cast<uint32_t>((q * NT + threadIdx.x) * 16)));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 8 * half + 2 * e;
+          acc[i][j][r] += __uint_as_float(w[e] << 16);
+          acc[i][j][r + 1] += __uint_as_float(w[e] & 0xffff0000u);
+        }
+      }
+}
+
 // Workgroups of the grid run their nb products, keeping the finished ones
 // packed in registers and the last one live in its accumulators; each
 // product's sum of squares goes to partials[sample, tile].  After the grid
@@ -774,7 +850,8 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
   const int tiles = p.tiles_m * p.tiles_n;
-  const Assign as = assign_of(p, list_index(p, blockIdx.x));
+  const int me = list_index(p, blockIdx.x);
+  const Assign as = assign_of(p, me);
   const int nb = as.nb;
   const int nk = static_cast<int>((p.K + G::BK - 1) / G::BK);
   dma::FragOffsets<G> fo;
@@ -788,9 +865,24 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
   const uint16_t* pa = static_cast<const uint16_t*>(p.a);
   const uint16_t* pb = static_cast<const uint16_t*>(p.b);
   Held<true> held[U > 1 ? U - 1 : 1];
-  f32x16 acc[2][2];
-  zero(acc);
-  const int nq = nb * nk;
+  // Split product (see pair_products): an owner's last unit covers k-tiles
+  // [0, k1) of its last sample; a helper first runs k-tiles [k1, nk) of its
+  // owner's last sample and tile, then its own units.
+  const int k1 = p.split_k1;
+  int role = 0, pair = 0, owner = me;  // role 1: owner, 2: helper
+  if (k1 > 0 && nb > 0) {
+    if (mask_has(p.owner_mask, me)) {
+      role = 1;
+      pair = mask_rank(p.owner_mask, me);
+    } else if (mask_has(p.helper_mask, me)) {
+      pair = mask_rank(p.helper_mask, me);
+      owner = mask_select(p.owner_mask, pair);
+      role = owner >= 0 ? 2 : 0;
+      if (owner < 0) owner = me;
+    }
+  }
+  auto unit_nk = [&](int u) { return role == 1 && u == nb - 1 ? k1 : nk; };
+  const int nq = role == 1 ? (nb - 1) * nk + k1 : nb * nk;
   dma::Job<G> job;  // loads of k-tile ik of unit iu, the next one to issue
   int iu = 0, ik = 0;
   int64_t m0, n0;
@@ -802,14 +894,38 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
   const int r0 = (as.g * BM) / as.ng, r1 = ((as.g + 1) * BM) / as.ng;
   float zpre[kFinishChunks][8] = {};
   const bool early = nb < U;
-  if (nq > 0) job.init(pa + as.b0 * p.sab, p.lda, pb + as.b0 * p.sbb, p.ldb, p.K, m0, n0);
+  f32x16 acc[2][2];
+  zero(acc);
+  if (role == 2) {
+    // helper: k-tiles [k1, nk) of the owner's last product first, handed over
+    // through the owner's exchange slot, then the hand-over flag
+    const Assign oa = assign_of(p, owner);
+    int64_t om0, on0;
+    tile_coords(p, oa.tile, om0, on0);
+    const int64_t ob = oa.b0 + oa.nb - 1;
+    const int64_t kr = int64_t(k1) * G::BK;
+    job.init(pa + ob * p.sab + kr * p.lda, p.lda, pb + ob * p.sbb + kr * p.ldb, p.ldb, p.K - kr,
+             om0, on0);
+    dma::gemm<DT, G, kStages>(job, nk - k1, fo, stages, acc);
+    hand_over(slot_of(p, owner), acc);
+    zero(acc);
+    wait_stores();  // (the ring's first wait below would drain them anyway)
+    __syncthreads();
+    if (threadIdx.x == 0)
+      __hip_atomic_store(p.pair_flag + pair, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    FDP_TS(8);
+  }
+  if (nq > 0)
+    job.init(pa + as.b0 * p.sab, p.lda, pb + as.b0 * p.sbb, p.ldb,
+             role == 1 && nb == 1 ? int64_t(k1) * G::BK : p.K, m0, n0);
   auto issue_next = [&](FDP_LDS char* stage) {
     job.issue(stage, ik);
-    if (++ik == nk) {
+    if (++ik == unit_nk(iu)) {
       ik = 0;
       if (++iu < nb) {
         const int64_t b = as.b0 + iu;
-        job.retarget(pa + b * p.sab, p.lda, pb + b * p.sbb, p.ldb, p.K);
+        job.retarget(pa + b * p.sab, p.lda, pb + b * p.sbb, p.ldb,
+                     role == 1 && iu == nb - 1 ? int64_t(k1) * G::BK : p.K);
       }
     }
   };
@@ -828,33 +944,57 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
         dma::barrier();
         if (q + kStages - 1 < nq) issue_next(stages.get((s + kStages - 1) % kStages));
         dma::compute_stage<DT, G>(stages.get(s), fo, acc);
-        if (++ck == nk) {
-          // unit cu done.  Rows/columns past M/N may hold the next row's
-          // values: leave them out of the norm.
-          float sq = 0.f;
+        if (++ck == unit_nk(cu)) {
+          {
+            const int own = cu;
+            // Rows/columns past M/N may hold the next row's values: leave
+            // them out of the norm.
+            float sq = 0.f;
 #pragma unroll
-          for (int a = 0; a < 2; ++a)
+            for (int a = 0; a < 2; ++a)
 #pragma unroll
-            for (int c = 0; c < 2; ++c) {
-              const bool ncol = n0 + acc_col(wn, c, lane) < p.N;
+              for (int c = 0; c < 2; ++c) {
+                const bool ncol = n0 + acc_col(wn, c, lane) < p.N;
 #pragma unroll
-              for (int r = 0; r < 16; ++r) {
-                const bool in = ncol && (m0 + acc_row(wm, a, lane, r) < p.M);
-                sq += in ? acc[a][c][r] * acc[a][c][r] : 0.f;
+                for (int r = 0; r < 16; ++r) {
+                  const bool in = ncol && (m0 + acc_row(wm, a, lane, r) < p.M);
+                  sq += in ? acc[a][c][r] * acc[a][c][r] : 0.f;
+                }
+              }
+            sq = wave_sum(sq);
+            if (lane == 0) red[wave] = sq;
+            __syncthreads();
+            if (threadIdx.x == 0)
+              st_coherent(p.partials + (as.b0 + own) * tiles + as.tile,
+                          (red[0] + red[1]) + (red[2] + red[3]));
+            FDP_TS(1 + own);
+            if (own + 1 < nb) {  // park it and start the next product
+#pragma unroll
+              for (int j = 0; j < U - 1; ++j)
+                if (j == own) held[j].put(acc);
+              zero(acc);
+              if (role == 1 && own + 2 == nb) {
+                // owner: the last product starts from the helper's share (its
+                // load latency overlaps that of the product's first k-tiles)
+                if (threadIdx.x == 0) {
+                  unsigned spins = 0;
+                  while (__hip_atomic_load(p.pair_flag + pair, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT) == 0u) {
+                    __builtin_amdgcn_s_sleep(kPollSleep);
+                    if (++spins > p.spin_limit) {
+                      atomicOr(p.err, 1);  // every workgroup's results are poisoned
+                      break;
+                    }
+                  }
+                }
+                __syncthreads();
+                take_over(slot_of(p, me), acc);
+                if (threadIdx.x == 0)
+                  __hip_atomic_store(p.pair_flag + pair, 0u, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
+                FDP_TS(11);
               }
             }
-          sq = wave_sum(sq);
-          if (lane == 0) red[wave] = sq;
-          __syncthreads();
-          if (threadIdx.x == 0)
-            st_coherent(p.partials + (as.b0 + cu) * tiles + as.tile,
-                        (red[0] + red[1]) + (red[2] + red[3]));
-          FDP_TS(1 + cu);
-          if (cu + 1 < nb) {  // park it and start the next product
-#pragma unroll
-            for (int j = 0; j < U - 1; ++j)
-              if (j == cu) held[j].put(acc);
-            zero(acc);
           }
           ck = 0;
           ++cu;
@@ -879,9 +1019,13 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
   // CU runs its last product faster than two sharing the CU, and a late wake-up
   // delays this tile's exchange).
   uint64_t quiet = 0;
-  if (nb > 0 && nb < U) {
-    const uint64_t now = wall_clock64();
-    quiet = now + (now - t_begin) * uint64_t(3 * (U - nb)) / uint64_t(5 * nb);
+  {
+    // in half products: the most loaded workgroups' work and this one's
+    const int most = 2 * U - (k1 > 0 ? 1 : 0), mine = 2 * nb + (role == 1 ? -1 : role == 2 ? 1 : 0);
+    if (nb > 0 && mine < most) {
+      const uint64_t now = wall_clock64();
+      quiet = now + (now - t_begin) * uint64_t(3 * (most - mine)) / uint64_t(5 * mine);
+    }
   }
   const unsigned arrival = grid_arrive(p.bar);
   if (early) noise_rows(p, m0, n0, r0, r1, zpre);
@@ -1011,7 +1155,12 @@ __global__ __launch_bounds__(NT) void clear_words_kernel(unsigned* p, int64_t n)
 
 // ---------------------------------------------------------- single-pass launch
 using KernelFn = void (*)(Args);
-constexpr size_t kWsHead = 256;   // err / barrier words at the head of the workspace
+// Control words at the head of the workspace, zero between calls: word 0 the
+// status word, word 1 the grid-barrier counter, words [kPairFlag0,
+// kPairFlag0 + kPairMax) the split-product flags.
+constexpr size_t kWsHead = 2048;
+constexpr int kPairFlag0 = 64;
+static_assert((kPairFlag0 + kPairMax) * sizeof(unsigned) <= kWsHead, "control words");
 constexpr int kGroupUnits = 4;    // samples held by one workgroup at most
 
 // Single-pass schedule for B samples over `tiles` 128x128 tiles on `slots`
@@ -1115,6 +1264,59 @@ inline void order_workgroups(const Args& c, int cus, uint16_t* perm) {
   }
 }
 
+// Split products.  With W = 2*CUs workgroups and entries of two sizes,
+// order_workgroups puts each most-loaded entry ("heavy", umax products) on a CU
+// of its own beside a lighter one, and the remaining lighter entries two to a
+// CU.  A CU with a heavy entry then carries one product more than a CU with
+// two light ones, and runs that product alone at the lone-workgroup rate.  Each
+// heavy entry ("owner") therefore contracts its last product over only the
+// first split_k1 k-tiles; the first lighter entry of a light-light CU
+// ("helper") contracts the rest, before its own products, and hands the
+// partial product over as bf16 through the owner's exchange slot.  Every CU
+// then carries umax + umin - 1/2 products.  The r-th owner in list order
+// pairs with the r-th helper.  No split when the counts differ, the grid is
+// not 2*CUs, or there are fewer than two k-tiles.
+inline void pair_products(Args& c, int cus) {
+  for (int w = 0; w < kPermMax / 32; ++w) c.owner_mask[w] = c.helper_mask[w] = 0u;
+  c.split_k1 = 0;
+  const int W = c.nwg;
+  const int nk = static_cast<int>((c.K + 63) / 64);
+  if (W != 2 * cus || W > kPermMax || nk < 2) return;
+  const int nb = static_cast<int>(c.chunk_nb), q = c.gq, big = c.gr * (q + 1);
+  auto units_of = [&](int j) {
+    int g, ng;
+    if (j < big) {
+      ng = q + 1;
+      g = j % ng;
+    } else {
+      ng = q;
+      g = (j - big) % q;
+    }
+    return ((g + 1) * nb) / ng - (g * nb) / ng;
+  };
+  int umax = 0, umin = 1 << 30;
+  for (int j = 0; j < W; ++j) {
+    const int u = units_of(j);
+    umax = u > umax ? u : umax;
+    umin = u < umin ? u : umin;
+  }
+  if (umax == umin || umin < 1) return;
+  int owners = 0, helpers = 0;
+  for (int j = 0; j < W; ++j)
+    if (units_of(j) == umax) ++owners;
+  for (int h = 0; h < cus; ++h)
+    if (units_of(c.perm[h]) < umax && units_of(c.perm[h + cus]) < umax) ++helpers;
+  if (owners == 0 || owners != helpers || owners > kPairMax) return;
+  for (int j = 0; j < W; ++j)
+    if (units_of(j) == umax) c.owner_mask[j / 32] |= 1u << (j % 32);
+  for (int h = 0; h < cus; ++h)
+    if (units_of(c.perm[h]) < umax && units_of(c.perm[h + cus]) < umax) {
+      const int j = c.perm[h];
+      c.helper_mask[j / 32] |= 1u << (j % 32);
+    }
+  c.split_k1 = nk / 2;
+}
+
 // `plain`: ordinary dispatch instead of a cooperative launch (the caller
 // guarantees that nothing else occupies the device during the call, so the
 // grid, sized to the computed occupancy, is resident at once).  `clean`: the
@@ -1141,6 +1343,7 @@ hipError_t try_grouped(Args a, int cus, bool plain, bool clean, hipStream_t s) {
     c.chunk_first = b0 == 0;
     c.chunk_last = b0 + c.chunk_nb >= a.B;
     order_workgroups(c, cus, c.perm);
+    pair_products(c, cus);
     KernelFn fn = grouped[ls.units - 1];
     int occ = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void*>(fn), NT,

@@ -133,16 +133,17 @@ int fdp_version(void);
  *            grid wait (seconds) still expire, the affected outputs (and
  *            norms/factors) are NaN and the status word below is set;
  *            bit 3 (FDP_WGRAD_CLEAN_WORKSPACE) states that the workspace's
- *            control words (its first 256 bytes) are zero -- a zero-filled
+ *            control words (its first 2048 bytes) are zero -- a zero-filled
  *            buffer, or one whose last use was a completed fdp_wgrad_clip call
- *            (of any shape), which always leaves them zero (the status word
- *            excepted) -- so the library skips clearing them.
+ *            (of any shape) whose status word stayed zero, which always
+ *            leaves them zero -- so the library skips clearing them.
  * workspace: device buffer of at least fdp_wgrad_clip_workspace_size() bytes,
  *            16-byte aligned.  Its first int is a status word: nonzero after
  *            the call completes means a bounded inter-workgroup wait of the
  *            single-pass kernel expired (results are then invalid).  With
- *            FDP_WGRAD_CLEAN_WORKSPACE the word is sticky: the caller resets
- *            it after reading a nonzero value.
+ *            FDP_WGRAD_CLEAN_WORKSPACE the word is sticky: after reading a
+ *            nonzero value the caller zeroes the first 2048 bytes (an expired
+ *            wait can leave other control words set).
  * ---------------------------------------------------------------------- */
 #define FDP_WGRAD_NOCLIP 1
 #define FDP_WGRAD_TWO_PASS 2

@@ -59,6 +59,31 @@ def test_wgrad_parity(shape, layout, dtype, path):
     assert_close(out2, ref, dtype, "out (input dtype)")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=str)
+@pytest.mark.parametrize("shape", [(8, 128, 3072, 768), (8, 200, 3000, 760)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_wgrad_split_products(shape, dtype):
+    """144 tiles x 8 samples on 512 workgroups: the 128 workgroups holding three
+    products each contract the last one over its first half of K only, and a
+    workgroup of a CU holding two lighter ones contracts the rest and hands it
+    over (2 and 4 k-tiles, a partial last k-tile, ragged tiles; the full cfg2
+    shape, K = 1024, is test_wgrad_cfg2_full_size).  Parity, norms, factors and
+    bitwise-equal repeats, in both launch modes."""
+    B, K, M, N = shape
+    a, b = make(B, K, M, N, dtype, "tn", seed=21)
+    _, n0, _ = O.wgrad_clip(a, b, 1.0, 1.0, "tn")
+    C = float(np.median(n0))
+    ref, nref, fref = O.wgrad_clip(a, b, C, 1.0, "tn")
+    for launch in ("plain", "cooperative"):
+        out, n, f = core.wgrad_clip(a, b, C, 1.0, out_dtype=torch.float32, return_stats=True,
+                                    launch=launch, check=True)
+        assert_close(out, ref, dtype, "out")
+        assert_elementwise(n, nref, dtype, "norms")
+        assert_elementwise(f, fref, dtype, "factors")
+        again = core.wgrad_clip(a, b, C, 1.0, out_dtype=torch.float32, launch=launch, check=True)
+        assert torch.equal(out, again)
+
+
 @pytest.mark.parametrize("dtype", DTYPES, ids=str)
 def test_wgrad_scale_noise_and_device_clip_args(dtype):
     B, K, M, N = 4, 96, 192, 160
@@ -106,7 +131,7 @@ def test_wgrad_deterministic(two_pass):
 def test_wgrad_reused_workspace_stays_clean(shape):
     """Calls that reuse one workspace without clearing it (FDP_WGRAD_CLEAN_WORKSPACE)
     match a call on a garbage-filled workspace that the library clears, and leave
-    the control words (the first 256 bytes) zero.  Tiles are shared by groups and a
+    the control words (the first 2048 bytes) zero.  Tiles are shared by groups and a
     call makes several launches; the tile tickets after the head are cleared by the
     kernel itself, so the dirty workspace's tickets start as garbage."""
     import ctypes
@@ -134,7 +159,7 @@ def test_wgrad_reused_workspace_stays_clean(shape):
         out = call(clean, _lib.WGRAD_CLEAN_WORKSPACE)
         torch.cuda.synchronize()
         assert torch.equal(out, ref)
-        assert torch.count_nonzero(clean[:256]) == 0
+        assert torch.count_nonzero(clean[:_lib.WGRAD_CONTROL_BYTES]) == 0
     exp, _, _ = O.wgrad_clip(a, b, 0.05, 1.0, "tn")
     assert_close(ref, exp, torch.bfloat16, "clipped sum")
 
