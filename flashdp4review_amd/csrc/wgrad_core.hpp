@@ -581,21 +581,33 @@ __device__ __forceinline__ float* staged_row(float* const (&q)[4], int r) {
   return quarter(q, r >> 5) + (r & 31) * BN;
 }
 
-// Noise for the 8 outputs (row m, columns n .. n+7 of the problem), unscaled;
-// entries past N are left alone.  Only the last launch of a batch adds noise.
-__device__ inline void noise8(const Args& p, int64_t m, int64_t n, float (&z)[8]) {
-  const NoiseSrc nz = p.noise;  // a value copy: no address of the kernel argument is taken
-  if (!p.chunk_last || !nz.on()) return;
-  const bool whole = n + 8 <= p.N;
-  if (whole && nz.z == nullptr && p.N % 4 == 0) {
-    nz.run(m * p.N + n, z);
+// Noise for the 8 outputs (row m, columns n .. n+7 of a row of length N),
+// unscaled; entries past N are zero.  Out of line: the Philox rounds are long,
+// and an inlined copy per call site made the single-pass kernel hundreds of KB.
+struct Z8 {
+  float v[8];
+};
+__device__ __attribute__((noinline)) Z8 noise8_draw(NoiseSrc nz, int64_t N, int64_t m, int64_t n) {
+  Z8 z = {};
+  const bool whole = n + 8 <= N;
+  if (whole && nz.z == nullptr && N % 4 == 0) {
+    nz.run(m * N + n, z.v);
   } else if (whole && nz.z == nullptr) {
-    nz.window(m * p.N + n, z);
+    nz.window(m * N + n, z.v);
   } else {
 #pragma unroll
     for (int e = 0; e < 8; ++e)
-      if (n + e < p.N) z[e] = nz.at(m * p.N + n + e);
+      if (n + e < N) z.v[e] = nz.at(m * N + n + e);
   }
+  return z;
+}
+// Only the last launch of a batch adds noise.
+__device__ inline void noise8(const Args& p, int64_t m, int64_t n, float (&z)[8]) {
+  const NoiseSrc nz = p.noise;  // a value copy: no address of the kernel argument is taken
+  if (!p.chunk_last || !nz.on()) return;
+  const Z8 d = noise8_draw(nz, p.N, m, n);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) z[e] = d.v[e];
 }
 
 // Final values of 8 consecutive outputs (row m, columns n .. n+7 of the
