@@ -60,7 +60,7 @@ def set_wgrad_launch(mode: str) -> str:
     (``check=True`` raises): results are never silently wrong.
     "cooperative": hipLaunchCooperativeKernel, which guarantees co-residency
     at the cost of the runtime's synchronisation around each launch (about
-    25 us per call on MI355X); use it when another kernel running at the
+    15 us per call on MI355X); use it when another kernel running at the
     same time may wait on this one.
     """
     global _launch_mode
