@@ -906,6 +906,11 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
   const int r0 = (as.g * BM) / as.ng, r1 = ((as.g + 1) * BM) / as.ng;
   float zpre[kFinishChunks][8] = {};
   const bool early = nb < U;
+  // The more loaded workgroup of a CU issues first (wave priority), so that
+  // the two of a CU finish their products together instead of the more loaded
+  // one running its last stretch alone.
+  const bool loaded = k1 > 0 ? role != 0 : nb == U;
+  if (loaded) __builtin_amdgcn_s_setprio(2);
   f32x16 acc[2][2];
   zero(acc);
   if (role == 2) {
@@ -1039,6 +1044,7 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
       quiet = now + (now - t_begin) * uint64_t(3 * (most - mine)) / uint64_t(5 * mine);
     }
   }
+  if (loaded) __builtin_amdgcn_s_setprio(0);
   const unsigned arrival = grid_arrive(p.bar);
   if (early) noise_rows(p, m0, n0, r0, r1, zpre);
   bool poisoned = grid_wait(p.bar, unsigned(p.nwg), arrival, p.err, p.spin_limit, &flag, quiet);
