@@ -577,6 +577,20 @@ __device__ __forceinline__ float* quarter(float* const (&q)[4], int i) {
     default: return q[3];
   }
 }
+// The 8 staged floats [col, col+8) of a row (col a multiple of 8), as two
+// 16-byte reads.  The 16 lanes reading one row take chunks 32 bytes apart, so
+// the chunks of the row's upper half read their second half first: each read
+// then covers all 64 banks once.
+__device__ __forceinline__ void staged8(const float* row, int col, float (&v)[8]) {
+  const bool up = (col & 64) != 0;
+  const f32x4 a = *reinterpret_cast<const f32x4*>(row + col + (up ? 4 : 0));
+  const f32x4 b = *reinterpret_cast<const f32x4*>(row + col + (up ? 0 : 4));
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    v[e] = up ? b[e] : a[e];
+    v[4 + e] = up ? a[e] : b[e];
+  }
+}
 __device__ __forceinline__ float* staged_row(float* const (&q)[4], int r) {
   return quarter(q, r >> 5) + (r & 31) * BN;
 }
@@ -710,9 +724,7 @@ __device__ inline void finish_rows(const Args& p, const Assign& as, int64_t m0, 
       const int c = c0 + k * NT;
       const int r = r0 + c / (BN / 8), col = (c % (BN / 8)) * 8;
       if (c < nchunks) {
-        const float* own = staged_row(q4, r) + col;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[k][e] = own[e];
+        staged8(staged_row(q4, r), col, v[k]);
       }
     }
     for (int gb = 0; gb < as.ng; gb += kSlotBatch + 1) {
@@ -1116,7 +1128,8 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
     for (int c = threadIdx.x; c < BM * (BN / 8); c += NT) {
       const int r = c / (BN / 8), col = (c % (BN / 8)) * 8;
       if (r >= r0 && r < r1) continue;
-      const float* src = staged_row(q4, r) + col;
+      float src[8];
+      staged8(staged_row(q4, r), col, src);
       u32x4 w;
 #pragma unroll
       for (int e = 0; e < 4; ++e)
