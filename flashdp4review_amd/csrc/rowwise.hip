@@ -76,6 +76,18 @@ __device__ __forceinline__ int64_t wave_elem(int lane, int i) {
   return (int64_t(lane) + 64 * i) * VEC;
 }
 
+// LDS position of element e of a wave's row in the LayerNorm backward fold.
+// A lane parks 8 consecutive elements, 32 bytes from the next lane's, so each
+// group of 8 is XOR-permuted by its lane's bits 3..5: every store of one
+// element per lane then covers the 64 banks once, and the fold's reads of 64
+// consecutive elements stay a permutation of one 64-float span.
+__host__ __device__ __forceinline__ int64_t fold_pos(int64_t e) {
+  return (e & ~int64_t(7)) | ((e & 7) ^ ((e >> 6) & 7));
+}
+// Floats per wave slice: the row rounded up to whole 128-float blocks, so that
+// every permuted group of 8 stays inside the slice.
+__host__ __device__ __forceinline__ int64_t fold_slice(int64_t H) { return (H + 127) / 128 * 128; }
+
 template <class DT, int EPL, int VEC>
 __device__ inline void load_row(const typename DT::storage* row, int64_t H, int lane,
                                 float (&o)[EPL]) {
@@ -705,25 +717,28 @@ __global__ __launch_bounds__(NTH) void ln_bwd_kernel(const typename DT::storage*
     store_row<DT, EPL, VEC>(dx + r * H, H, lane, gv);
   }
   // Fold the waves in order 0..W-1: every wave parks its row of P (then of
-  // Q) in its own LDS slice, and all threads sum the slices element-wise.
+  // Q) in its own LDS slice (fold_slice(H) floats, element e at fold_pos(e)),
+  // and all threads sum the slices element-wise.
   float* pP = partials + (b * chunks + chunk) * H;
   float* pQ = partials + ((B + b) * chunks + chunk) * H;
+  const int64_t slice = fold_slice(H);
 #pragma unroll
   for (int half = 0; half < 2; ++half) {
-    float* mine = lds + wave * H;
+    float* mine = lds + wave * slice;
 #pragma unroll
     for (int i = 0; i < EPL / VEC; ++i)
 #pragma unroll
       for (int j = 0; j < VEC; ++j) {
         const int64_t e = wave_elem<EPL, VEC>(lane, i) + j;
-        if (e < H) mine[e] = half == 0 ? P[i * VEC + j] : Q[i * VEC + j];
+        if (e < H) mine[fold_pos(e)] = half == 0 ? P[i * VEC + j] : Q[i * VEC + j];
       }
     __syncthreads();
     float* dst = half == 0 ? pP : pQ;
     for (int64_t e = threadIdx.x; e < H; e += NTH) {
-      float v = lds[e];
+      const int64_t at = fold_pos(e);
+      float v = lds[at];
 #pragma unroll
-      for (int ww = 1; ww < W; ++ww) v += lds[ww * H + e];
+      for (int ww = 1; ww < W; ++ww) v += lds[ww * slice + at];
       dst[e] = v;
     }
     __syncthreads();
@@ -953,7 +968,7 @@ void launch_ln_bwd_t(const RedPlan& p, const LnBwdIo& io, float* part, unsigned*
   using S = typename DT::storage;
   constexpr int NTH = ln_bwd_threads(EPL);
   hipLaunchKernelGGL((ln_bwd_kernel<DT, EPL, VEC, NTH>), dim3(p.chunks, io.B), dim3(NTH),
-                     sizeof(float) * (NTH / kWave) * io.H, s, static_cast<const S*>(io.dy),
+                     sizeof(float) * (NTH / kWave) * fold_slice(io.H), s, static_cast<const S*>(io.dy),
                      static_cast<const S*>(io.x), io.w, io.w_dtype, io.mean, io.rstd, io.T, io.H,
                      p.rows, p.chunks, static_cast<S*>(io.dx), part, io.B, tickets);
 }
