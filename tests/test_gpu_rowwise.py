@@ -74,7 +74,7 @@ def test_layernorm_fwd_parity(H, dtype):
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=str)
 @pytest.mark.parametrize("shape", [(16, 1024, 1024), (4, 33, 768), (2, 5, 100), (3, 64, 4096),
-                                   (1, 1, 64), (20, 8, 4096), (70, 3, 1000)],
+                                   (1, 1, 64), (20, 8, 4096), (70, 3, 1000), (3, 9, 1001)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_layernorm_bwd_parity(shape, dtype):
     """B*H up to 65536 takes the one-launch reduction, larger the two-launch one
