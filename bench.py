@@ -45,9 +45,9 @@ PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 # factor the same counter reads on a plain copy of known size.  None = not
 # measured for that workload.
 TRAFFIC_BYTES = {
-    "cfg2": 200963966,   # profiles/wgrad_group_kernel_cfg2.md
-    "cfg3": 229669923,   # profiles/wgrad_group_kernel_cfg3.md
-    "cfg4": 105497464,   # profiles/layernorm_bwd_clip_cfg4.md (2 kernels of one call)
+    "cfg2": 201179439,   # profiles/wgrad_group_kernel_cfg2.md
+    "cfg3": 229671862,   # profiles/wgrad_group_kernel_cfg3.md
+    "cfg4": 109712751,   # profiles/layernorm_bwd_clip_cfg4.md (2 kernels of one call)
 }
 
 
