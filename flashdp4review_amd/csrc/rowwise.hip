@@ -838,16 +838,17 @@ int ln_epl(int64_t H) {
 }
 
 
-// LayerNorm backward workgroup: 4 waves, about two workgroups per CU.  On a
-// 16x1024x1024 problem one, two and four per CU (16, 32 and 64 chunks per
-// sample) measured 28.6, 28.1 and 33.8 us per call: more chunks also mean
-// more partials for the reduction to read.
+// LayerNorm backward workgroup: 4 waves, about two workgroups per CU, with
+// chunks of at least 32 rows.  On a 16x1024x1024 problem one, two and four
+// per CU (chunks of 64, 32 and 16 rows) measured 28.6, 28.1 and 33.8 us per
+// call: a chunk's partials cost 8H bytes against its 6·rows·H bytes of rows,
+// and more chunks also mean more partials for the reduction to read.
 constexpr int ln_bwd_threads(int) { return 256; }
 
 RedPlan ln_plan(int64_t B, int64_t T, int64_t H, int cus) {
   RedPlan p{};
   p.cblocks = 1;
-  split_rows(p, B, T, cus, 2, 16);
+  split_rows(p, B, T, cus, 2, 32);
   finish_plan(p, B, H, 2);
   return p;
 }
