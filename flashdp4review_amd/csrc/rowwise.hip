@@ -815,6 +815,10 @@ void split_rows(RedPlan& p, int64_t B, int64_t T, int cus, int per_cu, int64_t m
   p.chunks = static_cast<int>(T > 0 ? (T + p.rows - 1) / p.rows : 1);
 }
 
+// Column sums: about four workgroups per CU, with chunks of at least 64 rows.
+// A chunk's fp32 partials cost 4H bytes against its 2·rows·H bytes of 16-bit
+// rows; on 8x1024xH bf16 bias gradients (H = 2048 .. 8192) minimums of 8 and
+// 128 rows measured 5-18% and 0-45% slower than 64.
 RedPlan col_plan(int64_t B, int64_t T, int64_t H, int dtype, int cus, bool aligned) {
   RedPlan p{};
   p.vec = aligned ? 16 / esize(dtype) : 1;
@@ -823,7 +827,7 @@ RedPlan col_plan(int64_t B, int64_t T, int64_t H, int dtype, int cus, bool align
   if (bs > NT) bs = NT;
   p.bs = static_cast<int>(bs);
   p.cblocks = static_cast<int>((nvec + bs - 1) / bs);
-  split_rows(p, B, T, cus, 4, 8);
+  split_rows(p, B, T, cus, 4, 64);
   finish_plan(p, B, H, 1);
   return p;
 }
