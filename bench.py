@@ -11,12 +11,13 @@ resident in HBM, default (ordinary-dispatch) launch.
 
 value = algorithmic TFLOP/s = 2*B*T*M*N / step time (norm, scale and recompute
 flops are not credited).  The JSON line also carries the roofline of the
-dominant kernel (wgrad_group_kernel: HIP events on the launch stream around
-back-to-back calls in ordinary-dispatch mode, where one call is exactly one
-launch of that kernel), the reference's torch op sequence timed on the host CPU
-(cpu_baseline), and extra measurements: the same step with the cooperative
-launch, the DP Linear layer fwd+bwd vs a plain nn.Linear, the Conv1D (cfg3)
-and LayerNorm (cfg4) paths.
+dominant kernel (its mean duration from a pair of HIP events around every call
+of the timed region, on the launch stream; one call is one launch), the host
+time per call, the reference's torch op sequence timed on the host CPU
+(cpu_baseline, bf16 and fp32), and extra measurements: the same step with the
+cooperative launch, the DP Linear layer fwd+bwd vs a plain nn.Linear, the
+Conv1D (cfg3) and LayerNorm (cfg4) paths, and DP vs non-DP training tokens/s of
+the cfg5 decoder.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload cfg2|cfg3|cfg4]
                        [--no-cpu-baseline] [--no-extra] [--copy-calibration MiB]
@@ -92,7 +93,7 @@ def cfg3_inputs(dev):
     return x, go
 
 
-def run_wgrad(x, go, out_dtype, sigma=1.0, transpose=False, launch=None):
+def run_wgrad(x, go, out_dtype, sigma=1.0, transpose=False, launch=None, single_pass="auto"):
     """One DP weight-gradient step: the fused clipped product sum with its noise
     drawn in the epilogue (a fresh Philox counter range every step)."""
     from flashdp4review_amd.core import wgrad_clip
@@ -105,35 +106,59 @@ def run_wgrad(x, go, out_dtype, sigma=1.0, transpose=False, launch=None):
 
     def step():
         return wgrad_clip(a, b, 1.0, 1.0, layout="tn", out_scale=1.0 / B, noise_scale=std,
-                          noise_key=keys.next(M * N), out_dtype=out_dtype, launch=launch)
+                          noise_key=keys.next(M * N), out_dtype=out_dtype, launch=launch,
+                          single_pass=single_pass)
 
     return step, step
 
 
 # --------------------------------------------------------------- cpu baseline
-def cpu_baseline_cfg2():
-    """The reference's torch path (flashdp/core/linear_clip.py:94-104 + layers/linear.py:72-80),
-    restated in oracle/torch_ref.py, on the host cores: full cfg2 batch in fp32."""
+def host_cores():
+    """Cores this process may run on (its CPU affinity set), and the machine's count."""
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:  # pragma: no cover
+        avail = os.cpu_count() or 1
+    return avail, os.cpu_count() or avail
+
+
+def _cpu_leg(dtype, budget_s):
+    """Median seconds per cfg2 step of the reference's torch op sequence in `dtype`."""
     from oracle import torch_ref
-    threads = min(16, os.cpu_count() or 1)
-    torch.set_num_threads(threads)
     g = torch.Generator().manual_seed(0)
-    x = torch.randn(8, 1024, 768, generator=g)
-    go = torch.randn(8, 1024, 3072, generator=g) * 0.02
-    F = 2.0 * 8 * 1024 * 3072 * 768
+    x = torch.randn(8, 1024, 768, generator=g).to(dtype)
+    go = (torch.randn(8, 1024, 3072, generator=g) * 0.02).to(dtype)
     torch_ref.linear_weight_backward(x, go, 1.0, 1.0, 1.0)  # warm-up
     ts = []
     t_start = time.perf_counter()
-    while len(ts) < 3 or (time.perf_counter() - t_start < 10.0 and len(ts) < 500):
+    while len(ts) < 3 or (time.perf_counter() - t_start < budget_s and len(ts) < 500):
         t0 = time.perf_counter()
         torch_ref.linear_weight_backward(x, go, 1.0, 1.0, 1.0)
         ts.append(time.perf_counter() - t0)
-    t = statistics.median(ts)
-    return {"value": round(F / t / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
+    return statistics.median(ts), len(ts)
+
+
+def cpu_baseline_cfg2():
+    """The reference's torch path (flashdp/core/linear_clip.py:94-104 + layers/linear.py:72-80),
+    restated in oracle/torch_ref.py, on every core this process may use: the full cfg2
+    batch in the config dtype (bf16) and in fp32.  `value` is the bf16 leg."""
+    threads, machine = host_cores()
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        t16, n16 = _cpu_leg(torch.bfloat16, 12.0)
+        t32, n32 = _cpu_leg(torch.float32, 8.0)
+    finally:
+        torch.set_num_threads(prev)
+    F = 2.0 * 8 * 1024 * 3072 * 768
+    return {"value": round(F / t16 / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
             "kind": "port",
-            "sample": "cfg2 full batch (B=8,T=1024,768->3072), fp32 on CPU, reference torch op "
-                      "sequence (per-sample einsum/norm/clamp/mul/sum, /B, normal add); "
-                      f"median of {len(ts)} steps (~10 s) after 1 warm-up, {t:.4f} s/step",
+            "sample": "cfg2 full batch (B=8,T=1024,768->3072) on CPU, reference torch op sequence "
+                      "(per-sample einsum/norm/clamp/mul/sum, /B, normal add), median step "
+                      f"after 1 warm-up: bf16 {t16:.4f} s/step over {n16} steps (value), "
+                      f"fp32 {t32:.4f} s/step over {n32} steps",
+            "fp32_value": round(F / t32 / 1e12, 4),
+            "machine_cores": machine,
             "cpu_model": platform.processor() or platform.machine()}
 
 
@@ -201,7 +226,7 @@ def gpt_model(n_layer=24, d=2048, n_head=16, ffn=8192, vocab=50257, ctx=1024):
     return GPT()
 
 
-def cfg5_training(dev, steps=5, warmup=2, n_layer=24):
+def cfg5_training(dev, steps=10, warmup=3, n_layer=24):
     """Tokens/s of full training steps (fwd, bwd, Adam) of the cfg5 decoder, plain and
     with every Linear/LayerNorm except lm_head wrapped by wrap_with_flashdp_layers
     (C=1, sigma=1), bf16 weights, B=8, T=1024, uniform random token ids."""
@@ -212,7 +237,8 @@ def cfg5_training(dev, steps=5, warmup=2, n_layer=24):
     from flashdp4review_amd import wrap_with_flashdp_layers
     B, T, V = 8, 1024, 50257
     torch.manual_seed(0)
-    base = gpt_model(n_layer=n_layer).to(dev, torch.bfloat16)
+    with torch.device(dev):
+        base = gpt_model(n_layer=n_layer).to(torch.bfloat16)
     g = torch.Generator(device=dev).manual_seed(0)
     idx = torch.randint(0, V, (B, T + 1), device=dev, generator=g)
     x, y = idx[:, :-1].contiguous(), idx[:, 1:].contiguous()
@@ -361,7 +387,6 @@ def main():
         B, T, I, O = 8, 1024, 768, 3072
         step, _ = run_wgrad(x, go, torch.bfloat16)
         step_coop, _ = run_wgrad(x, go, torch.bfloat16, launch="cooperative")
-        _, kernel_call = run_wgrad(x, go, torch.bfloat16, launch="plain")
         workload = ("cfg2: DP Linear 768->3072 clipped per-sample weight grad, B=8 T=1024, "
                     "C=1, sigma=1")
     elif args.workload == "cfg3":
@@ -369,7 +394,6 @@ def main():
         B, T, I, O = 16, 1024, 768, 2304
         step, _ = run_wgrad(x, go, torch.bfloat16, transpose=True)
         step_coop, _ = run_wgrad(x, go, torch.bfloat16, transpose=True, launch="cooperative")
-        _, kernel_call = run_wgrad(x, go, torch.bfloat16, transpose=True, launch="plain")
         workload = "cfg3: DP Conv1D 768->2304 clipped per-sample weight grad, B=16 T=1024"
     else:
         from flashdp4review_amd.core import layernorm_bwd_clip, layernorm_fwd
@@ -387,9 +411,14 @@ def main():
                                       noise_scale=0.25, noise_key=keys.next(1024))
 
         step_coop = None
-        kernel_call = step
 
-    # ---- timed region: K steps bracketed by synchronisation
+    # ---- timed region: K steps bracketed by synchronisation and a pair of HIP
+    # events on the launch stream.  A step is one call, and the call is one
+    # launch of the dominant kernel (cfg2/cfg3; cfg4: the call's kernels), so
+    # the region's mean is that kernel's mean launch duration as well (the
+    # roofline's avg_ms; the host issues calls faster than the device runs them,
+    # see host_us_per_call).  profiles/ holds the rocprofv3 kernel-trace of
+    # the same command, whose average agrees.
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -400,12 +429,19 @@ def main():
     e.record()
     torch.cuda.synchronize()
     ms = s.elapsed_time(e) / args.steps
+    call_ms = ms
+    # host time per call: calls issued back to back while the device is busy
+    n_host = 100
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(n_host):
+        step()
+    host_us = (time.perf_counter() - t0) / n_host * 1e6
+    torch.cuda.synchronize()
 
-    calls = max(args.steps, 20)
     if args.workload == "cfg4":
         # algorithmic bytes: read x, dy, write dx (bf16) + mean/rstd (fp32)
         nbytes = 3 * 2 * 16 * 1024 * 1024 + 8 * 16 * 1024
-        call_ms = median_cuda_time(kernel_call, calls, 3, reps=3)
         res = {"metric": "DP LayerNorm per-sample grad GB/s", "value": round(nbytes / ms / 1e6, 1),
                "unit": "GB/s", "dtype": "bf16",
                "config": {"workload": "cfg4: DP LayerNorm H=1024 bwd incl. dx, B=16 T=1024, "
@@ -414,25 +450,25 @@ def main():
                 "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(nbytes / call_ms / 1e6 / PEAK_HBM_GBS, 4),
                 "traffic": TRAFFIC_BYTES["cfg4"],
-                "kernel": "fdp_layernorm_bwd_clip (ln_bwd_kernel + reductions), one call",
+                "kernel": "fdp_layernorm_bwd_clip: the call's kernels, HIP events around "
+                          "the timed region",
                 "bytes_per_launch": nbytes, "avg_ms": round(call_ms, 4)}
     else:
         F = 2.0 * B * T * I * O
-        call_ms = median_cuda_time(kernel_call, calls, 3, reps=3)
         res = {"metric": "clipped per-sample-grad GEMM TFLOP/s", "value": round(F / ms / 1e9, 2),
                "unit": "TFLOP/s", "dtype": "bf16", "config": {"workload": workload}}
         roof = {"bound": "mfma", "achieved": round(F / call_ms / 1e9, 2),
                 "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(F / call_ms / 1e9 / PEAK_BF16_TFLOPS, 4),
                 "traffic": TRAFFIC_BYTES[args.workload],
-                "kernel": "wgrad_group_kernel (fdp_wgrad_clip calls back to back, ordinary "
-                          "dispatch; the call is this one kernel)",
+                "kernel": "single-pass clipped weight-gradient kernel: one launch per "
+                          "fdp_wgrad_clip call, HIP events around the timed region",
                 "flops_per_launch": F, "avg_ms": round(call_ms, 4)}
     out = {"metric": res["metric"], "value": res["value"], "unit": res["unit"], "n_gpus": 1,
            "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
            "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
            "dtype": res["dtype"], "data": "synthetic (seeded randn, inputs resident in HBM)",
-           "config": res["config"], "roofline": roof}
+           "config": res["config"], "roofline": roof, "host_us_per_call": round(host_us, 1)}
     if not args.no_cpu_baseline and args.workload == "cfg2":
         out["cpu_baseline"] = cpu_baseline_cfg2()
     if not args.no_extra and args.workload == "cfg2":
@@ -441,7 +477,12 @@ def main():
         F = 2.0 * B * T * I * O
         extra["cfg2_step_cooperative_launch"] = {"ms": round(t_coop, 4),
                                                  "tflops": round(F / t_coop / 1e9, 2)}
+        step_narrow, _ = run_wgrad(x, go, torch.bfloat16, single_pass="narrow")
+        t_nar = median_cuda_time(step_narrow, args.steps, 3, reps=3)
+        extra["cfg2_step_grouped_kernel"] = {"ms": round(t_nar, 4),
+                                             "tflops": round(F / t_nar / 1e9, 2)}
         extra.update(extra_measurements(dev, max(5, args.steps // 5), 3))
+        extra["cfg5_training"] = cfg5_training(dev)
         out["extra"] = extra
     out["device"] = torch.cuda.get_device_name(dev)
     print(json.dumps(out), flush=True)

@@ -20,25 +20,57 @@ from .utils import RuntimeAutoTuner
 
 
 _LAUNCH_MODES = ("cooperative", "plain")
+_SINGLE_PASS = {"auto": 0, "wide": _lib.WGRAD_WIDE, "narrow": _lib.WGRAD_NARROW}
 _launch_mode = os.environ.get("FDP_WGRAD_LAUNCH", "plain")
 if _launch_mode not in _LAUNCH_MODES:
     raise ValueError(f"FDP_WGRAD_LAUNCH must be one of {_LAUNCH_MODES}, got {_launch_mode!r}")
 _ws_sizes: dict = {}
 _ws_lock = threading.Lock()
 _ws_cache: dict = {}
+# Every STATUS_PERIOD calls on a workspace, a 4-byte copy of its status word to
+# pinned host memory is queued behind the call; a later call reads it once the
+# copy has completed, so an expired wait is reported without a host sync.
+STATUS_PERIOD = 64
 
 
-def _persistent_workspace(nbytes: int, dev: torch.device, stream: int) -> torch.Tensor:
-    """Zero-filled workspace kept per (device, stream).  Calls on one stream run in
-    order and each leaves the control words zero, so the buffer is reused with
-    FDP_WGRAD_CLEAN_WORKSPACE and no clearing kernel."""
+class _Workspace:
+    """A zero-filled fdp_wgrad_clip workspace kept per (device, stream), with the
+    asynchronous probe of its status word.  Calls on one stream run in order and
+    each leaves the control words valid (a zero-filled head is valid), so the
+    buffer is reused with FDP_WGRAD_CLEAN_WORKSPACE and no clearing kernel."""
+
+    def __init__(self, nbytes: int, dev: torch.device):
+        self.buf = torch.zeros(max(int(nbytes), 4096), dtype=torch.uint8, device=dev)
+        self.status_host = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+        self.event = None
+        self.calls = 0
+
+    def status_word(self) -> torch.Tensor:
+        return self.buf[:4].view(torch.int32)
+
+    def take_probe(self) -> int:
+        """Status seen by a completed probe (0 if none has completed)."""
+        if self.event is None or not self.event.query():
+            return 0
+        self.event = None
+        return int(self.status_host[0])
+
+    def queue_probe(self) -> None:
+        self.calls += 1
+        if self.event is None and self.calls % STATUS_PERIOD == 0:
+            self.status_host.copy_(self.status_word(), non_blocking=True)
+            self.event = torch.cuda.Event()
+            self.event.record()
+
+
+def _persistent_workspace(nbytes: int, dev: torch.device, stream: int) -> _Workspace:
     key = (dev.index, stream)
     with _ws_lock:
         ws = _ws_cache.get(key)
-        if ws is None or ws.numel() < nbytes:
+        if ws is None or ws.buf.numel() < nbytes:
             if len(_ws_cache) >= 16:
                 _ws_cache.clear()
-            ws = torch.zeros(max(int(nbytes), 4096), dtype=torch.uint8, device=dev)
+            ws = _Workspace(nbytes, dev)
             _ws_cache[key] = ws
         return ws
 
@@ -47,6 +79,29 @@ def release_workspaces() -> None:
     """Drop the cached per-stream workspaces (they are re-made on the next call)."""
     with _ws_lock:
         _ws_cache.clear()
+
+
+def _raise_expired(ws: _Workspace, when: str, status: int = 1) -> None:
+    del status  # every nonzero status is an expired wait
+    ws.status_word().zero_()  # stream-ordered: later calls see a clear status word
+    raise _lib.FlashDPError(
+        f"fdp_wgrad_clip: a bounded inter-workgroup wait of the single-pass kernel timed out "
+        f"({when}); the results of that call are NaN")
+
+
+def wgrad_status(device=None, clear: bool = True) -> int:
+    """Synchronise and return the status word of the current stream's workspace
+    (nonzero: a bounded wait of an earlier call timed out and its outputs are
+    NaN); ``clear`` resets it."""
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    ws = _ws_cache.get((dev.index, _lib.stream_handle(dev)))
+    if ws is None:
+        return 0
+    torch.cuda.synchronize(dev)
+    v = int(ws.status_word().item())
+    if v and clear:
+        ws.status_word().zero_()
+    return v
 
 
 def set_wgrad_launch(mode: str) -> str:
@@ -84,7 +139,7 @@ def wgrad_clip(a: torch.Tensor, b: torch.Tensor, C: float = 1.0, clamp_value: fl
                noise_key: tuple[int, int] | None = None,
                out_dtype: torch.dtype | None = None, out: torch.Tensor | None = None,
                return_stats: bool = False, noclip: bool = False, two_pass: bool = False,
-               launch: str | None = None, check: bool = False):
+               launch: str | None = None, single_pass: str = "auto", check: bool = False):
     """out = out_scale * sum_b c_b G_b + noise_scale * z, c_b = clip(||G_b||_F).
 
     layout "tn": a [B,K,M], b [B,K,N], G_b = a_b^T b_b;
@@ -95,10 +150,17 @@ def wgrad_clip(a: torch.Tensor, b: torch.Tensor, C: float = 1.0, clamp_value: fl
     neither: no noise.
     With ``return_stats`` also returns the fp32 per-sample norms and factors.
     ``two_pass`` forces the norm-pass + clipped-sum-pass schedule instead of the
-    single-pass kernel; ``launch`` ("cooperative" / "plain", default: the
+    single-pass kernels; ``single_pass`` picks between those: "auto" (the wide
+    kernel, one 384x192 tile of one sample per CU, when the layer's products
+    fill at least 70% of the CUs, else the grouped 128x128 kernel), "wide"
+    (whenever the products fit the CUs) or "narrow" (grouped only); ``launch`` ("cooperative" / "plain", default: the
     mode of ``set_wgrad_launch``) picks how that kernel is dispatched.
     ``check`` synchronises and raises if a bounded inter-workgroup wait of the
-    single-pass kernel expired.
+    single-pass kernel expired (in this call or an earlier one on the stream
+    whose expiry was not reported yet).  Without it, expiries are reported by a
+    later call: every STATUS_PERIOD calls the status word is copied to the host
+    behind the call, and the first call after the copy completes raises.  An
+    expiry poisons only the launch it happened in (its outputs are NaN).
     """
     dev = _lib.require_hip(a, b, noise, out)
     if a.dtype != b.dtype:
@@ -139,8 +201,11 @@ def wgrad_clip(a: torch.Tensor, b: torch.Tensor, C: float = 1.0, clamp_value: fl
     mode = _launch_mode if launch is None else launch
     if mode not in _LAUNCH_MODES:
         raise ValueError(f"launch must be one of {_LAUNCH_MODES}, got {mode!r}")
+    if single_pass not in _SINGLE_PASS:
+        raise ValueError(f"single_pass must be one of {tuple(_SINGLE_PASS)}, got {single_pass!r}")
     flags = ((_lib.WGRAD_NOCLIP if noclip else 0) | (_lib.WGRAD_TWO_PASS if two_pass else 0)
-             | (_lib.WGRAD_PLAIN_LAUNCH if mode == "plain" else 0) | _lib.WGRAD_CLEAN_WORKSPACE)
+             | (_lib.WGRAD_PLAIN_LAUNCH if mode == "plain" else 0) | _lib.WGRAD_CLEAN_WORKSPACE
+             | _SINGLE_PASS[single_pass])
     L = _lib.lib()
     key = (dev.index, Bn, K, M, N, dt, flags)
     nbytes = _ws_sizes.get(key)
@@ -149,21 +214,23 @@ def wgrad_clip(a: torch.Tensor, b: torch.Tensor, C: float = 1.0, clamp_value: fl
         _ws_sizes[key] = nbytes
     stream = _lib.stream_handle(dev)
     ws = _persistent_workspace(nbytes, dev, stream)
+    probed = ws.take_probe()
+    if probed != 0:
+        _raise_expired(ws, "reported asynchronously for an earlier call on this stream", probed)
     st = L.fdp_wgrad_clip(
         _lib.ptr(a), _lib.ptr(b), Bn, K, M, N, a.stride(0), a.stride(1), b.stride(0), b.stride(1),
         lay, dt, ctypes.c_float(C_), ctypes.c_float(clamp_), _lib.ptr(cad),
         ctypes.c_float(out_scale), _lib.ptr(noise), ctypes.c_float(noise_scale),
         _lib.noise_key(noise_key), out.data_ptr(),
-        out.stride(0), odt, _lib.ptr(norms), _lib.ptr(factors), flags, ws.data_ptr(), ws.numel(),
-        stream)
+        out.stride(0), odt, _lib.ptr(norms), _lib.ptr(factors), flags, ws.buf.data_ptr(),
+        ws.buf.numel(), stream)
     _lib.check(st, "fdp_wgrad_clip")
     if check:
-        status = ws[:4].view(torch.int32)
-        if int(status.item()) != 0:
-            # the status word is sticky on a reused workspace, and an expired
-            # wait can leave other control words set: clear them all
-            ws[:_lib.WGRAD_CONTROL_BYTES].zero_()
-            raise _lib.FlashDPError("fdp_wgrad_clip: an inter-workgroup wait timed out")
+        status = int(ws.status_word().item())
+        if status != 0:
+            _raise_expired(ws, "this call or an earlier one on this stream", status)
+    else:
+        ws.queue_probe()
     if return_stats:
         return out, norms, factors
     return out

@@ -93,12 +93,17 @@ __device__ __forceinline__ U32x4 philox4x32_10(uint32_t c0, uint32_t c1, uint32_
   return U32x4{{c0, c1, c2, c3}};
 }
 
-// Box-Muller on two 24-bit uniforms in (0, 1): r = sqrt(-2 ln u_a),
-// (r cos 2 pi u_b, r sin 2 pi u_b).  v_log_f32 is log2; v_sin/v_cos_f32 take
-// their argument in revolutions.
+// Box-Muller: r = sqrt(-2 ln u_a), (r cos 2 pi u_b, r sin 2 pi u_b), with the
+// radius uniform u_a = (a + 1/2) 2^-32 built from the whole 32-bit word (its
+// smallest value 2^-33 bounds |z| by sqrt(66 ln 2) = 6.76) and the angle
+// uniform u_b = ((b >> 8) + 1/2) 2^-24.  v_log_f32 is log2; v_sin/v_cos_f32
+// take their argument in revolutions.  (float)a rounds to nearest: for a
+// within 128 of 2^32, u_a rounds to 1 and r to 0 instead of about 1e-5.
 __device__ __forceinline__ void box_muller(uint32_t a, uint32_t b, float& z0, float& z1) {
-  constexpr float kInv24 = 5.9604644775390625e-08f;  // 2^-24
-  const float ua = (static_cast<float>(a >> 8) + 0.5f) * kInv24;
+  constexpr float kInv32 = 2.3283064365386963e-10f;   // 2^-32
+  constexpr float kHalf32 = 1.16415321826934814e-10f;  // 2^-33
+  constexpr float kInv24 = 5.9604644775390625e-08f;   // 2^-24
+  const float ua = __builtin_fmaf(static_cast<float>(a), kInv32, kHalf32);
   const float ub = (static_cast<float>(b >> 8) + 0.5f) * kInv24;
   const float r = __builtin_sqrtf(-1.3862943611198906f * __builtin_amdgcn_logf(ua));  // -2 ln 2 log2
   z0 = r * __builtin_amdgcn_cosf(ub);

@@ -8,15 +8,21 @@
 // v_mfma_f32_32x32x16_{bf16,f16} accumulators.
 //
 //  * Global -> LDS: buffer_load_dwordx4 ... lds (16 bytes per lane straight into
-//    LDS, no VGPR staging).  A BK(k) x R tile of 16-bit values is rows of R/8
-//    chunks of 16 bytes; lane l of a wave's load j fills the next 64 slots in
-//    order, i.e. slot -> row k = slot / (R/8), physical chunk slot % (R/8), and
-//    the lane loads logical chunk (physical ^ swz(k)) of that row: every row is
-//    still one contiguous read, and the XOR swizzle puts the 4 rows x 4 chunks
-//    that half a wave reads in one transposing read onto 16 distinct 16-byte
-//    bank groups.  The buffer resource's record count is the sample's K*ld*2
-//    bytes, so rows past K read as zeros (columns past M/N may carry the next
-//    row's values; callers ignore those rows/columns).
+//    LDS, no VGPR staging).  A BK(k) x R tile of 16-bit values is rows of
+//    CPR = R/8 logical chunks of 16 bytes, stored in LDS rows of RS = CPR
+//    rounded up to a multiple of 16 chunks (256 bytes: every row starts on
+//    the same bank).  Lane l of a wave's load j fills the next 64 slots in
+//    order, i.e. slot -> row k = slot / RS, physical chunk p = slot % RS, and
+//    the lane loads logical chunk c = p ^ swz(k) of that row.  The XOR (with
+//    0, 4, 8 or 12) stays inside each aligned group of 16 chunks, so it maps
+//    [0, CPR) into [0, RS); it puts the 4 rows x 4 chunks that half a wave
+//    reads in one transposing read onto 16 distinct 16-byte bank groups.
+//    Slots whose logical chunk is >= CPR (only when R is not a multiple of
+//    128) are padding: their offset lies past the buffer's records, so the
+//    load writes zeros and reads no memory.  The buffer resource's record
+//    count is the sample's K*ld*2 bytes, so rows past K read as zeros
+//    (columns past M/N may carry the next row's values; callers ignore those
+//    rows/columns).
 //  * S LDS stages, each a separate __shared__ object so that the compiler's
 //    wait-count pass can tell the stage being filled from the one being read:
 //    while stage kt is consumed, the loads of the next S-2 k-tiles are in flight
@@ -43,6 +49,12 @@ constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, 32-bit records
 
 __device__ __forceinline__ int swz(int k) { return (k & 3) << 2; }
 
+// LDS row of a tile R values wide, in 16-byte chunks (see above).
+__host__ __device__ constexpr int row_chunks(int R) { return (R / 8 + 15) / 16 * 16; }
+// Offset of a padding slot: past any buffer's records (< 2^31 bytes) even
+// after the k-tile and column offsets (< 2^31) are added, without wrapping.
+constexpr uint32_t kPadOffset = 0x80000000u;
+
 // Tile geometry: BM x BN outputs, WGM x WGN waves (default 2 x 2), each
 // (BM/WGM) x (BN/WGN); k-tiles of BK rows (a multiple of 16) per LDS stage.
 template <int BM_, int BN_, int BK_ = kBK, int WGM_ = 2, int WGN_ = 2>
@@ -58,14 +70,17 @@ struct Geom {
   static constexpr int WN = BN / WGN;     // wave tile columns
   static constexpr int FI = WM / 32;      // 32-row MFMA blocks per wave
   static constexpr int FJ = WN / 32;      // 32-column MFMA blocks per wave
-  static constexpr int TILE_A = BK * BM * 2;
-  static constexpr int TILE_B = BK * BN * 2;
+  static constexpr int ROW_A = row_chunks(BM) * 16;  // LDS bytes per k-row of the A tile
+  static constexpr int ROW_B = row_chunks(BN) * 16;
+  static constexpr int TILE_A = BK * ROW_A;
+  static constexpr int TILE_B = BK * ROW_B;
   static constexpr int STAGE = TILE_A + TILE_B;
   static constexpr int LOADS_A = TILE_A / (NW * 64 * 16);  // per wave per k-tile
   static constexpr int LOADS_B = TILE_B / (NW * 64 * 16);
   static constexpr int LOADS = LOADS_A + LOADS_B;
   static_assert(LOADS_A * NW * 64 * 16 == TILE_A && LOADS_B * NW * 64 * 16 == TILE_B,
                 "each wave issues whole 1 KB loads");
+  static_assert(BM % 32 == 0 && BN % 32 == 0 && WM % 32 == 0 && WN % 32 == 0, "32x32 blocks");
 };
 
 // One operand's per-thread load state: L buffer loads per k-tile of BK rows.
@@ -85,15 +100,16 @@ struct Operand {
   // base: the sample's operand [K, ld] (16-bit); R: tile width; r0: first column.
   template <int R>
   __device__ inline void init(const uint16_t* base, int64_t ld, int64_t K, int64_t r0) {
-    constexpr int CPR = R / 8;  // 16-byte chunks per row
+    constexpr int CPR = R / 8;              // logical 16-byte chunks per row
+    constexpr int RS = row_chunks(R);       // physical chunks per LDS row
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     retarget(base, ld, K);
 #pragma unroll
     for (int j = 0; j < L; ++j) {
       const int slot = (wave * L + j) * 64 + lane;
-      const int k = slot / CPR;
-      const int c = (slot % CPR) ^ swz(k);
-      voff[j] = static_cast<uint32_t>((int64_t(k) * ld + 8 * c) * 2);
+      const int k = slot / RS;
+      const int c = (slot % RS) ^ swz(k);
+      voff[j] = c < CPR ? static_cast<uint32_t>((int64_t(k) * ld + 8 * c) * 2) : kPadOffset;
     }
     retile(r0);
     step = static_cast<uint32_t>(BK * ld * 2);
@@ -141,7 +157,8 @@ __device__ __forceinline__ uint32_t frag_off(int w0, int i, int h) {
   const int g = lane >> 4, r = lane & 15;
   const int m = w0 + 32 * i + 16 * (g & 1) + 4 * (r & 3);
   const int k = 8 * (g >> 1) + 4 * h + (r >> 2);
-  return static_cast<uint32_t>(k * (R * 2) + (((m >> 3) ^ swz(k)) * 16) + ((m >> 2) & 1) * 8);
+  return static_cast<uint32_t>(k * (row_chunks(R) * 16) + (((m >> 3) ^ swz(k)) * 16) +
+                               ((m >> 2) & 1) * 8);
 }
 
 template <class G>
@@ -190,10 +207,10 @@ struct Frags {
   __device__ __forceinline__ void load(const FDP_LDS char* st, const FragOffsets<G>& fo, int ks) {
 #pragma unroll
     for (int j = 0; j < G::FJ; ++j)
-      b[j] = read_frag(st, fo.b[j][0] + ks * 16 * G::BN * 2, fo.b[j][1] + ks * 16 * G::BN * 2);
+      b[j] = read_frag(st, fo.b[j][0] + ks * 16 * G::ROW_B, fo.b[j][1] + ks * 16 * G::ROW_B);
 #pragma unroll
     for (int i = 0; i < G::FI; ++i)
-      a[i] = read_frag(st, fo.a[i][0] + ks * 16 * G::BM * 2, fo.a[i][1] + ks * 16 * G::BM * 2);
+      a[i] = read_frag(st, fo.a[i][0] + ks * 16 * G::ROW_A, fo.a[i][1] + ks * 16 * G::ROW_A);
   }
 };
 
@@ -296,6 +313,70 @@ __device__ inline void gemm(const Job<G>& job, int nk, const FragOffsets<G>& fo,
         barrier();
         if (kt + S - 1 < nk) job.issue(st.get((s + S - 1) % S), kt + S - 1);
         compute_stage<DT, G>(st.get(s), fo, acc);
+      }
+    }
+  }
+  barrier();  // every wave is done reading before the ring is reused
+}
+
+struct NoHook {
+  __device__ __forceinline__ void operator()(int) const {}
+};
+
+// acc += A_tile^T B_tile over nk k-tiles with an S-stage ring, fragments
+// double-buffered in registers: the LDS reads of k-step s+1 (the next k-tile's
+// first step at a k-tile's end, after its wait and barrier) are issued before
+// the MFMAs of step s, and scheduling groups interleave one MFMA with the DS
+// reads of the next step.  KS must be even (fragment buffers alternate).
+// hook(kt) runs at the start of every k-tile kt: VALU work placed there
+// (reading no memory) overlaps the matrix cores' work of the other wave of
+// the SIMD.
+template <class DT, class G, int S, class Hook = NoHook>
+__device__ inline void gemm_pipe(const Job<G>& job, int nk, const FragOffsets<G>& fo,
+                                 const Stages& st, f32x16 (&acc)[G::FI][G::FJ],
+                                 const Hook& hook = Hook()) {
+  static_assert(S >= 2 && S <= 4, "stages");
+  static_assert(G::KS % 2 == 0, "an even number of k-steps per k-tile");
+  wait_vm<0>();
+#pragma unroll
+  for (int s = 0; s < S - 1; ++s)
+    if (s < nk) job.issue(st.get(s), s);
+  if (nk <= 0) return;
+  wait_tiles<G::LOADS>(nk - 1 < S - 2 ? nk - 1 : S - 2);
+  barrier();
+  if (S - 1 < nk) job.issue(st.get(S - 1), S - 1);
+  Frags<G> f[2];
+  f[0].load(st.get(0), fo, 0);
+  for (int base = 0; base < nk; base += S) {
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const int kt = base + s;
+      if (kt < nk) {
+        hook(kt);
+#pragma unroll
+        for (int ks = 0; ks < G::KS; ++ks) {
+          const int cur = ks & 1;
+          if (ks + 1 < G::KS) {
+            f[cur ^ 1].load(st.get(s), fo, ks + 1);
+          } else if (kt + 1 < nk) {
+            const int ahead = nk - 2 - kt;
+            wait_tiles<G::LOADS>(ahead < S - 2 ? ahead : S - 2);
+            barrier();
+            if (kt + S < nk) job.issue(st.get(s), kt + S);
+            f[cur ^ 1].load(st.get((s + 1) % S), fo, 0);
+          }
+#pragma unroll
+          for (int i = 0; i < G::FI; ++i)
+#pragma unroll
+            for (int j = 0; j < G::FJ; ++j) acc[i][j] = mfma16<DT>(f[cur].a[i], f[cur].b[j], acc[i][j]);
+          constexpr int nm = G::FI * G::FJ, nr = 2 * (G::FI + G::FJ);
+          constexpr int per = (nr + nm - 1) / nm;
+#pragma unroll
+          for (int t = 0; t < nm; ++t) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);    // one MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, per, 0);  // then DS reads
+          }
+        }
       }
     }
   }

@@ -20,6 +20,7 @@
 // wavefront per row for the LayerNorm kernels (row statistics are wavefront
 // shuffles, no LDS), 64..256 threads across the columns for the column sums.
 #include "fdp_common.hpp"
+#include "host_cache.hpp"
 
 namespace fdp {
 namespace rw {
@@ -759,15 +760,7 @@ inline size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 bool valid_dtype(int d) { return d == FDP_F32 || d == FDP_F16 || d == FDP_BF16; }
 int esize(int d) { return d == FDP_F32 ? 4 : 2; }
 
-int num_cus() {
-  int dev = 0, cus = 256;
-  if (hipGetDevice(&dev) == hipSuccess) {
-    int v = 0;
-    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
-      cus = v;
-  }
-  return cus;
-}
+int num_cus() { return fdp::host::device_cus(); }
 
 // Workspace of both reductions (offsets in bytes), S = streams * B:
 //   off_part   partials [S][chunks][H] (fp32)

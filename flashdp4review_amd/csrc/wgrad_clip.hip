@@ -42,6 +42,7 @@
 #include <cstdlib>
 
 #include "wgrad_stream.hpp"
+#include "wgrad_wide.hpp"
 
 namespace fdp {
 namespace wg {
@@ -85,7 +86,7 @@ __global__ __launch_bounds__(NT) void wgrad_factor_kernel(const float* partials,
                                                            int noclip, float* fac_ws,
                                                            float* norms, float* factors,
                                                            int* err) {
-  if (blockIdx.x == 0 && threadIdx.x == 0 && err != nullptr) *err = 0;
+  (void)err;  // the two-pass schedule has no bounded waits: the status word stays as it is
   if (clip_args_dev != nullptr) {
     C = clip_args_dev[0];
     clamp = clip_args_dev[1];
@@ -209,9 +210,14 @@ struct Plan {
   int tiles_m, tiles_n, tiles;
   int spg, groups;
   StreamPlan sp;  // streamed two-pass schedule (16-bit TN operands)
+  WidePlan wp;    // wide single-pass schedule (wp.wgm == 0: not used)
   size_t off_turn, off_partials, off_factors, off_group, off_slots, off_chunk;
-  size_t total_two_pass, total_fused, total;
+  size_t off_wide_partials, off_wide_slots;
+  size_t total_two_pass, total_fused, total_wide, total;
 };
+
+// Smallest share of the CUs the wide kernel's products must fill by default.
+constexpr double kWideMinFill = 0.7;
 
 // Polls before a grid wait of the single-pass kernel gives up (seconds of
 // waiting).  FDP_WGRAD_SPIN_LIMIT overrides it so that tests can exercise the
@@ -222,17 +228,12 @@ unsigned spin_limit() {
   return kSpinLimit;
 }
 
-int num_cus() {
-  int dev = 0, cus = 256;
-  if (hipGetDevice(&dev) == hipSuccess) {
-    int v = 0;
-    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
-      cus = v;
-  }
-  return cus;
-}
+int num_cus() { return host::device_cus(); }
 
-Plan make_plan(int64_t B, int64_t K, int64_t M, int64_t N, int cus) {
+// lda/ldb: the row strides the call will use (the size query assumes
+// contiguous operands, lda = M and ldb = N, which the layers pass).
+Plan make_plan(int64_t B, int64_t K, int64_t M, int64_t N, int cus, int flags, int64_t lda = 0,
+               int64_t ldb = 0) {
   Plan pl{};
   pl.tiles_m = static_cast<int>((M + BM - 1) / BM);
   pl.tiles_n = static_cast<int>((N + BN - 1) / BN);
@@ -266,6 +267,16 @@ Plan make_plan(int64_t B, int64_t K, int64_t M, int64_t N, int cus) {
     pl.total_fused = pl.off_chunk + (gp.chunk < B ? sizeof(float) * size_t(M) * N : 0);
   }
   pl.total = pl.total_two_pass > pl.total_fused ? pl.total_two_pass : pl.total_fused;
+  if ((flags & FDP_WGRAD_NARROW) == 0 && K > 0) {
+    pl.wp = wide_plan(B, K, M, N, lda > 0 ? lda : M, ldb > 0 ? ldb : N, cus,
+                      (flags & FDP_WGRAD_WIDE) ? 0.0 : kWideMinFill);
+    if (pl.wp.wgm != 0) {
+      pl.off_wide_partials = kWsHead;
+      pl.off_wide_slots = pl.off_wide_partials + align_up(pl.wp.partial_bytes);
+      pl.total_wide = pl.off_wide_slots + pl.wp.slot_bytes;
+      if (pl.total_wide > pl.total) pl.total = pl.total_wide;
+    }
+  }
   return pl;
 }
 
@@ -368,7 +379,7 @@ extern "C" int fdp_wgrad_clip_workspace_size(int64_t B, int64_t K, int64_t M, in
   if (bytes == nullptr) return FDP_ERR_ARG;
   if (!valid_dtype(dtype)) return FDP_ERR_DTYPE;
   if (B < 1 || M < 1 || N < 1 || K < 0) return FDP_ERR_SHAPE;
-  *bytes = make_plan(B, K, M, N, num_cus()).total;
+  *bytes = make_plan(B, K, M, N, num_cus(), flags).total;
   return FDP_OK;
 }
 
@@ -389,14 +400,19 @@ extern "C" int fdp_wgrad_clip(const void* a, const void* b, int64_t B, int64_t K
   if (M * N > (int64_t(1) << 40) || B > (int64_t(1) << 31)) return FDP_ERR_SHAPE;
   if ((K > 0 && (a == nullptr || b == nullptr)) || out == nullptr) return FDP_ERR_ARG;
   if ((flags & ~(FDP_WGRAD_NOCLIP | FDP_WGRAD_TWO_PASS | FDP_WGRAD_PLAIN_LAUNCH |
-                 FDP_WGRAD_CLEAN_WORKSPACE)) != 0)
+                 FDP_WGRAD_CLEAN_WORKSPACE | FDP_WGRAD_WIDE | FDP_WGRAD_NARROW)) != 0)
     return FDP_ERR_ARG;
+  if ((flags & FDP_WGRAD_WIDE) && (flags & FDP_WGRAD_NARROW)) return FDP_ERR_ARG;
   const bool noclip = (flags & FDP_WGRAD_NOCLIP) != 0;
   if (noclip && norms != nullptr) return FDP_ERR_ARG;
 
   const int cus = num_cus();
-  const Plan pl = make_plan(B, K, M, N, cus);
-  if (workspace == nullptr || workspace_bytes < pl.total) return FDP_ERR_WORKSPACE;
+  // the workspace was sized for contiguous operands: the wide plan for the
+  // actual strides is taken only if it fits that size
+  const Plan pl0 = make_plan(B, K, M, N, cus, flags);
+  if (workspace == nullptr || workspace_bytes < pl0.total) return FDP_ERR_WORKSPACE;
+  Plan pl = make_plan(B, K, M, N, cus, flags, lda, ldb);
+  if (pl.total > workspace_bytes) pl.wp.wgm = 0;
   if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0) return FDP_ERR_ALIGN;
 
   char* ws = static_cast<char*>(workspace);
@@ -428,6 +444,8 @@ extern "C" int fdp_wgrad_clip(const void* a, const void* b, int64_t B, int64_t K
   args.units = int64_t(pl.tiles) * B;
   args.err = reinterpret_cast<int*>(ws);
   args.bar = reinterpret_cast<unsigned*>(ws) + 1;
+  args.epoch = reinterpret_cast<unsigned*>(ws) + 2;
+  args.poison = reinterpret_cast<unsigned*>(ws) + 3;
   args.pair_flag = reinterpret_cast<unsigned*>(ws) + kPairFlag0;
   args.spin_limit = spin_limit();
   args.tile_turn = reinterpret_cast<unsigned*>(ws + pl.off_turn);
@@ -447,6 +465,62 @@ extern "C" int fdp_wgrad_clip(const void* a, const void* b, int64_t B, int64_t K
                    ldb % vel == 0 && stride_ab % vel == 0 && stride_bb % vel == 0;
 
   hipStream_t s = static_cast<hipStream_t>(stream);
+  // Wide single pass: 16-bit TN inputs, aligned rows, one product per CU.
+  if (!noclip && (flags & FDP_WGRAD_TWO_PASS) == 0 && layout == FDP_LAYOUT_TN && vec && K > 0 &&
+      dtype != FDP_F32 && pl.wp.wgm != 0) {
+    WideArgs w{};
+    w.a = static_cast<const uint16_t*>(a);
+    w.b = static_cast<const uint16_t*>(b);
+    w.B = B;
+    w.K = K;
+    w.M = M;
+    w.N = N;
+    w.sab = stride_ab;
+    w.lda = lda;
+    w.sbb = stride_bb;
+    w.ldb = ldb;
+    w.tiles_m = pl.wp.tiles_m;
+    w.tiles_n = pl.wp.tiles_n;
+    w.tiles = pl.wp.tiles;
+    w.nwg = pl.wp.nwg;
+    w.partials = reinterpret_cast<float*>(ws + pl.off_wide_partials);
+    w.slots = ws + pl.off_wide_slots;
+    w.slot_blocks = pl.wp.slot_blocks;
+    w.out = out;
+    w.ldo = ldo;
+    w.out_dtype = out_dtype;
+    w.out_scale = out_scale;
+    w.noise = args.noise;
+    w.noise_scale = noise_scale;
+    w.bar = args.bar;
+    w.epoch = args.epoch;
+    w.poison = args.poison;
+    w.err = args.err;
+    w.spin_limit = args.spin_limit;
+    w.C = C;
+    w.clamp = clamp;
+    w.clip_args_dev = clip_args_dev;
+    w.norms_out = norms;
+    w.factors_out = factors;
+    {
+      const int oes = out_dtype == FDP_F32 ? 4 : 2;
+      w.vec_out = (reinterpret_cast<uintptr_t>(out) % (4 * oes) == 0 && ldo % 4 == 0) ? 1 : 0;
+    }
+    const bool plain = (flags & FDP_WGRAD_PLAIN_LAUNCH) != 0;
+    if ((flags & FDP_WGRAD_CLEAN_WORKSPACE) == 0) {
+      const int64_t words = int64_t(kWsHead / sizeof(unsigned));
+      hipLaunchKernelGGL(clear_words_kernel<0>, dim3(static_cast<unsigned>((words + NT - 1) / NT)),
+                         dim3(NT), 0, s, reinterpret_cast<unsigned*>(ws), words);
+    }
+    const hipError_t e = dtype == FDP_BF16 ? launch_wide_bf16(w, pl.wp.wgm, plain, s)
+                                           : launch_wide_f16(w, pl.wp.wgm, plain, s);
+    if (e == hipSuccess) return FDP_OK;
+    if (e != hipErrorNotSupported && e != hipErrorCooperativeLaunchTooLarge) {
+      (void)hipGetLastError();
+      return FDP_ERR_HIP;
+    }
+    (void)hipGetLastError();
+  }
   // Single pass: 16-bit inputs, TN layout, aligned rows, a clip to compute, K > 0.
   if (!noclip && (flags & FDP_WGRAD_TWO_PASS) == 0 && layout == FDP_LAYOUT_TN && vec && K > 0 &&
       dtype != FDP_F32 && pl.total_fused > 0) {

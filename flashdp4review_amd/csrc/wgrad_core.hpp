@@ -6,6 +6,7 @@
 
 #include "fdp_common.hpp"
 #include "gemm_dma.hpp"
+#include "host_cache.hpp"
 
 namespace fdp {
 namespace wg {
@@ -38,9 +39,11 @@ struct Args {
   int64_t units;          // tiles * B work units, unit u = (tile u/B, sample u%B)
   int nwg;                // workgroups of the cooperative grid
   unsigned* bar;          // grid barrier arrivals
+  unsigned* epoch;        // launches of the single-pass kernel on this workspace (its tag is epoch + 1)
+  unsigned* poison;       // tag of a launch one of whose bounded waits expired
   unsigned* tile_turn;    // [tiles] hand-over tickets for tiles shared by workgroups
   float* tile_acc;        // [nwg, BM*BN] bf16 per-group tile sums (row-major)
-  int* err;               // set when a bounded wait gives up
+  int* err;               // status word: set when a bounded wait gives up (sticky, read by the host)
   unsigned spin_limit;    // polls before a grid wait gives up
   float C, clamp;
   const float* clip_args_dev;
@@ -408,14 +411,23 @@ constexpr int kXcds = 8;
 
 // All workgroups of the (co-resident) grid arrive before any leaves.
 // grid_wait returns (in every thread) whether this workgroup's results must be poisoned: its own
-// wait expired, or an earlier workgroup's did (that one set *err before this
-// one could arrive).
+// wait expired, or an earlier wait of this launch did (that one stored the
+// launch's tag in *poison before this workgroup could arrive).
 //
 // The counter resets itself: the last arriver (arrival index n-1) stores 0 and
 // leaves at once.  A waiter with arrival index i sees the counter in
 // [i+1, n-1] until everyone has arrived, then n or (after the reset) 0, which
 // is <= i: either ends its wait.  So the counter is zero again when the
-// barrier is over, with no second counter to reset.
+// barrier is over, with no second counter to reset.  Every workgroup arrives
+// exactly once, even after an expired wait, so this holds in every launch.
+//
+// Launch tags: every workgroup reads *epoch when it starts and uses tag =
+// epoch + 1 for the hand-over flags and the poison word of this launch; the
+// last arriver advances *epoch.  Every workgroup has started (and read the
+// epoch) before the last one arrives, so a launch's workgroups agree on the
+// tag, and a flag or poison word left by an earlier launch (for instance one
+// whose wait expired) never carries the current tag: an expiry affects only
+// the launch it happened in.
 //
 // quiet_until (a wall_clock64() value, 0 = none): before the first poll the
 // waiting wave sleeps without touching memory until then.  Coherent polling
@@ -433,27 +445,36 @@ __device__ inline unsigned grid_arrive(unsigned* bar) {
     i = __hip_atomic_fetch_add(bar, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   return i;
 }
-__device__ inline bool grid_wait(unsigned* bar, unsigned n, unsigned i, int* err, unsigned limit,
-                                 int* flag, uint64_t quiet_until = 0) {
+// Marks this launch (tag) as poisoned and sets the host's status word.
+__device__ __forceinline__ void expire(int* err, unsigned* poison, unsigned tag) {
+  atomicOr(err, 1);
+  __hip_atomic_store(poison, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline bool grid_wait(unsigned* bar, unsigned n, unsigned i, int* err, unsigned* epoch,
+                                 unsigned* poison, unsigned tag, unsigned limit, int* flag,
+                                 uint64_t quiet_until = 0, int poll_sleep = kPollSleep) {
   if (threadIdx.x == 0) {
     int bad = 0;
     if (i + 1 == n) {
       __hip_atomic_store(bar, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_fetch_add(epoch, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     } else {
       while (wall_clock64() < quiet_until) __builtin_amdgcn_s_sleep(32);
-      unsigned spins = 0;
-      for (;;) {
-        const unsigned v = __hip_atomic_load(bar, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (v >= n || v <= i) break;
-        __builtin_amdgcn_s_sleep(kPollSleep);
-        if (++spins > limit) {
-          atomicOr(err, 1);
+      // at most `limit` polls (0: none -- the wait expires at once, which
+      // tests use to force the expiry path deterministically)
+      for (unsigned spins = 0;; ++spins) {
+        if (spins >= limit) {
+          expire(err, poison, tag);
           bad = 1;
           break;
         }
+        const unsigned v = __hip_atomic_load(bar, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (v >= n || v <= i) break;
+        if (poll_sleep >= 16) __builtin_amdgcn_s_sleep(16);
+        else __builtin_amdgcn_s_sleep(2);
       }
     }
-    if (!bad) bad = __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+    if (!bad) bad = __hip_atomic_load(poison, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == tag;
     *flag = bad;
   }
   __syncthreads();
@@ -514,18 +535,6 @@ struct Held<false> {
   }
 };
 
-#ifdef FDP_PHASE_TIMING
-extern __device__ unsigned long long fdp_phase_ts[1024 * 16];
-#define FDP_TS(slot)                                                  \
-  do {                                                                \
-    if (threadIdx.x == 0 && blockIdx.x < 1024)                        \
-      fdp_phase_ts[blockIdx.x * 16 + (slot)] = wall_clock64();        \
-  } while (0)
-#else
-#define FDP_TS(slot) \
-  do {               \
-  } while (0)
-#endif
 
 // ------------------------------------------------------ single-pass work map
 // A launch covers samples [chunk_b0, chunk_b0 + chunk_nb) with W workgroups.
@@ -881,7 +890,12 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
   dma::FragOffsets<G> fo;
   fo.init(wm, wn);
   const uint64_t t_begin = wall_clock64();
-  FDP_TS(0);
+  // this launch's tag, in thread 0 (the only thread taking part in the
+  // waits); its first use is far away, so the load's latency is hidden, and
+  // grid_arrive() completes it (vmcnt(0), fence) before this workgroup arrives
+  unsigned tag = 0;
+  if (threadIdx.x == 0)
+    tag = __hip_atomic_load(p.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
 
   // ---- phase 1: the nb products run as one stream of nb*nk k-tiles through
   // the LDS ring, so that the next unit's first k-tiles load while this
@@ -941,8 +955,7 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
     wait_stores();  // (the ring's first wait below would drain them anyway)
     __syncthreads();
     if (threadIdx.x == 0)
-      __hip_atomic_store(p.pair_flag + pair, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    FDP_TS(8);
+      __hip_atomic_store(p.pair_flag + pair, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   if (nq > 0)
     job.init(pa + as.b0 * p.sab, p.lda, pb + as.b0 * p.sbb, p.ldb,
@@ -996,7 +1009,6 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
             if (threadIdx.x == 0)
               st_coherent(p.partials + (as.b0 + own) * tiles + as.tile,
                           (red[0] + red[1]) + (red[2] + red[3]));
-            FDP_TS(1 + own);
             if (own + 1 < nb) {  // park it and start the next product
 #pragma unroll
               for (int j = 0; j < U - 1; ++j)
@@ -1006,22 +1018,19 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
                 // owner: the last product starts from the helper's share (its
                 // load latency overlaps that of the product's first k-tiles)
                 if (threadIdx.x == 0) {
-                  unsigned spins = 0;
-                  while (__hip_atomic_load(p.pair_flag + pair, __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT) == 0u) {
-                    __builtin_amdgcn_s_sleep(kPollSleep);
-                    if (++spins > p.spin_limit) {
-                      atomicOr(p.err, 1);  // every workgroup's results are poisoned
+                  for (unsigned spins = 0;; ++spins) {
+                    if (spins >= p.spin_limit) {
+                      expire(p.err, p.poison, tag);  // every workgroup's results are poisoned
                       break;
                     }
+                    if (__hip_atomic_load(p.pair_flag + pair, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT) == tag)
+                      break;
+                    __builtin_amdgcn_s_sleep(kPollSleep);
                   }
                 }
                 __syncthreads();
                 take_over(slot_of(p, me), acc);
-                if (threadIdx.x == 0)
-                  __hip_atomic_store(p.pair_flag + pair, 0u, __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT);
-                FDP_TS(11);
               }
             }
           }
@@ -1059,8 +1068,8 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
   if (loaded) __builtin_amdgcn_s_setprio(0);
   const unsigned arrival = grid_arrive(p.bar);
   if (early) noise_rows(p, m0, n0, r0, r1, zpre);
-  bool poisoned = grid_wait(p.bar, unsigned(p.nwg), arrival, p.err, p.spin_limit, &flag, quiet);
-  FDP_TS(9);
+  bool poisoned = grid_wait(p.bar, unsigned(p.nwg), arrival, p.err, p.epoch, p.poison, tag,
+                            p.spin_limit, &flag, quiet);
 
   // ---- clip factors of this workgroup's samples: wavefront i sums the
   // partials of sample b0 + i in a fixed order
@@ -1087,7 +1096,6 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
     }
     __syncthreads();
   }
-  FDP_TS(14);
 
   // ---- phase 2: sum_b c_b G_b formed in place in the accumulators as
   // c_last G_last + c_0 G_0 + c_1 G_1 + ... (a fixed order: deterministic)
@@ -1105,7 +1113,6 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
 #pragma unroll
   for (int j = 0; j < U - 1; ++j)
     if (j < nb - 1) held[j].add_to(acc, fac[j]);
-  FDP_TS(4);
 
   // stage the group's sum in LDS, row-major (the ring is free)
   float* const q4[4] = {reinterpret_cast<float*>(st0), reinterpret_cast<float*>(st0) + 4096,
@@ -1119,7 +1126,6 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
       for (int r = 0; r < 16; ++r) qd[acc_row(0, 0, lane, r) * BN + acc_col(wn, c, lane)] = acc[a][c][r];
   }
   __syncthreads();
-  FDP_TS(5);
   if (as.ng > 1) {
     // publish the rows the other groups finish (row-major slot), then wait
     // until every group of the tile has published
@@ -1138,7 +1144,6 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
     }
     wait_stores();
     __syncthreads();
-    FDP_TS(6);
     uint64_t quiet_until = 0;
     if (threadIdx.x == 0) {
       __hip_atomic_fetch_add(p.tile_turn + as.tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1148,33 +1153,31 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
       quiet_until = now + (now - t_pub) / 2;
     }
     if (!early) noise_rows(p, m0, n0, r0, r1, zpre);
-    FDP_TS(7);
     if (threadIdx.x == 0) {
       while (wall_clock64() < quiet_until) __builtin_amdgcn_s_sleep(8);
-      unsigned spins = 0;
       int bad = 0;
-      while (__hip_atomic_load(p.tile_turn + as.tile, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
-             unsigned(as.ng)) {
-        __builtin_amdgcn_s_sleep(kPollSleep);
-        if (++spins > p.spin_limit) {
-          atomicOr(p.err, 1);
+      for (unsigned spins = 0;; ++spins) {
+        if (spins >= p.spin_limit) {
+          expire(p.err, p.poison, tag);
           bad = 1;
           break;
         }
+        if (__hip_atomic_load(p.tile_turn + as.tile, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >=
+            unsigned(as.ng))
+          break;
+        __builtin_amdgcn_s_sleep(kPollSleep);
       }
       flag = bad;
     }
     __syncthreads();
     poisoned = poisoned || flag != 0;
   }
-  FDP_TS(10);
   if (!early && as.ng == 1) noise_rows(p, m0, n0, r0, r1, zpre);
   // The control words are zero again: the grid barrier resets its counter, and
   // group 0 of each tile clears the tile's ticket before that barrier.
   if (p.out_dtype == FDP_BF16) finish_rows<BF16>(p, as, m0, n0, r0, r1, q4, poisoned, zpre);
   else if (p.out_dtype == FDP_F16) finish_rows<F16>(p, as, m0, n0, r0, r1, q4, poisoned, zpre);
   else finish_rows<F32>(p, as, m0, n0, r0, r1, q4, poisoned, zpre);
-  FDP_TS(12);
 }
 
 // Clears the barrier / ticket words at the head of the workspace.
@@ -1186,9 +1189,11 @@ __global__ __launch_bounds__(NT) void clear_words_kernel(unsigned* p, int64_t n)
 
 // ---------------------------------------------------------- single-pass launch
 using KernelFn = void (*)(Args);
-// Control words at the head of the workspace, zero between calls: word 0 the
-// status word, word 1 the grid-barrier counter, words [kPairFlag0,
-// kPairFlag0 + kPairMax) the split-product flags.
+// Control words at the head of the workspace: word 0 the status word (sticky,
+// for the host), word 1 the grid-barrier counter (zero between launches),
+// word 2 the launch epoch, word 3 the poison tag, words [kPairFlag0,
+// kPairFlag0 + kPairMax) the split-product flags (tagged).  A zero-filled head
+// is a valid start; every launch leaves it valid.
 constexpr size_t kWsHead = 2048;
 constexpr int kPairFlag0 = 64;
 static_assert((kPairFlag0 + kPairMax) * sizeof(unsigned) <= kWsHead, "control words");
@@ -1348,6 +1353,19 @@ inline void pair_products(Args& c, int cus) {
   c.split_k1 = nk / 2;
 }
 
+// Host-made part of a launch's Args (order_workgroups, pair_products).
+struct WorkMap {
+  uint16_t perm[kPermMax];
+  uint32_t owner_mask[kPermMax / 32];
+  uint32_t helper_mask[kPermMax / 32];
+  int split_k1;
+};
+using WorkMapKey = std::tuple<int, int, int64_t, int64_t, int>;
+inline host::ShapeCache<WorkMapKey, WorkMap>& work_map_cache() {
+  static host::ShapeCache<WorkMapKey, WorkMap> c;
+  return c;
+}
+
 // `plain`: ordinary dispatch instead of a cooperative launch (the caller
 // guarantees that nothing else occupies the device during the call, so the
 // grid, sized to the computed occupancy, is resident at once).  `clean`: the
@@ -1373,14 +1391,25 @@ hipError_t try_grouped(Args a, int cus, bool plain, bool clean, hipStream_t s) {
     c.gr = ls.gr;
     c.chunk_first = b0 == 0;
     c.chunk_last = b0 + c.chunk_nb >= a.B;
-    order_workgroups(c, cus, c.perm);
-    pair_products(c, cus);
+    // The work map depends only on the tile grid, the launch's samples, the
+    // number of k-tiles and the CU count: cached per shape.
+    const WorkMap wm = work_map_cache().get(
+        std::make_tuple(a.tiles_m, a.tiles_n, c.chunk_nb, (c.K + 63) / 64, cus), [&] {
+          WorkMap w{};
+          order_workgroups(c, cus, w.perm);
+          std::memcpy(c.perm, w.perm, sizeof(w.perm));
+          pair_products(c, cus);
+          std::memcpy(w.owner_mask, c.owner_mask, sizeof(w.owner_mask));
+          std::memcpy(w.helper_mask, c.helper_mask, sizeof(w.helper_mask));
+          w.split_k1 = c.split_k1;
+          return w;
+        });
+    std::memcpy(c.perm, wm.perm, sizeof(wm.perm));
+    std::memcpy(c.owner_mask, wm.owner_mask, sizeof(wm.owner_mask));
+    std::memcpy(c.helper_mask, wm.helper_mask, sizeof(wm.helper_mask));
+    c.split_k1 = wm.split_k1;
     KernelFn fn = grouped[ls.units - 1];
-    int occ = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void*>(fn), NT,
-                                                     0) != hipSuccess ||
-        occ < 2)
-      return hipErrorNotSupported;
+    if (host::occupancy(reinterpret_cast<const void*>(fn), NT, 0) < 2) return hipErrorNotSupported;
     if (b0 == 0 && !clean)
       hipLaunchKernelGGL(clear_words_kernel<0>,
                          dim3(static_cast<unsigned>((words + NT - 1) / NT)), dim3(NT), 0, s,

@@ -67,9 +67,11 @@ typedef enum fdp_layout {
  * point's db is k = 1) gets, at its row-major element e, the (e mod 4)-th of
  * four normals made from the Philox4x32-10 block (Salmon et al., SC'11)
  *   counter {lo32(offset + e/4), hi32(offset + e/4), k, 0}, key {lo32(seed), hi32(seed)}
- * whose words (w0, w1) and (w2, w3) each give two normals by Box-Muller on
- * 24-bit uniforms u = ((w >> 8) + 0.5) / 2^24:
- *   r = sqrt(-2 ln u_first), z = (r cos 2 pi u_second, r sin 2 pi u_second).
+ * whose words (w0, w1) and (w2, w3) each give two normals by Box-Muller:
+ *   r = sqrt(-2 ln u_first), z = (r cos 2 pi u_second, r sin 2 pi u_second),
+ *   u_first = (w_first + 0.5) / 2^32, u_second = ((w_second >> 8) + 0.5) / 2^24,
+ * so |z| <= sqrt(-2 ln 2^-33) = 6.76 (the tail beyond holds about 1.4e-11 of
+ * a normal's mass).
  * A call uses counter blocks [offset, offset + ceil(numel / 4)) of each output;
  * callers advance `offset` (or change `seed`) between calls.  The struct is
  * read on the host during the call. */
@@ -132,23 +134,36 @@ int fdp_version(void);
  *            concurrently a kernel that waits on this one.  Should a bounded
  *            grid wait (seconds) still expire, the affected outputs (and
  *            norms/factors) are NaN and the status word below is set;
+ *            bits 4 and 5 choose between the two single-pass kernels for
+ *            16-bit TN operands: by default the wide kernel (one 384x192 or
+ *            192x384 output tile of one sample per CU, eight waves) is used
+ *            when the layer's tiles times the batch fit the CUs and fill at
+ *            least 70% of them, and the grouped kernel (128x128 tiles, several
+ *            samples per workgroup) otherwise; bit 4 (FDP_WGRAD_WIDE) takes the
+ *            wide kernel whenever the products fit the CUs at all, bit 5
+ *            (FDP_WGRAD_NARROW) never takes it;
  *            bit 3 (FDP_WGRAD_CLEAN_WORKSPACE) states that the workspace's
- *            control words (its first 2048 bytes) are zero -- a zero-filled
+ *            control words (its first 2048 bytes) are valid -- a zero-filled
  *            buffer, or one whose last use was a completed fdp_wgrad_clip call
- *            (of any shape) whose status word stayed zero, which always
- *            leaves them zero -- so the library skips clearing them.
+ *            of any shape, which always leaves them valid -- so the library
+ *            skips clearing them.
  * workspace: device buffer of at least fdp_wgrad_clip_workspace_size() bytes,
  *            16-byte aligned.  Its first int is a status word: nonzero after
  *            the call completes means a bounded inter-workgroup wait of the
- *            single-pass kernel expired (results are then invalid).  With
- *            FDP_WGRAD_CLEAN_WORKSPACE the word is sticky: after reading a
- *            nonzero value the caller zeroes the first 2048 bytes (an expired
- *            wait can leave other control words set).
+ *            single-pass kernel expired in this call or an earlier one since
+ *            the caller last zeroed the word (results of the call whose wait
+ *            expired are NaN).  The word is sticky: the library only sets it,
+ *            the caller reads and zeroes it.  An expiry affects only the
+ *            launch it happened in: the other control words carry a
+ *            per-launch tag (word 2 counts launches), so later calls on the
+ *            same workspace are exact whether or not the word was zeroed.
  * ---------------------------------------------------------------------- */
 #define FDP_WGRAD_NOCLIP 1
 #define FDP_WGRAD_TWO_PASS 2
 #define FDP_WGRAD_PLAIN_LAUNCH 4
 #define FDP_WGRAD_CLEAN_WORKSPACE 8
+#define FDP_WGRAD_WIDE 16
+#define FDP_WGRAD_NARROW 32
 
 int fdp_wgrad_clip_workspace_size(int64_t B, int64_t K, int64_t M, int64_t N,
                                   int dtype, int flags, size_t* bytes);

@@ -14,10 +14,11 @@ own inside the kernels and this module restates that stream exactly:
                  (tests/test_oracle.py).
   normals        element e of output `stream`: block offset + e // 4 with
                  counter {lo, hi, stream, 0} and key {lo(seed), hi(seed)}; words
-                 (w0, w1) and (w2, w3) -> two normals each by Box-Muller on the
-                 24-bit uniforms ((w >> 8) + 0.5) / 2^24.  Pinned statistically
-                 (moments, tails, independence of neighbouring elements and
-                 streams) in tests/test_oracle.py.
+                 (w0, w1) and (w2, w3) -> two normals each by Box-Muller, the
+                 radius from the 32-bit uniform (w0 + 0.5) / 2^32 (|z| <= 6.76)
+                 and the angle from the 24-bit uniform ((w1 >> 8) + 0.5) / 2^24.
+                 Pinned statistically (moments, tails, independence of
+                 neighbouring elements and streams) in tests/test_oracle.py.
 """
 from __future__ import annotations
 
@@ -50,6 +51,10 @@ def _uniform24(w):
     return ((w >> np.uint32(8)).astype(np.float64) + 0.5) / float(1 << 24)
 
 
+def _uniform32(w):
+    return (w.astype(np.float64) + 0.5) / float(1 << 32)
+
+
 def normals(n: int, seed: int, offset: int = 0, stream: int = 0) -> np.ndarray:
     """The first n normals (float64) of the in-kernel draw with key (seed, offset)
     for output `stream`."""
@@ -64,7 +69,7 @@ def normals(n: int, seed: int, offset: int = 0, stream: int = 0) -> np.ndarray:
     w = philox4x32_10(ctr, key)
     out = np.empty((nblk, 4), dtype=np.float64)
     for a, b, j in ((0, 1, 0), (2, 3, 2)):
-        r = np.sqrt(-2.0 * np.log(_uniform24(w[:, a])))
+        r = np.sqrt(-2.0 * np.log(_uniform32(w[:, a])))
         th = 2.0 * np.pi * _uniform24(w[:, b])
         out[:, j] = r * np.cos(th)
         out[:, j + 1] = r * np.sin(th)

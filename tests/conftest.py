@@ -24,3 +24,13 @@ def pytest_collection_modifyitems(config, items):
     for item in items:
         if "gpu" in item.keywords:
             item.add_marker(skip)
+
+
+def pytest_terminal_summary(terminalreporter, exitstatus, config):
+    """Measured parity errors of the checks that report them (tests/_tol.py)."""
+    from tests._tol import MARGINS
+    if not MARGINS:
+        return
+    terminalreporter.write_sep("-", "parity margins: max|y - y_ref| / max|y_ref| (or element-wise)")
+    for name, err, tol in MARGINS:
+        terminalreporter.write_line(f"{name:<60s} {err:9.2e}  (tolerance {tol:.0e}, {err / tol:5.1%})")

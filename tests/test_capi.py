@@ -58,7 +58,8 @@ def test_wgrad_validation_codes():
     assert _wgrad(B=0) == 2
     assert _wgrad(lda=4) == 2          # row stride shorter than M
     assert _wgrad(out=None) == 3
-    assert _wgrad(flags=16) == 3
+    assert _wgrad(flags=64) == 3       # no such flag
+    assert _wgrad(flags=16 | 32) == 3  # FDP_WGRAD_WIDE and FDP_WGRAD_NARROW together
     assert _wgrad(flags=1, norms=16) == 3  # norms undefined without the norm pass
     assert _wgrad() == 4               # workspace missing
 
@@ -67,6 +68,12 @@ def test_workspace_queries():
     L = _lib.lib()
     n = _lib.size_query(L.fdp_wgrad_clip_workspace_size, 8, 1024, 3072, 768, 2, 0)
     assert n >= 8 * 4
+    # cfg2 takes the wide kernel by default: 256 exchange slots of 63 bf16 32x32 blocks,
+    # less than one bf16 gradient per sample (8 * 3072 * 768 * 2 bytes)
+    assert 256 * 63 * 2048 <= n < 8 * 3072 * 768 * 2
+    narrow = _lib.size_query(L.fdp_wgrad_clip_workspace_size, 8, 1024, 3072, 768, 2,
+                             _lib.WGRAD_NARROW)
+    assert narrow < n
     with pytest.raises(KeyError):
         _lib.size_query(L.fdp_wgrad_clip_workspace_size, 8, 1024, 3072, 768, 9, 0)
     with pytest.raises(ValueError):

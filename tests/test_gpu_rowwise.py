@@ -94,9 +94,10 @@ def test_layernorm_bwd_parity(shape, dtype):
         param_dtype=torch.float32, return_stats=True)
     ref = O.layernorm_bwd_clip(g, x, w, 1e-5, C=C, noise_multiplier=0.7, z_w=zw, z_b=zb,
                                mean=mean, rstd=rstd)
-    assert_close(dx, ref["dx"], dtype, "dx")
-    assert_close(dw, ref["dw"], dtype, "dgamma")
-    assert_close(db, ref["db"], dtype, "dbeta")
+    tag = f"cfg4 LN bwd ({dtype})" if shape == (16, 1024, 1024) else None
+    assert_close(dx, ref["dx"], dtype, "dx", margin=tag and tag + ": dx")
+    assert_close(dw, ref["dw"], dtype, "dgamma", margin=tag and tag + ": dgamma")
+    assert_close(db, ref["db"], dtype, "dbeta", margin=tag and tag + ": dbeta")
     assert_elementwise(norms[:B], ref["norms_w"], dtype, "norms gamma")
     assert_elementwise(norms[B:], ref["norms_b"], dtype, "norms beta")
     assert_elementwise(fac[:B], ref["fac_w"], dtype, "factors gamma")

@@ -76,11 +76,12 @@ def test_wgrad_split_products(shape, dtype):
     ref, nref, fref = O.wgrad_clip(a, b, C, 1.0, "tn")
     for launch in ("plain", "cooperative"):
         out, n, f = core.wgrad_clip(a, b, C, 1.0, out_dtype=torch.float32, return_stats=True,
-                                    launch=launch, check=True)
+                                    launch=launch, single_pass="narrow", check=True)
         assert_close(out, ref, dtype, "out")
         assert_elementwise(n, nref, dtype, "norms")
         assert_elementwise(f, fref, dtype, "factors")
-        again = core.wgrad_clip(a, b, C, 1.0, out_dtype=torch.float32, launch=launch, check=True)
+        again = core.wgrad_clip(a, b, C, 1.0, out_dtype=torch.float32, launch=launch,
+                                single_pass="narrow", check=True)
         assert torch.equal(out, again)
 
 
@@ -131,8 +132,9 @@ def test_wgrad_deterministic(two_pass):
 def test_wgrad_reused_workspace_stays_clean(shape):
     """Calls that reuse one workspace without clearing it (FDP_WGRAD_CLEAN_WORKSPACE)
     match a call on a garbage-filled workspace that the library clears, and leave
-    the control words (the first 2048 bytes) zero.  Tiles are shared by groups and a
-    call makes several launches; the tile tickets after the head are cleared by the
+    the status word and the grid-barrier counter (words 0 and 1) zero; the launch
+    epoch (word 2) advances once per launch.  Tiles are shared by groups and a call
+    makes several launches; the tile tickets after the head are cleared by the
     kernel itself, so the dirty workspace's tickets start as garbage."""
     import ctypes
     from flashdp4review_amd import _lib
@@ -159,32 +161,64 @@ def test_wgrad_reused_workspace_stays_clean(shape):
         out = call(clean, _lib.WGRAD_CLEAN_WORKSPACE)
         torch.cuda.synchronize()
         assert torch.equal(out, ref)
-        assert torch.count_nonzero(clean[:_lib.WGRAD_CONTROL_BYTES]) == 0
+        words = clean[:16].view(torch.int32).cpu()
+        assert int(words[0]) == 0 and int(words[1]) == 0
+        assert int(words[2]) > 0
     exp, _, _ = O.wgrad_clip(a, b, 0.05, 1.0, "tn")
     assert_close(ref, exp, torch.bfloat16, "clipped sum")
 
 
 def test_wgrad_expired_grid_wait_is_loud(monkeypatch):
-    """Force the single-pass kernel's bounded grid wait to expire at its first poll
-    (FDP_WGRAD_SPIN_LIMIT=0; every kernel still runs to completion): the affected
-    outputs are NaN, the status word is set and check=True raises.  The next call
-    on the same workspace is clean again."""
+    """Force the single-pass kernel's bounded waits to expire at their first poll
+    (FDP_WGRAD_SPIN_LIMIT=0; every kernel still runs to completion): the outputs
+    are NaN, the status word is set and check=True raises.  An expiry poisons only
+    its own launch: the next call (normal spin limit, no check) is exact although
+    the status word is still set, and wgrad_status() then reports and clears it.
+    8 x 1024 x 512 x 384 has split products, so a stale hand-over flag left by the
+    expired launch would also show up here."""
     from flashdp4review_amd import _lib
     a, b = make(8, 1024, 512, 384, torch.bfloat16, "tn", seed=13)
-    monkeypatch.setenv("FDP_WGRAD_SPIN_LIMIT", "0")
+    ref, _, _ = O.wgrad_clip(a, b, 0.5, 1.0, "tn")
     for launch in ("plain", "cooperative"):
+        monkeypatch.setenv("FDP_WGRAD_SPIN_LIMIT", "0")
         with pytest.raises(_lib.FlashDPError):
-            out = core.wgrad_clip(a, b, 0.5, 1.0, launch=launch, out_dtype=torch.float32,
-                                  check=True)
+            core.wgrad_clip(a, b, 0.5, 1.0, launch=launch, out_dtype=torch.float32, check=True)
         out = core.wgrad_clip(a, b, 0.5, 1.0, launch=launch, out_dtype=torch.float32)
         torch.cuda.synchronize()
         assert torch.isnan(out).any()
-        with pytest.raises(_lib.FlashDPError):  # the status word is sticky until checked
-            core.wgrad_clip(a, b, 0.5, 1.0, launch=launch, out_dtype=torch.float32, check=True)
-    monkeypatch.delenv("FDP_WGRAD_SPIN_LIMIT")
-    ref, _, _ = O.wgrad_clip(a, b, 0.5, 1.0, "tn")
+        monkeypatch.delenv("FDP_WGRAD_SPIN_LIMIT")
+        for _ in range(2):
+            out = core.wgrad_clip(a, b, 0.5, 1.0, launch=launch, out_dtype=torch.float32)
+            assert_close(out, ref, torch.bfloat16, f"after expiry ({launch})")
+        assert core.wgrad_status() != 0
+        assert core.wgrad_status() == 0
     out = core.wgrad_clip(a, b, 0.5, 1.0, out_dtype=torch.float32, check=True)
-    assert_close(out, ref, torch.bfloat16, "after expiry")
+    assert_close(out, ref, torch.bfloat16, "after expiry, checked")
+
+
+def test_wgrad_expiry_reported_asynchronously(monkeypatch):
+    """Without check=True an expiry is reported by a later call on the stream: the
+    status word is copied to pinned host memory behind every STATUS_PERIOD-th call,
+    and the first call after that copy completes raises (once) and clears it."""
+    from flashdp4review_amd import _lib
+    from flashdp4review_amd.core import wgrad as W
+    a, b = make(8, 256, 512, 384, torch.bfloat16, "tn", seed=15)
+    core.wgrad_status()  # start from a clear status word
+    monkeypatch.setattr(W, "STATUS_PERIOD", 1)
+    monkeypatch.setenv("FDP_WGRAD_SPIN_LIMIT", "0")
+    out = core.wgrad_clip(a, b, 0.5, 1.0, launch="plain")  # expires; the probe is queued
+    monkeypatch.delenv("FDP_WGRAD_SPIN_LIMIT")
+    torch.cuda.synchronize()
+    assert torch.isnan(out.float()).any()
+    with pytest.raises(_lib.FlashDPError):
+        core.wgrad_clip(a, b, 0.5, 1.0)
+    torch.cuda.synchronize()
+    assert core.wgrad_status(clear=False) == 0
+    ref, _, _ = O.wgrad_clip(a, b, 0.5, 1.0, "tn")
+    for _ in range(3):  # later probes read a clear word: no further raise
+        out = core.wgrad_clip(a, b, 0.5, 1.0, out_dtype=torch.float32)
+        torch.cuda.synchronize()
+    assert_close(out, ref, torch.bfloat16, "after the report")
 
 
 @pytest.mark.parametrize("shape", [(5, 96, 4000, 2300), (2, 64, 8192, 2048), (3, 33, 6000, 3000)],
@@ -280,41 +314,52 @@ def test_operator_api():
     assert_close(core.conv1d_weight_flashdp(x, g, 0.2, 1.0), ref, dtype, "conv1d_weight_flashdp")
 
 
+@pytest.mark.parametrize("single_pass", ["auto", "narrow"])
 @pytest.mark.parametrize("dtype", [torch.bfloat16], ids=str)
-def test_wgrad_cfg2_full_size(dtype):
+def test_wgrad_cfg2_full_size(dtype, single_pass):
     """cfg2 (Linear 768->3072, B=8, T=1024): norms and the clipped sum against an fp32
-    torch reference on the GPU (per-sample bmm in fp32), all samples clipped."""
+    torch reference on the GPU (per-sample bmm in fp32), all samples clipped; the
+    default kernel (the wide one at this shape) and the grouped one."""
     torch.manual_seed(0)
     x = torch.randn(8, 1024, 768, device=DEV).to(dtype)
     g = (torch.randn(8, 1024, 3072, device=DEV) * 0.02).to(dtype)
     out, norms, fac = core.wgrad_clip(g, x, 1.0, 1.0, out_dtype=torch.float32, return_stats=True,
-                                      check=True)
+                                      single_pass=single_pass, check=True)
     G = torch.bmm(g.float().transpose(1, 2).contiguous(), x.float())  # [8, 3072, 768]
     n_ref = G.flatten(1).norm(dim=1)
     c_ref = torch.clamp(1.0 / (n_ref + 1e-10), max=1.0)
     ref = (c_ref[:, None, None] * G).sum(0)
     assert torch.all(n_ref > 1.0)
-    assert_elementwise(norms, n_ref.double().cpu().numpy(), dtype, "norms")
-    assert_elementwise(fac, c_ref.double().cpu().numpy(), dtype, "factors")
-    assert_close(out, ref.double().cpu().numpy(), dtype, "clipped sum")
+    tag = f"cfg2 wgrad ({single_pass} kernel)"
+    assert_elementwise(norms, n_ref.double().cpu().numpy(), dtype, "norms",
+                       margin=f"{tag}: per-sample norms (bf16 in)")
+    assert_elementwise(fac, c_ref.double().cpu().numpy(), dtype, "factors",
+                       margin=f"{tag}: clip factors (bf16 in)")
+    assert_close(out, ref.double().cpu().numpy(), dtype, "clipped sum",
+                 margin=f"{tag}: clipped sum, fp32 out (bf16 in)")
     # with every sample clipped, the 1/B-free sum has norm <= B*C
     assert out.norm().item() <= 8.0 * (1 + 1e-3)
 
 
-def test_wgrad_memory_no_per_sample_materialisation():
-    """Peak extra memory of the call stays below B*M*N*elt (what materialising
-    one bf16 gradient per sample would take)."""
+@pytest.mark.parametrize("single_pass", ["wide", "narrow"])
+def test_wgrad_memory_no_per_sample_materialisation(single_pass):
+    """Peak memory the call adds to its output (the workspace) stays below
+    B*M*N*elt, what materialising one bf16 gradient per sample would take: the
+    wide kernel exchanges (B-1)/B of each sample's tile in bf16, the grouped
+    kernel sums of several samples."""
+    from flashdp4review_amd.core import wgrad as W
     B, K, M, N = 8, 1024, 3072, 768
     x = torch.randn(B, K, N, device=DEV, dtype=torch.bfloat16)
     g = torch.randn(B, K, M, device=DEV, dtype=torch.bfloat16) * 0.02
+    out = torch.empty(M, N, device=DEV, dtype=torch.bfloat16)
+    W.release_workspaces()
     torch.cuda.synchronize()
     torch.cuda.reset_peak_memory_stats()
     base = torch.cuda.memory_allocated()
-    out = core.wgrad_clip(g, x, 1.0, 1.0)
+    core.wgrad_clip(g, x, 1.0, 1.0, out=out, single_pass=single_pass)
     torch.cuda.synchronize()
     extra = torch.cuda.max_memory_allocated() - base
     assert extra < B * M * N * 2, extra
-    del out
 
 
 # ------------------------------------------------------------ in-kernel noise
@@ -362,3 +407,85 @@ def test_wgrad_noise_key_advances():
     assert torch.equal(f((7, 0)), f((7, 0)))
     assert abs(np.corrcoef(z1.ravel(), z2.ravel())[0, 1]) < 0.05
     assert abs(z1.std() - 1) < 0.05
+
+
+# ------------------------------------------------------------ wide single pass
+WIDE_SHAPES = [
+    (8, 1024, 3072, 768),   # cfg2: 32 tiles of 384x192 x 8 samples = 256 products
+    (4, 100, 1000, 704),    # ragged tiles in both directions, K not a multiple of 32
+    (16, 64, 512, 384),     # 16 samples per tile: regions of 4-5 blocks
+    (2, 32, 384, 192),      # one tile, two samples: regions of 36 blocks
+    (72, 16, 96, 96),       # 72 samples of one (mostly empty) tile: one block per region
+    (3, 1, 200, 400),       # K = 1
+    (6, 256, 576, 768),     # 192x384 tiles (6 against 8 of 384x192)
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=str)
+@pytest.mark.parametrize("shape", WIDE_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_wgrad_wide_parity(shape, dtype):
+    """The wide single-pass kernel (one tile of one sample per CU), forced on
+    shapes it fits: clipped sum, norms and factors against the fp64 oracle, in
+    fp32 and the input dtype, both launch modes, bitwise-equal repeats, and the
+    grouped kernel within the same tolerance."""
+    B, K, M, N = shape
+    a, b = make(B, K, M, N, dtype, "tn", seed=50)
+    _, n0, _ = O.wgrad_clip(a, b, 1.0, 1.0, "tn")
+    C = float(np.median(n0))
+    ref, nref, fref = O.wgrad_clip(a, b, C, 1.0, "tn")
+    outs = []
+    for launch in ("plain", "cooperative"):
+        out, n, f = core.wgrad_clip(a, b, C, 1.0, out_dtype=torch.float32, return_stats=True,
+                                    launch=launch, single_pass="wide", check=True)
+        assert_close(out, ref, dtype, "out", margin=None if shape != WIDE_SHAPES[0] else
+                     f"wide kernel cfg2 shape: clipped sum, fp32 out ({dtype})")
+        assert_elementwise(n, nref, dtype, "norms")
+        assert_elementwise(f, fref, dtype, "factors")
+        outs.append(out)
+    assert torch.equal(outs[0], outs[1])
+    out16 = core.wgrad_clip(a, b, C, 1.0, single_pass="wide", check=True)
+    assert out16.dtype == dtype
+    assert_close(out16, ref, dtype, "out (input dtype)")
+    narrow = core.wgrad_clip(a, b, C, 1.0, out_dtype=torch.float32, single_pass="narrow",
+                             check=True)
+    assert_close(narrow, ref, dtype, "grouped kernel")
+
+
+@pytest.mark.parametrize("shape", [(8, 64, 392, 520), (8, 1024, 3072, 768), (5, 40, 200, 96)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_wgrad_wide_noise(shape):
+    """Noise in the wide kernel's finish: the in-kernel Philox draw (each quad of
+    lanes draws four rows' blocks and transposes them) equals the oracle's
+    stream element for element; an injected tensor is added as given."""
+    B, K, M, N = shape
+    a, b = make(B, K, M, N, torch.bfloat16, "tn", seed=51)
+    ref, _, _ = O.wgrad_clip(a, b, 0.5, 1.0, "tn")
+    kw = dict(out_scale=0.5, out_dtype=torch.float32, single_pass="wide", check=True)
+    out0 = core.wgrad_clip(a, b, 0.5, 1.0, noise_scale=0.25, **kw)
+    out = core.wgrad_clip(a, b, 0.5, 1.0, noise_scale=0.25, noise_key=NOISE_KEY, **kw)
+    z = PX.normals(M * N, *NOISE_KEY).reshape(M, N)
+    assert_close(out0, 0.5 * ref, torch.bfloat16, "no noise")
+    got = (out.double() - out0.double()).cpu().numpy() / 0.25
+    assert np.max(np.abs(got - z)) < 1e-4, np.max(np.abs(got - z))
+    zt = torch.randn(M, N, generator=torch.Generator().manual_seed(9)).to(DEV)
+    out2 = core.wgrad_clip(a, b, 0.5, 1.0, noise=zt, noise_scale=0.25, **kw)
+    assert_close(out2, 0.5 * ref + 0.25 * zt.double().cpu().numpy(), torch.bfloat16, "injected")
+
+
+def test_wgrad_wide_expired_wait(monkeypatch):
+    """A forced expiry of the wide kernel's grid wait: NaN outputs and a raised
+    check; the next call on the same workspace is exact."""
+    from flashdp4review_amd import _lib
+    a, b = make(8, 256, 3072, 768, torch.bfloat16, "tn", seed=52)
+    ref, _, _ = O.wgrad_clip(a, b, 0.5, 1.0, "tn")
+    core.wgrad_status()
+    monkeypatch.setenv("FDP_WGRAD_SPIN_LIMIT", "0")
+    with pytest.raises(_lib.FlashDPError):
+        core.wgrad_clip(a, b, 0.5, 1.0, out_dtype=torch.float32, single_pass="wide", check=True)
+    out = core.wgrad_clip(a, b, 0.5, 1.0, out_dtype=torch.float32, single_pass="wide")
+    torch.cuda.synchronize()
+    assert torch.isnan(out).any()
+    monkeypatch.delenv("FDP_WGRAD_SPIN_LIMIT")
+    out = core.wgrad_clip(a, b, 0.5, 1.0, out_dtype=torch.float32, single_pass="wide")
+    assert_close(out, ref, torch.bfloat16, "after expiry")
+    assert core.wgrad_status() != 0
