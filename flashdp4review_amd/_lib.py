@@ -64,6 +64,10 @@ SIGNATURES = {
                                 _c_i64, _c_i64, _c_int, _c_int, _c_f, _c_f, _c_p, _c_f, _c_p,
                                 _c_f, _c_key, _c_p, _c_i64, _c_int, _c_p, _c_p, _c_int, _c_p,
                                 ctypes.c_size_t, _c_p]),
+    "fdp_wgrad_clip_noalloc": (_c_int, [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+                                        _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_f, _c_f, _c_p,
+                                        _c_f, _c_p, _c_f, _c_key, _c_p, _c_i64, _c_int, _c_p, _c_p,
+                                        _c_int, _c_p]),
     "fdp_colsum_clip_workspace_size": (_c_int, [_c_i64, _c_i64, _c_i64, _c_int, _c_sz_p]),
     "fdp_colsum_clip": (_c_int, [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_f, _c_f,
                                  _c_p, _c_f, _c_p, _c_f, _c_key, _c_p, _c_int, _c_p, _c_p, _c_p,
@@ -110,7 +114,7 @@ def check(status: int, what: str) -> None:
     msg = f"{what}: {lib().fdp_strerror(status).decode()} (status {status})"
     if status == 1:
         raise KeyError(msg)
-    if status in (2, 3, 6):
+    if status in (2, 3, 6, 7):
         raise ValueError(msg)
     raise FlashDPError(msg)
 

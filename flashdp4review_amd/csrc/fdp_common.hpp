@@ -287,4 +287,10 @@ struct CoherentSpan {
   }
 };
 
+// Argument checks shared by fdp_wgrad_clip and fdp_wgrad_clip_noalloc (host
+// only, touches no device): FDP_OK or the status the entry point returns.
+int wgrad_check_args(const void* a, const void* b, int64_t B, int64_t K, int64_t M, int64_t N,
+                     int64_t lda, int64_t ldb, int layout, int dtype, const void* out,
+                     int64_t ldo, int out_dtype, const float* norms, int flags);
+
 }  // namespace fdp

@@ -1120,6 +1120,7 @@ extern "C" const char* fdp_strerror(int status) {
     case FDP_ERR_WORKSPACE: return "workspace missing or too small";
     case FDP_ERR_HIP: return "HIP launch failed";
     case FDP_ERR_ALIGN: return "pointer alignment violated";
+    case FDP_ERR_TOO_LARGE: return "problem needs more than the no-allocation scratch array";
     default: return "unknown status";
   }
 }

@@ -383,14 +383,10 @@ extern "C" int fdp_wgrad_clip_workspace_size(int64_t B, int64_t K, int64_t M, in
   return FDP_OK;
 }
 
-extern "C" int fdp_wgrad_clip(const void* a, const void* b, int64_t B, int64_t K, int64_t M,
-                              int64_t N, int64_t stride_ab, int64_t lda, int64_t stride_bb,
-                              int64_t ldb, int layout, int dtype, float C, float clamp,
-                              const float* clip_args_dev, float out_scale, const void* noise,
-                              float noise_scale, const fdp_noise_key* noise_key, void* out,
-                              int64_t ldo, int out_dtype,
-                              float* norms, float* factors, int flags, void* workspace,
-                              size_t workspace_bytes, void* stream) {
+int fdp::wgrad_check_args(const void* a, const void* b, int64_t B, int64_t K, int64_t M,
+                          int64_t N, int64_t lda, int64_t ldb, int layout, int dtype,
+                          const void* out, int64_t ldo, int out_dtype, const float* norms,
+                          int flags) {
   if (!valid_dtype(dtype) || !valid_dtype(out_dtype)) return FDP_ERR_DTYPE;
   if (layout != FDP_LAYOUT_TN && layout != FDP_LAYOUT_NN) return FDP_ERR_ARG;
   if (B < 1 || M < 1 || N < 1 || K < 0) return FDP_ERR_SHAPE;
@@ -403,8 +399,22 @@ extern "C" int fdp_wgrad_clip(const void* a, const void* b, int64_t B, int64_t K
                  FDP_WGRAD_CLEAN_WORKSPACE | FDP_WGRAD_WIDE | FDP_WGRAD_NARROW)) != 0)
     return FDP_ERR_ARG;
   if ((flags & FDP_WGRAD_WIDE) && (flags & FDP_WGRAD_NARROW)) return FDP_ERR_ARG;
+  if ((flags & FDP_WGRAD_NOCLIP) != 0 && norms != nullptr) return FDP_ERR_ARG;
+  return FDP_OK;
+}
+
+extern "C" int fdp_wgrad_clip(const void* a, const void* b, int64_t B, int64_t K, int64_t M,
+                              int64_t N, int64_t stride_ab, int64_t lda, int64_t stride_bb,
+                              int64_t ldb, int layout, int dtype, float C, float clamp,
+                              const float* clip_args_dev, float out_scale, const void* noise,
+                              float noise_scale, const fdp_noise_key* noise_key, void* out,
+                              int64_t ldo, int out_dtype,
+                              float* norms, float* factors, int flags, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  const int bad = fdp::wgrad_check_args(a, b, B, K, M, N, lda, ldb, layout, dtype, out, ldo,
+                                        out_dtype, norms, flags);
+  if (bad != FDP_OK) return bad;
   const bool noclip = (flags & FDP_WGRAD_NOCLIP) != 0;
-  if (noclip && norms != nullptr) return FDP_ERR_ARG;
 
   const int cus = num_cus();
   // the workspace was sized for contiguous operands: the wide plan for the

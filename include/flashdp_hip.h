@@ -49,7 +49,8 @@ typedef enum fdp_status {
   FDP_ERR_ARG = 3,       /* NULL pointer, bad flag        -> ValueError   */
   FDP_ERR_WORKSPACE = 4, /* workspace too small           -> RuntimeError */
   FDP_ERR_HIP = 5,       /* HIP launch error              -> RuntimeError */
-  FDP_ERR_ALIGN = 6      /* pointer alignment violated    -> ValueError   */
+  FDP_ERR_ALIGN = 6,     /* pointer alignment violated    -> ValueError   */
+  FDP_ERR_TOO_LARGE = 7  /* needs more than the no-allocation scratch -> ValueError */
 } fdp_status;
 
 /* Operand layouts of the per-sample product G_b (b = 0..B-1).
@@ -175,6 +176,34 @@ int fdp_wgrad_clip(const void* a, const void* b, int64_t B, int64_t K, int64_t M
                    float noise_scale, const fdp_noise_key* noise_key, void* out,
                    int64_t ldo, int out_dtype, float* norms, float* factors, int flags,
                    void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * fdp_wgrad_clip for callers that cannot allocate device memory.
+ *
+ * No counterpart in the reference: it serves callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments and results as fdp_wgrad_clip, without the
+ * workspace: the library uses a file-scope device array of
+ * FDP_NOALLOC_SCRATCH_BYTES (64 MiB) that each GPU it runs on holds until the
+ * process ends (its address is resolved per device on the first call).  The
+ * call allocates nothing and uses the ordinary launch (FDP_WGRAD_PLAIN_LAUNCH
+ * is implied; FDP_WGRAD_CLEAN_WORKSPACE is ignored: every call clears the
+ * array's control words with a fill kernel).  Problems whose
+ * fdp_wgrad_clip_workspace_size exceeds the array return FDP_ERR_TOO_LARGE
+ * without launching.  All calls on one GPU share the array: calls that
+ * overlap on one GPU race, so the caller serialises them.  The array's
+ * status word is not visible to the caller: an expired bounded wait shows
+ * only as NaN outputs.
+ * ---------------------------------------------------------------------- */
+#define FDP_NOALLOC_SCRATCH_BYTES (64u << 20)
+
+int fdp_wgrad_clip_noalloc(const void* a, const void* b, int64_t B, int64_t K, int64_t M,
+                           int64_t N, int64_t stride_ab, int64_t lda, int64_t stride_bb,
+                           int64_t ldb, int layout, int dtype, float C, float clamp,
+                           const float* clip_args_dev, float out_scale, const void* noise,
+                           float noise_scale, const fdp_noise_key* noise_key, void* out,
+                           int64_t ldo, int out_dtype, float* norms, float* factors, int flags,
+                           void* stream);
 
 /* ------------------------------------------------------------------------
  * Clipped per-sample column sums over the middle axis:

@@ -64,6 +64,28 @@ def test_wgrad_validation_codes():
     assert _wgrad() == 4               # workspace missing
 
 
+def test_noalloc_validation_codes():
+    """fdp_wgrad_clip_noalloc validates like fdp_wgrad_clip and rejects problems
+    whose workspace exceeds its scratch array (FDP_ERR_TOO_LARGE) before it
+    touches a device, so these run without one."""
+    L = _lib.lib()
+
+    def call(B=2, K=4, M=8, N=8, dtype=2, flags=0):
+        return L.fdp_wgrad_clip_noalloc(1, 1, B, K, M, N, K * M, M, K * N, N, 0, dtype, 1.0, 1.0,
+                                        None, 1.0, None, 0.0, None, 1, N, 2, None, None, flags,
+                                        None)
+    assert call(dtype=7) == 1
+    assert call(B=0) == 2
+    assert call(flags=64) == 3
+    limit = 64 << 20
+    big = [s for s in [(128, 16, 2048, 2048), (512, 16, 2048, 2048), (1024, 8, 1024, 1024)]
+           if _lib.size_query(L.fdp_wgrad_clip_workspace_size, *s, 2, 4) > limit]
+    assert big
+    assert call(*big[0]) == 7
+    with pytest.raises(ValueError):
+        _lib.check(7, "fdp_wgrad_clip_noalloc")
+
+
 def test_workspace_queries():
     L = _lib.lib()
     n = _lib.size_query(L.fdp_wgrad_clip_workspace_size, 8, 1024, 3072, 768, 2, 0)
