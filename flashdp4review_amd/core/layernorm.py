@@ -18,7 +18,11 @@ import torch
 from .. import _lib
 from .clip_fn import clip_args_of
 
-MAX_HIDDEN = 4096  # one wavefront holds a whole row in registers
+# Rows of up to 4096 elements take one wavefront each, longer ones 16
+# wavefronts (16 elements per thread).  The reference's fused kernel accepts
+# rows of up to 64 KB (flashdp/core/layernorm_clip.py:217-221): the same
+# 16384 elements in fp32, up to 32768 in 16-bit dtypes.
+MAX_HIDDEN = 16384
 
 
 def _rows(x: torch.Tensor, H: int) -> int:

@@ -19,6 +19,10 @@
 // small.  Rows are read with 16-byte loads, one
 // wavefront per row for the LayerNorm kernels (row statistics are wavefront
 // shuffles, no LDS), 64..256 threads across the columns for the column sums.
+#include <atomic>
+#include <type_traits>
+#include <chrono>
+
 #include "fdp_common.hpp"
 #include "host_cache.hpp"
 
@@ -70,11 +74,12 @@ struct Vec<F32, 4> {  // 4 x fp32 = 16 bytes
   }
 };
 
-// Element e of lane `lane` in a row handled by one wavefront: vector
-// v = lane + 64*i covers elements v*VEC .. v*VEC+VEC-1.
-template <int EPL, int VEC>
-__device__ __forceinline__ int64_t wave_elem(int lane, int i) {
-  return (int64_t(lane) + 64 * i) * VEC;
+// Element e of thread `lane` in a row handled by LANES threads (one
+// wavefront, or LANES/64 wavefronts sharing a long row): vector
+// v = lane + LANES*i covers elements v*VEC .. v*VEC+VEC-1.
+template <int EPL, int VEC, int LANES = 64>
+__device__ __forceinline__ int wave_elem(int lane, int i) {
+  return (lane + LANES * i) * VEC;  // < 2^31: rows hold at most 16384 elements
 }
 
 // LDS position of element e of a wave's row in the LayerNorm backward fold.
@@ -89,40 +94,42 @@ __host__ __device__ __forceinline__ int64_t fold_pos(int64_t e) {
 // every permuted group of 8 stays inside the slice.
 __host__ __device__ __forceinline__ int64_t fold_slice(int64_t H) { return (H + 127) / 128 * 128; }
 
-template <class DT, int EPL, int VEC>
-__device__ inline void load_row(const typename DT::storage* row, int64_t H, int lane,
-                                float (&o)[EPL]) {
-#pragma unroll
-  for (int i = 0; i < EPL / VEC; ++i) {
-    const int64_t e = wave_elem<EPL, VEC>(lane, i);
-    if (e < H) {
-      Vec<DT, VEC>::load(row + e, o + i * VEC);
-    } else {
-#pragma unroll
-      for (int j = 0; j < VEC; ++j) o[i * VEC + j] = 0.f;
-    }
-  }
-}
-template <class DT, int EPL, int VEC>
-__device__ inline void store_row(typename DT::storage* row, int64_t H, int lane,
-                                 const float (&v)[EPL]) {
-#pragma unroll
-  for (int i = 0; i < EPL / VEC; ++i) {
-    const int64_t e = wave_elem<EPL, VEC>(lane, i);
-    if (e < H) Vec<DT, VEC>::store(row + e, v + i * VEC);
-  }
-}
 // Parameter vectors (gamma/beta) in an arbitrary dtype, default `dflt` if NULL.
-template <int EPL, int VEC>
-__device__ inline void load_param(const void* p, int dtype, int64_t H, int lane, float dflt,
-                                  float (&o)[EPL]) {
+// One uniform branch on the dtype, then straight-line loads: all EPL loads are
+// in flight together (a per-element dtype switch made each load wait for the
+// previous one, EPL round trips at every workgroup's start).
+template <int EPL, int VEC, int LANES, class S, class Cvt>
+__device__ inline void load_param_as(const S* p, int64_t H, int lane, Cvt cvt, float (&o)[EPL]) {
+  S raw[EPL];
 #pragma unroll
-  for (int i = 0; i < EPL / VEC; ++i) {
+  for (int i = 0; i < EPL / VEC; ++i)
 #pragma unroll
     for (int j = 0; j < VEC; ++j) {
-      const int64_t e = wave_elem<EPL, VEC>(lane, i) + j;
-      o[i * VEC + j] = (p != nullptr && e < H) ? load_as_f32(p, e, dtype) : (e < H ? dflt : 0.f);
+      const int e = wave_elem<EPL, VEC, LANES>(lane, i) + j;
+      const S v = p[e < static_cast<int>(H) ? e : 0];  // clamped: no branch around the load
+      raw[i * VEC + j] = e < static_cast<int>(H) ? v : S(0);
     }
+#pragma unroll
+  for (int k = 0; k < EPL; ++k) o[k] = cvt(raw[k]);
+}
+template <int EPL, int VEC, int LANES = 64>
+__device__ inline void load_param(const void* p, int dtype, int64_t H, int lane, float dflt,
+                                  float (&o)[EPL]) {
+  if (p == nullptr) {
+#pragma unroll
+    for (int i = 0; i < EPL / VEC; ++i)
+#pragma unroll
+      for (int j = 0; j < VEC; ++j)
+        o[i * VEC + j] = wave_elem<EPL, VEC, LANES>(lane, i) + j < static_cast<int>(H) ? dflt : 0.f;
+  } else if (dtype == FDP_F32) {
+    load_param_as<EPL, VEC, LANES>(static_cast<const float*>(p), H, lane,
+                                   [](float v) { return v; }, o);
+  } else if (dtype == FDP_BF16) {
+    load_param_as<EPL, VEC, LANES>(static_cast<const uint16_t*>(p), H, lane,
+                                   [](uint16_t v) { return BF16::to_f32(v); }, o);
+  } else {
+    load_param_as<EPL, VEC, LANES>(static_cast<const uint16_t*>(p), H, lane,
+                                   [](uint16_t v) { return F16::to_f32(v); }, o);
   }
 }
 
@@ -532,68 +539,128 @@ __global__ __launch_bounds__(NT) void reduce_kernel(const float* partials, int c
 
 // ================================================================= LayerNorm
 constexpr int kLnThreads = 512;  // forward: 8 wavefronts, one row each at a time
+// Backward: rows in flight per row group.  On cfg4 (16x1024x1024 bf16, one
+// launch) 1, 2 and 4 measured 27.5, 28.2 and 29.8 us per call.
+constexpr int kLnLookahead = 1;
 
-// Raw (undecoded) row fragment of one lane: lets the next row's loads be in
-// flight while the current row is processed.
-template <class DT, int EPL, int VEC>
+// Row I/O goes through a raw buffer resource over the row's bytes: accesses
+// past the end read zero and are dropped, so loads and stores need no branch.
+// (With a branch around each load or store the compiler could not count the
+// memory operations in flight at the loop's back edge and waited for all of
+// them -- the next row's prefetch included -- at every row.)
+// A value known to be the same in every lane of the wavefront, read from the
+// first lane (so it lives in scalar registers and feeds scalar loads).
+__device__ __forceinline__ int64_t uniform_i64(int64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(static_cast<uint64_t>(v) >> 32));
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+// Every caller's row and range are the same across the wavefront: reading
+// them from the first lane puts the resource in scalar registers (otherwise
+// the compiler loops over the lanes' values around every access).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const void* row, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(row);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a >> 32));
+  void* base = reinterpret_cast<void*>((static_cast<uint64_t>(hi) << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(base, static_cast<short>(0),
+                                           static_cast<int>(__builtin_amdgcn_readfirstlane(bytes)),
+                                           kRawBufferWord3);
+}
+
+// Raw (undecoded) row fragment of one thread: lets the next row's loads be in
+// flight while the current row is processed.  `on` false issues the loads
+// against a zero-length range: they read zero and touch no memory.
+template <class DT, int EPL, int VEC, int LANES = 64>
 struct RawRow;
-template <class DT, int EPL>
-struct RawRow<DT, EPL, 8> {  // 16-bit, 16-byte vectors
-  uint4 q[EPL / 8];
-  __device__ __forceinline__ void load(const uint16_t* row, int64_t H, int lane) {
+template <class DT, int EPL, int LANES>
+struct RawRow<DT, EPL, 8, LANES> {  // 16-bit, 16-byte vectors
+  u32x4 q[EPL / 8];
+  __device__ __forceinline__ void load(const uint16_t* row, int64_t H, int lane, bool on = true) {
+    const auto r = row_rsrc(row, on ? static_cast<uint32_t>(H * 2) : 0u);
 #pragma unroll
-    for (int i = 0; i < EPL / 8; ++i) {
-      const int64_t e = wave_elem<EPL, 8>(lane, i);
-      q[i] = e < H ? *reinterpret_cast<const uint4*>(row + e) : make_uint4(0, 0, 0, 0);
-    }
+    for (int i = 0; i < EPL / 8; ++i)
+      q[i] = __builtin_amdgcn_raw_buffer_load_b128(r, wave_elem<EPL, 8, LANES>(lane, i) * 2, 0, 0);
   }
   __device__ __forceinline__ void decode(float (&o)[EPL]) const {
 #pragma unroll
     for (int i = 0; i < EPL / 8; ++i) {
-      const uint32_t w[4] = {q[i].x, q[i].y, q[i].z, q[i].w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        o[i * 8 + 2 * j] = DT::to_f32(static_cast<uint16_t>(w[j] & 0xffffu));
-        o[i * 8 + 2 * j + 1] = DT::to_f32(static_cast<uint16_t>(w[j] >> 16));
+        o[i * 8 + 2 * j] = DT::to_f32(static_cast<uint16_t>(q[i][j] & 0xffffu));
+        o[i * 8 + 2 * j + 1] = DT::to_f32(static_cast<uint16_t>(q[i][j] >> 16));
       }
     }
   }
 };
-template <int EPL>
-struct RawRow<F32, EPL, 4> {  // fp32, 16-byte vectors
-  float4 q[EPL / 4];
-  __device__ __forceinline__ void load(const float* row, int64_t H, int lane) {
+template <int EPL, int LANES>
+struct RawRow<F32, EPL, 4, LANES> {  // fp32, 16-byte vectors
+  u32x4 q[EPL / 4];
+  __device__ __forceinline__ void load(const float* row, int64_t H, int lane, bool on = true) {
+    const auto r = row_rsrc(row, on ? static_cast<uint32_t>(H * 4) : 0u);
 #pragma unroll
-    for (int i = 0; i < EPL / 4; ++i) {
-      const int64_t e = wave_elem<EPL, 4>(lane, i);
-      q[i] = e < H ? *reinterpret_cast<const float4*>(row + e) : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
+    for (int i = 0; i < EPL / 4; ++i)
+      q[i] = __builtin_amdgcn_raw_buffer_load_b128(r, wave_elem<EPL, 4, LANES>(lane, i) * 4, 0, 0);
   }
   __device__ __forceinline__ void decode(float (&o)[EPL]) const {
 #pragma unroll
-    for (int i = 0; i < EPL / 4; ++i) {
-      o[4 * i] = q[i].x;
-      o[4 * i + 1] = q[i].y;
-      o[4 * i + 2] = q[i].z;
-      o[4 * i + 3] = q[i].w;
-    }
+    for (int i = 0; i < EPL / 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[4 * i + j] = __uint_as_float(q[i][j]);
   }
 };
-template <class DT, int EPL>
-struct RawRow<DT, EPL, 1> {  // any dtype, element loads (unaligned rows)
-  typename DT::storage q[EPL];
-  __device__ __forceinline__ void load(const typename DT::storage* row, int64_t H, int lane) {
+template <class DT, int EPL, int LANES>
+struct RawRow<DT, EPL, 1, LANES> {  // any dtype, element loads (unaligned rows)
+  uint32_t q[EPL];
+  __device__ __forceinline__ void load(const typename DT::storage* row, int64_t H, int lane,
+                                      bool on = true) {
+    constexpr int ES = sizeof(typename DT::storage);
+    const auto r = row_rsrc(row, on ? static_cast<uint32_t>(H * ES) : 0u);
 #pragma unroll
     for (int i = 0; i < EPL; ++i) {
-      const int64_t e = wave_elem<EPL, 1>(lane, i);
-      q[i] = e < H ? row[e] : typename DT::storage(0);
+      const int off = wave_elem<EPL, 1, LANES>(lane, i) * ES;
+      if constexpr (ES == 4) q[i] = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+      else q[i] = __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
     }
   }
   __device__ __forceinline__ void decode(float (&o)[EPL]) const {
 #pragma unroll
-    for (int i = 0; i < EPL; ++i) o[i] = DT::to_f32(q[i]);
+    for (int i = 0; i < EPL; ++i) {
+      if constexpr (sizeof(typename DT::storage) == 4) o[i] = __uint_as_float(q[i]);
+      else o[i] = DT::to_f32(static_cast<uint16_t>(q[i]));
+    }
   }
 };
+
+// Row store: `on` false drops the whole row (a zero-length resource).
+template <class DT, int EPL, int VEC, int LANES = 64>
+__device__ inline void store_row(typename DT::storage* row, int64_t H, int lane,
+                                 const float (&v)[EPL], bool on = true) {
+  constexpr int ES = sizeof(typename DT::storage);
+  const auto r = row_rsrc(row, on ? static_cast<uint32_t>(H * ES) : 0u);
+#pragma unroll
+  for (int i = 0; i < EPL / VEC; ++i) {
+    const int off = wave_elem<EPL, VEC, LANES>(lane, i) * ES;
+    if constexpr (VEC == 8) {  // 16-bit
+      u32x4 o;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        o[j] = DT::from_f32(v[i * 8 + 2 * j]) | (uint32_t(DT::from_f32(v[i * 8 + 2 * j + 1])) << 16);
+      __builtin_amdgcn_raw_buffer_store_b128(o, r, off, 0, 0);
+    } else if constexpr (VEC == 4) {  // fp32
+      u32x4 o;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[j] = __float_as_uint(v[i * 4 + j]);
+      __builtin_amdgcn_raw_buffer_store_b128(o, r, off, 0, 0);
+    } else if constexpr (ES == 4) {
+      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v[i]), r, off, 0, 0);
+    } else {
+      __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(DT::from_f32(v[i])), r, off, 0,
+                                            0);
+    }
+  }
+}
 
 // One wavefront per row, rows dealt grid-stride to the wavefronts, the next
 // row's loads issued before the current row is normalised.
@@ -612,11 +679,12 @@ __global__ __launch_bounds__(kLnThreads) void ln_fwd_kernel(const typename DT::s
   load_param<EPL, VEC>(bias, w_dtype, H, lane, 0.f, bv);
   const float inv_h = 1.f / static_cast<float>(H);
   RawRow<DT, EPL, VEC> rx;
-  if (wid < rows) rx.load(x + wid * H, H, lane);
+  rx.load(x + (wid < rows ? wid : 0) * H, H, lane, wid < rows);
   for (int64_t r = wid; r < rows; r += nw) {
     float xv[EPL];
     rx.decode(xv);
-    if (r + nw < rows) rx.load(x + (r + nw) * H, H, lane);
+    const bool more = r + nw < rows;
+    rx.load(x + (more ? r + nw : r) * H, H, lane, more);
     float s = 0.f;
 #pragma unroll
     for (int i = 0; i < EPL; ++i) s += xv[i];
@@ -626,7 +694,7 @@ __global__ __launch_bounds__(kLnThreads) void ln_fwd_kernel(const typename DT::s
     for (int i = 0; i < EPL / VEC; ++i)
 #pragma unroll
       for (int j = 0; j < VEC; ++j) {
-        const float d = wave_elem<EPL, VEC>(lane, i) + j < H ? xv[i * VEC + j] - mu : 0.f;
+        const float d = wave_elem<EPL, VEC>(lane, i) + j < static_cast<int>(H) ? xv[i * VEC + j] - mu : 0.f;
         q += d * d;
       }
     const float var = wave_sum_dpp(q) * inv_h;
@@ -642,32 +710,30 @@ __global__ __launch_bounds__(kLnThreads) void ln_fwd_kernel(const typename DT::s
   }
 }
 
-// grid (chunks, B).  Wave w handles rows t = chunk*rows + w, +W, ... with the
-// next row's x / dy / mean / rstd loads in flight while the current row is
-// processed: writes dx and accumulates P = sum dy*x_hat, Q = sum dy in
-// registers; the W = NTH/64 waves are folded in wave order through LDS into
-// the chunk's partials (stream b: P, stream B+b: Q).  Workgroup (0,0) zeroes
-// the reduction's two tickets.
-template <class DT, int EPL, int VEC, int NTH>
-__global__ __launch_bounds__(NTH) void ln_bwd_kernel(const typename DT::storage* dy,
-                                                    const typename DT::storage* x, const void* w,
-                                                    int w_dtype, const float* mean,
-                                                    const float* rstd, int64_t T, int64_t H,
-                                                    int64_t rows, int chunks,
-                                                    typename DT::storage* dx, float* partials,
-                                                    int64_t B, unsigned* tickets) {
-  constexpr int W = NTH / kWave;
-  if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x < 2)
-    __hip_atomic_store(tickets + threadIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  extern __shared__ __attribute__((aligned(16))) char smem_raw[];
-  float* lds = reinterpret_cast<float*>(smem_raw);  // [W][H]
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t b = blockIdx.y;
-  const int chunk = blockIdx.x;
-  const int64_t t0 = int64_t(chunk) * rows;
-  const int64_t t1 = t0 + rows < T ? t0 + rows : T;
+// One (chunk, sample) workgroup of the LayerNorm backward.  Rows are shared by
+// NWR wavefronts (L = 64*NWR threads, EPL elements each); the workgroup's
+// G = NTH/L row groups take rows t = t0 + g, t0 + g + G, ... < t1 of sample b,
+// with the next row's x / dy / mean / rstd loads in flight while the current
+// row is processed: writes dx and accumulates P = sum dy*x_hat, Q = sum dy in
+// registers.  With NWR > 1 a row's two sums are wavefront sums added in
+// wavefront order through LDS (double-buffered by parity; every thread runs
+// the same trip count, so the barrier is uniform).  The G row groups are then
+// folded in order through LDS (`lds`: G * fold_slice(H) floats), and
+// put(0, e, P_e) / put(1, e, Q_e) receives the chunk's sums.
+template <class DT, int EPL, int VEC, int NTH, int NWR, int LA, class Put>
+__device__ inline void ln_bwd_chunk(const typename DT::storage* dy,
+                                    const typename DT::storage* x, const void* w, int w_dtype,
+                                    const float* mean, const float* rstd, int64_t T, int64_t H,
+                                    int64_t b, int64_t t0, int64_t t1,
+                                    typename DT::storage* dx, float* lds, Put put) {
+  constexpr int L = NWR * kWave;
+  constexpr int G = NTH / L;
+  static_assert(G >= 1 && G * L == NTH, "whole row groups");
+  __shared__ float red[2][G][NWR][2];
+  const int lid = threadIdx.x % L, g = threadIdx.x / L;
+  const int lane = threadIdx.x & 63, wig = lid >> 6;
   float wv[EPL];
-  load_param<EPL, VEC>(w, w_dtype, H, lane, 1.f, wv);
+  load_param<EPL, VEC, L>(w, w_dtype, H, lid, 1.f, wv);
   float P[EPL], Q[EPL];
 #pragma unroll
   for (int i = 0; i < EPL; ++i) {
@@ -675,75 +741,481 @@ __global__ __launch_bounds__(NTH) void ln_bwd_kernel(const typename DT::storage*
     Q[i] = 0.f;
   }
   const float inv_h = 1.f / static_cast<float>(H);
-  RawRow<DT, EPL, VEC> rx, rg;
-  float mu_n = 0.f, rs_n = 0.f;
-  int64_t t = t0 + wave;
-  if (t < t1) {
-    rx.load(x + (b * T + t) * H, H, lane);
-    rg.load(dy + (b * T + t) * H, H, lane);
-    mu_n = mean[b * T + t];
-    rs_n = rstd[b * T + t];
+  // LA rows per row group are in flight: the loop is unrolled by LA with one
+  // register slot per row (a slot is refilled right after it is decoded, so no
+  // registers are copied across iterations), and every group runs the same
+  // number of iterations, padded to a multiple of LA.  Rows past t1 are loaded
+  // against zero-length ranges (no memory touched) with the statistics of row
+  // t0, and their dx stores are dropped: no branch around any load or store,
+  // so the compiler can count the memory operations in flight.  An empty
+  // chunk (T = 0) touches no row and no statistic.
+  if (t1 > t0) {
+    RawRow<DT, EPL, VEC, L> rx[LA], rg[LA];
+    float mu_n[LA], rs_n[LA];
+    const int64_t base = b * T;
+#pragma unroll
+    for (int j = 0; j < LA; ++j) {
+      const int64_t t = t0 + g + int64_t(j) * G;
+      const bool on = t < t1;
+      const int64_t row = uniform_i64(base + (on ? t : t0));
+      rx[j].load(x + row * H, H, lid, on);
+      rg[j].load(dy + row * H, H, lid, on);
+      mu_n[j] = mean[row];
+      rs_n[j] = rstd[row];
+    }
+    const int64_t trips = (t1 - t0 + G - 1) / G;
+    const int64_t padded = (trips + LA - 1) / LA * LA;
+    for (int64_t it = 0; it < padded; it += LA) {
+#pragma unroll
+      for (int j = 0; j < LA; ++j) {
+        const int64_t t = t0 + g + (it + j) * G;
+        const bool valid = t < t1;  // uniform within a row group
+        const int par = static_cast<int>((it + j) & 1);  // consecutive rows alternate
+        const int64_t r = uniform_i64(base + (valid ? t : t0));
+        float xv[EPL], gv[EPL];
+        rx[j].decode(xv);
+        rg[j].decode(gv);
+        const float mu = mu_n[j], rs = rs_n[j];
+        const int64_t tn = t + int64_t(LA) * G;
+        const bool more = tn < t1;
+        const int64_t rn = uniform_i64(base + (more ? tn : t0));
+        rx[j].load(x + rn * H, H, lid, more);
+        rg[j].load(dy + rn * H, H, lid, more);
+        mu_n[j] = mean[rn];
+        rs_n[j] = rstd[rn];
+        float s1 = 0.f, s2 = 0.f;
+        if (valid) {
+#pragma unroll
+          for (int i = 0; i < EPL / VEC; ++i)
+#pragma unroll
+            for (int jj = 0; jj < VEC; ++jj) {
+              const int k = i * VEC + jj;
+              const bool in = wave_elem<EPL, VEC, L>(lid, i) + jj < static_cast<int>(H);
+              xv[k] = in ? (xv[k] - mu) * rs : 0.f;  // x_hat
+              const float wdy = wv[k] * gv[k];
+              s1 += xv[k] * wdy;
+              s2 += wdy;
+              P[k] += gv[k] * xv[k];
+              Q[k] += gv[k];
+            }
+          s1 = wave_sum_dpp(s1);
+          s2 = wave_sum_dpp(s2);
+        }
+        if constexpr (NWR > 1) {
+          if (lane == 0) {
+            red[par][g][wig][0] = s1;
+            red[par][g][wig][1] = s2;
+          }
+          __syncthreads();
+          s1 = 0.f;
+          s2 = 0.f;
+#pragma unroll
+          for (int q = 0; q < NWR; ++q) {
+            s1 += red[par][g][q][0];
+            s2 += red[par][g][q][1];
+          }
+        }
+        const float c1 = s1 * inv_h, c2 = s2 * inv_h;
+#pragma unroll
+        for (int k = 0; k < EPL; ++k) gv[k] = (wv[k] * gv[k] - (xv[k] * c1 + c2)) * rs;
+        store_row<DT, EPL, VEC, L>(dx + r * H, H, lid, gv, valid);
+      }
+    }
   }
-  for (; t < t1; t += W) {
+  // Fold the row groups in order 0..G-1: every group parks its P (then Q) in
+  // its own LDS slice (fold_slice(H) floats, element e at fold_pos(e)), and all
+  // threads sum the slices element-wise.
+  const int64_t slice = fold_slice(H);
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    float* mine = lds + g * slice;
+#pragma unroll
+    for (int i = 0; i < EPL / VEC; ++i)
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) {
+        const int e = wave_elem<EPL, VEC, L>(lid, i) + j;
+        if (e < H) mine[fold_pos(e)] = half == 0 ? P[i * VEC + j] : Q[i * VEC + j];
+      }
+    __syncthreads();
+    for (int64_t e = threadIdx.x; e < H; e += NTH) {
+      const int64_t at = fold_pos(e);
+      float v = lds[at];
+#pragma unroll
+      for (int gg = 1; gg < G; ++gg) v += lds[gg * slice + at];
+      put(half, e, v);
+    }
+    __syncthreads();
+  }
+}
+
+// grid (chunks, B): ln_bwd_chunk of every (chunk, sample), the chunk's sums
+// written as partials (stream b: P, stream B+b: Q).  Workgroup (0,0) zeroes
+// the reduction's two tickets.
+template <class DT, int EPL, int VEC, int NTH, int NWR>
+__global__ __launch_bounds__(NTH) void ln_bwd_kernel(const typename DT::storage* dy,
+                                                    const typename DT::storage* x, const void* w,
+                                                    int w_dtype, const float* mean,
+                                                    const float* rstd, int64_t T, int64_t H,
+                                                    int64_t rows, int chunks,
+                                                    typename DT::storage* dx, float* partials,
+                                                    int64_t B, unsigned* tickets) {
+  if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x < 2)
+    __hip_atomic_store(tickets + threadIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  extern __shared__ __attribute__((aligned(16))) char smem_raw[];
+  const int64_t b = blockIdx.y;
+  const int chunk = blockIdx.x;
+  const int64_t t0 = int64_t(chunk) * rows;
+  const int64_t t1 = t0 + rows < T ? t0 + rows : T;
+  float* pP = partials + (b * chunks + chunk) * H;
+  float* pQ = partials + ((B + b) * chunks + chunk) * H;
+  ln_bwd_chunk<DT, EPL, VEC, NTH, NWR, kLnLookahead>(dy, x, w, w_dtype, mean, rstd, T, H, b,
+                                                     t0, t1, dx,
+                                                     reinterpret_cast<float*>(smem_raw),
+                                                     [&](int half, int64_t e, float v) {
+                                                       (half == 0 ? pP : pQ)[e] = v;
+                                                     });
+}
+
+// Tickets shared by the workgroups of one launch: word = (tag << 32) | count,
+// where tag is unique to the launch (the host's call counter), so a word left
+// by an earlier launch -- or never written -- is recognised as stale and the
+// workspace needs no clearing.  Every workgroup claims the word at its start
+// (ticket_claim: if the tag is stale, swap in (tag, 0)); a failed swap means
+// the word has changed, and only this launch's workgroups change it, always
+// to this tag.  So when a workgroup arrives (ticket_arrive, a single
+// fetch-and-add after its rows), the word holds this launch's tag and counts
+// only this launch's arrivals.  No workgroup waits for another, and neither
+// step retries.  ticket_arrive is true for the n-th (last) arrival.
+__device__ inline void ticket_claim(unsigned long long* word, uint32_t tag) {
+  unsigned long long old = __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (static_cast<uint32_t>(old >> 32) != tag)
+    __hip_atomic_compare_exchange_strong(word, &old, static_cast<unsigned long long>(tag) << 32,
+                                         __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline bool ticket_arrive(unsigned long long* word, uint32_t n) {
+  const unsigned long long prev =
+      __hip_atomic_fetch_add(word, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return static_cast<uint32_t>(prev) + 1u == n;
+}
+
+// What the one-launch LayerNorm backward needs beyond the rows.
+struct LnFusedArgs {
+  float* partials;             // [B][chunks][2H]: the chunk sums (P then Q)
+  float* sums;                 // [B][2H]: the per-sample sums
+  float* fac;                  // [2B]: clip factors (gamma then beta)
+  unsigned long long* tickets; // [B + 1]: per-sample, then the last sample's
+  uint32_t tag;
+  CombineArgs e;               // clip, scale, noise, outputs (parts unused)
+};
+
+// The LayerNorm backward in one launch, for B*H <= 65536 and B <= kFacChunk.
+// grid (chunks, B), NTH threads.  Every workgroup runs ln_bwd_chunk and
+// publishes its chunk sums (agent-coherent stores); the last chunk of sample
+// b to arrive adds the sample's chunks in chunk order, forms the two norms
+// and clip factors and publishes the sums; the last sample to arrive forms
+// out = out_scale * sum_b c_b * sums_b + noise_scale * z in sample order for
+// dgamma and dbeta.  No workgroup waits for another.
+template <class DT, int EPL, int VEC, int NTH, int NWR, bool V4, int LA = kLnLookahead>
+__global__ __launch_bounds__(NTH) void ln_bwd_fused_kernel(
+    const typename DT::storage* dy, const typename DT::storage* x, const void* w, int w_dtype,
+    const float* mean, const float* rstd, int64_t T, int64_t H, int64_t rows, int chunks,
+    typename DT::storage* dx, LnFusedArgs f) {
+  constexpr int W = NTH / kWave;
+  constexpr int IW = Item<V4>::W;
+  extern __shared__ __attribute__((aligned(16))) char smem_raw[];
+  __shared__ float red[W][2];
+  __shared__ int role;
+  const int64_t b = blockIdx.y;
+  const int chunk = blockIdx.x;
+  const int64_t B = f.e.B;
+  const int64_t t0 = int64_t(chunk) * rows;
+  const int64_t t1 = t0 + rows < T ? t0 + rows : T;
+  const int64_t per = 2 * H;  // floats per (sample, chunk)
+  float* mine = f.partials + (b * chunks + chunk) * per;
+  if (threadIdx.x == 0) {
+    ticket_claim(f.tickets + b, f.tag);
+    ticket_claim(f.tickets + B, f.tag);
+  }
+  ln_bwd_chunk<DT, EPL, VEC, NTH, NWR, LA>(dy, x, w, w_dtype, mean, rstd, T, H, b, t0, t1, dx,
+                                           reinterpret_cast<float*>(smem_raw),
+                                           [&](int half, int64_t e, float v) {
+                                             st_coherent(mine + half * H + e, v);
+                                           });
+  wait_stores();
+  __syncthreads();
+  if (threadIdx.x == 0)
+    role = ticket_arrive(f.tickets + b, static_cast<uint32_t>(chunks)) ? 1 : 0;
+  __syncthreads();
+  if (role == 0) return;
+
+  // ---- the sample's sums, norms and clip factors (last chunk of sample b)
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t items = per / IW;
+  const uint32_t pbytes = static_cast<uint32_t>(B * chunks * per * 4);
+  const uint32_t sbytes = static_cast<uint32_t>(B * per * 4);
+  const int64_t pbase = b * chunks * per;
+  float ssp = 0.f, ssq = 0.f;
+  for (int64_t it = threadIdx.x; it < items; it += NTH) {
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; c < chunks; c += 16) {
+      f32x4 v[16];
+#pragma unroll
+      for (int q = 0; q < 16; ++q)
+        v[q] = c + q < chunks
+                   ? ld_item<V4, true>(f.partials, pbase + int64_t(c + q) * per + it * IW, pbytes)
+                   : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int q = 0; q < 16; ++q)
+        if (c + q < chunks) acc += v[q];
+    }
+    st_item<V4, true>(f.sums, b * per + it * IW, sbytes, acc);
+    Item<V4> item;
+    item.v = acc;
+    if (it * IW < H) ssp += item.sq();
+    else ssq += item.sq();
+  }
+  ssp = wave_sum_dpp(ssp);
+  ssq = wave_sum_dpp(ssq);
+  if (lane == 0) {
+    red[wave][0] = ssp;
+    red[wave][1] = ssq;
+  }
+  __syncthreads();
+  float C = f.e.C, clamp = f.e.clamp;
+  if (f.e.clip_args_dev != nullptr) {
+    C = f.e.clip_args_dev[0];
+    clamp = f.e.clip_args_dev[1];
+  }
+  if (threadIdx.x == 0) {
+    float qp = 0.f, qq = 0.f;
+#pragma unroll
+    for (int q = 0; q < W; ++q) {
+      qp += red[q][0];
+      qq += red[q][1];
+    }
+    const float np = sqrtf(qp), nq = sqrtf(qq);
+    const float cp = clip_factor(np, C, clamp), cq = clip_factor(nq, C, clamp);
+    st_coherent(f.fac + b, cp);
+    st_coherent(f.fac + B + b, cq);
+    if (f.e.norms) {
+      f.e.norms[b] = np;
+      f.e.norms[B + b] = nq;
+    }
+    if (f.e.factors) {
+      f.e.factors[b] = cp;
+      f.e.factors[B + b] = cq;
+    }
+  }
+  wait_stores();
+  __syncthreads();
+  if (threadIdx.x == 0)
+    role = ticket_arrive(f.tickets + B, static_cast<uint32_t>(B)) ? 2 : 0;
+  __syncthreads();
+  if (role != 2) return;
+
+  // ---- dgamma, dbeta (last sample): the clipped sum in sample order
+  float* fac = reinterpret_cast<float*>(smem_raw);  // [2B] (B <= kFacChunk)
+  for (int64_t i = threadIdx.x; i < 2 * B; i += NTH) fac[i] = ld_coherent(f.fac + i);
+  __syncthreads();
+  for (int64_t it = threadIdx.x; it < items; it += NTH) {
+    const int k = it * IW < H ? 0 : 1;
+    const int64_t col = it * IW - k * H;
+    const float* fk = fac + k * B;
+    f32x4 tot = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int64_t s0 = 0; s0 < B; s0 += 16) {
+      f32x4 v[16];
+#pragma unroll
+      for (int q = 0; q < 16; ++q)
+        v[q] = s0 + q < B ? ld_item<V4, true>(f.sums, (s0 + q) * per + it * IW, sbytes)
+                          : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int q = 0; q < 16; ++q)
+        if (s0 + q < B) tot += fk[s0 + q] * v[q];
+    }
+    void* out = k == 0 ? f.e.out0 : f.e.out1;
+    if (out == nullptr) continue;
+    const NoiseSrc noise = k == 0 ? f.e.noise0 : f.e.noise1;
+    float z[4] = {0.f, 0.f, 0.f, 0.f};
+    if (noise.z != nullptr) {
+#pragma unroll
+      for (int e = 0; e < IW; ++e) z[e] = noise.at(col + e);
+    } else if (noise.draw) {
+      noise.window(col, z);
+    }
+#pragma unroll
+    for (int e = 0; e < IW; ++e)
+      store_from_f32(out, col + e, f.e.out_dtype, tot[e] * f.e.out_scale + f.e.noise_scale * z[e]);
+  }
+}
+
+// ------------------------------------------------- rows shared by wavefronts
+// Rows of more than 1024 elements: several wavefronts share each row, every
+// thread holding EPL <= 16 elements (element e of thread l at
+// (l + L*i)*VEC + j, L threads per row), which keeps the per-thread arrays in
+// registers.  A row's statistics are wavefront sums added in wavefront order
+// through LDS, double-buffered by row parity.  The workgroup walks its rows
+// one at a time with the next row's loads in flight; all threads run the same
+// trip count, so the barriers are uniform.
+constexpr int kSplitWaves = 16;              // wavefronts per long row
+constexpr int kSplitLanes = kSplitWaves * kWave;
+
+// grid-stride over rows, one row per workgroup of NW wavefronts at a time
+template <class DT, int EPL, int VEC, int NW>
+__global__ __launch_bounds__(NW * kWave) void ln_fwd_split_kernel(
+    const typename DT::storage* x, const void* w, const void* bias, int w_dtype, int64_t rows,
+    int64_t H, float eps, typename DT::storage* y, float* mean, float* rstd) {
+  constexpr int L = NW * kWave;
+  __shared__ float red[2][2][NW];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  float wv[EPL], bv[EPL];
+  load_param<EPL, VEC, L>(w, w_dtype, H, tid, 1.f, wv);
+  load_param<EPL, VEC, L>(bias, w_dtype, H, tid, 0.f, bv);
+  const float inv_h = 1.f / static_cast<float>(H);
+  const int64_t step = gridDim.x;
+  RawRow<DT, EPL, VEC, L> rx;
+  int64_t r = blockIdx.x;
+  rx.load(x + (r < rows ? r : 0) * H, H, tid, r < rows);
+  for (int par = 0; r < rows; r += step, par ^= 1) {
+    float xv[EPL];
+    rx.decode(xv);
+    const bool more = r + step < rows;
+    rx.load(x + (more ? r + step : r) * H, H, tid, more);
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) sum += xv[i];
+    sum = wave_sum_dpp(sum);
+    if (lane == 0) red[par][0][wave] = sum;
+    __syncthreads();
+    float tot = 0.f;
+#pragma unroll
+    for (int q = 0; q < NW; ++q) tot += red[par][0][q];
+    const float mu = tot * inv_h;
+    float sq = 0.f;
+#pragma unroll
+    for (int i = 0; i < EPL / VEC; ++i)
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) {
+        const float d = wave_elem<EPL, VEC, L>(tid, i) + j < static_cast<int>(H) ? xv[i * VEC + j] - mu : 0.f;
+        sq += d * d;
+      }
+    sq = wave_sum_dpp(sq);
+    if (lane == 0) red[par][1][wave] = sq;
+    __syncthreads();
+    float var = 0.f;
+#pragma unroll
+    for (int q = 0; q < NW; ++q) var += red[par][1][q];
+    const float rs = 1.f / sqrtf(var * inv_h + eps);
+    float yv[EPL];
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) yv[i] = (xv[i] - mu) * rs * wv[i] + bv[i];
+    store_row<DT, EPL, VEC, L>(y + r * H, H, tid, yv);
+    if (tid == 0) {
+      if (mean) mean[r] = mu;
+      if (rstd) rstd[r] = rs;
+    }
+  }
+}
+
+// grid (chunks, B): the workgroup walks the chunk's rows of sample b; every
+// thread accumulates P = sum dy*x_hat and Q = sum dy of its own columns in
+// LDS (the 128 registers a 1024-thread workgroup allows hold gamma, x_hat, dy
+// and the raw rows; P and Q in registers spilled) and writes them as the
+// chunk's partials (no fold: the columns are disjoint).  Workgroup (0,0)
+// zeroes the reduction's two tickets.
+template <class DT, int EPL, int VEC>
+__global__ __launch_bounds__(kSplitLanes) void ln_bwd_split_kernel(
+    const typename DT::storage* dy, const typename DT::storage* x, const void* w, int w_dtype,
+    const float* mean, const float* rstd, int64_t T, int64_t H, int64_t rows, int chunks,
+    typename DT::storage* dx, float* partials, int64_t B, unsigned* tickets) {
+  constexpr int NW = kSplitWaves, L = kSplitLanes;
+  if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x < 2)
+    __hip_atomic_store(tickets + threadIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __shared__ float red[2][2][NW];
+  __shared__ float accP[L * EPL], accQ[L * EPL];  // element e at e (own columns only)
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int Hn = static_cast<int>(H);
+  const int64_t b = blockIdx.y;
+  const int chunk = blockIdx.x;
+  const int64_t t0 = int64_t(chunk) * rows;
+  const int64_t t1 = t0 + rows < T ? t0 + rows : T;
+  float wv[EPL];
+  load_param<EPL, VEC, L>(w, w_dtype, H, tid, 1.f, wv);
+#pragma unroll
+  for (int i = 0; i < EPL / VEC; ++i)
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) {
+      const int e = wave_elem<EPL, VEC, L>(tid, i) + j;
+      accP[e] = 0.f;
+      accQ[e] = 0.f;
+    }
+  const float inv_h = 1.f / static_cast<float>(H);
+  RawRow<DT, EPL, VEC, L> rx, rg;
+  int64_t t = t0;
+  float mu_n = 0.f, rs_n = 0.f;
+  if (t0 < t1) {  // (an empty chunk, T = 0, touches no row and no statistic)
+    rx.load(x + (b * T + t0) * H, H, tid);
+    rg.load(dy + (b * T + t0) * H, H, tid);
+    mu_n = mean[b * T + t0];
+    rs_n = rstd[b * T + t0];
+  }
+  for (int par = 0; t < t1; ++t, par ^= 1) {
     const int64_t r = b * T + t;
     float xv[EPL], gv[EPL];
     rx.decode(xv);
     rg.decode(gv);
     const float mu = mu_n, rs = rs_n;
-    const int64_t tn = t + W;
-    if (tn < t1) {
-      rx.load(x + (b * T + tn) * H, H, lane);
-      rg.load(dy + (b * T + tn) * H, H, lane);
-      mu_n = mean[b * T + tn];
-      rs_n = rstd[b * T + tn];
-    }
+    const bool more = t + 1 < t1;
+    const int64_t rn = more ? r + 1 : r;
+    rx.load(x + rn * H, H, tid, more);
+    rg.load(dy + rn * H, H, tid, more);
+    mu_n = mean[rn];
+    rs_n = rstd[rn];
     float s1 = 0.f, s2 = 0.f;
 #pragma unroll
     for (int i = 0; i < EPL / VEC; ++i)
 #pragma unroll
       for (int j = 0; j < VEC; ++j) {
         const int k = i * VEC + j;
-        const bool in = wave_elem<EPL, VEC>(lane, i) + j < H;
+        const int e = wave_elem<EPL, VEC, L>(tid, i) + j;
+        const bool in = e < Hn;
         xv[k] = in ? (xv[k] - mu) * rs : 0.f;  // x_hat
         const float wdy = wv[k] * gv[k];
         s1 += xv[k] * wdy;
         s2 += wdy;
-        P[k] += gv[k] * xv[k];
-        Q[k] += gv[k];
+        accP[e] += gv[k] * xv[k];
+        accQ[e] += gv[k];
       }
-    const float c1 = wave_sum_dpp(s1) * inv_h;
-    const float c2 = wave_sum_dpp(s2) * inv_h;
-#pragma unroll
-    for (int k = 0; k < EPL; ++k) gv[k] = (wv[k] * gv[k] - (xv[k] * c1 + c2)) * rs;
-    store_row<DT, EPL, VEC>(dx + r * H, H, lane, gv);
-  }
-  // Fold the waves in order 0..W-1: every wave parks its row of P (then of
-  // Q) in its own LDS slice (fold_slice(H) floats, element e at fold_pos(e)),
-  // and all threads sum the slices element-wise.
-  float* pP = partials + (b * chunks + chunk) * H;
-  float* pQ = partials + ((B + b) * chunks + chunk) * H;
-  const int64_t slice = fold_slice(H);
-#pragma unroll
-  for (int half = 0; half < 2; ++half) {
-    float* mine = lds + wave * slice;
-#pragma unroll
-    for (int i = 0; i < EPL / VEC; ++i)
-#pragma unroll
-      for (int j = 0; j < VEC; ++j) {
-        const int64_t e = wave_elem<EPL, VEC>(lane, i) + j;
-        if (e < H) mine[fold_pos(e)] = half == 0 ? P[i * VEC + j] : Q[i * VEC + j];
-      }
-    __syncthreads();
-    float* dst = half == 0 ? pP : pQ;
-    for (int64_t e = threadIdx.x; e < H; e += NTH) {
-      const int64_t at = fold_pos(e);
-      float v = lds[at];
-#pragma unroll
-      for (int ww = 1; ww < W; ++ww) v += lds[ww * slice + at];
-      dst[e] = v;
+    s1 = wave_sum_dpp(s1);
+    s2 = wave_sum_dpp(s2);
+    if (lane == 0) {
+      red[par][0][wave] = s1;
+      red[par][1][wave] = s2;
     }
     __syncthreads();
+    float a1 = 0.f, a2 = 0.f;
+#pragma unroll
+    for (int q = 0; q < NW; ++q) {
+      a1 += red[par][0][q];
+      a2 += red[par][1][q];
+    }
+    const float c1 = a1 * inv_h, c2 = a2 * inv_h;
+#pragma unroll
+    for (int k = 0; k < EPL; ++k) gv[k] = (wv[k] * gv[k] - (xv[k] * c1 + c2)) * rs;
+    store_row<DT, EPL, VEC, L>(dx + r * H, H, tid, gv);
   }
+  float* pP = partials + (b * chunks + chunk) * H;
+  float* pQ = partials + ((B + b) * chunks + chunk) * H;
+#pragma unroll
+  for (int i = 0; i < EPL / VEC; ++i)
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) {
+      const int e = wave_elem<EPL, VEC, L>(tid, i) + j;
+      if (e < Hn) {
+        pP[e] = accP[e];
+        pQ[e] = accQ[e];
+      }
+    }
 }
 
 }  // namespace rw
@@ -773,8 +1245,10 @@ struct RedPlan {
   int vec, bs, cblocks, chunks, parts, iblocks;
   bool v4;
   bool one_launch;  // reduce_kernel instead of chunk_sum_kernel + combine_kernel
+  bool fused;       // LayerNorm: ln_bwd_fused_kernel (the reduction in the row launch)
   int64_t rows;
   size_t off_part, off_frob, off_sums, off_sq, off_ticket, total;
+  size_t off_fac;   // fused: clip factors [2B]
 };
 
 // Per-stream sums of at most this many elements are combined by one workgroup
@@ -825,13 +1299,40 @@ RedPlan col_plan(int64_t B, int64_t T, int64_t H, int dtype, int cus, bool align
   return p;
 }
 
-constexpr int64_t kMaxLnH = 4096;  // 64 elements per lane, one wave per row
+// How a LayerNorm row of H elements is spread over threads, at most 16
+// elements per thread (the backward kernel's per-thread columns, x_hat, dy
+// and gamma stay in registers; 32 or 64 per lane spilled):
+//   H <= 512: one wavefront, 8 each;   H <= 1024: one wavefront, 16 each;
+//   H <= 2048: 2 wavefronts, 16 each;  H <= 4096: 4 wavefronts, 16 each;
+//   H <= 8192: 16 wavefronts (a 1024-thread workgroup per row), 8 each;
+//   H <= 16384: 16 wavefronts, 16 each.
+// Rows of up to 4096 elements are processed several to a workgroup, longer
+// ones one per workgroup (ln_*_split_kernel).
+struct LnShape {
+  int nwr, epl;
+};
+constexpr int64_t kMaxWaveH = 4096;
+constexpr int64_t kMaxLnH = int64_t(kSplitLanes) * 16;
 
-// Elements per lane for a row of H (EPL in {8,16,32,64}).
-int ln_epl(int64_t H) {
-  int epl = 8;
-  while (int64_t(epl) * 64 < H) epl *= 2;
-  return epl;
+LnShape ln_shape(int64_t H) {
+  if (H <= 512) return {1, 8};
+  if (H <= 1024) return {1, 16};
+  if (H <= 2048) return {2, 16};
+  if (H <= kMaxWaveH) return {4, 16};
+  if (H <= 8192) return {kSplitWaves, 8};
+  return {kSplitWaves, 16};
+}
+
+// f(NWR, EPL) with both as compile-time constants.
+template <class F>
+void with_ln_shape(LnShape sh, F&& f) {
+  using std::integral_constant;
+  if (sh.nwr == 1 && sh.epl == 8) f(integral_constant<int, 1>{}, integral_constant<int, 8>{});
+  else if (sh.nwr == 1) f(integral_constant<int, 1>{}, integral_constant<int, 16>{});
+  else if (sh.nwr == 2) f(integral_constant<int, 2>{}, integral_constant<int, 16>{});
+  else if (sh.nwr == 4) f(integral_constant<int, 4>{}, integral_constant<int, 16>{});
+  else if (sh.epl == 8) f(integral_constant<int, kSplitWaves>{}, integral_constant<int, 8>{});
+  else f(integral_constant<int, kSplitWaves>{}, integral_constant<int, 16>{});
 }
 
 
@@ -842,12 +1343,49 @@ int ln_epl(int64_t H) {
 // and more chunks also mean more partials for the reduction to read.
 constexpr int ln_bwd_threads(int) { return 256; }
 
+// The one-launch LayerNorm backward: 8-wave workgroups, one per CU, chunks of
+// at least 32 rows; taken when the last-arriving workgroups' serial work stays
+// small: at most 16 chunks per sample for the per-sample sums and B*H <= 65536
+// (B <= 1024) for the sum over samples.  Per call (bf16, T=1024) against the
+// two-launch path: 16x1024: 27.5 / 27.1 us; 32x1024: 42.6 / 44.6 us;
+// 8x2048 (32 chunks per sample, left to the two-launch path): 33.8 / 30.0 us.
+constexpr int kLnFusedThreads = 512;
+constexpr int kLnFusedMaxChunks = 16;
+
 RedPlan ln_plan(int64_t B, int64_t T, int64_t H, int cus) {
   RedPlan p{};
   p.cblocks = 1;
-  split_rows(p, B, T, cus, 2, 32);
+  if (H <= kMaxWaveH && B * H <= kOneLaunchElems && B <= kFacChunk) {
+    split_rows(p, B, T, cus, 1, 32);
+    const size_t per = size_t(2) * H;
+    const size_t part = sizeof(float) * size_t(B) * p.chunks * per;
+    if (p.chunks <= kLnFusedMaxChunks && part < (size_t(1) << 31)) {
+      p.fused = true;
+      p.v4 = H % 4 == 0;
+      p.off_part = 0;
+      p.off_sums = align_up(part);
+      p.off_fac = p.off_sums + align_up(sizeof(float) * size_t(B) * per);
+      p.off_ticket = p.off_fac + align_up(sizeof(float) * 2 * size_t(B));
+      p.total = p.off_ticket + align_up(sizeof(unsigned long long) * size_t(B + 1));
+      return p;
+    }
+  }
+  // rows of more than kMaxWaveH take one 1024-thread workgroup per CU
+  split_rows(p, B, T, cus, H > kMaxWaveH ? 1 : 2, 32);
   finish_plan(p, B, H, 2);
   return p;
+}
+
+// Launch tag of the one-launch LayerNorm backward: unique per call in this
+// process (its tickets count only arrivals carrying the same tag), starting
+// from a clock-derived value so that a stale word in reused memory is unlikely
+// to carry it either.
+uint32_t next_ln_tag() {
+  static std::atomic<uint32_t> counter{static_cast<uint32_t>(
+      std::chrono::steady_clock::now().time_since_epoch().count() * 2654435761u)};
+  uint32_t t = counter.fetch_add(1, std::memory_order_relaxed) + 1;
+  if (t == 0) t = counter.fetch_add(1, std::memory_order_relaxed) + 1;
+  return t;
 }
 
 // chunk sums -> per-sample norms, clip factors and the clipped, scaled sum.
@@ -911,42 +1449,44 @@ void launch_colsum_dt(const RedPlan& p, const void* u, const void* v, int64_t B,
   else launch_colsum<DT, 8>(p, u, v, B, T, H, ws, frob, s);
 }
 
-template <class DT, int EPL, int VEC>
-void launch_ln_fwd_t(const void* x, const void* w, const void* b, int w_dtype, int64_t rows,
-                     int64_t H, float eps, void* y, float* mean, float* rstd, int cus,
-                     hipStream_t s) {
-  using S = typename DT::storage;
-  constexpr int W = kLnThreads / kWave;
-  // enough wavefronts for ~4 rows each, at most 2 workgroups per CU
-  int64_t grid = (rows + 4 * W - 1) / (4 * W);
-  const int64_t cap = int64_t(cus) * 2;
-  if (grid > cap) grid = cap;
-  if (grid < 1) grid = 1;
-  hipLaunchKernelGGL((ln_fwd_kernel<DT, EPL, VEC>), dim3(static_cast<unsigned>(grid)),
-                     dim3(kLnThreads), 0, s, static_cast<const S*>(x), w, b, w_dtype, rows, H, eps,
-                     static_cast<S*>(y), mean, rstd);
-}
-
+// Rows of up to 1024 elements: ln_fwd_kernel, enough wavefronts for ~4 rows
+// each, at most 2 workgroups per CU.  Longer rows: one row per workgroup of
+// NWR wavefronts, grid-stride, about 2048 threads per CU.
 template <class DT, int VEC>
-void launch_ln_fwd_v(int epl, const void* x, const void* w, const void* b, int w_dtype,
-                     int64_t rows, int64_t H, float eps, void* y, float* mean, float* rstd,
-                     int cus, hipStream_t s) {
-  switch (epl) {
-    case 8: launch_ln_fwd_t<DT, 8, VEC>(x, w, b, w_dtype, rows, H, eps, y, mean, rstd, cus, s); break;
-    case 16: launch_ln_fwd_t<DT, 16, VEC>(x, w, b, w_dtype, rows, H, eps, y, mean, rstd, cus, s); break;
-    case 32: launch_ln_fwd_t<DT, 32, VEC>(x, w, b, w_dtype, rows, H, eps, y, mean, rstd, cus, s); break;
-    default: launch_ln_fwd_t<DT, 64, VEC>(x, w, b, w_dtype, rows, H, eps, y, mean, rstd, cus, s); break;
-  }
+void launch_ln_fwd(LnShape sh, const void* x, const void* w, const void* b, int w_dtype,
+                   int64_t rows, int64_t H, float eps, void* y, float* mean, float* rstd, int cus,
+                   hipStream_t s) {
+  using S = typename DT::storage;
+  with_ln_shape(sh, [&](auto nwr_c, auto epl_c) {
+    constexpr int NWR = decltype(nwr_c)::value, EPL = decltype(epl_c)::value;
+    if constexpr (NWR == 1) {
+      constexpr int W = kLnThreads / kWave;
+      int64_t grid = (rows + 4 * W - 1) / (4 * W);
+      const int64_t cap = int64_t(cus) * 2;
+      if (grid > cap) grid = cap;
+      if (grid < 1) grid = 1;
+      hipLaunchKernelGGL((ln_fwd_kernel<DT, EPL, VEC>), dim3(static_cast<unsigned>(grid)),
+                         dim3(kLnThreads), 0, s, static_cast<const S*>(x), w, b, w_dtype, rows, H,
+                         eps, static_cast<S*>(y), mean, rstd);
+    } else {
+      int64_t grid = int64_t(cus) * (2048 / (NWR * kWave));
+      if (grid > rows) grid = rows;
+      hipLaunchKernelGGL((ln_fwd_split_kernel<DT, EPL, VEC, NWR>),
+                         dim3(static_cast<unsigned>(grid)), dim3(NWR * kWave), 0, s,
+                         static_cast<const S*>(x), w, b, w_dtype, rows, H, eps,
+                         static_cast<S*>(y), mean, rstd);
+    }
+  });
 }
 
 template <class DT>
-void launch_ln_fwd(bool vec, int epl, const void* x, const void* w, const void* b, int w_dtype,
-                   int64_t rows, int64_t H, float eps, void* y, float* mean, float* rstd, int cus,
-                   hipStream_t s) {
-  if (!vec) launch_ln_fwd_v<DT, 1>(epl, x, w, b, w_dtype, rows, H, eps, y, mean, rstd, cus, s);
+void launch_ln_fwd_dt(bool vec, LnShape sh, const void* x, const void* w, const void* b,
+                      int w_dtype, int64_t rows, int64_t H, float eps, void* y, float* mean,
+                      float* rstd, int cus, hipStream_t s) {
+  if (!vec) launch_ln_fwd<DT, 1>(sh, x, w, b, w_dtype, rows, H, eps, y, mean, rstd, cus, s);
   else if constexpr (DT::code == FDP_F32)
-    launch_ln_fwd_v<DT, 4>(epl, x, w, b, w_dtype, rows, H, eps, y, mean, rstd, cus, s);
-  else launch_ln_fwd_v<DT, 8>(epl, x, w, b, w_dtype, rows, H, eps, y, mean, rstd, cus, s);
+    launch_ln_fwd<DT, 4>(sh, x, w, b, w_dtype, rows, H, eps, y, mean, rstd, cus, s);
+  else launch_ln_fwd<DT, 8>(sh, x, w, b, w_dtype, rows, H, eps, y, mean, rstd, cus, s);
 }
 
 struct LnBwdIo {
@@ -960,34 +1500,71 @@ struct LnBwdIo {
   void* dx;
 };
 
-template <class DT, int EPL, int VEC>
-void launch_ln_bwd_t(const RedPlan& p, const LnBwdIo& io, float* part, unsigned* tickets,
-                     hipStream_t s) {
-  using S = typename DT::storage;
-  constexpr int NTH = ln_bwd_threads(EPL);
-  hipLaunchKernelGGL((ln_bwd_kernel<DT, EPL, VEC, NTH>), dim3(p.chunks, io.B), dim3(NTH),
-                     sizeof(float) * (NTH / kWave) * fold_slice(io.H), s, static_cast<const S*>(io.dy),
-                     static_cast<const S*>(io.x), io.w, io.w_dtype, io.mean, io.rstd, io.T, io.H,
-                     p.rows, p.chunks, static_cast<S*>(io.dx), part, io.B, tickets);
-}
-
+// Two-launch backward (rows, then launch_reduce): rows of up to 4096 elements
+// in 4-wave workgroups, longer ones in one 1024-thread workgroup per row.
 template <class DT, int VEC>
-void launch_ln_bwd_v(int epl, const RedPlan& p, const LnBwdIo& io, float* part,
-                     unsigned* tickets, hipStream_t s) {
-  switch (epl) {
-    case 8: launch_ln_bwd_t<DT, 8, VEC>(p, io, part, tickets, s); break;
-    case 16: launch_ln_bwd_t<DT, 16, VEC>(p, io, part, tickets, s); break;
-    case 32: launch_ln_bwd_t<DT, 32, VEC>(p, io, part, tickets, s); break;
-    default: launch_ln_bwd_t<DT, 64, VEC>(p, io, part, tickets, s); break;
-  }
+void launch_ln_bwd(LnShape sh, const RedPlan& p, const LnBwdIo& io, float* part,
+                   unsigned* tickets, hipStream_t s) {
+  using S = typename DT::storage;
+  with_ln_shape(sh, [&](auto nwr_c, auto epl_c) {
+    constexpr int NWR = decltype(nwr_c)::value, EPL = decltype(epl_c)::value;
+    if constexpr (NWR == kSplitWaves) {
+      hipLaunchKernelGGL((ln_bwd_split_kernel<DT, EPL, VEC>), dim3(p.chunks, io.B),
+                         dim3(kSplitLanes), 0, s, static_cast<const S*>(io.dy),
+                         static_cast<const S*>(io.x), io.w, io.w_dtype, io.mean, io.rstd, io.T,
+                         io.H, p.rows, p.chunks, static_cast<S*>(io.dx), part, io.B, tickets);
+    } else {
+      constexpr int NTH = ln_bwd_threads(EPL);
+      constexpr int G = NTH / (NWR * kWave);
+      hipLaunchKernelGGL((ln_bwd_kernel<DT, EPL, VEC, NTH, NWR>), dim3(p.chunks, io.B),
+                         dim3(NTH), sizeof(float) * G * fold_slice(io.H), s,
+                         static_cast<const S*>(io.dy), static_cast<const S*>(io.x), io.w,
+                         io.w_dtype, io.mean, io.rstd, io.T, io.H, p.rows, p.chunks,
+                         static_cast<S*>(io.dx), part, io.B, tickets);
+    }
+  });
 }
 
 template <class DT>
-void launch_ln_bwd(bool vec, int epl, const RedPlan& p, const LnBwdIo& io, float* part,
-                   unsigned* tickets, hipStream_t s) {
-  if (!vec) launch_ln_bwd_v<DT, 1>(epl, p, io, part, tickets, s);
-  else if constexpr (DT::code == FDP_F32) launch_ln_bwd_v<DT, 4>(epl, p, io, part, tickets, s);
-  else launch_ln_bwd_v<DT, 8>(epl, p, io, part, tickets, s);
+void launch_ln_bwd_dt(bool vec, LnShape sh, const RedPlan& p, const LnBwdIo& io, float* part,
+                      unsigned* tickets, hipStream_t s) {
+  if (!vec) launch_ln_bwd<DT, 1>(sh, p, io, part, tickets, s);
+  else if constexpr (DT::code == FDP_F32) launch_ln_bwd<DT, 4>(sh, p, io, part, tickets, s);
+  else launch_ln_bwd<DT, 8>(sh, p, io, part, tickets, s);
+}
+
+// One-launch backward (rows of up to 4096 elements).
+template <class DT, int VEC, bool V4>
+void launch_ln_fused(LnShape sh, const RedPlan& p, const LnBwdIo& io, const LnFusedArgs& f,
+                     hipStream_t s) {
+  using S = typename DT::storage;
+  with_ln_shape(sh, [&](auto nwr_c, auto epl_c) {
+    constexpr int NWR = decltype(nwr_c)::value, EPL = decltype(epl_c)::value;
+    if constexpr (NWR < kSplitWaves) {
+      constexpr int G = kLnFusedThreads / (NWR * kWave);
+      size_t lds = sizeof(float) * G * fold_slice(io.H);
+      if (lds < sizeof(float) * 2 * size_t(io.B)) lds = sizeof(float) * 2 * size_t(io.B);
+      hipLaunchKernelGGL((ln_bwd_fused_kernel<DT, EPL, VEC, kLnFusedThreads, NWR, V4>),
+                         dim3(p.chunks, io.B), dim3(kLnFusedThreads), lds, s,
+                         static_cast<const S*>(io.dy), static_cast<const S*>(io.x), io.w,
+                         io.w_dtype, io.mean, io.rstd, io.T, io.H, p.rows, p.chunks,
+                         static_cast<S*>(io.dx), f);
+    }
+  });
+}
+
+// Aligned 16-byte rows imply H % 4 == 0 (V4); element rows take either.
+template <class DT>
+void launch_ln_fused_dt(bool vec, LnShape sh, const RedPlan& p, const LnBwdIo& io,
+                        const LnFusedArgs& f, hipStream_t s) {
+  if (!vec) {
+    if (p.v4) launch_ln_fused<DT, 1, true>(sh, p, io, f, s);
+    else launch_ln_fused<DT, 1, false>(sh, p, io, f, s);
+  } else if constexpr (DT::code == FDP_F32) {
+    launch_ln_fused<DT, 4, true>(sh, p, io, f, s);
+  } else {
+    launch_ln_fused<DT, 8, true>(sh, p, io, f, s);
+  }
 }
 
 bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
@@ -1052,12 +1629,12 @@ extern "C" int fdp_layernorm_fwd(const void* x, const void* w, const void* b, in
   if (rows == 0) return FDP_OK;
   if (x == nullptr || y == nullptr) return FDP_ERR_ARG;
   const bool vec = aligned16(x) && aligned16(y) && (H * esize(dtype)) % 16 == 0;
-  const int epl = ln_epl(H);
+  const LnShape sh = ln_shape(H);
   const int cus = num_cus();
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (dtype == FDP_BF16) launch_ln_fwd<BF16>(vec, epl, x, w, b, w_dtype, rows, H, eps, y, mean, rstd, cus, s);
-  else if (dtype == FDP_F16) launch_ln_fwd<F16>(vec, epl, x, w, b, w_dtype, rows, H, eps, y, mean, rstd, cus, s);
-  else launch_ln_fwd<F32>(vec, epl, x, w, b, w_dtype, rows, H, eps, y, mean, rstd, cus, s);
+  if (dtype == FDP_BF16) launch_ln_fwd_dt<BF16>(vec, sh, x, w, b, w_dtype, rows, H, eps, y, mean, rstd, cus, s);
+  else if (dtype == FDP_F16) launch_ln_fwd_dt<F16>(vec, sh, x, w, b, w_dtype, rows, H, eps, y, mean, rstd, cus, s);
+  else launch_ln_fwd_dt<F32>(vec, sh, x, w, b, w_dtype, rows, H, eps, y, mean, rstd, cus, s);
   return hipGetLastError() == hipSuccess ? FDP_OK : FDP_ERR_HIP;
 }
 
@@ -1091,14 +1668,29 @@ extern "C" int fdp_layernorm_bwd_clip(const void* dy, const void* x, const void*
   char* ws = static_cast<char*>(workspace);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool vec = aligned16(dy) && aligned16(x) && aligned16(dx) && (H * esize(dtype)) % 16 == 0;
-  const int epl = ln_epl(H);
+  const LnShape sh = ln_shape(H);
   const LnBwdIo io{dy, x, w, w_dtype, mean, rstd, B, T, H, dx};
   float* part = reinterpret_cast<float*>(ws + p.off_part);
-  unsigned* tickets = reinterpret_cast<unsigned*>(ws + p.off_ticket);
-  if (dtype == FDP_BF16) launch_ln_bwd<BF16>(vec, epl, p, io, part, tickets, s);
-  else if (dtype == FDP_F16) launch_ln_bwd<F16>(vec, epl, p, io, part, tickets, s);
-  else launch_ln_bwd<F32>(vec, epl, p, io, part, tickets, s);
   const fdp_noise_key* key = noise_scale != 0.f ? noise_key : nullptr;
+  if (p.fused) {
+    LnFusedArgs f{};
+    f.partials = part;
+    f.sums = reinterpret_cast<float*>(ws + p.off_sums);
+    f.fac = reinterpret_cast<float*>(ws + p.off_fac);
+    f.tickets = reinterpret_cast<unsigned long long*>(ws + p.off_ticket);
+    f.tag = next_ln_tag();
+    f.e = CombineArgs{nullptr, 0, B, H, C, clamp, clip_args_dev, out_scale,
+                      make_noise(noise_w, w_dtype, key, 0), make_noise(noise_b, w_dtype, key, 1),
+                      noise_scale, dw, db, w_dtype, norms, factors};
+    if (dtype == FDP_BF16) launch_ln_fused_dt<BF16>(vec, sh, p, io, f, s);
+    else if (dtype == FDP_F16) launch_ln_fused_dt<F16>(vec, sh, p, io, f, s);
+    else launch_ln_fused_dt<F32>(vec, sh, p, io, f, s);
+    return hipGetLastError() == hipSuccess ? FDP_OK : FDP_ERR_HIP;
+  }
+  unsigned* tickets = reinterpret_cast<unsigned*>(ws + p.off_ticket);
+  if (dtype == FDP_BF16) launch_ln_bwd_dt<BF16>(vec, sh, p, io, part, tickets, s);
+  else if (dtype == FDP_F16) launch_ln_bwd_dt<F16>(vec, sh, p, io, part, tickets, s);
+  else launch_ln_bwd_dt<F32>(vec, sh, p, io, part, tickets, s);
   const Epilogue e{C,        clamp,
                    clip_args_dev,
                    out_scale, noise_scale,

@@ -95,10 +95,11 @@ def test_dpconv1d_matches_linear_transposed(dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=str)
-@pytest.mark.parametrize("use_fused", [True, False])
-def test_dplayernorm(dtype, use_fused):
-    """cfg4-style LayerNorm (H=1024, gamma=1, beta=0) with seeded noise."""
-    B, T, H = 4, 128, 1024
+@pytest.mark.parametrize("use_fused,H", [(True, 1024), (False, 1024), (True, 8192)])
+def test_dplayernorm(dtype, use_fused, H):
+    """cfg4-style LayerNorm (gamma=1, beta=0) with seeded noise; H=8192 takes
+    the kernels that share a row among wavefronts."""
+    B, T = 4, 128
     ln = DPLayerNorm(H, use_fused=use_fused, C=1.0, noise_multiplier=1.0).to(DEV, dtype)
     ln.record_stats = True
     ln.noise_generator = torch.Generator(device=DEV).manual_seed(77)

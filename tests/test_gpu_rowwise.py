@@ -57,7 +57,7 @@ def test_bias_ops(dtype):
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=str)
-@pytest.mark.parametrize("H", [1024, 768, 2048, 100, 4096, 8])
+@pytest.mark.parametrize("H", [1024, 768, 2048, 100, 4096, 8, 4097, 8192, 12000, 16384])
 def test_layernorm_fwd_parity(H, dtype):
     x = randn((3, 37, H), dtype, 5)
     w = randn((H,), dtype, 6)
@@ -74,11 +74,18 @@ def test_layernorm_fwd_parity(H, dtype):
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=str)
 @pytest.mark.parametrize("shape", [(16, 1024, 1024), (4, 33, 768), (2, 5, 100), (3, 64, 4096),
-                                   (1, 1, 64), (20, 8, 4096), (70, 3, 1000), (3, 9, 1001)],
+                                   (1, 1, 64), (20, 8, 4096), (70, 3, 1000), (3, 9, 1001),
+                                   (4, 128, 8192), (2, 40, 16384), (3, 17, 5000), (1, 3, 4100),
+                                   (4, 1024, 512)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_layernorm_bwd_parity(shape, dtype):
-    """B*H up to 65536 takes the one-launch reduction, larger the two-launch one
-    (the last two shapes)."""
+    """Paths: B*H <= 65536 with at most 16 row chunks per sample runs in one
+    launch (cfg4 and the small shapes); 4x1024x512 (32 chunks per sample) runs
+    the rows, then the one-workgroup-per-stream reduction; 20x8x4096 and
+    70x3x1000 (B*H > 65536) the rows, then the two reduction kernels.  Rows of
+    1025..4096 elements share a row among 2 or 4 wavefronts; above 4096 among
+    16 (8192, 16384, 5000, 4100; 5000 and 4100 leave threads without columns,
+    4100 is also unaligned in 16-bit)."""
     B, T, H = shape
     x = randn(shape, dtype, 8)
     w = randn((H,), dtype, 9)
@@ -102,6 +109,29 @@ def test_layernorm_bwd_parity(shape, dtype):
     assert_elementwise(norms[B:], ref["norms_b"], dtype, "norms beta")
     assert_elementwise(fac[:B], ref["fac_w"], dtype, "factors gamma")
     assert_elementwise(fac[B:], ref["fac_b"], dtype, "factors beta")
+
+
+@pytest.mark.parametrize("shape", [(2, 0, 64), (16, 0, 1024)], ids=lambda s: "x".join(map(str, s)))
+def test_layernorm_bwd_empty_rows(shape):
+    """T = 0: no row is read, the per-sample sums are zero, so the clip factors
+    are min(clamp, C / 1e-10) = clamp and dgamma / dbeta are the noise alone."""
+    B, T, H = shape
+    dtype = torch.bfloat16
+    x = torch.zeros(shape, dtype=dtype, device=DEV)
+    g = torch.zeros(shape, dtype=dtype, device=DEV)
+    w = randn((H,), dtype, 13)
+    mean = torch.zeros((B, T), dtype=torch.float32, device=DEV)
+    rstd = torch.ones((B, T), dtype=torch.float32, device=DEV)
+    zw, zb = randn((H,), dtype, 14), randn((H,), dtype, 15)
+    dx, dw, db, norms, fac = core.layernorm_bwd_clip(
+        g, x, w, mean, rstd, 1.0, 1.0, noise_w=zw, noise_b=zb, noise_scale=0.5,
+        param_dtype=torch.float32, return_stats=True)
+    ref = O.layernorm_bwd_clip(g, x, w, 1e-5, C=1.0, noise_multiplier=0.5 * np.sqrt(B),
+                               z_w=zw, z_b=zb, mean=mean, rstd=rstd)
+    assert dx.numel() == 0
+    assert_close(dw, ref["dw"], dtype, "dgamma")
+    assert_close(db, ref["db"], dtype, "dbeta")
+    assert torch.all(norms == 0) and torch.all(fac == 1.0)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=str)
