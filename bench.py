@@ -289,6 +289,78 @@ def cfg5_training(dev, steps=10, warmup=3, n_layer=24):
 
 
 # ---------------------------------------------------------------------- extras
+def weight_and_bias_cost(dev, steps, warmup):
+    """cfg2 with a bias: the clipped weight gradient alone, with the bias formed
+    in the same launch (fdp_wgrad_bias_clip), and the bias by the separate
+    column-sum kernel (what a call without the fused path adds)."""
+    from flashdp4review_amd.core import colsum_clip, wgrad_clip
+    from flashdp4review_amd.layers.utils import NoiseStream
+    x, go, _ = cfg2_inputs(dev)
+    B, T, O = go.shape
+    keys = NoiseStream()
+    bo = torch.empty(O, dtype=torch.bfloat16, device=dev)
+    std = 1.0 / math.sqrt(B)
+
+    def w_only():
+        wgrad_clip(go, x, 1.0, 1.0, out_scale=1.0 / B, noise_scale=std,
+                   noise_key=keys.next(O * x.shape[2]))
+
+    def w_and_b():
+        wgrad_clip(go, x, 1.0, 1.0, out_scale=1.0 / B, noise_scale=std,
+                   noise_key=keys.next(O * x.shape[2]), bias_out=bo, bias_scale=1.0 / (B * T),
+                   bias_noise_scale=std, bias_noise_key=keys.next(O))
+
+    def b_only():
+        colsum_clip(go, None, 1.0, 1.0, norm="frob", out_scale=1.0 / (B * T), noise_scale=std,
+                    noise_key=keys.next(O))
+
+    tw = median_cuda_time(w_only, steps, warmup, reps=3)
+    twb = median_cuda_time(w_and_b, steps, warmup, reps=3)
+    tb = median_cuda_time(b_only, steps, warmup, reps=3)
+    return {"weight_ms": round(tw, 4), "weight_and_bias_one_launch_ms": round(twb, 4),
+            "bias_column_sum_kernel_ms": round(tb, 4),
+            "bias_cost_in_launch_us": round((twb - tw) * 1e3, 2)}
+
+
+def dx_overlap(dev, steps, warmup):
+    """DPLinear backward at cfg2: dX = g W (a plain GEMM) and the clipped dW/db
+    call, one after the other on one stream, or with dX on a second stream
+    (default priority) so that it runs beside the DP kernel's tail."""
+    from flashdp4review_amd.core import wgrad_clip
+    from flashdp4review_amd.layers.utils import NoiseStream
+    x, go, _ = cfg2_inputs(dev)
+    B, T, O = go.shape
+    W = (torch.randn(O, x.shape[2], device=dev) * 0.02).to(torch.bfloat16)
+    bo = torch.empty(O, dtype=torch.bfloat16, device=dev)
+    keys = NoiseStream()
+    std = 1.0 / math.sqrt(B)
+    side = torch.cuda.Stream(device=dev)
+
+    def dp():
+        wgrad_clip(go, x, 1.0, 1.0, out_scale=1.0 / B, noise_scale=std,
+                   noise_key=keys.next(O * x.shape[2]), bias_out=bo, bias_scale=1.0 / (B * T),
+                   bias_noise_scale=std, bias_noise_key=keys.next(O))
+
+    def serial():
+        go @ W
+        dp()
+
+    def overlapped():
+        main = torch.cuda.current_stream(dev)
+        side.wait_stream(main)
+        dp()
+        with torch.cuda.stream(side):
+            go @ W
+        main.wait_stream(side)
+
+    t_dx = median_cuda_time(lambda: go @ W, steps, warmup, reps=3)
+    t_dp = median_cuda_time(dp, steps, warmup, reps=3)
+    t_ser = median_cuda_time(serial, steps, warmup, reps=3)
+    t_ovl = median_cuda_time(overlapped, steps, warmup, reps=3)
+    return {"dx_gemm_ms": round(t_dx, 4), "dp_weight_bias_ms": round(t_dp, 4),
+            "serial_ms": round(t_ser, 4), "dx_on_second_stream_ms": round(t_ovl, 4)}
+
+
 def extra_measurements(dev, steps, warmup):
     import torch.nn as nn
     from flashdp4review_amd import DPLayerNorm, DPLinear
@@ -310,6 +382,15 @@ def extra_measurements(dev, steps, warmup):
     t_dp = median_cuda_time(fb(dpl), steps, warmup, reps=3)
     out["linear_cfg2_fwd_bwd_ms"] = {"dp": round(t_dp, 4), "non_dp": round(t_lin, 4),
                                      "dp_over_non_dp_throughput": round(t_lin / t_dp, 4)}
+    # the same with a bias: DPLinear forms dW and db in one call (fdp_wgrad_bias_clip)
+    linb = nn.Linear(768, 3072, bias=True).to(dev, torch.bfloat16)
+    dplb = DPLinear(768, 3072, bias=True, C=1.0, noise_multiplier=1.0).to(dev, torch.bfloat16)
+    t_linb = median_cuda_time(fb(linb), steps, warmup, reps=3)
+    t_dpb = median_cuda_time(fb(dplb), steps, warmup, reps=3)
+    out["linear_cfg2_bias_fwd_bwd_ms"] = {"dp": round(t_dpb, 4), "non_dp": round(t_linb, 4),
+                                          "dp_over_non_dp_throughput": round(t_linb / t_dpb, 4)}
+    out["cfg2_weight_and_bias"] = weight_and_bias_cost(dev, steps, warmup)
+    out["cfg2_dx_overlap"] = dx_overlap(dev, steps, warmup)
     # cfg3: Conv1D orientation (x^T g, [768, 2304]) with partially active clipping
     x3, g3 = cfg3_inputs(dev)
     _, gemm3 = run_wgrad(x3, g3, torch.bfloat16, transpose=True)

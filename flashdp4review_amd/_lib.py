@@ -46,6 +46,18 @@ class NoiseKey(ctypes.Structure):
 _c_key = ctypes.POINTER(NoiseKey)
 
 
+class BiasOut(ctypes.Structure):
+    """fdp_bias_out: where and how fdp_wgrad_bias_clip writes the bias of
+    operand a (include/flashdp_hip.h)."""
+    _fields_ = [("out", ctypes.c_void_p), ("out_dtype", ctypes.c_int),
+                ("out_scale", ctypes.c_float), ("noise", ctypes.c_void_p),
+                ("noise_scale", ctypes.c_float), ("noise_key", _c_key),
+                ("norms", ctypes.c_void_p), ("factors", ctypes.c_void_p)]
+
+
+_c_bias = ctypes.POINTER(BiasOut)
+
+
 def noise_key(key) -> "ctypes._Pointer | None":
     """(seed, offset) -> a fdp_noise_key pointer for the call (None -> NULL)."""
     if key is None:
@@ -64,6 +76,12 @@ SIGNATURES = {
                                 _c_i64, _c_i64, _c_int, _c_int, _c_f, _c_f, _c_p, _c_f, _c_p,
                                 _c_f, _c_key, _c_p, _c_i64, _c_int, _c_p, _c_p, _c_int, _c_p,
                                 ctypes.c_size_t, _c_p]),
+    "fdp_wgrad_bias_clip_workspace_size": (_c_int, [_c_i64, _c_i64, _c_i64, _c_i64, _c_int,
+                                                    _c_int, _c_sz_p]),
+    "fdp_wgrad_bias_clip": (_c_int, [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+                                     _c_i64, _c_i64, _c_int, _c_int, _c_f, _c_f, _c_p, _c_f, _c_p,
+                                     _c_f, _c_key, _c_p, _c_i64, _c_int, _c_p, _c_p, _c_int,
+                                     _c_bias, _c_p, ctypes.c_size_t, _c_p]),
     "fdp_wgrad_clip_noalloc": (_c_int, [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                         _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_f, _c_f, _c_p,
                                         _c_f, _c_p, _c_f, _c_key, _c_p, _c_i64, _c_int, _c_p, _c_p,

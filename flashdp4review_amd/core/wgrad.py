@@ -139,7 +139,10 @@ def wgrad_clip(a: torch.Tensor, b: torch.Tensor, C: float = 1.0, clamp_value: fl
                noise_key: tuple[int, int] | None = None,
                out_dtype: torch.dtype | None = None, out: torch.Tensor | None = None,
                return_stats: bool = False, noclip: bool = False, two_pass: bool = False,
-               launch: str | None = None, single_pass: str = "auto", check: bool = False):
+               launch: str | None = None, single_pass: str = "auto", check: bool = False,
+               bias_out: torch.Tensor | None = None, bias_scale: float = 1.0,
+               bias_noise: torch.Tensor | None = None, bias_noise_scale: float = 1.0,
+               bias_noise_key: tuple[int, int] | None = None):
     """out = out_scale * sum_b c_b G_b + noise_scale * z, c_b = clip(||G_b||_F).
 
     layout "tn": a [B,K,M], b [B,K,N], G_b = a_b^T b_b;
@@ -161,12 +164,24 @@ def wgrad_clip(a: torch.Tensor, b: torch.Tensor, C: float = 1.0, clamp_value: fl
     later call: every STATUS_PERIOD calls the status word is copied to the host
     behind the call, and the first call after the copy completes raises.  An
     expiry poisons only the launch it happened in (its outputs are NaN).
+
+    ``bias_out`` (an [M] tensor, layout "tn", a contiguous) also writes the
+    bias of a (fdp_wgrad_bias_clip, the DP Linear bias gradient):
+    bias_out[m] = bias_scale * sum_b c'_b sum_k a_b[k, m] + bias_noise_scale * zb[m],
+    c'_b = clip(||a_b||_F) with the same C / clamp; zb is ``bias_noise`` or the
+    draw of ``bias_noise_key``.  The wide kernel forms it in the same launch;
+    other schedules run the column-sum kernel after the weight gradient.  With
+    ``return_stats`` the bias's norms and factors follow the weight's.
     """
-    dev = _lib.require_hip(a, b, noise, out)
+    dev = _lib.require_hip(a, b, noise, out, bias_out, bias_noise)
     if a.dtype != b.dtype:
         raise KeyError(f"operand dtypes differ: {a.dtype} vs {b.dtype}")
     dt = _lib.dtype_code(a.dtype)
     a, b = _inner_contig(a), _inner_contig(b)
+    if bias_out is not None:
+        if layout != "tn" or noclip:
+            raise ValueError("the bias of a needs layout 'tn' and a clip")
+        a = a.contiguous()
     if layout == "tn":
         Bn, K, M = a.shape
         lay = _lib.LAYOUT_TN
@@ -198,6 +213,21 @@ def wgrad_clip(a: torch.Tensor, b: torch.Tensor, C: float = 1.0, clamp_value: fl
     if return_stats:
         factors = torch.empty(Bn, dtype=torch.float32, device=dev)
         norms = None if noclip else torch.empty(Bn, dtype=torch.float32, device=dev)
+    bias_arg = bnorms = bfactors = None
+    if bias_out is not None:
+        if bias_out.shape != (M,) or not bias_out.is_contiguous():
+            raise ValueError(f"bias_out must be a contiguous [{M}] tensor")
+        if bias_noise is not None:
+            if bias_noise.numel() != M:
+                raise ValueError(f"bias_noise must have {M} elements")
+            bias_noise = bias_noise.reshape(M).to(bias_out.dtype).contiguous()
+        if return_stats:
+            bnorms = torch.empty(Bn, dtype=torch.float32, device=dev)
+            bfactors = torch.empty(Bn, dtype=torch.float32, device=dev)
+        bias_arg = _lib.BiasOut(bias_out.data_ptr(), _lib.dtype_code(bias_out.dtype),
+                                float(bias_scale), _lib.ptr(bias_noise), float(bias_noise_scale),
+                                _lib.noise_key(bias_noise_key), _lib.ptr(bnorms),
+                                _lib.ptr(bfactors))
     mode = _launch_mode if launch is None else launch
     if mode not in _LAUNCH_MODES:
         raise ValueError(f"launch must be one of {_LAUNCH_MODES}, got {mode!r}")
@@ -207,24 +237,30 @@ def wgrad_clip(a: torch.Tensor, b: torch.Tensor, C: float = 1.0, clamp_value: fl
              | (_lib.WGRAD_PLAIN_LAUNCH if mode == "plain" else 0) | _lib.WGRAD_CLEAN_WORKSPACE
              | _SINGLE_PASS[single_pass])
     L = _lib.lib()
-    key = (dev.index, Bn, K, M, N, dt, flags)
+    key = (dev.index, Bn, K, M, N, dt, flags, bias_arg is not None)
     nbytes = _ws_sizes.get(key)
     if nbytes is None:
-        nbytes = _lib.size_query(L.fdp_wgrad_clip_workspace_size, Bn, K, M, N, dt, flags)
+        query = (L.fdp_wgrad_clip_workspace_size if bias_arg is None
+                 else L.fdp_wgrad_bias_clip_workspace_size)
+        nbytes = _lib.size_query(query, Bn, K, M, N, dt, flags)
         _ws_sizes[key] = nbytes
     stream = _lib.stream_handle(dev)
     ws = _persistent_workspace(nbytes, dev, stream)
     probed = ws.take_probe()
     if probed != 0:
         _raise_expired(ws, "reported asynchronously for an earlier call on this stream", probed)
-    st = L.fdp_wgrad_clip(
-        _lib.ptr(a), _lib.ptr(b), Bn, K, M, N, a.stride(0), a.stride(1), b.stride(0), b.stride(1),
-        lay, dt, ctypes.c_float(C_), ctypes.c_float(clamp_), _lib.ptr(cad),
-        ctypes.c_float(out_scale), _lib.ptr(noise), ctypes.c_float(noise_scale),
-        _lib.noise_key(noise_key), out.data_ptr(),
-        out.stride(0), odt, _lib.ptr(norms), _lib.ptr(factors), flags, ws.buf.data_ptr(),
-        ws.buf.numel(), stream)
-    _lib.check(st, "fdp_wgrad_clip")
+    args = (_lib.ptr(a), _lib.ptr(b), Bn, K, M, N, a.stride(0), a.stride(1), b.stride(0),
+            b.stride(1), lay, dt, ctypes.c_float(C_), ctypes.c_float(clamp_), _lib.ptr(cad),
+            ctypes.c_float(out_scale), _lib.ptr(noise), ctypes.c_float(noise_scale),
+            _lib.noise_key(noise_key), out.data_ptr(), out.stride(0), odt, _lib.ptr(norms),
+            _lib.ptr(factors), flags)
+    if bias_arg is None:
+        st = L.fdp_wgrad_clip(*args, ws.buf.data_ptr(), ws.buf.numel(), stream)
+        _lib.check(st, "fdp_wgrad_clip")
+    else:
+        st = L.fdp_wgrad_bias_clip(*args, ctypes.byref(bias_arg), ws.buf.data_ptr(),
+                                   ws.buf.numel(), stream)
+        _lib.check(st, "fdp_wgrad_bias_clip")
     if check:
         status = int(ws.status_word().item())
         if status != 0:
@@ -232,7 +268,7 @@ def wgrad_clip(a: torch.Tensor, b: torch.Tensor, C: float = 1.0, clamp_value: fl
     else:
         ws.queue_probe()
     if return_stats:
-        return out, norms, factors
+        return (out, norms, factors) if bias_arg is None else (out, norms, factors, bnorms, bfactors)
     return out
 
 

@@ -322,6 +322,10 @@ __device__ inline void gemm(const Job<G>& job, int nk, const FragOffsets<G>& fo,
 struct NoHook {
   __device__ __forceinline__ void operator()(int) const {}
 };
+struct NoFragHook {
+  template <class F>
+  __device__ __forceinline__ void operator()(int, int, const F&) const {}
+};
 
 // acc += A_tile^T B_tile over nk k-tiles with an S-stage ring, fragments
 // double-buffered in registers: the LDS reads of k-step s+1 (the next k-tile's
@@ -330,11 +334,13 @@ struct NoHook {
 // reads of the next step.  KS must be even (fragment buffers alternate).
 // hook(kt) runs at the start of every k-tile kt: VALU work placed there
 // (reading no memory) overlaps the matrix cores' work of the other wave of
-// the SIMD.
-template <class DT, class G, int S, class Hook = NoHook>
+// the SIMD.  fhook(kt, ks, frags) runs after the MFMAs of k-step ks are
+// issued, with that step's operand fragments (VALU work on them overlaps
+// the MFMAs in flight).
+template <class DT, class G, int S, class Hook = NoHook, class FragHook = NoFragHook>
 __device__ inline void gemm_pipe(const Job<G>& job, int nk, const FragOffsets<G>& fo,
                                  const Stages& st, f32x16 (&acc)[G::FI][G::FJ],
-                                 const Hook& hook = Hook()) {
+                                 const Hook& hook = Hook(), const FragHook& fhook = FragHook()) {
   static_assert(S >= 2 && S <= 4, "stages");
   static_assert(G::KS % 2 == 0, "an even number of k-steps per k-tile");
   wait_vm<0>();
@@ -376,6 +382,7 @@ __device__ inline void gemm_pipe(const Job<G>& job, int nk, const FragOffsets<G>
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);    // one MFMA
             __builtin_amdgcn_sched_group_barrier(0x100, per, 0);  // then DS reads
           }
+          fhook(kt, ks, f[cur]);
         }
       }
     }

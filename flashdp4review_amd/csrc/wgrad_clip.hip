@@ -212,7 +212,7 @@ struct Plan {
   StreamPlan sp;  // streamed two-pass schedule (16-bit TN operands)
   WidePlan wp;    // wide single-pass schedule (wp.wgm == 0: not used)
   size_t off_turn, off_partials, off_factors, off_group, off_slots, off_chunk;
-  size_t off_wide_partials, off_wide_slots;
+  size_t off_wide_partials, off_wide_slots, off_wide_bias_part, off_wide_bias_sq;
   size_t total_two_pass, total_fused, total_wide, total;
 };
 
@@ -273,7 +273,9 @@ Plan make_plan(int64_t B, int64_t K, int64_t M, int64_t N, int cus, int flags, i
     if (pl.wp.wgm != 0) {
       pl.off_wide_partials = kWsHead;
       pl.off_wide_slots = pl.off_wide_partials + align_up(pl.wp.partial_bytes);
-      pl.total_wide = pl.off_wide_slots + pl.wp.slot_bytes;
+      pl.off_wide_bias_part = pl.off_wide_slots + align_up(pl.wp.slot_bytes);
+      pl.off_wide_bias_sq = pl.off_wide_bias_part + align_up(pl.wp.bias_part_bytes);
+      pl.total_wide = pl.off_wide_bias_sq + pl.wp.bias_sq_bytes;
       if (pl.total_wide > pl.total) pl.total = pl.total_wide;
     }
   }
@@ -403,14 +405,17 @@ int fdp::wgrad_check_args(const void* a, const void* b, int64_t B, int64_t K, in
   return FDP_OK;
 }
 
-extern "C" int fdp_wgrad_clip(const void* a, const void* b, int64_t B, int64_t K, int64_t M,
-                              int64_t N, int64_t stride_ab, int64_t lda, int64_t stride_bb,
-                              int64_t ldb, int layout, int dtype, float C, float clamp,
-                              const float* clip_args_dev, float out_scale, const void* noise,
-                              float noise_scale, const fdp_noise_key* noise_key, void* out,
-                              int64_t ldo, int out_dtype,
-                              float* norms, float* factors, int flags, void* workspace,
-                              size_t workspace_bytes, void* stream) {
+namespace {
+
+// fdp_wgrad_clip; with `bias`, the wide kernel also forms the bias of operand
+// a when it runs (*bias_done = true), and otherwise leaves it to the caller.
+int wgrad_clip_impl(const void* a, const void* b, int64_t B, int64_t K, int64_t M, int64_t N,
+                    int64_t stride_ab, int64_t lda, int64_t stride_bb, int64_t ldb, int layout,
+                    int dtype, float C, float clamp, const float* clip_args_dev, float out_scale,
+                    const void* noise, float noise_scale, const fdp_noise_key* noise_key,
+                    void* out, int64_t ldo, int out_dtype, float* norms, float* factors,
+                    int flags, void* workspace, size_t workspace_bytes, void* stream,
+                    const fdp_bias_out* bias, bool* bias_done) {
   const int bad = fdp::wgrad_check_args(a, b, B, K, M, N, lda, ldb, layout, dtype, out, ldo,
                                         out_dtype, norms, flags);
   if (bad != FDP_OK) return bad;
@@ -512,6 +517,18 @@ extern "C" int fdp_wgrad_clip(const void* a, const void* b, int64_t B, int64_t K
     w.clip_args_dev = clip_args_dev;
     w.norms_out = norms;
     w.factors_out = factors;
+    if (bias != nullptr) {
+      w.bias_part = reinterpret_cast<float*>(ws + pl.off_wide_bias_part);
+      w.bias_sq = reinterpret_cast<float*>(ws + pl.off_wide_bias_sq);
+      w.bias_out = bias->out;
+      w.bias_dtype = bias->out_dtype;
+      w.bias_scale = bias->out_scale;
+      w.bias_noise = make_noise(bias->noise, bias->out_dtype,
+                                bias->noise_scale != 0.f ? bias->noise_key : nullptr, 0);
+      w.bias_noise_scale = bias->noise_scale;
+      w.bias_norms = bias->norms;
+      w.bias_factors = bias->factors;
+    }
     {
       const int oes = out_dtype == FDP_F32 ? 4 : 2;
       w.vec_out = (reinterpret_cast<uintptr_t>(out) % (4 * oes) == 0 && ldo % 4 == 0) ? 1 : 0;
@@ -524,7 +541,10 @@ extern "C" int fdp_wgrad_clip(const void* a, const void* b, int64_t B, int64_t K
     }
     const hipError_t e = dtype == FDP_BF16 ? launch_wide_bf16(w, pl.wp.wgm, plain, s)
                                            : launch_wide_f16(w, pl.wp.wgm, plain, s);
-    if (e == hipSuccess) return FDP_OK;
+    if (e == hipSuccess) {
+      if (bias_done != nullptr) *bias_done = bias != nullptr;
+      return FDP_OK;
+    }
     if (e != hipErrorNotSupported && e != hipErrorCooperativeLaunchTooLarge) {
       (void)hipGetLastError();
       return FDP_ERR_HIP;
@@ -566,4 +586,70 @@ extern "C" int fdp_wgrad_clip(const void* a, const void* b, int64_t B, int64_t K
                                 factors, fac_ws, s);
   }
   return e == hipSuccess ? FDP_OK : FDP_ERR_HIP;
+}
+
+}  // namespace
+
+extern "C" int fdp_wgrad_clip(const void* a, const void* b, int64_t B, int64_t K, int64_t M,
+                              int64_t N, int64_t stride_ab, int64_t lda, int64_t stride_bb,
+                              int64_t ldb, int layout, int dtype, float C, float clamp,
+                              const float* clip_args_dev, float out_scale, const void* noise,
+                              float noise_scale, const fdp_noise_key* noise_key, void* out,
+                              int64_t ldo, int out_dtype,
+                              float* norms, float* factors, int flags, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  return wgrad_clip_impl(a, b, B, K, M, N, stride_ab, lda, stride_bb, ldb, layout, dtype, C, clamp,
+                         clip_args_dev, out_scale, noise, noise_scale, noise_key, out, ldo,
+                         out_dtype, norms, factors, flags, workspace, workspace_bytes, stream,
+                         nullptr, nullptr);
+}
+
+// The weight gradient's workspace, then (256-aligned) the column sums' for the
+// bias when the wide kernel does not form it.
+extern "C" int fdp_wgrad_bias_clip_workspace_size(int64_t B, int64_t K, int64_t M, int64_t N,
+                                                  int dtype, int flags, size_t* bytes) {
+  if (bytes == nullptr) return FDP_ERR_ARG;
+  size_t w = 0, c = 0;
+  int st = fdp_wgrad_clip_workspace_size(B, K, M, N, dtype, flags, &w);
+  if (st != FDP_OK) return st;
+  st = fdp_colsum_clip_workspace_size(B, K, M, dtype, &c);
+  if (st != FDP_OK) return st;
+  *bytes = align_up(w) + c;
+  return FDP_OK;
+}
+
+extern "C" int fdp_wgrad_bias_clip(const void* a, const void* b, int64_t B, int64_t K, int64_t M,
+                                   int64_t N, int64_t stride_ab, int64_t lda, int64_t stride_bb,
+                                   int64_t ldb, int layout, int dtype, float C, float clamp,
+                                   const float* clip_args_dev, float out_scale, const void* noise,
+                                   float noise_scale, const fdp_noise_key* noise_key, void* out,
+                                   int64_t ldo, int out_dtype, float* norms, float* factors,
+                                   int flags, const fdp_bias_out* bias, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
+  const int bad = fdp::wgrad_check_args(a, b, B, K, M, N, lda, ldb, layout, dtype, out, ldo,
+                                        out_dtype, norms, flags);
+  if (bad != FDP_OK) return bad;
+  if (bias == nullptr || bias->out == nullptr) return FDP_ERR_ARG;
+  if (!valid_dtype(bias->out_dtype)) return FDP_ERR_DTYPE;
+  // the bias is of a = [B, K, M] over K, contiguous (the column-sum kernel
+  // reads it that way when the wide kernel does not run); the clip is not
+  // optional
+  if (layout != FDP_LAYOUT_TN || (flags & FDP_WGRAD_NOCLIP) != 0) return FDP_ERR_ARG;
+  if (lda != M || stride_ab != K * M) return FDP_ERR_SHAPE;
+  size_t wbytes = 0, cbytes = 0;
+  int st = fdp_wgrad_clip_workspace_size(B, K, M, N, dtype, flags, &wbytes);
+  if (st != FDP_OK) return st;
+  st = fdp_colsum_clip_workspace_size(B, K, M, dtype, &cbytes);
+  if (st != FDP_OK) return st;
+  const size_t wspan = align_up(wbytes);
+  if (workspace == nullptr || workspace_bytes < wspan + cbytes) return FDP_ERR_WORKSPACE;
+  bool done = false;
+  st = wgrad_clip_impl(a, b, B, K, M, N, stride_ab, lda, stride_bb, ldb, layout, dtype, C, clamp,
+                       clip_args_dev, out_scale, noise, noise_scale, noise_key, out, ldo,
+                       out_dtype, norms, factors, flags, workspace, wspan, stream, bias, &done);
+  if (st != FDP_OK || done) return st;
+  return fdp_colsum_clip(a, nullptr, B, K, M, dtype, FDP_NORM_FROB, C, clamp, clip_args_dev,
+                         bias->out_scale, bias->noise, bias->noise_scale, bias->noise_key,
+                         bias->out, bias->out_dtype, bias->norms, bias->factors,
+                         static_cast<char*>(workspace) + wspan, workspace_bytes - wspan, stream);
 }

@@ -69,6 +69,18 @@ struct WideArgs {
   float* norms_out;
   float* factors_out;
   int vec_out;  // out rows hold whole aligned quads: 4 outputs per vector store
+  // The bias of operand a (kernel's BIAS = true):
+  //   bias[m] = bias_scale * sum_b c'_b sum_k a_b[k, m] + bias_noise_scale * zb[m],
+  //   c'_b = clip(||a_b||_F) with the weight's C and clamp.
+  float* bias_part;  // [B, tiles_m, tiles_n, BM]: column sums over a workgroup's k-tiles
+  float* bias_sq;    // [B, tiles]: sums of squares of a over a workgroup's (m-block, k-tiles)
+  void* bias_out;
+  int bias_dtype;
+  float bias_scale;
+  NoiseSrc bias_noise;
+  float bias_noise_scale;
+  float* bias_norms;
+  float* bias_factors;
 };
 
 // Block bid (0..71) of the tile belongs to region (bid * ng) / 72: ng
@@ -101,7 +113,36 @@ __device__ __forceinline__ void quad_transpose(const float (&in)[4], float (&out
   }
 }
 
-template <class DT, int WGM, int WGN>
+// BIAS: also the bias of operand a.  The column sums and squares of a come from
+// the A fragments the MFMAs already hold: k-tile kt of an m-block is counted by
+// the tile with n-index kt % tiles_n, k-step ks by the wave of the row group
+// with column index ks (two v_dot2 per 2 elements: with ones, and with itself).
+// acc + x.lo + x.hi and acc + x.lo^2 + x.hi^2 for two packed 16-bit values.
+template <class DT>
+__device__ __forceinline__ float dot2_ones(uint32_t x, float acc) {
+  if constexpr (DT::code == FDP_BF16) {
+    typedef __attribute__((ext_vector_type(2))) __bf16 v2;
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2, x),
+                                           __builtin_bit_cast(v2, 0x3f803f80u), acc, false);
+  } else {
+    typedef __attribute__((ext_vector_type(2))) _Float16 v2;
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(v2, x), __builtin_bit_cast(v2, 0x3c003c00u),
+                                  acc, false);
+  }
+}
+template <class DT>
+__device__ __forceinline__ float dot2_self(uint32_t x, float acc) {
+  if constexpr (DT::code == FDP_BF16) {
+    typedef __attribute__((ext_vector_type(2))) __bf16 v2;
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2, x), __builtin_bit_cast(v2, x),
+                                           acc, false);
+  } else {
+    typedef __attribute__((ext_vector_type(2))) _Float16 v2;
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(v2, x), __builtin_bit_cast(v2, x), acc, false);
+  }
+}
+
+template <class DT, int WGM, int WGN, bool BIAS>
 __global__ __launch_bounds__(kWideThreads, 1) void wgrad_wide_kernel(WideArgs p) {
   using G = dma::Geom<96 * WGM, 96 * WGN, 32, WGM, WGN>;
   static_assert(G::NW == 8 && G::FI == 3 && G::FJ == 3, "8 waves of 3x3 blocks");
@@ -111,6 +152,7 @@ __global__ __launch_bounds__(kWideThreads, 1) void wgrad_wide_kernel(WideArgs p)
   __shared__ __attribute__((aligned(16))) char st2[G::STAGE];
   __shared__ float red[8];
   __shared__ float fac[kWideBlocks];  // clip factors of the tile's samples (ng <= 72)
+  __shared__ float bfac[BIAS ? kWideBlocks : 1];  // bias clip factors
   __shared__ int flag;
   // The own region (at most 36 blocks when ng >= 2) is staged in the free ring,
   // kStageBlocks whole blocks per stage array.
@@ -182,6 +224,29 @@ __global__ __launch_bounds__(kWideThreads, 1) void wgrad_wide_kernel(WideArgs p)
     }
   };
 
+  // bias of a: this lane's rows (wm + 32 i + lane % 32, k half lane / 32)
+  const int tile_m = static_cast<int>(m0 / G::BM), tile_n = static_cast<int>(n0 / G::BN);
+  float bcs[3] = {0.f, 0.f, 0.f}, bsq = 0.f;
+  auto fhook = [&](int kt, int ks, const dma::Frags<G>& f) {
+    if constexpr (BIAS) {
+      if (kt % p.tiles_n == tile_n && (wave % WGN) == ks) {
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+          const uint32_t w4[4] = {f.a[i].x, f.a[i].y, f.a[i].z, f.a[i].w};
+          float cs = bcs[i], q = 0.f;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            cs = dot2_ones<DT>(w4[e], cs);
+            q = dot2_self<DT>(w4[e], q);
+          }
+          bcs[i] = cs;
+          // rows past M may hold the next row's values: left out of the norm
+          bsq += m0 + wm + 32 * i + (lane & 31) < p.M ? q : 0.f;
+        }
+      }
+    }
+  };
+
   // ---- 1. the product
   f32x16 acc[3][3];
 #pragma unroll
@@ -202,13 +267,38 @@ __global__ __launch_bounds__(kWideThreads, 1) void wgrad_wide_kernel(WideArgs p)
       if (pre_noise && kt > 0 && kt % kPreNoiseEvery == 0 && kt / kPreNoiseEvery <= kPreNoiseDraws)
         draw_early(kt / kPreNoiseEvery - 1);
     };
-    dma::gemm_pipe<DT, G, S>(job, nk, fo, stages, acc, hook);
+    dma::gemm_pipe<DT, G, S>(job, nk, fo, stages, acc, hook, fhook);
     if (pre_noise) {
       const int done = (nk - 1) / kPreNoiseEvery;  // draws made inside the loop
 #pragma unroll 1
       for (int j = done < kPreNoiseDraws ? done : kPreNoiseDraws; j < kPreNoiseDraws; ++j)
         draw_early(j);
     }
+  }
+  if constexpr (BIAS) {
+    // lanes l and l + 32 hold one row's two k halves; the WGN waves of a row
+    // group (one k-step each) are added in wave order through LDS (st2 is
+    // free: gemm_pipe ended on a barrier, and the own region never reaches it)
+    __shared__ float bred[8];
+    float* colp = reinterpret_cast<float*>(st2);  // [WGN][BM]
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      const float v = bcs[i] + __shfl_xor(bcs[i], 32, kWave);
+      if (lane < 32) colp[(wave % WGN) * G::BM + wm + 32 * i + lane] = v;
+    }
+    const float q = wave_sum_dpp(bsq);
+    if (lane == 0) bred[wave] = q;
+    __syncthreads();
+    float* part = p.bias_part + ((int64_t(sample) * p.tiles_m + tile_m) * p.tiles_n + tile_n) * G::BM;
+    for (int r = threadIdx.x; r < G::BM; r += kWideThreads) {
+      float v = colp[r];
+#pragma unroll
+      for (int q2 = 1; q2 < WGN; ++q2) v += colp[q2 * G::BM + r];
+      st_coherent(part + r, v);
+    }
+    if (threadIdx.x == 0)
+      st_coherent(p.bias_sq + int64_t(sample) * p.tiles + tile,
+                  ((bred[0] + bred[1]) + (bred[2] + bred[3])) + ((bred[4] + bred[5]) + (bred[6] + bred[7])));
   }
   {
     // rows/columns past M/N may hold the next row's values: left out of the norm
@@ -305,8 +395,58 @@ __global__ __launch_bounds__(kWideThreads, 1) void wgrad_wide_kernel(WideArgs p)
           if (p.factors_out) p.factors_out[s] = cf;
         }
       }
+      if constexpr (BIAS) {
+        const float* bpart = p.bias_sq + int64_t(s) * p.tiles;
+        float bq = 0.f;
+        for (int t = lane; t < p.tiles; t += kWave) bq += ld_coherent(bpart + t);
+        bq = wave_sum_dpp(bq);
+        if (lane == 0) {
+          const float n = poisoned ? __builtin_nanf("") : sqrtf(bq);
+          const float cf = poisoned ? n : clip_factor(n, C, clamp);
+          bfac[s] = cf;
+          if (tile == 0 && s == sample) {
+            if (p.bias_norms) p.bias_norms[s] = n;
+            if (p.bias_factors) p.bias_factors[s] = cf;
+          }
+        }
+      }
     }
     __syncthreads();  // (also: the own region is staged)
+  }
+
+  // ---- 4b. the bias: workgroup L finishes outputs [L * per, (L + 1) * per),
+  // one per thread: sum over (sample s, k-range q) in that order of
+  // c'_s * part[s][q], 16 agent-coherent loads in flight at a time
+  if constexpr (BIAS) {
+    const int64_t per = (p.M + p.nwg - 1) / p.nwg;
+    const uint32_t pbytes = static_cast<uint32_t>(int64_t(ng) * p.tiles_m * p.tiles_n * G::BM * 4);
+    const auto rs = __builtin_amdgcn_make_buffer_rsrc(p.bias_part, static_cast<short>(0),
+                                                      static_cast<int>(pbytes), kRawBufferWord3);
+    const int J = ng * p.tiles_n;
+    for (int64_t m = int64_t(L) * per + threadIdx.x;
+         m < p.M && m < (int64_t(L) + 1) * per; m += kWideThreads) {
+      const int64_t tmb = m / G::BM, r = m % G::BM;
+      float v = 0.f;
+#pragma unroll 1
+      for (int j0 = 0; j0 < J; j0 += 16) {
+        float x[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          const int j = j0 + u < J ? j0 + u : J - 1;
+          const int sj = j / p.tiles_n, qj = j % p.tiles_n;
+          const int64_t e = ((int64_t(sj) * p.tiles_m + tmb) * p.tiles_n + qj) * G::BM + r;
+          x[u] = __uint_as_float(
+              __builtin_amdgcn_raw_buffer_load_b32(rs, static_cast<uint32_t>(e * 4), 0, kCoherent));
+        }
+#pragma unroll
+        for (int u = 0; u < 16; ++u)
+          if (j0 + u < J) v += bfac[(j0 + u) / p.tiles_n] * x[u];
+      }
+      v *= p.bias_scale;
+      if (p.bias_noise.on()) v += p.bias_noise_scale * p.bias_noise.at(m);
+      if (poisoned) v = __builtin_nanf("");
+      store_from_f32(p.bias_out, m, p.bias_dtype, v);
+    }
   }
 
   // ---- 5. finish: out = out_scale * sum_g c_g G_g + noise_scale * z, one item
@@ -478,11 +618,15 @@ __global__ __launch_bounds__(kWideThreads, 1) void wgrad_wide_kernel(WideArgs p)
 // outputs; applicable when every product gets a CU of its own, the products
 // fill at least `min_fill` of the device, and the row strides keep a
 // sample's operand under 2^31 bytes (32-bit buffer records).
+// Rows of a 384x192 (wgm 4) or 192x384 (wgm 2) tile, in units of 96.
+constexpr int wgm_rows(int wgm) { return wgm; }
+
 struct WidePlan {
   int wgm;  // 4: 384x192, 2: 192x384, 0: not applicable
   int tiles_m, tiles_n, tiles, nwg;
   int slot_blocks;
   size_t partial_bytes, slot_bytes;
+  size_t bias_part_bytes, bias_sq_bytes;  // the bias of a (reserved whether asked or not)
 };
 inline WidePlan wide_plan(int64_t B, int64_t K, int64_t M, int64_t N, int64_t lda, int64_t ldb,
                           int cus, double min_fill) {
@@ -510,13 +654,19 @@ inline WidePlan wide_plan(int64_t B, int64_t K, int64_t M, int64_t N, int64_t ld
   w.slot_blocks = kWideBlocks - static_cast<int>(kWideBlocks / B);
   w.partial_bytes = sizeof(float) * size_t(units);
   w.slot_bytes = size_t(units) * size_t(w.slot_blocks) * kWideBlockBytes;
+  w.bias_part_bytes = sizeof(float) * size_t(B) * w.tiles_m * w.tiles_n * (96 * wgm_rows(w.wgm));
+  w.bias_sq_bytes = sizeof(float) * size_t(units);
   return w;
 }
 
 template <class DT>
 hipError_t launch_wide_t(const WideArgs& a, int wgm, bool plain, hipStream_t s) {
-  const void* fn = wgm == 4 ? reinterpret_cast<const void*>(&wgrad_wide_kernel<DT, 4, 2>)
-                            : reinterpret_cast<const void*>(&wgrad_wide_kernel<DT, 2, 4>);
+  const bool bias = a.bias_out != nullptr;
+  const void* fn =
+      wgm == 4 ? (bias ? reinterpret_cast<const void*>(&wgrad_wide_kernel<DT, 4, 2, true>)
+                       : reinterpret_cast<const void*>(&wgrad_wide_kernel<DT, 4, 2, false>))
+               : (bias ? reinterpret_cast<const void*>(&wgrad_wide_kernel<DT, 2, 4, true>)
+                       : reinterpret_cast<const void*>(&wgrad_wide_kernel<DT, 2, 4, false>));
   if (host::occupancy(fn, kWideThreads, 0) < 1) return hipErrorNotSupported;
   WideArgs c = a;
   void* params[] = {&c};

@@ -4,9 +4,11 @@ Reference: flashdp/layers/linear.py:11-106.  Backward math (per parameter tensor
   dX = g W                                                       (unclipped)
   dW = (1/B) sum_b clip(||g_b^T x_b||_F) g_b^T x_b + (sigma/sqrt(B)) z_W
   db = (1/(B*T)) sum_b clip(||g_b||_F) sum_t g_bt  + (sigma/sqrt(B)) z_b
-with clip(n) = min(clamp_value, C/(n + 1e-10)).  dW and db each run as one fused
-HIP call (fdp_wgrad_clip / fdp_colsum_clip): norm, clip, 1/B and noise add
-happen on the device, and grad_output is never modified.
+with clip(n) = min(clamp_value, C/(n + 1e-10)).  dW and db run as one HIP call
+(fdp_wgrad_bias_clip; fdp_wgrad_clip / fdp_colsum_clip when only one of them
+is needed): norm, clip, 1/B and noise add happen on the device, and
+grad_output is never modified.  Where the wide single-pass kernel runs, the
+bias comes from the grad_output fragments it already holds (no second pass).
 """
 from __future__ import annotations
 
@@ -79,16 +81,28 @@ class _DPLinearFunction(Function):
         if ctx.needs_input_grad[0]:
             w = weight if weight.dtype == g3.dtype else weight.to(g3.dtype)
             grad_input = (g3 @ w).reshape(input.shape)
+        want_bias = ctx.has_bias and ctx.needs_input_grad[2]
         if ctx.needs_input_grad[1]:
             z, key = noise_args(std, gen, nstream, weight.shape, weight.dtype, weight.device)
-            r = wgrad_clip(g3, x3.to(g3.dtype), C, clamp_value, layout="tn", out_scale=1.0 / B,
-                           noise=z, noise_scale=std, noise_key=key, out_dtype=weight.dtype,
-                           return_stats=stats is not None)
+            extra = {}
+            if want_bias:  # both in one call (noise drawn in the same order: weight, bias)
+                O = g3.shape[-1]
+                zb, keyb = noise_args(std, gen, nstream, (O,), ctx.bias_dtype, g3.device)
+                grad_bias = torch.empty(O, dtype=ctx.bias_dtype, device=g3.device)
+                extra = dict(bias_out=grad_bias, bias_scale=1.0 / (B * T), bias_noise=zb,
+                             bias_noise_scale=std, bias_noise_key=keyb)
+            r = wgrad_clip(g3.contiguous() if want_bias else g3, x3.to(g3.dtype), C, clamp_value,
+                           layout="tn", out_scale=1.0 / B, noise=z, noise_scale=std,
+                           noise_key=key, out_dtype=weight.dtype,
+                           return_stats=stats is not None, **extra)
             if stats is not None:
-                grad_weight, stats["norms_w"], stats["fac_w"] = r
+                grad_weight, stats["norms_w"], stats["fac_w"] = r[:3]
+                if want_bias:
+                    stats["norms_b"], stats["fac_b"] = r[3], r[4]
             else:
                 grad_weight = r
-        if ctx.has_bias and ctx.needs_input_grad[2]:
+            want_bias = False
+        if want_bias:
             O = g3.shape[-1]
             z, key = noise_args(std, gen, nstream, (O,), ctx.bias_dtype, g3.device)
             r = colsum_clip(g3, None, C, clamp_value, norm="frob", out_scale=1.0 / (B * T),

@@ -178,6 +178,51 @@ int fdp_wgrad_clip(const void* a, const void* b, int64_t B, int64_t K, int64_t M
                    void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
+ * The weight and bias gradients of a DP Linear layer in one call
+ * (replaces the pair linear_weight_flashdp + linear_bias_grad_clip in the
+ * reference's DPLinear backward, flashdp/layers/linear.py:72-92, with
+ * flashdp/core/linear_clip.py:107-123):
+ *
+ *   out  = as fdp_wgrad_clip (layout FDP_LAYOUT_TN, a = grad_output [B,K,M],
+ *          b = input [B,K,N]),
+ *   bias[m] = bias->out_scale * sum_b c'_b sum_k a_b[k,m] + bias->noise_scale * zb[m],
+ *   c'_b = min(clamp, C / (||a_b||_F + 1e-10))   (the weight's C, clamp),
+ *
+ * i.e. linear_bias_grad_clip with out_scale = 1/(B*K) (its mean over B*T)
+ * and noise_scale = sigma/sqrt(B).  zb is bias->noise (M values of
+ * bias->out_dtype) or, without one, the in-kernel draw of bias->noise_key
+ * (stream 0, as fdp_colsum_clip).  a must be contiguous (stride_ab = K*M,
+ * lda = M); FDP_WGRAD_NOCLIP is not accepted.  When the wide single-pass
+ * kernel runs, it forms the bias from the operand fragments it already holds
+ * (no second pass over a); otherwise the call runs fdp_colsum_clip
+ * (FDP_NORM_FROB) after the weight gradient.  bias->norms / bias->factors
+ * (optional, B floats) receive ||a_b||_F and c'_b.
+ * Workspace: fdp_wgrad_bias_clip_workspace_size bytes; its first
+ * fdp_wgrad_clip_workspace_size bytes (rounded up to 256) are the weight
+ * gradient's workspace, with the same rules (FDP_WGRAD_CLEAN_WORKSPACE).
+ * ---------------------------------------------------------------------- */
+typedef struct fdp_bias_out {
+  void* out;
+  int out_dtype;
+  float out_scale;
+  const void* noise;
+  float noise_scale;
+  const fdp_noise_key* noise_key;
+  float* norms;
+  float* factors;
+} fdp_bias_out;
+
+int fdp_wgrad_bias_clip_workspace_size(int64_t B, int64_t K, int64_t M, int64_t N, int dtype,
+                                       int flags, size_t* bytes);
+int fdp_wgrad_bias_clip(const void* a, const void* b, int64_t B, int64_t K, int64_t M, int64_t N,
+                        int64_t stride_ab, int64_t lda, int64_t stride_bb, int64_t ldb,
+                        int layout, int dtype, float C, float clamp, const float* clip_args_dev,
+                        float out_scale, const void* noise, float noise_scale,
+                        const fdp_noise_key* noise_key, void* out, int64_t ldo, int out_dtype,
+                        float* norms, float* factors, int flags, const fdp_bias_out* bias,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
  * fdp_wgrad_clip for callers that cannot allocate device memory.
  *
  * No counterpart in the reference: it serves callers that cannot allocate

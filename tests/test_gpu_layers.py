@@ -47,6 +47,29 @@ def test_dplinear_cfg1(dtype, sigma):
     assert np.all(ref["norms_w"] > 1.0)  # all samples clipped at this config
 
 
+def test_dplinear_cfg2_bias_in_one_launch():
+    """cfg2: DPLinear 768 -> 3072 with bias, B=8, T=1024, bf16: the backward's
+    weight and bias gradients come from one wide-kernel launch (the bias from
+    the grad_output fragments the product already holds); parity with the
+    float64 oracle of the reference's two separate ops."""
+    torch.manual_seed(0)
+    dtype = torch.bfloat16
+    lin = DPLinear(768, 3072, bias=True, C=1.0, noise_multiplier=1.0).to(DEV, dtype)
+    lin.record_stats = True
+    lin.noise_generator = torch.Generator(device=DEV).manual_seed(4321)
+    x = torch.randn(8, 1024, 768, device=DEV).to(dtype).requires_grad_(True)
+    g = (torch.randn(8, 1024, 3072, device=DEV) * 0.01).to(dtype)
+    lin(x).backward(g)
+    zw, zb = draws(4321, [(3072, 768), (3072,)], dtype)
+    ref = O.linear_backward(x.detach(), g, lin.weight.detach(), 1.0, 1.0, 1.0, zw, zb)
+    assert_close(lin.weight.grad, ref["dw"], dtype, "dW", margin="cfg2 DPLinear: dW")
+    assert_close(lin.bias.grad, ref["db"], dtype, "db", margin="cfg2 DPLinear: db (fused bias)")
+    st = lin.last_stats
+    assert_elementwise(st["norms_b"], ref["norms_b"], dtype, "bias norms")
+    assert_elementwise(st["fac_b"], ref["fac_b"], dtype, "bias factors")
+    assert_elementwise(st["norms_w"], ref["norms_w"], dtype, "weight norms")
+
+
 @pytest.mark.parametrize("shape", [(6, 20), (3, 4, 5, 20)], ids=["2d", "4d"])
 def test_dplinear_other_ranks(shape):
     """2-D inputs (T=1) and >3-D inputs (T = product of middle axes) return

@@ -489,3 +489,123 @@ def test_wgrad_wide_expired_wait(monkeypatch):
     out = core.wgrad_clip(a, b, 0.5, 1.0, out_dtype=torch.float32, single_pass="wide")
     assert_close(out, ref, torch.bfloat16, "after expiry")
     assert core.wgrad_status() != 0
+
+
+# ------------------------------------------------- weight and bias in one call
+BIAS_SHAPES = [
+    (8, 1024, 3072, 768),  # cfg2: the DP Linear 768 -> 3072 layer, B=8, T=1024
+    (12, 64, 1000, 704),   # ragged tiles in both directions (rows of 16-byte multiples)
+    (4, 96, 1536, 384),    # 192x384 or 384x192 tiles, contraction of 3 k-tiles
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=str)
+@pytest.mark.parametrize("shape", BIAS_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_wgrad_bias_fused_in_wide_kernel(shape, dtype):
+    """fdp_wgrad_bias_clip through the C ABI: with the wide kernel the bias of a
+    comes from the same launch -- the column-sum half of the workspace (filled
+    with a canary) is never touched -- and matches the float64 oracle
+    (flashdp/core/linear_clip.py:116-123: norm of the whole a_b, mean over
+    B*K) and the column-sum kernel's result (FDP_WGRAD_NARROW: the fallback);
+    the weight gradient is the one fdp_wgrad_clip gives, bit for bit."""
+    import ctypes
+    from flashdp4review_amd import _lib
+    B, K, M, N = shape
+    print(f"bias fused: shape={shape} dtype={dtype}", flush=True)
+    a, b = make(B, K, M, N, dtype, "tn", seed=21)
+    L = _lib.lib()
+    dt = _lib.dtype_code(dtype)
+    _, wn, _ = O.wgrad_clip(a, b, 1.0, 1.0, "tn")
+    C = float(np.median(wn))
+    zb = (torch.randn(M, generator=torch.Generator().manual_seed(5)) * 1.0).to(dtype).to(DEV)
+    zw = torch.randn(M, N, generator=torch.Generator().manual_seed(6)).to(DEV)  # fp32, as out
+    stream = _lib.stream_handle(torch.device(DEV))
+
+    def run(flags, with_bias=True, canary=False):
+        out = torch.empty(M, N, dtype=torch.float32, device=DEV)
+        norms = torch.empty(B, dtype=torch.float32, device=DEV)
+        fac = torch.empty(B, dtype=torch.float32, device=DEV)
+        bo = torch.empty(M, dtype=dtype, device=DEV)
+        bn = torch.empty(B, dtype=torch.float32, device=DEV)
+        bf = torch.empty(B, dtype=torch.float32, device=DEV)
+        common = (a.data_ptr(), b.data_ptr(), B, K, M, N, a.stride(0), a.stride(1), b.stride(0),
+                  b.stride(1), _lib.LAYOUT_TN, dt, ctypes.c_float(C), ctypes.c_float(1.0), None,
+                  ctypes.c_float(1.0 / B), zw.data_ptr(), ctypes.c_float(0.25), None,
+                  out.data_ptr(), N, _lib.FDP_F32, norms.data_ptr(), fac.data_ptr(), flags)
+        if not with_bias:
+            nb = _lib.size_query(L.fdp_wgrad_clip_workspace_size, B, K, M, N, dt, flags)
+            ws = torch.zeros(nb, dtype=torch.uint8, device=DEV)
+            assert L.fdp_wgrad_clip(*common, ws.data_ptr(), nb, stream) == 0
+            torch.cuda.synchronize()
+            return out, norms, fac
+        wb = _lib.size_query(L.fdp_wgrad_clip_workspace_size, B, K, M, N, dt, flags)
+        nb = _lib.size_query(L.fdp_wgrad_bias_clip_workspace_size, B, K, M, N, dt, flags)
+        span = (wb + 255) // 256 * 256
+        ws = torch.zeros(nb, dtype=torch.uint8, device=DEV)
+        if canary:
+            ws[span:] = 0xA5
+        bias = _lib.BiasOut(bo.data_ptr(), dt, 1.0 / (B * K), zb.data_ptr(), 0.5, None,
+                            bn.data_ptr(), bf.data_ptr())
+        st = L.fdp_wgrad_bias_clip(*common, ctypes.byref(bias), ws.data_ptr(), nb, stream)
+        assert st == 0, L.fdp_strerror(st)
+        torch.cuda.synchronize()
+        untouched = bool(torch.all(ws[span:] == 0xA5)) if canary else None
+        return out, norms, fac, bo, bn, bf, untouched
+
+    out, norms, fac, bo, bn, bf, untouched = run(_lib.WGRAD_WIDE, canary=True)
+    assert untouched, "the bias took the column-sum fallback instead of the wide kernel"
+    w_only = run(_lib.WGRAD_WIDE, with_bias=False)
+    assert torch.equal(out, w_only[0]) and torch.equal(norms, w_only[1])
+    ref_b, ref_bn, ref_bf = O.colsum_clip(a, None, C, 1.0, "frob", 1.0 / (B * K), zb, 0.5)
+    tag = f"bias fused in the wide kernel {shape} ({dtype})" if shape == BIAS_SHAPES[0] else None
+    assert_close(bo, ref_b, dtype, "bias", margin=tag)
+    assert_elementwise(bn, ref_bn, dtype, "bias norms")
+    assert_elementwise(bf, ref_bf, dtype, "bias factors")
+    ref_w, _, _ = O.wgrad_clip(a, b, C, 1.0, "tn", out_scale=1.0 / B, noise=zw, noise_scale=0.25)
+    assert_close(out, ref_w, dtype, "weight")
+    # the fallback (narrow schedule + column-sum kernel) agrees
+    out2, _, _, bo2, bn2, _, untouched2 = run(_lib.WGRAD_NARROW, canary=True)
+    assert not untouched2
+    assert_close(bo2, ref_b, dtype, "bias (column-sum fallback)")
+    assert_elementwise(bn2, bn.double().cpu().numpy(), dtype, "bias norms fused vs fallback")
+
+
+def test_wgrad_bias_in_kernel_noise_matches_fallback():
+    """The bias noise drawn in the wide kernel is the column-sum kernel's draw
+    for the same key (Philox stream 0, element m), so the two paths agree."""
+    import ctypes
+    from flashdp4review_amd import _lib
+    B, K, M, N = 8, 256, 3072, 768
+    a, b = make(B, K, M, N, torch.bfloat16, "tn", seed=22)
+    outs = []
+    for sp in ("wide", "narrow"):
+        bo = torch.empty(M, dtype=torch.float32, device=DEV)
+        core.wgrad_clip(a, b, 0.05, 1.0, out_dtype=torch.float32, bias_out=bo,
+                        bias_scale=1.0 / (B * K), bias_noise_key=(777, 12), bias_noise_scale=0.5,
+                        single_pass=sp, check=True)
+        outs.append(bo)
+    z = torch.from_numpy(PX.normals(M, 777, 12, 0)).float()
+    ref, _, _ = O.colsum_clip(a, None, 0.05, 1.0, "frob", 1.0 / (B * K), z, 0.5)
+    assert_close(outs[0], ref, torch.bfloat16, "bias with in-kernel noise (wide)")
+    assert_close(outs[1], ref, torch.bfloat16, "bias with in-kernel noise (column sums)")
+
+
+def test_wgrad_bias_argument_checks():
+    import ctypes
+    from flashdp4review_amd import _lib
+    L = _lib.lib()
+    a, b = make(2, 8, 16, 16, torch.bfloat16, "nn")
+    out = torch.empty(16, 16, device=DEV)
+    bo = torch.empty(16, device=DEV)
+    bias = _lib.BiasOut(bo.data_ptr(), _lib.FDP_F32, 1.0, None, 0.0, None, None, None)
+
+    def call(layout, flags=0, bias_p=ctypes.byref(bias)):
+        return L.fdp_wgrad_bias_clip(a.data_ptr(), b.data_ptr(), 2, 8, 16, 16, 128, 16, 128, 16,
+                                     layout, _lib.FDP_BF16, ctypes.c_float(1.0),
+                                     ctypes.c_float(1.0), None, ctypes.c_float(1.0), None,
+                                     ctypes.c_float(0.0), None, out.data_ptr(), 16, _lib.FDP_F32,
+                                     None, None, flags, bias_p, None, 0, None)
+    assert call(_lib.LAYOUT_NN) == 3          # the bias of a needs layout TN
+    assert call(_lib.LAYOUT_TN, _lib.WGRAD_NOCLIP) == 3
+    assert call(_lib.LAYOUT_TN, 0, None) == 3  # no bias description
+    assert call(_lib.LAYOUT_TN) == 4           # workspace missing
