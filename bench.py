@@ -46,9 +46,9 @@ PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 # factor the same counter reads on a plain copy of known size.  None = not
 # measured for that workload.
 TRAFFIC_BYTES = {
-    "cfg2": 201179439,   # profiles/wgrad_group_kernel_cfg2.md
-    "cfg3": 229671862,   # profiles/wgrad_group_kernel_cfg3.md
-    "cfg4": 109712751,   # profiles/layernorm_bwd_clip_cfg4.md (2 kernels of one call)
+    "cfg2": 134241360,   # profiles/wgrad_wide_kernel_cfg2.md
+    "cfg3": 229718239,   # profiles/wgrad_group_kernel_cfg3.md
+    "cfg4": 105551999,   # profiles/layernorm_bwd_clip_cfg4.md (one launch per call)
 }
 
 
@@ -531,8 +531,8 @@ def main():
                 "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(nbytes / call_ms / 1e6 / PEAK_HBM_GBS, 4),
                 "traffic": TRAFFIC_BYTES["cfg4"],
-                "kernel": "fdp_layernorm_bwd_clip: the call's kernels, HIP events around "
-                          "the timed region",
+                "kernel": "ln_bwd_fused_kernel: one launch per fdp_layernorm_bwd_clip call, "
+                          "HIP events around the timed region",
                 "bytes_per_launch": nbytes, "avg_ms": round(call_ms, 4)}
     else:
         F = 2.0 * B * T * I * O

@@ -42,6 +42,8 @@
 #include <cstdlib>
 
 #include "wgrad_stream.hpp"
+#include <tuple>
+
 #include "wgrad_wide.hpp"
 
 namespace fdp {
@@ -284,6 +286,15 @@ Plan make_plan(int64_t B, int64_t K, int64_t M, int64_t N, int cus, int flags, i
 
 bool valid_dtype(int d) { return d == FDP_F32 || d == FDP_F16 || d == FDP_BF16; }
 
+// make_plan depends only on its arguments: computed once per shape.
+Plan cached_plan(int64_t B, int64_t K, int64_t M, int64_t N, int cus, int flags, int64_t lda = 0,
+                 int64_t ldb = 0) {
+  using Key = std::tuple<int64_t, int64_t, int64_t, int64_t, int, int, int64_t, int64_t>;
+  static host::ShapeCache<Key, Plan> cache;
+  return cache.get(Key{B, K, M, N, cus, flags, lda, ldb},
+                   [&] { return make_plan(B, K, M, N, cus, flags, lda, ldb); });
+}
+
 template <class Core, int LAYOUT, bool VEC>
 hipError_t launch_passes(const Args& a, const Plan& pl, bool noclip, float C, float clamp,
                          const float* clip_args_dev, float* norms, float* factors, float* fac_ws,
@@ -381,7 +392,7 @@ extern "C" int fdp_wgrad_clip_workspace_size(int64_t B, int64_t K, int64_t M, in
   if (bytes == nullptr) return FDP_ERR_ARG;
   if (!valid_dtype(dtype)) return FDP_ERR_DTYPE;
   if (B < 1 || M < 1 || N < 1 || K < 0) return FDP_ERR_SHAPE;
-  *bytes = make_plan(B, K, M, N, num_cus(), flags).total;
+  *bytes = cached_plan(B, K, M, N, num_cus(), flags).total;
   return FDP_OK;
 }
 
@@ -424,9 +435,9 @@ int wgrad_clip_impl(const void* a, const void* b, int64_t B, int64_t K, int64_t 
   const int cus = num_cus();
   // the workspace was sized for contiguous operands: the wide plan for the
   // actual strides is taken only if it fits that size
-  const Plan pl0 = make_plan(B, K, M, N, cus, flags);
+  const Plan pl0 = cached_plan(B, K, M, N, cus, flags);
   if (workspace == nullptr || workspace_bytes < pl0.total) return FDP_ERR_WORKSPACE;
-  Plan pl = make_plan(B, K, M, N, cus, flags, lda, ldb);
+  Plan pl = cached_plan(B, K, M, N, cus, flags, lda, ldb);
   if (pl.total > workspace_bytes) pl.wp.wgm = 0;
   if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0) return FDP_ERR_ALIGN;
 

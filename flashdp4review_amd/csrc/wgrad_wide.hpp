@@ -72,7 +72,8 @@ struct WideArgs {
   // The bias of operand a (kernel's BIAS = true):
   //   bias[m] = bias_scale * sum_b c'_b sum_k a_b[k, m] + bias_noise_scale * zb[m],
   //   c'_b = clip(||a_b||_F) with the weight's C and clamp.
-  float* bias_part;  // [B, tiles_m, tiles_n, BM]: column sums over a workgroup's k-tiles
+  float* bias_part;  // [tiles_m, BM, B, tiles_n]: column sums over a workgroup's k-tiles
+                     // (an output's B * tiles_n partials are contiguous)
   float* bias_sq;    // [B, tiles]: sums of squares of a over a workgroup's (m-block, k-tiles)
   void* bias_out;
   int bias_dtype;
@@ -289,12 +290,13 @@ __global__ __launch_bounds__(kWideThreads, 1) void wgrad_wide_kernel(WideArgs p)
     const float q = wave_sum_dpp(bsq);
     if (lane == 0) bred[wave] = q;
     __syncthreads();
-    float* part = p.bias_part + ((int64_t(sample) * p.tiles_m + tile_m) * p.tiles_n + tile_n) * G::BM;
+    const int J = ng * p.tiles_n;  // partials per output
+    float* part = p.bias_part + int64_t(tile_m) * G::BM * J + sample * p.tiles_n + tile_n;
     for (int r = threadIdx.x; r < G::BM; r += kWideThreads) {
       float v = colp[r];
 #pragma unroll
       for (int q2 = 1; q2 < WGN; ++q2) v += colp[q2 * G::BM + r];
-      st_coherent(part + r, v);
+      st_coherent(part + int64_t(r) * J, v);
     }
     if (threadIdx.x == 0)
       st_coherent(p.bias_sq + int64_t(sample) * p.tiles + tile,
@@ -416,31 +418,33 @@ __global__ __launch_bounds__(kWideThreads, 1) void wgrad_wide_kernel(WideArgs p)
 
   // ---- 4b. the bias: workgroup L finishes outputs [L * per, (L + 1) * per),
   // one per thread: sum over (sample s, k-range q) in that order of
-  // c'_s * part[s][q], 16 agent-coherent loads in flight at a time
+  // c'_s * part[s][q]; an output's partials are contiguous, loaded as 16-byte
+  // agent-coherent vectors, 8 in flight at a time
   if constexpr (BIAS) {
     const int64_t per = (p.M + p.nwg - 1) / p.nwg;
-    const uint32_t pbytes = static_cast<uint32_t>(int64_t(ng) * p.tiles_m * p.tiles_n * G::BM * 4);
-    const auto rs = __builtin_amdgcn_make_buffer_rsrc(p.bias_part, static_cast<short>(0),
-                                                      static_cast<int>(pbytes), kRawBufferWord3);
     const int J = ng * p.tiles_n;
+    const uint32_t pbytes = static_cast<uint32_t>(int64_t(p.tiles_m) * G::BM * J * 4);
+    const CoherentSpan span(p.bias_part, pbytes);
     for (int64_t m = int64_t(L) * per + threadIdx.x;
          m < p.M && m < (int64_t(L) + 1) * per; m += kWideThreads) {
-      const int64_t tmb = m / G::BM, r = m % G::BM;
+      const uint32_t base = static_cast<uint32_t>(m * J * 4);
       float v = 0.f;
+      if (J % 4 == 0) {
 #pragma unroll 1
-      for (int j0 = 0; j0 < J; j0 += 16) {
-        float x[16];
+        for (int j0 = 0; j0 < J; j0 += 32) {
+          f32x4 x[8];
 #pragma unroll
-        for (int u = 0; u < 16; ++u) {
-          const int j = j0 + u < J ? j0 + u : J - 1;
-          const int sj = j / p.tiles_n, qj = j % p.tiles_n;
-          const int64_t e = ((int64_t(sj) * p.tiles_m + tmb) * p.tiles_n + qj) * G::BM + r;
-          x[u] = __uint_as_float(
-              __builtin_amdgcn_raw_buffer_load_b32(rs, static_cast<uint32_t>(e * 4), 0, kCoherent));
+          for (int u = 0; u < 8; ++u)
+            x[u] = j0 + 4 * u < J ? span.load4(base + (j0 + 4 * u) * 4) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int u = 0; u < 8; ++u)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (j0 + 4 * u + e < J) v += bfac[(j0 + 4 * u + e) / p.tiles_n] * x[u][e];
         }
-#pragma unroll
-        for (int u = 0; u < 16; ++u)
-          if (j0 + u < J) v += bfac[(j0 + u) / p.tiles_n] * x[u];
+      } else {
+#pragma unroll 1
+        for (int j = 0; j < J; ++j) v += bfac[j / p.tiles_n] * ld_coherent(p.bias_part + m * J + j);
       }
       v *= p.bias_scale;
       if (p.bias_noise.on()) v += p.bias_noise_scale * p.bias_noise.at(m);

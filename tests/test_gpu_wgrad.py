@@ -609,3 +609,32 @@ def test_wgrad_bias_argument_checks():
     assert call(_lib.LAYOUT_TN, _lib.WGRAD_NOCLIP) == 3
     assert call(_lib.LAYOUT_TN, 0, None) == 3  # no bias description
     assert call(_lib.LAYOUT_TN) == 4           # workspace missing
+
+
+def test_wgrad_prepared_call_matches_checked_call():
+    """The first call of a signature (no stats, no injected noise, contiguous
+    operands) is checked in full and recorded; later calls of the same
+    signature go straight to the library.  Both give the same result, and a
+    later call with another shape or bias length is checked again."""
+    from flashdp4review_amd.core import wgrad as W
+    B, K, M, N = 8, 256, 3072, 768
+    a, b = make(B, K, M, N, torch.bfloat16, "tn", seed=31)
+    bo1 = torch.empty(M, dtype=torch.bfloat16, device=DEV)
+    bo2 = torch.empty(M, dtype=torch.bfloat16, device=DEV)
+    W._prepared.clear()
+    kw = dict(out_scale=1.0 / B, noise_scale=0.3, noise_key=(9, 0), bias_scale=1.0 / (B * K),
+              bias_noise_scale=0.3, bias_noise_key=(9, 10**6))
+    first = W.wgrad_clip(a, b, 0.1, 1.0, bias_out=bo1, **kw)
+    assert len(W._prepared) == 1
+    second = W.wgrad_clip(a, b, 0.1, 1.0, bias_out=bo2, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(first, second) and torch.equal(bo1, bo2)
+    # without noise the prepared call matches the oracle
+    W.wgrad_clip(a, b, 0.1, 1.0, out_scale=1.0 / B, noise_scale=0.0)
+    plain = W.wgrad_clip(a, b, 0.1, 1.0, out_scale=1.0 / B, noise_scale=0.0)
+    ref, _, _ = O.wgrad_clip(a, b, 0.1, 1.0, "tn", out_scale=1.0 / B)
+    assert_close(plain, ref, torch.bfloat16, "prepared call")
+    with pytest.raises(ValueError):
+        W.wgrad_clip(a, b, 0.1, 1.0, bias_out=torch.empty(M - 1, dtype=torch.bfloat16,
+                                                          device=DEV), **kw)
+    W._prepared.clear()
