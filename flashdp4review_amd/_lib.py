@@ -126,6 +126,23 @@ def lib() -> ctypes.CDLL:
     return _lib
 
 
+_fast = None
+
+
+def fast_call():
+    """The _fdp_call extension (the per-call path into the library without
+    ctypes' argument conversion), or None if it was not built."""
+    global _fast
+    if _fast is None:
+        lib()  # the library first: the extension links against it
+        try:
+            from . import _fdp_call
+            _fast = _fdp_call
+        except ImportError:
+            _fast = False
+    return _fast or None
+
+
 def check(status: int, what: str) -> None:
     if status == 0:
         return
@@ -167,7 +184,14 @@ def ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_handle(device: torch.device) -> int:
+    """The HIP stream torch currently uses on `device` (its raw handle)."""
+    if _raw_stream is not None:
+        idx = device.index
+        return _raw_stream(idx if idx is not None else torch.cuda.current_device())
     return torch.cuda.current_stream(device).cuda_stream
 
 

@@ -5,6 +5,10 @@ parallel, then linked into ``flashdp4review_amd/libflashdp_hip.so``.  The
 library is what ``flashdp4review_amd._lib`` loads with ctypes; nothing is
 JIT-compiled at import time.
 
+The per-call path of the Python operators, ``_fdp_call`` (csrc/py/fdp_call.cpp,
+CPython C API, host code only), is compiled with the host C++ compiler and
+linked against the library.
+
 Usage: ``python -m flashdp4review_amd.build`` (or ``__graft_entry__.build()``).
 """
 from __future__ import annotations
@@ -13,6 +17,7 @@ import os
 import shutil
 import subprocess
 import sys
+import sysconfig
 from concurrent.futures import ThreadPoolExecutor
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
@@ -71,7 +76,27 @@ def build(verbose: bool = False) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}{r.stderr}")
     os.replace(tmp, LIB_PATH)
+    build_call_module()
     return LIB_PATH
+
+
+CALL_SRC = os.path.join(CSRC, "py", "fdp_call.cpp")
+CALL_PATH = os.path.join(PKG_DIR, "_fdp_call" + (sysconfig.get_config_var("EXT_SUFFIX") or ".so"))
+
+
+def build_call_module() -> str:
+    """The CPython extension _fdp_call, linked against libflashdp_hip.so (rpath
+    $ORIGIN, so it loads the library next to it)."""
+    cxx = os.environ.get("CXX") or shutil.which("g++") or "g++"
+    tmp = CALL_PATH + ".tmp"
+    cmd = [cxx, "-O2", "-std=c++17", "-shared", "-fPIC", "-Wall",
+           f"-I{sysconfig.get_paths()['include']}", CALL_SRC, "-o", tmp,
+           f"-L{PKG_DIR}", "-lflashdp_hip", "-Wl,-rpath,$ORIGIN"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"building _fdp_call failed:\n{r.stdout}{r.stderr}")
+    os.replace(tmp, CALL_PATH)
+    return CALL_PATH
 
 
 if __name__ == "__main__":

@@ -65,6 +65,9 @@ class _Workspace:
 
 def _persistent_workspace(nbytes: int, dev: torch.device, stream: int) -> _Workspace:
     key = (dev.index, stream)
+    ws = _ws_cache.get(key)  # (a dict read is atomic; the lock guards replacement)
+    if ws is not None and ws.buf.numel() >= nbytes:
+        return ws
     with _ws_lock:
         ws = _ws_cache.get(key)
         if ws is None or ws.buf.numel() < nbytes:
@@ -129,11 +132,13 @@ class _Prepared:
     """A checked call signature of wgrad_clip (contiguous operands, no injected
     noise, no stats): the per-call work left is the output allocation, the
     stream's workspace and the library call."""
-    __slots__ = ("fn", "name", "bias", "dims", "out_shape", "out_dtype", "odt", "flags",
+    __slots__ = ("fn", "fast", "name", "bias", "dims", "out_shape", "out_dtype", "odt", "flags",
                  "nbytes", "dev")
 
     def __init__(self, bias, dims, out_shape, out_dtype, odt, flags, nbytes, dev):
         L = _lib.lib()
+        fc = _lib.fast_call()
+        self.fast = None if fc is None else (fc.wgrad_bias if bias else fc.wgrad)
         self.fn = L.fdp_wgrad_bias_clip if bias else L.fdp_wgrad_clip
         self.name = "fdp_wgrad_bias_clip" if bias else "fdp_wgrad_clip"
         self.bias = bias
@@ -151,6 +156,24 @@ class _Prepared:
             if probed != 0:
                 _raise_expired(ws, "reported asynchronously for an earlier call on this stream",
                                probed)
+        if self.fast is not None:
+            # (the extension masks keys to 64 bits and takes ints for floats)
+            if noise_key is not None and type(noise_key) is not tuple:
+                noise_key = tuple(noise_key)
+            common = (a.data_ptr(), b.data_ptr(), *self.dims, C, clamp, out_scale, noise_scale,
+                      noise_key, out.data_ptr(), self.out_shape[1], self.odt, self.flags)
+            if self.bias:
+                if bias_noise_key is not None and type(bias_noise_key) is not tuple:
+                    bias_noise_key = tuple(bias_noise_key)
+                st = self.fast(*common, bias_out.data_ptr(), _lib.dtype_code(bias_out.dtype),
+                               bias_scale, bias_noise_scale, bias_noise_key, ws.buf.data_ptr(),
+                               ws.buf.numel(), stream)
+            else:
+                st = self.fast(*common, ws.buf.data_ptr(), ws.buf.numel(), stream)
+            if st != 0:
+                _lib.check(st, self.name)
+            ws.queue_probe()
+            return out
         key = None if noise_key is None else ctypes.byref(
             _lib.NoiseKey(noise_key[0] & _U64, noise_key[1] & _U64))
         args = (a.data_ptr(), b.data_ptr(), *self.dims, float(C), float(clamp), None,

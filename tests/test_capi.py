@@ -51,6 +51,23 @@ def _wgrad(**kw):
     return _lib.lib().fdp_wgrad_clip(*args.values())
 
 
+def test_call_module_loads_and_validates():
+    """_fdp_call (the per-call path without ctypes) loads next to the library,
+    and its calls reach the library's checks (no device needed for these)."""
+    F = _lib.fast_call()
+    assert F is not None
+    common = (1, 1, 2, 4, 8, 8, 32, 8, 32, 8, 0, 7, 1.0, 1.0, 1.0, 0.0, None, 1, 8, 2, 0)
+    assert F.wgrad(*common, None, 0, None) == 1          # bad dtype
+    assert F.wgrad_bias(*common, 1, 2, 1.0, 0.0, None, None, 0, None) == 1
+    ok = common[:11] + (2,) + common[12:]
+    assert F.wgrad(*ok, None, 0, None) == 4               # workspace missing
+    assert F.wgrad_bias(*ok, None, 2, 1.0, 0.0, None, None, 0, None) == 3  # no bias output
+    with pytest.raises(TypeError):
+        F.wgrad(*ok, None, 0)                              # wrong argument count
+    with pytest.raises(TypeError):
+        F.wgrad(*ok[:16], [1, 2], *ok[17:], None, 0, None)  # key must be a tuple
+
+
 def test_wgrad_validation_codes():
     assert _wgrad(dtype=7) == 1
     assert _wgrad(odt=-1) == 1
