@@ -138,6 +138,74 @@ def _cpu_leg(dtype, budget_s):
     return statistics.median(ts), len(ts)
 
 
+def _timed(fn, budget_s):
+    """Median seconds per call of fn after one warm-up (at least 3 calls)."""
+    fn()
+    ts = []
+    t_start = time.perf_counter()
+    while len(ts) < 3 or (time.perf_counter() - t_start < budget_s and len(ts) < 500):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts), len(ts)
+
+
+def cpu_baselines_cfg3_cfg4(budget_s=4.0):
+    """The reference's torch path on the host cores for cfg3 (Conv1D weight
+    gradient x^T g with the bias clip, flashdp/core/transformers_conv1d_clip.py:22-39
+    via the same per-sample op sequence) and cfg4 (LayerNorm backward with the
+    per-sample dgamma/dbeta clip and noise, flashdp/layers/layernorm.py:92-155),
+    full batches, in bf16 (the config dtype) and fp32."""
+    from oracle import torch_ref
+    threads, machine = host_cores()
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    out = {}
+    try:
+        g = torch.Generator().manual_seed(0)
+        res3 = {}
+        for dt in (torch.bfloat16, torch.float32):
+            x = torch.randn(16, 1024, 768, generator=g).to(dt)
+            go = (torch.randn(16, 1024, 2304, generator=g) * 0.02).to(dt)
+
+            def step3():
+                torch_ref.linear_weight_backward(go, x, 1.0, 1.0, 1.0)  # x^T g: [768, 2304]
+                torch_ref.linear_bias_grad_clip(go.clone(), 1.0, 1.0)
+            t, n = _timed(step3, budget_s)
+            res3[str(dt).split(".")[1]] = (t, n)
+        F3 = 2.0 * 16 * 1024 * 768 * 2304
+        out["cpu_cfg3"] = {"value": round(F3 / res3["bfloat16"][0] / 1e12, 4), "unit": "TFLOP/s",
+                           "fp32_value": round(F3 / res3["float32"][0] / 1e12, 4),
+                           "cores": threads, "kind": "port",
+                           "sample": "cfg3 full batch (B=16,T=1024, Conv1D 768->2304) on CPU: "
+                                     "clipped dW + noise and the clipped bias, median step: bf16 "
+                                     f"{res3['bfloat16'][0]:.4f} s over {res3['bfloat16'][1]} "
+                                     f"steps, fp32 {res3['float32'][0]:.4f} s over "
+                                     f"{res3['float32'][1]} steps"}
+        res4 = {}
+        for dt in (torch.bfloat16, torch.float32):
+            x = torch.randn(16, 1024, 1024, generator=g).to(dt)
+            go = (torch.randn(16, 1024, 1024, generator=g) * 0.01).to(dt)
+            w = torch.ones(1024, dtype=dt)
+            t, n = _timed(lambda: torch_ref.layernorm_backward(x, w, go, 1e-5, 1.0, 1.0, 1.0),
+                          budget_s)
+            res4[str(dt).split(".")[1]] = (t, n)
+        nbytes = 3 * 2 * 16 * 1024 * 1024 + 8 * 16 * 1024
+        out["cpu_cfg4"] = {"value": round(nbytes / res4["bfloat16"][0] / 1e9, 2), "unit": "GB/s",
+                           "fp32_value": round(nbytes / res4["float32"][0] / 1e9, 2),
+                           "cores": threads, "kind": "port",
+                           "sample": "cfg4 full batch (B=16,T=1024,H=1024) on CPU: LayerNorm "
+                                     "backward (torch autograd dx) with per-sample clipped "
+                                     "dgamma/dbeta and noise, median step: bf16 "
+                                     f"{res4['bfloat16'][0]:.4f} s over {res4['bfloat16'][1]} "
+                                     f"steps, fp32 {res4['float32'][0]:.4f} s over "
+                                     f"{res4['float32'][1]} steps (GB/s on the bf16 algorithmic "
+                                     "bytes)"}
+    finally:
+        torch.set_num_threads(prev)
+    return out
+
+
 def cpu_baseline_cfg2():
     """The reference's torch path (flashdp/core/linear_clip.py:94-104 + layers/linear.py:72-80),
     restated in oracle/torch_ref.py, on every core this process may use: the full cfg2
@@ -564,6 +632,8 @@ def main():
                                              "tflops": round(F / t_nar / 1e9, 2)}
         extra.update(extra_measurements(dev, max(5, args.steps // 5), 3))
         extra["cfg5_training"] = cfg5_training(dev)
+        if not args.no_cpu_baseline:
+            extra.update(cpu_baselines_cfg3_cfg4())
         out["extra"] = extra
     out["device"] = torch.cuda.get_device_name(dev)
     print(json.dumps(out), flush=True)
