@@ -429,6 +429,24 @@ def dx_overlap(dev, steps, warmup):
             "serial_ms": round(t_ser, 4), "dx_on_second_stream_ms": round(t_ovl, 4)}
 
 
+def library_gemms_cfg2(dev, steps, warmup):
+    """The same products through hipBLASLt (torch): the non-DP weight gradient
+    of the cfg2 layer (one GEMM over all B*T rows, as nn.Linear's backward
+    forms it) and the per-sample products materialised by one batched GEMM
+    (bmm, no norm, clip or sum).  Both have the clipped kernel's FLOP count."""
+    x, go, _ = cfg2_inputs(dev)
+    B, T, O = go.shape
+    I = x.shape[2]
+    g2, x2 = go.reshape(B * T, O), x.reshape(B * T, I)
+    gt = go.transpose(1, 2).contiguous()  # [B, O, T]
+    F = 2.0 * B * T * I * O
+    t_mm = median_cuda_time(lambda: g2.t() @ x2, steps, warmup, reps=3)
+    t_bmm = median_cuda_time(lambda: torch.bmm(gt, x), steps, warmup, reps=3)
+    return {"non_dp_weight_grad_mm": {"ms": round(t_mm, 4), "tflops": round(F / t_mm / 1e9, 2)},
+            "per_sample_bmm_unclipped": {"ms": round(t_bmm, 4),
+                                         "tflops": round(F / t_bmm / 1e9, 2)}}
+
+
 def extra_measurements(dev, steps, warmup):
     import torch.nn as nn
     from flashdp4review_amd import DPLayerNorm, DPLinear
@@ -630,6 +648,7 @@ def main():
         t_nar = median_cuda_time(step_narrow, args.steps, 3, reps=3)
         extra["cfg2_step_grouped_kernel"] = {"ms": round(t_nar, 4),
                                              "tflops": round(F / t_nar / 1e9, 2)}
+        extra["cfg2_library_gemms"] = library_gemms_cfg2(dev, max(5, args.steps // 5), 3)
         extra.update(extra_measurements(dev, max(5, args.steps // 5), 3))
         extra["cfg5_training"] = cfg5_training(dev)
         if not args.no_cpu_baseline:

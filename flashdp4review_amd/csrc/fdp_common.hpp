@@ -36,6 +36,12 @@ struct BF16 {
   __device__ static inline uint16_t from_f32(float f) {
     return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
   }
+  // lo | hi << 16, both rounded as from_f32, in one v_cvt_pk_bf16_f32
+  __device__ static inline uint32_t pack2(float lo, float hi) {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 h2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2{lo, hi}), h2));
+  }
 };
 struct F16 {
   using storage = uint16_t;
@@ -45,6 +51,9 @@ struct F16 {
   }
   __device__ static inline uint16_t from_f32(float f) {
     return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+  }
+  __device__ static inline uint32_t pack2(float lo, float hi) {
+    return uint32_t(from_f32(lo)) | (uint32_t(from_f32(hi)) << 16);
   }
 };
 

@@ -645,8 +645,7 @@ __device__ inline void store_row(typename DT::storage* row, int64_t H, int lane,
     if constexpr (VEC == 8) {  // 16-bit
       u32x4 o;
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        o[j] = DT::from_f32(v[i * 8 + 2 * j]) | (uint32_t(DT::from_f32(v[i * 8 + 2 * j + 1])) << 16);
+      for (int j = 0; j < 4; ++j) o[j] = DT::pack2(v[i * 8 + 2 * j], v[i * 8 + 2 * j + 1]);
       __builtin_amdgcn_raw_buffer_store_b128(o, r, off, 0, 0);
     } else if constexpr (VEC == 4) {  // fp32
       u32x4 o;
@@ -783,21 +782,24 @@ __device__ inline void ln_bwd_chunk(const typename DT::storage* dy,
         rg[j].load(dy + rn * H, H, lid, more);
         mu_n[j] = mean[rn];
         rs_n[j] = rstd[rn];
+        // Elements past H read dy = 0 and w = 0 (x_hat stays finite), so they
+        // add nothing to s1, s2, P and Q, and their dx stores are dropped: no
+        // per-element range test.  Rows past t1 read zeros and skip the sums.
         float s1 = 0.f, s2 = 0.f;
+        float wdy[EPL];
+#pragma unroll
+        for (int k = 0; k < EPL; ++k) {
+          xv[k] = (xv[k] - mu) * rs;  // x_hat
+          wdy[k] = wv[k] * gv[k];
+        }
         if (valid) {
 #pragma unroll
-          for (int i = 0; i < EPL / VEC; ++i)
-#pragma unroll
-            for (int jj = 0; jj < VEC; ++jj) {
-              const int k = i * VEC + jj;
-              const bool in = wave_elem<EPL, VEC, L>(lid, i) + jj < static_cast<int>(H);
-              xv[k] = in ? (xv[k] - mu) * rs : 0.f;  // x_hat
-              const float wdy = wv[k] * gv[k];
-              s1 += xv[k] * wdy;
-              s2 += wdy;
-              P[k] += gv[k] * xv[k];
-              Q[k] += gv[k];
-            }
+          for (int k = 0; k < EPL; ++k) {
+            s1 = fmaf(xv[k], wdy[k], s1);
+            s2 += wdy[k];
+            P[k] = fmaf(gv[k], xv[k], P[k]);
+            Q[k] += gv[k];
+          }
           s1 = wave_sum_dpp(s1);
           s2 = wave_sum_dpp(s2);
         }
@@ -815,9 +817,10 @@ __device__ inline void ln_bwd_chunk(const typename DT::storage* dy,
             s2 += red[par][g][q][1];
           }
         }
-        const float c1 = s1 * inv_h, c2 = s2 * inv_h;
+        // dx = rs (w dy - x_hat c1 - c2), c1 = s1 / H, c2 = s2 / H
+        const float b1 = -rs * (s1 * inv_h), b2 = -rs * (s2 * inv_h);
 #pragma unroll
-        for (int k = 0; k < EPL; ++k) gv[k] = (wv[k] * gv[k] - (xv[k] * c1 + c2)) * rs;
+        for (int k = 0; k < EPL; ++k) gv[k] = fmaf(rs, wdy[k], fmaf(xv[k], b1, b2));
         store_row<DT, EPL, VEC, L>(dx + r * H, H, lid, gv, valid);
       }
     }
