@@ -500,8 +500,7 @@ struct Held<true> {  // 64 fp32 accumulators -> 32 bf16 pairs (RNE)
       for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int q = 0; q < 8; ++q)
-          v[i][j][q] = uint32_t(BF16::from_f32(acc[i][j][2 * q])) |
-                       (uint32_t(BF16::from_f32(acc[i][j][2 * q + 1])) << 16);
+          v[i][j][q] = BF16::pack2(acc[i][j][2 * q], acc[i][j][2 * q + 1]);
   }
   __device__ __forceinline__ void add_to(f32x16 (&tot)[2][2], float c) const {
 #pragma unroll
@@ -830,8 +829,7 @@ __device__ inline void hand_over(const float* slot, const f32x16 (&acc)[2][2]) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int r = 8 * half + 2 * e;
-          w[e] = uint32_t(BF16::from_f32(acc[i][j][r])) |
-                 (uint32_t(BF16::from_f32(acc[i][j][r + 1])) << 16);
+          w[e] = BF16::pack2(acc[i][j][r], acc[i][j][r + 1]);
         }
         sp.store4(static_cast<uint32_t>((q * NT + threadIdx.x) * 16), __builtin_bit_cast(f32x4, w));
       }
@@ -1139,7 +1137,7 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
       u32x4 w;
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        w[e] = uint32_t(BF16::from_f32(src[2 * e])) | (uint32_t(BF16::from_f32(src[2 * e + 1])) << 16);
+        w[e] = BF16::pack2(src[2 * e], src[2 * e + 1]);
       mine.store4(static_cast<uint32_t>((r * BN + col) * 2), __builtin_bit_cast(f32x4, w));
     }
     wait_stores();

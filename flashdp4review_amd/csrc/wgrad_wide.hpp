@@ -358,8 +358,7 @@ __global__ __launch_bounds__(kWideThreads, 1) void wgrad_wide_kernel(WideArgs p)
           u32x4 w;
 #pragma unroll
           for (int e = 0; e < 4; ++e)
-            w[e] = uint32_t(BF16::from_f32(acc[i][j][8 * h + 2 * e])) |
-                   (uint32_t(BF16::from_f32(acc[i][j][8 * h + 2 * e + 1])) << 16);
+            w[e] = BF16::pack2(acc[i][j][8 * h + 2 * e], acc[i][j][8 * h + 2 * e + 1]);
           if (bid < rb0 || bid >= rb1) {
             slot.store4(static_cast<uint32_t>((slot_block(bid, rb0, rb1) * 2 + h) * 1024 + lane * 16),
                         __builtin_bit_cast(f32x4, w));
