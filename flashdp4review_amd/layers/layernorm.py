@@ -6,6 +6,8 @@ HIP LayerNorm kernels (fdp_layernorm_fwd / fdp_layernorm_bwd_clip).  Backward:
   P_b = sum_t g_bt * x_hat_bt,  Q_b = sum_t g_bt                 (per sample b)
   dgamma = (1/B) sum_b clip(||P_b||) P_b + (sigma/sqrt(B)) z_gamma
   dbeta  = (1/B) sum_b clip(||Q_b||) Q_b + (sigma/sqrt(B)) z_beta
+(sigma/sqrt(B) is the reference's noise std; set_noise_convention("dpsgd")
+selects sigma*C/B.)
 The reference's default fused backward instead clamps lock-group partial sums
 element-wise (flashdp/core/layernorm_clip.py:118-127) and its non-fused
 backward adds both noise draws to dgamma (flashdp/layers/layernorm.py:140-155);
@@ -99,7 +101,7 @@ class _DPLayerNormFunction(Function):
         C, clamp_value, sigma, gen, nstream = ctx.cfg
         H = x.shape[-1]
         B = x.shape[0] if x.dim() > 1 else 1
-        std = noise_std(sigma, B)
+        std = noise_std(sigma, B, C)
         need_dw = w is not None and ctx.needs_input_grad[1]
         need_db = ctx.has_bias and ctx.needs_input_grad[2]
         zw = zb = key = None

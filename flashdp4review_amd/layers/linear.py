@@ -4,6 +4,8 @@ Reference: flashdp/layers/linear.py:11-106.  Backward math (per parameter tensor
   dX = g W                                                       (unclipped)
   dW = (1/B) sum_b clip(||g_b^T x_b||_F) g_b^T x_b + (sigma/sqrt(B)) z_W
   db = (1/(B*T)) sum_b clip(||g_b||_F) sum_t g_bt  + (sigma/sqrt(B)) z_b
+(sigma/sqrt(B) is the reference's noise std; set_noise_convention("dpsgd")
+selects sigma*C/B.)
 with clip(n) = min(clamp_value, C/(n + 1e-10)).  dW and db run as one HIP call
 (fdp_wgrad_bias_clip; fdp_wgrad_clip / fdp_colsum_clip when only one of them
 is needed): norm, clip, 1/B and noise add happen on the device, and
@@ -75,7 +77,7 @@ class _DPLinearFunction(Function):
         C, clamp_value, sigma, gen, nstream = ctx.cfg
         x3, g3 = as_btf(input), as_btf(grad_output)
         B, T = x3.shape[0], x3.shape[1]
-        std = noise_std(sigma, B)
+        std = noise_std(sigma, B, C)
         stats = {} if ctx.module is not None else None
         grad_input = grad_weight = grad_bias = None
         if ctx.needs_input_grad[0]:

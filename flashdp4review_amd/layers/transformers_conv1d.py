@@ -8,6 +8,8 @@ so that dX and dW see the scaled grad_output.  Here:
   dX = g W^T                                                     (unclipped)
   dW = (1/B) sum_b clip(||x_b^T g_b||_F) x_b^T g_b + (sigma/sqrt(B)) z_W
   db = (1/(B*T)) sum_b clip(||g_b||_F) sum_t g_bt  + (sigma/sqrt(B)) z_b
+(sigma/sqrt(B) is the reference's noise std; set_noise_convention("dpsgd")
+selects sigma*C/B.)
 so DPConv1D(W) computes exactly DPLinear(W^T)'s gradients, transposed.
 """
 from __future__ import annotations
@@ -87,7 +89,7 @@ class _DPConv1DFunction(Function):
         C, clamp_value, sigma, gen, nstream = ctx.cfg
         x3, g3 = as_btf(input), as_btf(grad_output)
         B, T = x3.shape[0], x3.shape[1]
-        std = noise_std(sigma, B)
+        std = noise_std(sigma, B, C)
         stats = {} if ctx.module is not None else None
         grad_input = grad_weight = grad_bias = None
         if ctx.needs_input_grad[0]:

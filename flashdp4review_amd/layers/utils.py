@@ -35,9 +35,35 @@ def as_btf(t: torch.Tensor) -> torch.Tensor:
     return t
 
 
-def noise_std(noise_multiplier: float, batch: int) -> float:
-    """Standard deviation of the Gaussian noise: noise_multiplier / sqrt(B), added
-    after the 1/B average (flashdp/layers/linear.py:74-80)."""
+# Standard deviation of the noise the DP layers add after the 1/B average:
+#   "reference": noise_multiplier / sqrt(B), what the reference draws
+#                (flashdp/layers/linear.py:74-80, layers/layernorm.py:140-155);
+#                the default;
+#   "dpsgd":     noise_multiplier * C / B, i.e. (sum_b clip(G_b) + N(0, (sigma C)^2)) / B,
+#                the Gaussian mechanism of DP-SGD (Abadi et al., 2016).
+NOISE_CONVENTIONS = ("reference", "dpsgd")
+_noise_convention = "reference"
+
+
+def set_noise_convention(name: str) -> None:
+    """Select the noise standard deviation of every DP layer's backward (process-wide):
+    "reference" (sigma / sqrt(B), the default) or "dpsgd" (sigma * C / B)."""
+    global _noise_convention
+    if name not in NOISE_CONVENTIONS:
+        raise ValueError(f"noise convention must be one of {NOISE_CONVENTIONS}, got {name!r}")
+    _noise_convention = name
+
+
+def get_noise_convention() -> str:
+    return _noise_convention
+
+
+def noise_std(noise_multiplier: float, batch: int, C: float = 1.0) -> float:
+    """Standard deviation of the Gaussian noise added after the 1/B average under
+    the selected convention: noise_multiplier / sqrt(B) ("reference",
+    flashdp/layers/linear.py:74-80) or noise_multiplier * C / B ("dpsgd")."""
+    if _noise_convention == "dpsgd":
+        return float(noise_multiplier) * float(C) / batch
     return float(noise_multiplier) / math.sqrt(batch)
 
 

@@ -142,6 +142,39 @@ def test_dplayernorm(dtype, use_fused, H):
     assert_elementwise(ln.last_stats["norms_b"], ref["norms_b"], dtype, "beta norms")
 
 
+def test_dpsgd_noise_convention():
+    """set_noise_convention("dpsgd"): the layers add noise of std sigma*C/B (DP-SGD's
+    (sum_b clip(G_b) + N(0, (sigma C)^2)) / B) instead of sigma/sqrt(B); checked against
+    the oracle drawing sigma' / sqrt(B) with sigma' = sigma*C/sqrt(B)."""
+    import flashdp4review_amd as fdp
+    B, T, C, sigma = 4, 16, 0.5, 1.3
+    torch.manual_seed(3)
+    lin = DPLinear(256, 128, bias=True, C=C, noise_multiplier=sigma).to(DEV)
+    lin.noise_generator = torch.Generator(device=DEV).manual_seed(99)
+    ln = DPLayerNorm(256, C=C, noise_multiplier=sigma).to(DEV)
+    ln.noise_generator = torch.Generator(device=DEV).manual_seed(98)
+    x = torch.randn(B, T, 256, device=DEV, requires_grad=True)
+    g = torch.randn(B, T, 128, device=DEV) * 0.01
+    xl = torch.randn(B, T, 256, device=DEV, requires_grad=True)
+    gl = torch.randn(B, T, 256, device=DEV) * 0.01
+    fdp.set_noise_convention("dpsgd")
+    try:
+        lin(x).backward(g)
+        ln(xl).backward(gl)
+    finally:
+        fdp.set_noise_convention("reference")
+    s_eq = sigma * C / math.sqrt(B)
+    zw, zb = draws(99, [(128, 256), (128,)], torch.float32)
+    ref = O.linear_backward(x.detach(), g, lin.weight.detach(), C, 1.0, s_eq, zw, zb)
+    assert_close(lin.weight.grad, ref["dw"], torch.float32, "dpsgd noise: dW")
+    assert_close(lin.bias.grad, ref["db"], torch.float32, "dpsgd noise: db")
+    zg, zbe = draws(98, [(256,), (256,)], torch.float32)
+    refl = O.layernorm_bwd_clip(gl, xl.detach(), ln.weight.detach(), 1e-5, C=C,
+                                noise_multiplier=s_eq, z_w=zg, z_b=zbe)
+    assert_close(ln.weight.grad, refl["dw"], torch.float32, "dpsgd noise: dgamma")
+    assert_close(ln.bias.grad, refl["db"], torch.float32, "dpsgd noise: dbeta")
+
+
 def test_wrapped_mlp_trains():
     """A wrapped 2-layer MLP with LayerNorm steps under Adam and its loss decreases
     with sigma = 0 (sanity of the whole backward wiring)."""

@@ -162,6 +162,21 @@ def test_helpers():
     assert as_btf(torch.zeros(3, 5)).shape == (3, 1, 5)
     assert as_btf(torch.zeros(3, 2, 4, 5)).shape == (3, 8, 5)
     assert noise_std(1.0, 4) == 0.5
+    assert noise_std(1.0, 4, C=3.0) == 0.5  # the reference's convention ignores C
+
+
+def test_noise_convention():
+    """sigma / sqrt(B) by default (flashdp/layers/linear.py:74-80); sigma * C / B opt-in."""
+    assert fdp.get_noise_convention() == "reference"
+    try:
+        fdp.set_noise_convention("dpsgd")
+        assert noise_std(2.0, 8, C=0.5) == 2.0 * 0.5 / 8
+        with pytest.raises(ValueError):
+            fdp.set_noise_convention("textbook")
+        assert fdp.get_noise_convention() == "dpsgd"
+    finally:
+        fdp.set_noise_convention("reference")
+    assert noise_std(2.0, 8, C=0.5) == 2.0 / 8 ** 0.5
     assert clip_args_of(torch.tensor([2.0, 0.5]), torch.device("cuda", 0))[:2] == (2.0, 0.5)
     assert clip_args_of((3, 1), torch.device("cpu")) == (3.0, 1.0, None)
     with pytest.raises(ValueError):
