@@ -331,7 +331,11 @@ struct NoFragHook {
 // double-buffered in registers: the LDS reads of k-step s+1 (the next k-tile's
 // first step at a k-tile's end, after its wait and barrier) are issued before
 // the MFMAs of step s, and scheduling groups interleave one MFMA with the DS
-// reads of the next step.  KS must be even (fragment buffers alternate).
+// reads of the next step.  The refill of the stage a k-tile frees (k-tile
+// kt + S) is issued after that k-tile's last MFMAs rather than right after
+// the barrier: the waves leave the barrier straight into matrix work (on the
+// wide kernel's cfg2 call 57.1-57.5 against 59.8-59.9 us per call).  KS must
+// be even (fragment buffers alternate).
 // hook(kt) runs at the start of every k-tile kt: VALU work placed there
 // (reading no memory) overlaps the matrix cores' work of the other wave of
 // the SIMD.  fhook(kt, ks, frags) runs after the MFMAs of k-step ks are
@@ -368,7 +372,6 @@ __device__ inline void gemm_pipe(const Job<G>& job, int nk, const FragOffsets<G>
             const int ahead = nk - 2 - kt;
             wait_tiles<G::LOADS>(ahead < S - 2 ? ahead : S - 2);
             barrier();
-            if (kt + S < nk) job.issue(st.get(s), kt + S);
             f[cur ^ 1].load(st.get((s + 1) % S), fo, 0);
           }
 #pragma unroll
@@ -382,6 +385,8 @@ __device__ inline void gemm_pipe(const Job<G>& job, int nk, const FragOffsets<G>
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);    // one MFMA
             __builtin_amdgcn_sched_group_barrier(0x100, per, 0);  // then DS reads
           }
+          // the freed stage's refill goes out behind this step's MFMAs
+          if (ks + 1 == G::KS && kt + S < nk) job.issue(st.get(s), kt + S);
           fhook(kt, ks, f[cur]);
         }
       }
