@@ -268,6 +268,21 @@ def test_wgrad_stream_two_pass(shape, dtype):
     assert_close(out2, ref2, dtype, "out (scale, noise)")
 
 
+def test_wgrad_stream_zero_factors():
+    """C = 0 makes every clip factor 0: the streamed clipped sum loads zeros for
+    each sample and the output is exactly out_scale * 0 + noise_scale * z."""
+    B, K, M, N = 3, 64, 4096, 1536
+    a, b = make(B, K, M, N, torch.bfloat16, "tn", seed=33)
+    noise = torch.randn(M, N, generator=torch.Generator().manual_seed(6)).to(DEV)
+    out, norms, fac = core.wgrad_clip(a, b, 0.0, 1.0, out_scale=0.5, noise=noise, noise_scale=0.25,
+                                      out_dtype=torch.float32, return_stats=True, two_pass=True,
+                                      check=True)
+    assert torch.all(fac == 0)
+    assert torch.equal(out, 0.25 * noise)
+    _, norms_ref, _ = O.wgrad_clip(a, b, 1.0, 1.0, "tn")
+    assert_elementwise(norms, norms_ref, torch.bfloat16, "norms")
+
+
 def test_wgrad_workspace_reused_across_shapes():
     """Consecutive calls of different shapes share the cached per-stream workspace;
     each shape lays it out differently (one call's partial norms sit where the
