@@ -18,11 +18,20 @@ import torch
 from .. import _lib
 from .clip_fn import clip_args_of
 
-# Rows of up to 4096 elements take one wavefront each, longer ones 16
-# wavefronts (16 elements per thread).  The reference's fused kernel accepts
-# rows of up to 64 KB (flashdp/core/layernorm_clip.py:217-221): the same
-# 16384 elements in fp32, up to 32768 in 16-bit dtypes.
-MAX_HIDDEN = 16384
+# Rows of up to 4096 elements take one wavefront each, up to 16384 a
+# 1024-thread workgroup each (16 elements per thread); longer rows are swept in
+# segments, so the kernels take rows of any length.  The reference's fused
+# kernels stop at rows of 64 KB (flashdp/core/layernorm_clip.py:217-221) and its
+# non-fused layer has no limit (flashdp/layers/layernorm.py:77-96): the
+# fused-mode entry points keep that limit and its error.
+FUSED_MAX_ROW_BYTES = 65536
+
+
+def check_fused_row(x: torch.Tensor) -> None:
+    """The reference's fused-mode limit: RuntimeError for rows of more than
+    64 KB (flashdp/core/layernorm_clip.py:217-221)."""
+    if x.shape[-1] * x.element_size() > FUSED_MAX_ROW_BYTES:
+        raise RuntimeError("This layer norm doesn't support feature dim >= 64KB.")
 
 
 def _rows(x: torch.Tensor, H: int) -> int:
@@ -34,8 +43,6 @@ def layernorm_fwd(x: torch.Tensor, weight: torch.Tensor | None, bias: torch.Tens
     """y, mean [rows] fp32, rstd [rows] fp32 over the last axis."""
     dev = _lib.require_hip(x, weight, bias)
     H = x.shape[-1]
-    if H > MAX_HIDDEN:
-        raise RuntimeError(f"This layer norm doesn't support feature dim > {MAX_HIDDEN}.")
     x = x.contiguous()
     rows = _rows(x, H)
     dt = _lib.dtype_code(x.dtype)
@@ -72,8 +79,6 @@ def layernorm_bwd_clip(grad_output: torch.Tensor, x: torch.Tensor, weight: torch
     (dgamma's per-sample values first, then dbeta's)."""
     dev = _lib.require_hip(grad_output, x, weight, mean, rstd, noise_w, noise_b)
     H = x.shape[-1]
-    if H > MAX_HIDDEN:
-        raise RuntimeError(f"This layer norm doesn't support feature dim > {MAX_HIDDEN}.")
     if grad_output.shape != x.shape:
         raise ValueError("grad_output and input shapes differ")
     B = x.shape[0] if x.dim() > 1 else 1
@@ -120,6 +125,7 @@ def layernorm_bwd_clip(grad_output: torch.Tensor, x: torch.Tensor, weight: torch
 # ------------------------------------------------------------ reference names
 def layernorm_fwd_fused(input: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, eps: float):
     """(y, {'mean','rstd'}, {'BLOCK_SIZE','num_warps','eps'})  (layernorm_clip.py:201-239)."""
+    check_fused_row(input)
     H = input.shape[-1]
     y, mean, rstd = layernorm_fwd(input, weight, bias, eps)
     block = 1 << max(0, (H - 1).bit_length())

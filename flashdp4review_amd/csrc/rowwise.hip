@@ -79,7 +79,7 @@ struct Vec<F32, 4> {  // 4 x fp32 = 16 bytes
 // v = lane + LANES*i covers elements v*VEC .. v*VEC+VEC-1.
 template <int EPL, int VEC, int LANES = 64>
 __device__ __forceinline__ int wave_elem(int lane, int i) {
-  return (lane + LANES * i) * VEC;  // < 2^31: rows hold at most 16384 elements
+  return (lane + LANES * i) * VEC;  // < 2^31: a row (or a long row's segment) holds <= 16384
 }
 
 // LDS position of element e of a wave's row in the LayerNorm backward fold.
@@ -577,6 +577,12 @@ struct RawRow;
 template <class DT, int EPL, int LANES>
 struct RawRow<DT, EPL, 8, LANES> {  // 16-bit, 16-byte vectors
   u32x4 q[EPL / 8];
+  // hides the held bytes from the optimiser, so that a later decode is
+  // recomputed instead of an earlier one being kept live
+  __device__ __forceinline__ void opaque() {
+#pragma unroll
+    for (int i = 0; i < EPL / 8; ++i) __asm__ volatile("" : "+v"(q[i]));
+  }
   __device__ __forceinline__ void load(const uint16_t* row, int64_t H, int lane, bool on = true) {
     const auto r = row_rsrc(row, on ? static_cast<uint32_t>(H * 2) : 0u);
 #pragma unroll
@@ -597,6 +603,10 @@ struct RawRow<DT, EPL, 8, LANES> {  // 16-bit, 16-byte vectors
 template <int EPL, int LANES>
 struct RawRow<F32, EPL, 4, LANES> {  // fp32, 16-byte vectors
   u32x4 q[EPL / 4];
+  __device__ __forceinline__ void opaque() {
+#pragma unroll
+    for (int i = 0; i < EPL / 4; ++i) __asm__ volatile("" : "+v"(q[i]));
+  }
   __device__ __forceinline__ void load(const float* row, int64_t H, int lane, bool on = true) {
     const auto r = row_rsrc(row, on ? static_cast<uint32_t>(H * 4) : 0u);
 #pragma unroll
@@ -613,6 +623,10 @@ struct RawRow<F32, EPL, 4, LANES> {  // fp32, 16-byte vectors
 template <class DT, int EPL, int LANES>
 struct RawRow<DT, EPL, 1, LANES> {  // any dtype, element loads (unaligned rows)
   uint32_t q[EPL];
+  __device__ __forceinline__ void opaque() {
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) __asm__ volatile("" : "+v"(q[i]));
+  }
   __device__ __forceinline__ void load(const typename DT::storage* row, int64_t H, int lane,
                                       bool on = true) {
     constexpr int ES = sizeof(typename DT::storage);
@@ -1221,6 +1235,432 @@ __global__ __launch_bounds__(kSplitLanes) void ln_bwd_split_kernel(
     }
 }
 
+// ----------------------------------------------------------- very long rows
+// Rows of more than 16384 elements do not fit the registers of one
+// workgroup, so they are swept in segments of kLongSeg elements (1024
+// threads, 8 each; element e of a segment at wave_elem<8, VEC, 1024>), with
+// the next segment's loads in flight while one is used.  Every sweep adds in
+// a fixed order: per thread over the segments, then wavefronts in order.
+constexpr int kLongLanes = kSplitLanes;
+constexpr int kLongEpt = 8;
+constexpr int64_t kLongSeg = int64_t(kLongLanes) * kLongEpt;
+
+// Workgroup sums of two values, wavefronts added in order through LDS
+// (`red` double-buffered by `par`: consecutive calls alternate it, so one
+// barrier per call suffices).
+template <int NW>
+__device__ __forceinline__ void block_sum2(float& a, float& b, float (&red)[2][2][NW], int par) {
+  a = wave_sum_dpp(a);
+  b = wave_sum_dpp(b);
+  if ((threadIdx.x & 63) == 0) {
+    red[par][0][threadIdx.x >> 6] = a;
+    red[par][1][threadIdx.x >> 6] = b;
+  }
+  __syncthreads();
+  a = 0.f;
+  b = 0.f;
+#pragma unroll
+  for (int q = 0; q < NW; ++q) {
+    a += red[par][0][q];
+    b += red[par][1][q];
+  }
+}
+
+// Segment `sg` of a long row: its first element and its length.
+__device__ __forceinline__ int64_t seg_len(int64_t H, int64_t sg) {
+  const int64_t n = H - sg * kLongSeg;
+  return n < kLongSeg ? n : kLongSeg;
+}
+
+// A parameter vector's segment: the pointer moved to element h0 (NULL stays
+// NULL, load_param then supplies the default).
+__device__ __forceinline__ const void* param_at(const void* p, int dtype, int64_t h0) {
+  if (p == nullptr) return nullptr;
+  return static_cast<const char*>(p) + h0 * (dtype == FDP_F32 ? 4 : 2);
+}
+
+// A long row's parameter segment (hn elements from p; NULL: `dflt`), in the
+// element layout of RawRow<DT, 8, VEC, LANES>: raw buffer loads, so elements
+// past the segment read zero with no clamping and one offset register.
+template <int E, int VEC, int LANES>
+__device__ inline void load_param_seg(const void* p, int dtype, int64_t hn, int lane, float dflt,
+                                      float (&o)[E]) {
+  if (p == nullptr) {
+#pragma unroll
+    for (int i = 0; i < E / VEC; ++i)
+#pragma unroll
+      for (int j = 0; j < VEC; ++j)
+        o[i * VEC + j] = wave_elem<E, VEC, LANES>(lane, i) + j < hn ? dflt : 0.f;
+    return;
+  }
+  const int es = dtype == FDP_F32 ? 4 : 2;
+  const auto r = row_rsrc(p, static_cast<uint32_t>(hn * es));
+  if constexpr (VEC > 1) {
+    // VEC consecutive elements per vector: 16-byte (or, 16-bit with VEC = 4,
+    // 8-byte) loads when the segment is 16-byte aligned.  Rows taken with
+    // VEC > 1 hold a multiple of VEC elements, so no vector straddles the end.
+    if (reinterpret_cast<uintptr_t>(p) % 16 == 0) {
+#pragma unroll
+      for (int i = 0; i < E / VEC; ++i) {
+        const int e0 = wave_elem<E, VEC, LANES>(lane, i);
+        if (dtype == FDP_F32) {
+#pragma unroll
+          for (int v = 0; v < VEC / 4; ++v) {
+            const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(r, (e0 + 4 * v) * 4, 0, 0);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) o[i * VEC + 4 * v + k] = __uint_as_float(q[k]);
+          }
+        } else {
+          uint32_t q[VEC / 2];
+          if constexpr (VEC == 8) {
+            const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(r, e0 * 2, 0, 0);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) q[k] = t[k];
+          } else {
+            const auto t = __builtin_amdgcn_raw_buffer_load_b64(r, e0 * 2, 0, 0);
+            q[0] = t[0];
+            q[1] = t[1];
+          }
+#pragma unroll
+          for (int k = 0; k < VEC / 2; ++k) {
+            const uint16_t lo = static_cast<uint16_t>(q[k] & 0xffffu);
+            const uint16_t hi = static_cast<uint16_t>(q[k] >> 16);
+            o[i * VEC + 2 * k] = dtype == FDP_BF16 ? BF16::to_f32(lo) : F16::to_f32(lo);
+            o[i * VEC + 2 * k + 1] = dtype == FDP_BF16 ? BF16::to_f32(hi) : F16::to_f32(hi);
+          }
+        }
+      }
+      return;
+    }
+  }
+  if (dtype == FDP_F32) {
+#pragma unroll
+    for (int i = 0; i < E / VEC; ++i)
+#pragma unroll
+      for (int j = 0; j < VEC; ++j)
+        o[i * VEC + j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+            r, (wave_elem<E, VEC, LANES>(lane, i) + j) * 4, 0, 0));
+  } else {
+    uint16_t raw[E];
+#pragma unroll
+    for (int i = 0; i < E / VEC; ++i)
+#pragma unroll
+      for (int j = 0; j < VEC; ++j)
+        raw[i * VEC + j] = __builtin_amdgcn_raw_buffer_load_b16(
+            r, (wave_elem<E, VEC, LANES>(lane, i) + j) * 2, 0, 0);
+    if (dtype == FDP_BF16) {
+#pragma unroll
+      for (int k = 0; k < E; ++k) o[k] = BF16::to_f32(raw[k]);
+    } else {
+#pragma unroll
+      for (int k = 0; k < E; ++k) o[k] = F16::to_f32(raw[k]);
+    }
+  }
+}
+
+// The same pointer, opaque to the optimiser: parameter loads through it stay
+// where they are written (once per row, L2 hits) instead of being hoisted out
+// of the row loop, where every segment's gamma and beta would stay live in
+// registers (2 * NS * 8 per thread) and spill.
+__device__ __forceinline__ const void* per_row(const void* p) {
+  __asm__ volatile("" : "+s"(p));
+  return p;
+}
+
+// Forward, grid-stride over rows, one row per 1024-thread workgroup at a time:
+// three sweeps over the row (sum; centred sum of squares; output), the second
+// and third mostly from L2.
+template <class DT, int VEC>
+__global__ __launch_bounds__(kLongLanes) void ln_fwd_long_kernel(
+    const typename DT::storage* x, const void* w, const void* bias, int w_dtype, int64_t rows,
+    int64_t H, float eps, typename DT::storage* y, float* mean, float* rstd) {
+  constexpr int NW = kLongLanes / kWave, E = kLongEpt, L = kLongLanes;
+  __shared__ float red[2][2][NW];
+  const int tid = threadIdx.x;
+  const int64_t nseg = (H + kLongSeg - 1) / kLongSeg;
+  const float inv_h = 1.f / static_cast<float>(H);
+  int par = 0;
+  for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+    const typename DT::storage* xr = x + r * H;
+    RawRow<DT, E, VEC, L> cur, nxt;
+    // sweep 1: the sum (elements past the row read zero)
+    float s = 0.f, unused = 0.f;
+    cur.load(xr, seg_len(H, 0), tid);
+    for (int64_t sg = 0; sg < nseg; ++sg) {
+      const bool more = sg + 1 < nseg;
+      nxt.load(xr + (more ? sg + 1 : sg) * kLongSeg, seg_len(H, more ? sg + 1 : sg), tid, more);
+      float xv[E];
+      cur.decode(xv);
+#pragma unroll
+      for (int k = 0; k < E; ++k) s += xv[k];
+      cur = nxt;
+    }
+    block_sum2<NW>(s, unused, red, par);
+    par ^= 1;
+    const float mu = s * inv_h;
+    // sweep 2: the centred sum of squares, elements past the row masked
+    float q = 0.f;
+    unused = 0.f;
+    cur.load(xr, seg_len(H, 0), tid);
+    for (int64_t sg = 0; sg < nseg; ++sg) {
+      const bool more = sg + 1 < nseg;
+      nxt.load(xr + (more ? sg + 1 : sg) * kLongSeg, seg_len(H, more ? sg + 1 : sg), tid, more);
+      const int64_t hn = seg_len(H, sg);
+      float xv[E];
+      cur.decode(xv);
+#pragma unroll
+      for (int i = 0; i < E / VEC; ++i)
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) {
+          const float d = wave_elem<E, VEC, L>(tid, i) + j < hn ? xv[i * VEC + j] - mu : 0.f;
+          q += d * d;
+        }
+      cur = nxt;
+    }
+    block_sum2<NW>(q, unused, red, par);
+    par ^= 1;
+    const float rs = 1.f / sqrtf(q * inv_h + eps);
+    // sweep 3: y = (x - mu) * rs * w + b
+    cur.load(xr, seg_len(H, 0), tid);
+    for (int64_t sg = 0; sg < nseg; ++sg) {
+      const bool more = sg + 1 < nseg;
+      nxt.load(xr + (more ? sg + 1 : sg) * kLongSeg, seg_len(H, more ? sg + 1 : sg), tid, more);
+      const int64_t h0 = sg * kLongSeg, hn = seg_len(H, sg);
+      float xv[E], wv[E], bv[E], yv[E];
+      load_param_seg<E, VEC, L>(param_at(w, w_dtype, h0), w_dtype, hn, tid, 1.f, wv);
+      load_param_seg<E, VEC, L>(param_at(bias, w_dtype, h0), w_dtype, hn, tid, 0.f, bv);
+      cur.decode(xv);
+#pragma unroll
+      for (int k = 0; k < E; ++k) yv[k] = (xv[k] - mu) * rs * wv[k] + bv[k];
+      store_row<DT, E, VEC, L>(y + r * H + h0, hn, tid, yv);
+      cur = nxt;
+    }
+    if (tid == 0) {
+      if (mean) mean[r] = mu;
+      if (rstd) rstd[r] = rs;
+    }
+  }
+}
+
+// Rows of at most NS segments (NS * 8192 elements): the row's raw bytes are
+// loaded into registers once, every segment's loads in flight together, and
+// the three sweeps read the registers.  Segments past the row load nothing
+// and hold zeros, so the sums are those of ln_fwd_long_kernel.
+template <class DT, int VEC, int NS>
+__global__ __launch_bounds__(kLongLanes) void ln_fwd_held_kernel(
+    const typename DT::storage* x, const void* w, const void* bias, int w_dtype, int64_t rows,
+    int64_t H, float eps, typename DT::storage* y, float* mean, float* rstd) {
+  constexpr int NW = kLongLanes / kWave, E = kLongEpt, L = kLongLanes;
+  __shared__ float red[2][2][NW];
+  const int tid = threadIdx.x;
+  const int nseg = static_cast<int>((H + kLongSeg - 1) / kLongSeg);  // <= NS
+  const float inv_h = 1.f / static_cast<float>(H);
+  int par = 0;
+  for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+    const typename DT::storage* xr = x + r * H;
+    RawRow<DT, E, VEC, L> seg[NS];
+#pragma unroll
+    for (int sg = 0; sg < NS; ++sg) {
+      const bool on = sg < nseg;
+      seg[sg].load(xr + (on ? sg : 0) * kLongSeg, on ? seg_len(H, sg) : 0, tid, on);
+    }
+    float s = 0.f, unused = 0.f;
+#pragma unroll
+    for (int sg = 0; sg < NS; ++sg) {
+      float xv[E];
+      seg[sg].decode(xv);
+#pragma unroll
+      for (int k = 0; k < E; ++k) s += xv[k];
+    }
+    block_sum2<NW>(s, unused, red, par);
+    par ^= 1;
+#pragma unroll
+    for (int sg = 0; sg < NS; ++sg) seg[sg].opaque();
+    const float mu = s * inv_h;
+    float q = 0.f;
+    unused = 0.f;
+#pragma unroll
+    for (int sg = 0; sg < NS; ++sg) {
+      const int64_t hn = sg < nseg ? seg_len(H, sg) : 0;
+      float xv[E];
+      seg[sg].decode(xv);
+#pragma unroll
+      for (int i = 0; i < E / VEC; ++i)
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) {
+          const float d = wave_elem<E, VEC, L>(tid, i) + j < hn ? xv[i * VEC + j] - mu : 0.f;
+          q += d * d;
+        }
+    }
+    block_sum2<NW>(q, unused, red, par);
+    par ^= 1;
+#pragma unroll
+    for (int sg = 0; sg < NS; ++sg) seg[sg].opaque();
+    const float rs = 1.f / sqrtf(q * inv_h + eps);
+    const void* wr = per_row(w);
+    const void* br = per_row(bias);
+#pragma unroll
+    for (int sg = 0; sg < NS; ++sg) {
+      if (sg < nseg) {
+        const int64_t h0 = sg * kLongSeg, hn = seg_len(H, sg);
+        float xv[E], wv[E], bv[E], yv[E];
+        load_param_seg<E, VEC, L>(param_at(wr, w_dtype, h0), w_dtype, hn, tid, 1.f, wv);
+        load_param_seg<E, VEC, L>(param_at(br, w_dtype, h0), w_dtype, hn, tid, 0.f, bv);
+        seg[sg].decode(xv);
+#pragma unroll
+        for (int k = 0; k < E; ++k) yv[k] = (xv[k] - mu) * rs * wv[k] + bv[k];
+        store_row<DT, E, VEC, L>(y + r * H + h0, hn, tid, yv);
+      }
+    }
+    if (tid == 0) {
+      if (mean) mean[r] = mu;
+      if (rstd) rstd[r] = rs;
+    }
+  }
+}
+
+// Backward, first launch: for every row (grid-stride, one row per 1024-thread
+// workgroup at a time) c1 = sum(x_hat w dy) / H and c2 = sum(w dy) / H into
+// cst[r].  Elements past the row read dy = 0 and w = 0, so they add nothing.
+// NS > 0: rows of at most NS segments, every segment of x and dy loaded at
+// once; NS = 0: any row, streamed one segment ahead.
+template <class DT, int VEC, int NS>
+__global__ __launch_bounds__(kLongLanes) void ln_rowstat_long_kernel(
+    const typename DT::storage* dy, const typename DT::storage* x, const void* w, int w_dtype,
+    const float* mean, const float* rstd, int64_t rows, int64_t H, float2* cst) {
+  constexpr int NW = kLongLanes / kWave, E = kLongEpt, L = kLongLanes;
+  __shared__ float red[2][2][NW];
+  const int tid = threadIdx.x;
+  const int64_t nseg = (H + kLongSeg - 1) / kLongSeg;
+  const float inv_h = 1.f / static_cast<float>(H);
+  int par = 0;
+  for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+    const float mu = mean[r], rs = rstd[r];
+    const typename DT::storage* xr = x + r * H;
+    const typename DT::storage* gr = dy + r * H;
+    float s1 = 0.f, s2 = 0.f;
+    const void* wr = per_row(w);
+    // one segment's contribution (elements past the row add nothing)
+    auto add = [&](const RawRow<DT, E, VEC, L>& sx, const RawRow<DT, E, VEC, L>& sgr,
+                   int64_t sg) {
+      float xv[E], gv[E], wv[E];
+      load_param_seg<E, VEC, L>(param_at(wr, w_dtype, sg * kLongSeg), w_dtype, seg_len(H, sg), tid,
+                            1.f, wv);
+      sx.decode(xv);
+      sgr.decode(gv);
+#pragma unroll
+      for (int k = 0; k < E; ++k) {
+        const float wdy = wv[k] * gv[k];
+        s1 = fmaf((xv[k] - mu) * rs, wdy, s1);
+        s2 += wdy;
+      }
+    };
+    if constexpr (NS > 0) {
+      RawRow<DT, E, VEC, L> sx[NS], sg_[NS];
+#pragma unroll
+      for (int sg = 0; sg < NS; ++sg) {
+        const bool on = sg < nseg;
+        const int64_t off = (on ? sg : 0) * kLongSeg, n = on ? seg_len(H, sg) : 0;
+        sx[sg].load(xr + off, n, tid, on);
+        sg_[sg].load(gr + off, n, tid, on);
+      }
+#pragma unroll
+      for (int sg = 0; sg < NS; ++sg)
+        if (sg < nseg) add(sx[sg], sg_[sg], sg);
+    } else {
+      RawRow<DT, E, VEC, L> cx, cg, nx, ng;
+      cx.load(xr, seg_len(H, 0), tid);
+      cg.load(gr, seg_len(H, 0), tid);
+      for (int64_t sg = 0; sg < nseg; ++sg) {
+        const bool more = sg + 1 < nseg;
+        const int64_t sn = more ? sg + 1 : sg;
+        nx.load(xr + sn * kLongSeg, seg_len(H, sn), tid, more);
+        ng.load(gr + sn * kLongSeg, seg_len(H, sn), tid, more);
+        add(cx, cg, sg);
+        cx = nx;
+        cg = ng;
+      }
+    }
+    block_sum2<NW>(s1, s2, red, par);
+    par ^= 1;
+    if (tid == 0) cst[r] = make_float2(s1 * inv_h, s2 * inv_h);
+  }
+}
+
+// Backward, second launch: grid (column blocks, chunks, B).  A 256-thread
+// workgroup owns kColsBlock columns (8 per thread) of one chunk's rows of
+// sample b: it writes their dx and the chunk's partial column sums P and Q
+// in ln_bwd_kernel's layout, with the next row's loads in flight.
+// Workgroup (0,0,0) zeroes the reduction's two tickets.
+constexpr int kColsThreads = 256;
+constexpr int64_t kColsBlock = int64_t(kColsThreads) * kLongEpt;
+
+template <class DT, int VEC>
+__global__ __launch_bounds__(kColsThreads) void ln_bwd_cols_kernel(
+    const typename DT::storage* dy, const typename DT::storage* x, const void* w, int w_dtype,
+    const float* mean, const float* rstd, const float2* cst, int64_t T, int64_t H, int64_t rows,
+    int chunks, typename DT::storage* dx, float* partials, int64_t B, unsigned* tickets) {
+  constexpr int E = kLongEpt, L = kColsThreads;
+  if (blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0 && threadIdx.x < 2)
+    __hip_atomic_store(tickets + threadIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const int tid = threadIdx.x;
+  const int64_t h0 = int64_t(blockIdx.x) * kColsBlock;
+  const int64_t hn = H - h0 < kColsBlock ? H - h0 : kColsBlock;
+  const int chunk = blockIdx.y;
+  const int64_t b = blockIdx.z;
+  const int64_t t0 = int64_t(chunk) * rows;
+  const int64_t t1 = t0 + rows < T ? t0 + rows : T;
+  float wv[E], P[E], Q[E];
+  load_param_seg<E, VEC, L>(param_at(w, w_dtype, h0), w_dtype, hn, tid, 1.f, wv);
+#pragma unroll
+  for (int k = 0; k < E; ++k) {
+    P[k] = 0.f;
+    Q[k] = 0.f;
+  }
+  if (t1 > t0) {  // (an empty chunk, T = 0, touches no row and no statistic)
+    RawRow<DT, E, VEC, L> rx, rg;
+    int64_t r = b * T + t0;
+    rx.load(x + r * H + h0, hn, tid);
+    rg.load(dy + r * H + h0, hn, tid);
+    float mu_n = mean[r], rs_n = rstd[r];
+    float2 c_n = cst[r];
+    for (int64_t t = t0; t < t1; ++t, ++r) {
+      float xv[E], gv[E];
+      rx.decode(xv);
+      rg.decode(gv);
+      const float mu = mu_n, rs = rs_n, c1 = c_n.x, c2 = c_n.y;
+      const bool more = t + 1 < t1;
+      const int64_t rn = more ? r + 1 : r;
+      rx.load(x + rn * H + h0, hn, tid, more);
+      rg.load(dy + rn * H + h0, hn, tid, more);
+      mu_n = mean[rn];
+      rs_n = rstd[rn];
+      c_n = cst[rn];
+      // dx = rs (w dy - x_hat c1 - c2); columns past H read dy = 0, w = 0
+#pragma unroll
+      for (int k = 0; k < E; ++k) {
+        const float xh = (xv[k] - mu) * rs;
+        P[k] = fmaf(gv[k], xh, P[k]);
+        Q[k] += gv[k];
+        gv[k] = rs * (wv[k] * gv[k] - fmaf(xh, c1, c2));
+      }
+      store_row<DT, E, VEC, L>(dx + r * H + h0, hn, tid, gv);
+    }
+  }
+  float* pP = partials + (b * chunks + chunk) * H + h0;
+  float* pQ = partials + ((B + b) * chunks + chunk) * H + h0;
+#pragma unroll
+  for (int i = 0; i < E / VEC; ++i)
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) {
+      const int e = wave_elem<E, VEC, L>(tid, i) + j;
+      if (e < hn) {
+        pP[e] = P[i * VEC + j];
+        pQ[e] = Q[i * VEC + j];
+      }
+    }
+}
+
 }  // namespace rw
 }  // namespace fdp
 
@@ -1249,9 +1689,11 @@ struct RedPlan {
   bool v4;
   bool one_launch;  // reduce_kernel instead of chunk_sum_kernel + combine_kernel
   bool fused;       // LayerNorm: ln_bwd_fused_kernel (the reduction in the row launch)
+  bool long_rows;   // LayerNorm rows of more than kMaxLnH: ln_rowstat_long + ln_bwd_cols
   int64_t rows;
   size_t off_part, off_frob, off_sums, off_sq, off_ticket, total;
   size_t off_fac;   // fused: clip factors [2B]
+  size_t off_cst;   // long rows: per-row (c1, c2) [B*T]
 };
 
 // Per-stream sums of at most this many elements are combined by one workgroup
@@ -1315,7 +1757,10 @@ struct LnShape {
   int nwr, epl;
 };
 constexpr int64_t kMaxWaveH = 4096;
-constexpr int64_t kMaxLnH = int64_t(kSplitLanes) * 16;
+constexpr int64_t kMaxLnH = int64_t(kSplitLanes) * 16;  // longer rows: the *_long kernels
+// Longest row accepted: per-row offsets and the partials' indices stay in
+// range well beyond it.
+constexpr int64_t kMaxRowH = int64_t(1) << 30;
 
 LnShape ln_shape(int64_t H) {
   if (H <= 512) return {1, 8};
@@ -1372,6 +1817,16 @@ RedPlan ln_plan(int64_t B, int64_t T, int64_t H, int cus) {
       p.total = p.off_ticket + align_up(sizeof(unsigned long long) * size_t(B + 1));
       return p;
     }
+  }
+  if (H > kMaxLnH) {
+    // 2048-column blocks of 256 threads, about eight workgroups per CU
+    p.long_rows = true;
+    p.cblocks = static_cast<int>((H + kColsBlock - 1) / kColsBlock);
+    split_rows(p, B, T, cus, 8, 32);
+    finish_plan(p, B, H, 2);
+    p.off_cst = p.total;
+    p.total += align_up(sizeof(float2) * size_t(B) * size_t(T));
+    return p;
   }
   // rows of more than kMaxWaveH take one 1024-thread workgroup per CU
   split_rows(p, B, T, cus, H > kMaxWaveH ? 1 : 2, 32);
@@ -1482,10 +1937,39 @@ void launch_ln_fwd(LnShape sh, const void* x, const void* w, const void* b, int 
   });
 }
 
+// Rows of more than kMaxLnH elements: one row per 1024-thread workgroup,
+// grid-stride, two workgroups per CU; rows of up to 4 segments held in
+// registers (8 spilled), longer ones swept three times.
+template <class DT, int VEC>
+void launch_ln_fwd_long(const void* x, const void* w, const void* b, int w_dtype, int64_t rows,
+                        int64_t H, float eps, void* y, float* mean, float* rstd, int cus,
+                        hipStream_t s) {
+  using S = typename DT::storage;
+  int64_t grid = int64_t(cus) * 2;
+  if (grid > rows) grid = rows;
+  const int64_t nseg = (H + kLongSeg - 1) / kLongSeg;
+  const dim3 g(static_cast<unsigned>(grid)), t(kLongLanes);
+  const S* xs = static_cast<const S*>(x);
+  S* ys = static_cast<S*>(y);
+  if (nseg <= 4)
+    hipLaunchKernelGGL((ln_fwd_held_kernel<DT, VEC, 4>), g, t, 0, s, xs, w, b, w_dtype, rows, H,
+                       eps, ys, mean, rstd);
+  else
+    hipLaunchKernelGGL((ln_fwd_long_kernel<DT, VEC>), g, t, 0, s, xs, w, b, w_dtype, rows, H, eps,
+                       ys, mean, rstd);
+}
+
 template <class DT>
 void launch_ln_fwd_dt(bool vec, LnShape sh, const void* x, const void* w, const void* b,
                       int w_dtype, int64_t rows, int64_t H, float eps, void* y, float* mean,
                       float* rstd, int cus, hipStream_t s) {
+  if (H > kMaxLnH) {
+    if (!vec) launch_ln_fwd_long<DT, 1>(x, w, b, w_dtype, rows, H, eps, y, mean, rstd, cus, s);
+    else if constexpr (DT::code == FDP_F32)
+      launch_ln_fwd_long<DT, 4>(x, w, b, w_dtype, rows, H, eps, y, mean, rstd, cus, s);
+    else launch_ln_fwd_long<DT, 8>(x, w, b, w_dtype, rows, H, eps, y, mean, rstd, cus, s);
+    return;
+  }
   if (!vec) launch_ln_fwd<DT, 1>(sh, x, w, b, w_dtype, rows, H, eps, y, mean, rstd, cus, s);
   else if constexpr (DT::code == FDP_F32)
     launch_ln_fwd<DT, 4>(sh, x, w, b, w_dtype, rows, H, eps, y, mean, rstd, cus, s);
@@ -1534,6 +2018,47 @@ void launch_ln_bwd_dt(bool vec, LnShape sh, const RedPlan& p, const LnBwdIo& io,
   if (!vec) launch_ln_bwd<DT, 1>(sh, p, io, part, tickets, s);
   else if constexpr (DT::code == FDP_F32) launch_ln_bwd<DT, 4>(sh, p, io, part, tickets, s);
   else launch_ln_bwd<DT, 8>(sh, p, io, part, tickets, s);
+}
+
+// Rows of more than kMaxLnH elements: the per-row statistics (one row per
+// 1024-thread workgroup, two per CU), then the column blocks; launch_reduce
+// follows as for the other two-launch shapes.
+template <class DT, int VEC>
+void launch_ln_bwd_long(const RedPlan& p, const LnBwdIo& io, float2* cst, float* part,
+                        unsigned* tickets, int cus, hipStream_t s) {
+  using S = typename DT::storage;
+  const int64_t rows = io.B * io.T;
+  if (rows > 0) {
+    int64_t grid = int64_t(cus) * 2;
+    if (grid > rows) grid = rows;
+    const dim3 g(static_cast<unsigned>(grid)), t(kLongLanes);
+    const S* dys = static_cast<const S*>(io.dy);
+    const S* xs = static_cast<const S*>(io.x);
+    bool held = false;  // 16-bit rows of at most four segments: x and dy loaded at once
+    if constexpr (VEC == 8) {
+      held = io.H <= 4 * kLongSeg;
+      if (held)
+        hipLaunchKernelGGL((ln_rowstat_long_kernel<DT, VEC, 4>), g, t, 0, s, dys, xs, io.w,
+                           io.w_dtype, io.mean, io.rstd, rows, io.H, cst);
+    }
+    if (!held)
+      hipLaunchKernelGGL((ln_rowstat_long_kernel<DT, VEC, 0>), g, t, 0, s, dys, xs, io.w,
+                         io.w_dtype, io.mean, io.rstd, rows, io.H, cst);
+  }
+  hipLaunchKernelGGL((ln_bwd_cols_kernel<DT, VEC>),
+                     dim3(static_cast<unsigned>(p.cblocks), static_cast<unsigned>(p.chunks),
+                          static_cast<unsigned>(io.B)),
+                     dim3(kColsThreads), 0, s, static_cast<const S*>(io.dy),
+                     static_cast<const S*>(io.x), io.w, io.w_dtype, io.mean, io.rstd, cst, io.T,
+                     io.H, p.rows, p.chunks, static_cast<S*>(io.dx), part, io.B, tickets);
+}
+
+template <class DT>
+void launch_ln_bwd_long_dt(bool vec, const RedPlan& p, const LnBwdIo& io, float2* cst,
+                           float* part, unsigned* tickets, int cus, hipStream_t s) {
+  if (!vec) launch_ln_bwd_long<DT, 1>(p, io, cst, part, tickets, cus, s);
+  else if constexpr (DT::code == FDP_F32) launch_ln_bwd_long<DT, 4>(p, io, cst, part, tickets, cus, s);
+  else launch_ln_bwd_long<DT, 8>(p, io, cst, part, tickets, cus, s);
 }
 
 // One-launch backward (rows of up to 4096 elements).
@@ -1628,7 +2153,7 @@ extern "C" int fdp_layernorm_fwd(const void* x, const void* w, const void* b, in
                                  int64_t H, float eps, int dtype, int w_dtype, void* y,
                                  float* mean, float* rstd, void* stream) {
   if (!valid_dtype(dtype) || !valid_dtype(w_dtype)) return FDP_ERR_DTYPE;
-  if (rows < 0 || H < 1 || H > kMaxLnH) return FDP_ERR_SHAPE;
+  if (rows < 0 || H < 1 || H > kMaxRowH) return FDP_ERR_SHAPE;
   if (rows == 0) return FDP_OK;
   if (x == nullptr || y == nullptr) return FDP_ERR_ARG;
   const bool vec = aligned16(x) && aligned16(y) && (H * esize(dtype)) % 16 == 0;
@@ -1645,7 +2170,7 @@ extern "C" int fdp_layernorm_bwd_clip_workspace_size(int64_t B, int64_t T, int64
                                                      size_t* bytes) {
   if (bytes == nullptr) return FDP_ERR_ARG;
   if (!valid_dtype(dtype)) return FDP_ERR_DTYPE;
-  if (B < 1 || T < 0 || H < 1 || H > kMaxLnH) return FDP_ERR_SHAPE;
+  if (B < 1 || T < 0 || H < 1 || H > kMaxRowH) return FDP_ERR_SHAPE;
   *bytes = ln_plan(B, T, H, num_cus()).total;
   return FDP_OK;
 }
@@ -1659,7 +2184,7 @@ extern "C" int fdp_layernorm_bwd_clip(const void* dy, const void* x, const void*
                                       void* dx, void* dw, void* db, float* norms, float* factors,
                                       void* workspace, size_t workspace_bytes, void* stream) {
   if (!valid_dtype(dtype) || !valid_dtype(w_dtype)) return FDP_ERR_DTYPE;
-  if (B < 1 || T < 0 || H < 1 || H > kMaxLnH) return FDP_ERR_SHAPE;
+  if (B < 1 || T < 0 || H < 1 || H > kMaxRowH) return FDP_ERR_SHAPE;
   if (B > 32767) return FDP_ERR_SHAPE;  // the 2B streams index grid.y
   if (T > 0 && (dy == nullptr || x == nullptr || dx == nullptr || mean == nullptr ||
                 rstd == nullptr))
@@ -1691,9 +2216,18 @@ extern "C" int fdp_layernorm_bwd_clip(const void* dy, const void* x, const void*
     return hipGetLastError() == hipSuccess ? FDP_OK : FDP_ERR_HIP;
   }
   unsigned* tickets = reinterpret_cast<unsigned*>(ws + p.off_ticket);
-  if (dtype == FDP_BF16) launch_ln_bwd_dt<BF16>(vec, sh, p, io, part, tickets, s);
-  else if (dtype == FDP_F16) launch_ln_bwd_dt<F16>(vec, sh, p, io, part, tickets, s);
-  else launch_ln_bwd_dt<F32>(vec, sh, p, io, part, tickets, s);
+  if (p.long_rows) {
+    float2* cst = reinterpret_cast<float2*>(ws + p.off_cst);
+    if (dtype == FDP_BF16) launch_ln_bwd_long_dt<BF16>(vec, p, io, cst, part, tickets, cus, s);
+    else if (dtype == FDP_F16) launch_ln_bwd_long_dt<F16>(vec, p, io, cst, part, tickets, cus, s);
+    else launch_ln_bwd_long_dt<F32>(vec, p, io, cst, part, tickets, cus, s);
+  } else if (dtype == FDP_BF16) {
+    launch_ln_bwd_dt<BF16>(vec, sh, p, io, part, tickets, s);
+  } else if (dtype == FDP_F16) {
+    launch_ln_bwd_dt<F16>(vec, sh, p, io, part, tickets, s);
+  } else {
+    launch_ln_bwd_dt<F32>(vec, sh, p, io, part, tickets, s);
+  }
   const Epilogue e{C,        clamp,
                    clip_args_dev,
                    out_scale, noise_scale,

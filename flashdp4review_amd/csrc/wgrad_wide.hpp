@@ -173,8 +173,6 @@ __global__ __launch_bounds__(kWideThreads, 1) void wgrad_wide_kernel(WideArgs p)
   const int L = logical_wg(hw, p.nwg);
   const int ng = static_cast<int>(p.B);
   const int sample = L / p.tiles, tile = L % p.tiles;
-  // logical workgroup (and exchange slot) of sample gg of this tile
-  auto unit_of = [&](int gg) { return gg * p.tiles + tile; };
   int64_t m0, n0;
   {
     // bands of kBandRows tile rows walked column by column

@@ -12,6 +12,9 @@ The reference's default fused backward instead clamps lock-group partial sums
 element-wise (flashdp/core/layernorm_clip.py:118-127) and its non-fused
 backward adds both noise draws to dgamma (flashdp/layers/layernorm.py:140-155);
 ``use_fused`` is kept and both settings compute the per-sample math above.
+As in the reference, fused mode rejects rows of more than 64 KB
+(flashdp/core/layernorm_clip.py:217-221) and the non-fused mode takes rows of
+any length.
 """
 from __future__ import annotations
 
@@ -23,6 +26,7 @@ import torch.nn as nn
 from torch.autograd.function import Function
 
 from ..core import layernorm_bwd_clip, layernorm_fwd
+from ..core.layernorm import check_fused_row
 from .utils import DPParameter as Parameter
 from .utils import NoiseStream, draw_noise, noise_std
 
@@ -71,6 +75,7 @@ class DPLayerNorm(nn.LayerNorm):
                 raise NotImplementedError(
                     "In fused mode, currently layernorm only support normalized_dim=-1. "
                     "Set use_fused=False to use the default implementation.")
+            check_fused_row(input)
         elif tuple(input.shape[input.dim() - k:]) != self.normalized_shape:
             raise NotImplementedError("normalized_shape must match the trailing input dims")
         return _DPLayerNormFunction.apply(input, self.weight, self.bias, self)

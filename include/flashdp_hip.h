@@ -284,7 +284,8 @@ int fdp_colsum_clip(const void* u, const void* v, int64_t B, int64_t T, int64_t 
  *   y_r = (x_r - mean_r) * rstd_r * w + b
  * Replaces: layernorm_fwd_fused_triton / _layer_norm_fwd_fused
  *           (flashdp/core/layernorm_clip.py:11-60,201-239).
- * x, y     : [rows, H] contiguous, dtype `dtype`.
+ * x, y     : [rows, H] contiguous, dtype `dtype`; 1 <= H <= 2^30 (rows of more
+ *            than 64 KB, which the reference's fused kernel rejects, included).
  * w, b     : [H] of `w_dtype`; either may be NULL (weight 1 / bias 0).
  * mean,rstd: [rows] fp32 (either may be NULL).
  * ---------------------------------------------------------------------- */
@@ -304,7 +305,8 @@ int fdp_layernorm_fwd(const void* x, const void* w, const void* b, int64_t rows,
  *           math of layernorm_dw_clip / layernorm_db_clip
  *           (flashdp/core/layernorm_clip.py:163-198) and one noise draw each
  *           (flashdp/layers/layernorm.py:139-155).
- * dy, x, dx: [B, T, H] contiguous, dtype `dtype` (dx may alias nothing).
+ * dy, x, dx: [B, T, H] contiguous, dtype `dtype` (dx may alias nothing);
+ *            1 <= H <= 2^30.
  * w        : [H] of `w_dtype` or NULL (weight 1).
  * mean,rstd: [B*T] fp32 from fdp_layernorm_fwd.
  * dw, db   : [H] of `w_dtype`; either may be NULL to skip it.

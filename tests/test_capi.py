@@ -117,9 +117,11 @@ def test_workspace_queries():
         _lib.size_query(L.fdp_wgrad_clip_workspace_size, 8, 1024, 3072, 768, 9, 0)
     with pytest.raises(ValueError):
         _lib.size_query(L.fdp_colsum_clip_workspace_size, 0, 4, 4, 2)
-    with pytest.raises(ValueError):  # rows longer than 16 wavefronts hold
-        _lib.size_query(L.fdp_layernorm_bwd_clip_workspace_size, 2, 4, 16385, 2)
+    with pytest.raises(ValueError):  # rows beyond 2^30 elements
+        _lib.size_query(L.fdp_layernorm_bwd_clip_workspace_size, 2, 4, (1 << 30) + 1, 2)
     assert _lib.size_query(L.fdp_layernorm_bwd_clip_workspace_size, 2, 4, 16384, 2) > 0
+    # longer rows also hold the per-row statistics: 8 bytes per row beyond the partials
+    assert _lib.size_query(L.fdp_layernorm_bwd_clip_workspace_size, 2, 4, 40000, 2) >= 2 * 4 * 8
     assert _lib.size_query(L.fdp_layernorm_bwd_clip_workspace_size, 16, 1024, 1024, 2) > 0
 
 
@@ -128,7 +130,9 @@ def test_other_validation_codes():
     st = L.fdp_colsum_clip(1, None, 2, 3, 4, 2, 9, 1.0, 1.0, None, 1.0, None, 0.0, None, 1, 2,
                            None, None, None, 0, None)
     assert st == 3  # bad norm kind
-    st = L.fdp_layernorm_fwd(1, None, None, 4, 16385, 1e-5, 2, 2, 1, None, None, None)
+    # rows beyond 2^30 elements (every shorter row is launched, so no fake pointer below
+    # may carry a valid shape)
+    st = L.fdp_layernorm_fwd(1, None, None, 4, (1 << 30) + 1, 1e-5, 2, 2, 1, None, None, None)
     assert st == 2
     st = L.fdp_layernorm_fwd(1, None, None, 4, 64, 1e-5, 5, 2, 1, None, None, None)
     assert st == 1

@@ -118,11 +118,13 @@ def test_dpconv1d_matches_linear_transposed(dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=str)
-@pytest.mark.parametrize("use_fused,H", [(True, 1024), (False, 1024), (True, 8192)])
+@pytest.mark.parametrize("use_fused,H", [(True, 1024), (False, 1024), (True, 8192),
+                                         (False, 40000)])
 def test_dplayernorm(dtype, use_fused, H):
     """cfg4-style LayerNorm (gamma=1, beta=0) with seeded noise; H=8192 takes
-    the kernels that share a row among wavefronts."""
-    B, T = 4, 128
+    the kernels that share a row among wavefronts, H=40000 (beyond the fused
+    mode's 64 KB rows) the segment-swept ones."""
+    B, T = 4, (128 if H <= 8192 else 16)
     ln = DPLayerNorm(H, use_fused=use_fused, C=1.0, noise_multiplier=1.0).to(DEV, dtype)
     ln.record_stats = True
     ln.noise_generator = torch.Generator(device=DEV).manual_seed(77)

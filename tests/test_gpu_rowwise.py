@@ -57,8 +57,11 @@ def test_bias_ops(dtype):
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=str)
-@pytest.mark.parametrize("H", [1024, 768, 2048, 100, 4096, 8, 4097, 8192, 12000, 16384])
+@pytest.mark.parametrize("H", [1024, 768, 2048, 100, 4096, 8, 4097, 8192, 12000, 16384,
+                               16385, 20480, 32768])
 def test_layernorm_fwd_parity(H, dtype):
+    """Rows above 16384 elements are swept in segments (16385 is unaligned in
+    every dtype and ends in a one-element segment)."""
     x = randn((3, 37, H), dtype, 5)
     w = randn((H,), dtype, 6)
     b = randn((H,), dtype, 7)
@@ -76,7 +79,8 @@ def test_layernorm_fwd_parity(H, dtype):
 @pytest.mark.parametrize("shape", [(16, 1024, 1024), (4, 33, 768), (2, 5, 100), (3, 64, 4096),
                                    (1, 1, 64), (20, 8, 4096), (70, 3, 1000), (3, 9, 1001),
                                    (4, 128, 8192), (2, 40, 16384), (3, 17, 5000), (1, 3, 4100),
-                                   (4, 1024, 512)],
+                                   (4, 1024, 512), (2, 9, 32768), (3, 17, 16385), (5, 8, 20000),
+                                   (2, 70, 40000)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_layernorm_bwd_parity(shape, dtype):
     """Paths: B*H <= 65536 with at most 16 row chunks per sample runs in one
@@ -85,7 +89,10 @@ def test_layernorm_bwd_parity(shape, dtype):
     70x3x1000 (B*H > 65536) the rows, then the two reduction kernels.  Rows of
     1025..4096 elements share a row among 2 or 4 wavefronts; above 4096 among
     16 (8192, 16384, 5000, 4100; 5000 and 4100 leave threads without columns,
-    4100 is also unaligned in 16-bit)."""
+    4100 is also unaligned in 16-bit).  Longer rows take the per-row statistics
+    launch, then 2048-column blocks, then the reduction: one launch for
+    2x9x32768 and 3x17x16385 (unaligned), two for 5x8x20000 and 2x70x40000
+    (three chunks of rows per sample)."""
     B, T, H = shape
     x = randn(shape, dtype, 8)
     w = randn((H,), dtype, 9)
@@ -111,7 +118,8 @@ def test_layernorm_bwd_parity(shape, dtype):
     assert_elementwise(fac[B:], ref["fac_b"], dtype, "factors beta")
 
 
-@pytest.mark.parametrize("shape", [(2, 0, 64), (16, 0, 1024)], ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("shape", [(2, 0, 64), (16, 0, 1024), (2, 0, 20000)],
+                         ids=lambda s: "x".join(map(str, s)))
 def test_layernorm_bwd_empty_rows(shape):
     """T = 0: no row is read, the per-sample sums are zero, so the clip factors
     are min(clamp, C / 1e-10) = clamp and dgamma / dbeta are the noise alone."""

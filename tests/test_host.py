@@ -181,3 +181,24 @@ def test_noise_convention():
     assert clip_args_of((3, 1), torch.device("cpu")) == (3.0, 1.0, None)
     with pytest.raises(ValueError):
         clip_args_of(torch.tensor([1.0, 2.0, 3.0]), torch.device("cpu"))
+
+
+def test_layernorm_fused_row_limit():
+    """Fused mode keeps the reference's limit of 64 KB rows and its error
+    (flashdp/core/layernorm_clip.py:217-221); rows at the limit pass the check
+    (the CPU tensor is then refused for want of the HIP path)."""
+    from flashdp4review_amd.core import layernorm_fwd_fused
+    for H, dtype in [(32769, torch.bfloat16), (16385, torch.float32)]:
+        ln = DPLayerNorm(H, use_fused=True, dtype=dtype)
+        with pytest.raises(RuntimeError, match="64KB"):
+            ln(torch.zeros(1, 2, H, dtype=dtype))
+        with pytest.raises(RuntimeError, match="64KB"):
+            layernorm_fwd_fused(torch.zeros(2, H, dtype=dtype), None, None, 1e-5)
+    for H, dtype in [(32768, torch.bfloat16), (16384, torch.float32)]:
+        with pytest.raises(RuntimeError) as e:
+            DPLayerNorm(H, use_fused=True, dtype=dtype)(torch.zeros(1, 2, H, dtype=dtype))
+        assert "64KB" not in str(e.value)
+    # the non-fused mode has no row limit
+    with pytest.raises(RuntimeError) as e:
+        DPLayerNorm(40000, use_fused=False)(torch.zeros(1, 2, 40000))
+    assert "64KB" not in str(e.value)
