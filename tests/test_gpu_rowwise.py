@@ -118,6 +118,37 @@ def test_layernorm_bwd_parity(shape, dtype):
     assert_elementwise(fac[B:], ref["fac_b"], dtype, "factors beta")
 
 
+@pytest.mark.parametrize("H", [20480, 40000])
+@pytest.mark.parametrize("params", ["fp32", "misaligned"])
+def test_layernorm_long_rows_parameter_layouts(H, params):
+    """Long bf16 rows with fp32 gamma/beta (the autocast layout: 16-byte loads of
+    two 4-element halves) or with gamma/beta starting 2 bytes past an aligned
+    address (element loads); forward and backward against the oracle."""
+    B, T, dtype = 2, 12, torch.bfloat16
+    x = randn((B, T, H), dtype, 31)
+    g = randn((B, T, H), dtype, 32, 0.01)
+    if params == "fp32":
+        w, b = randn((H,), torch.float32, 33), randn((H,), torch.float32, 34)
+    else:
+        w = randn((H + 1,), dtype, 33)[1:]
+        b = randn((H + 1,), dtype, 34)[1:]
+        assert w.data_ptr() % 16 != 0 and b.data_ptr() % 16 != 0
+    y, mean, rstd = core.layernorm_fwd(x, w, b, 1e-5)
+    yr, mr, rr = O.layernorm_fwd(x, w, b, 1e-5)
+    assert_close(y, yr, dtype, "y")
+    assert_elementwise(rstd.reshape(rr.shape), rr, dtype, "rstd")
+    r0 = O.layernorm_bwd_clip(g, x, w, 1e-5, C=1.0, mean=mean, rstd=rstd)
+    C = float(np.median(r0["norms_w"]))
+    dx, dw, db, norms, fac = core.layernorm_bwd_clip(g, x, w, mean, rstd, C, 1.0,
+                                                     noise_scale=0.0, return_stats=True)
+    ref = O.layernorm_bwd_clip(g, x, w, 1e-5, C=C, mean=mean, rstd=rstd)
+    assert_close(dx, ref["dx"], dtype, "dx")
+    assert_close(dw, ref["dw"], dtype, "dgamma")
+    assert_close(db, ref["db"], dtype, "dbeta")
+    assert_elementwise(norms[:B], ref["norms_w"], dtype, "norms gamma")
+    assert_elementwise(fac[B:], ref["fac_b"], dtype, "factors beta")
+
+
 @pytest.mark.parametrize("shape", [(2, 0, 64), (16, 0, 1024), (2, 0, 20000)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_layernorm_bwd_empty_rows(shape):
