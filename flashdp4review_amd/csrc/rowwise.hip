@@ -1266,7 +1266,7 @@ __device__ __forceinline__ void block_sum2(float& a, float& b, float (&red)[2][2
   }
 }
 
-// Segment `sg` of a long row: its first element and its length.
+// Length of segment `sg` of a long row (it starts at element sg * kLongSeg).
 __device__ __forceinline__ int64_t seg_len(int64_t H, int64_t sg) {
   const int64_t n = H - sg * kLongSeg;
   return n < kLongSeg ? n : kLongSeg;
