@@ -149,6 +149,39 @@ def test_layernorm_long_rows_parameter_layouts(H, params):
     assert_elementwise(fac[B:], ref["fac_b"], dtype, "factors beta")
 
 
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+@pytest.mark.parametrize("shape", [(1, 7, 16391), (3, 5, 24577), (2, 6, 32776), (2, 3, 49157),
+                                   (1, 4, 65536), (1, 3, 81921)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_layernorm_long_row_lengths(shape, dtype):
+    """Row lengths around the long-row paths' boundaries: last segments of 1, 7 or
+    8192 elements, rows held in registers (up to 32768) and swept three times
+    (longer), odd lengths that leave 16-bit rows unaligned, and 2048-column
+    blocks ending mid-block; forward and backward against the oracle."""
+    B, T, H = shape
+    x = randn(shape, dtype, 41)
+    g = randn(shape, dtype, 42, 0.01)
+    w, b = randn((H,), dtype, 43), randn((H,), dtype, 44)
+    y, mean, rstd = core.layernorm_fwd(x, w, b, 1e-5)
+    yr, _, rr = O.layernorm_fwd(x, w, b, 1e-5)
+    assert_close(y, yr, dtype, "y")
+    assert_elementwise(rstd.reshape(rr.shape), rr, dtype, "rstd")
+    r0 = O.layernorm_bwd_clip(g, x, w, 1e-5, C=1.0, mean=mean, rstd=rstd)
+    C = float(np.median(r0["norms_w"]))
+    zw = randn((H,), dtype, 45)
+    dx, dw, db, norms, fac = core.layernorm_bwd_clip(g, x, w, mean, rstd, C, 1.0, noise_w=zw,
+                                                     noise_scale=0.3, param_dtype=torch.float32,
+                                                     return_stats=True)
+    ref = O.layernorm_bwd_clip(g, x, w, 1e-5, C=C, noise_multiplier=0.3 * np.sqrt(B), z_w=zw,
+                               z_b=torch.zeros(H), mean=mean, rstd=rstd)
+    assert_close(dx, ref["dx"], dtype, "dx")
+    assert_close(dw, ref["dw"], dtype, "dgamma")
+    assert_close(db, ref["db"], dtype, "dbeta")
+    assert_elementwise(norms[:B], ref["norms_w"], dtype, "norms gamma")
+    assert_elementwise(norms[B:], ref["norms_b"], dtype, "norms beta")
+    assert_elementwise(fac[:B], ref["fac_w"], dtype, "factors gamma")
+
+
 @pytest.mark.parametrize("shape", [(2, 0, 64), (16, 0, 1024), (2, 0, 20000)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_layernorm_bwd_empty_rows(shape):
