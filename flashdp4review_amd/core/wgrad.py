@@ -248,8 +248,8 @@ def wgrad_clip(a: torch.Tensor, b: torch.Tensor, C: float = 1.0, clamp_value: fl
     simple = (clip_args is None and noise is None and out is None and not return_stats
               and not check and bias_noise is None)
     if simple:
-        fkey = (a.shape, a.stride(), b.shape, b.stride(), a.dtype, b.dtype, a.device, layout,
-                out_dtype, noclip, two_pass, launch or _launch_mode, single_pass,
+        fkey = (a.shape, a.stride(), b.shape, b.stride(), a.dtype, b.dtype, a.device, b.device,
+                layout, out_dtype, noclip, two_pass, launch or _launch_mode, single_pass,
                 None if bias_out is None else (bias_out.shape, bias_out.dtype, bias_out.device,
                                                bias_out.is_contiguous()))
         prep = _prepared.get(fkey)
@@ -260,6 +260,7 @@ def wgrad_clip(a: torch.Tensor, b: torch.Tensor, C: float = 1.0, clamp_value: fl
     if a.dtype != b.dtype:
         raise KeyError(f"operand dtypes differ: {a.dtype} vs {b.dtype}")
     dt = _lib.dtype_code(a.dtype)
+    a0, b0 = a, b
     a, b = _inner_contig(a), _inner_contig(b)
     if bias_out is not None:
         if layout != "tn" or noclip:
@@ -350,9 +351,13 @@ def wgrad_clip(a: torch.Tensor, b: torch.Tensor, C: float = 1.0, clamp_value: fl
             _raise_expired(ws, "this call or an earlier one on this stream", status)
     else:
         ws.queue_probe()
-    if simple and a.is_contiguous() and b.is_contiguous() and len(_prepared) < 256:
-        # this call's arguments checked out: later calls of the same signature
-        # (shapes, strides, dtypes, device, options) go straight to the library
+    if (simple and a is a0 and b is b0 and a.is_contiguous() and b.is_contiguous()
+            and len(_prepared) < 256):
+        # this call's arguments checked out and reached the kernel as given (no
+        # copy was made): later calls of the same signature (shapes, strides,
+        # dtypes, devices, options) go straight to the library.  A call that
+        # needed a contiguous copy is never cached, since a later tensor with
+        # the same strides would reach the kernel uncopied.
         _prepared[fkey] = _Prepared(bias_arg is not None, (Bn, K, M, N, a.stride(0), a.stride(1),
                                     b.stride(0), b.stride(1), lay, dt), (M, N), out_dtype, odt,
                                     flags, nbytes, dev)

@@ -653,3 +653,50 @@ def test_wgrad_prepared_call_matches_checked_call():
         W.wgrad_clip(a, b, 0.1, 1.0, bias_out=torch.empty(M - 1, dtype=torch.bfloat16,
                                                           device=DEV), **kw)
     W._prepared.clear()
+
+
+@pytest.mark.parametrize("which", ["a", "b"])
+def test_wgrad_prepared_call_never_caches_a_copied_operand(which):
+    """A call whose operand is a strided view (last axis not unit-stride) runs on a
+    contiguous copy.  Such a call is not recorded for the prepared path, so a
+    second call with an operand of the same shape and strides is checked and
+    copied again instead of reaching the kernel as a raw pointer with the
+    copy's strides.  Both calls match the oracle."""
+    from flashdp4review_amd.core import wgrad as W
+    B, K, M, N = 4, 96, 256, 192
+    a, b = make(B, K, M, N, torch.bfloat16, "tn", seed=41)
+    W._prepared.clear()
+    for rep in range(2):
+        if which == "a":
+            base = a.transpose(1, 2).contiguous()   # [B, M, K]
+            aa, bb = base.transpose(1, 2), b        # a view [B, K, M] with stride(2) = K
+            assert aa.stride(2) != 1
+        else:
+            base = b.transpose(1, 2).contiguous()
+            aa, bb = a, base.transpose(1, 2)
+            assert bb.stride(2) != 1
+        out = W.wgrad_clip(aa, bb, 0.05, 1.0, out_scale=1.0 / B)
+        ref, _, _ = O.wgrad_clip(a, b, 0.05, 1.0, "tn", out_scale=1.0 / B)
+        assert_close(out, ref, torch.bfloat16, f"strided view, call {rep}")
+        assert len(W._prepared) == 0
+    W._prepared.clear()
+
+
+def test_dplinear_strided_input_twice():
+    """DPLinear's backward with an input that is a transposed view, run twice:
+    the second backward matches the oracle like the first."""
+    from flashdp4review_amd import DPLinear
+    from flashdp4review_amd.core import wgrad as W
+    torch.manual_seed(7)
+    W._prepared.clear()
+    lin = DPLinear(192, 256, bias=True, C=0.05, noise_multiplier=0.0).to(DEV, torch.bfloat16)
+    for rep in range(2):
+        base = torch.randn(4, 192, 96, device=DEV).to(torch.bfloat16)
+        x = base.transpose(1, 2).requires_grad_(True)    # [4, 96, 192], stride(2) = 96
+        g = (torch.randn(4, 96, 256, device=DEV) * 0.02).to(torch.bfloat16)
+        lin.weight.grad = lin.bias.grad = None
+        lin(x).backward(g)
+        ref = O.linear_backward(x.detach(), g, lin.weight.detach(), 0.05, 1.0)
+        assert_close(lin.weight.grad, ref["dw"], torch.bfloat16, f"dW, backward {rep}")
+        assert_close(lin.bias.grad, ref["db"], torch.bfloat16, f"db, backward {rep}")
+    W._prepared.clear()
