@@ -214,7 +214,7 @@ def wgrad_clip(a: torch.Tensor, b: torch.Tensor, C: float = 1.0, clamp_value: fl
                launch: str | None = None, single_pass: str = "auto", check: bool = False,
                bias_out: torch.Tensor | None = None, bias_scale: float = 1.0,
                bias_noise: torch.Tensor | None = None, bias_noise_scale: float = 1.0,
-               bias_noise_key: tuple[int, int] | None = None):
+               bias_noise_key: tuple[int, int] | None = None, bias_operand: str = "a"):
     """out = out_scale * sum_b c_b G_b + noise_scale * z, c_b = clip(||G_b||_F).
 
     layout "tn": a [B,K,M], b [B,K,N], G_b = a_b^T b_b;
@@ -237,13 +237,16 @@ def wgrad_clip(a: torch.Tensor, b: torch.Tensor, C: float = 1.0, clamp_value: fl
     behind the call, and the first call after the copy completes raises.  An
     expiry poisons only the launch it happened in (its outputs are NaN).
 
-    ``bias_out`` (an [M] tensor, layout "tn", a contiguous) also writes the
-    bias of a (fdp_wgrad_bias_clip, the DP Linear bias gradient):
-    bias_out[m] = bias_scale * sum_b c'_b sum_k a_b[k, m] + bias_noise_scale * zb[m],
-    c'_b = clip(||a_b||_F) with the same C / clamp; zb is ``bias_noise`` or the
-    draw of ``bias_noise_key``.  The wide kernel forms it in the same launch;
-    other schedules run the column-sum kernel after the weight gradient.  With
-    ``return_stats`` the bias's norms and factors follow the weight's.
+    ``bias_out`` (layout "tn") also writes the bias of one operand
+    (fdp_wgrad_bias_clip): of a (``bias_operand="a"``, an [M] tensor: the DP
+    Linear bias, a = grad_output) or of b (``"b"``, an [N] tensor: the DP
+    Conv1D bias, b = grad_output):
+    bias_out[c] = bias_scale * sum_b c'_b sum_k op_b[k, c] + bias_noise_scale * zb[c],
+    c'_b = clip(||op_b||_F) with the same C / clamp; zb is ``bias_noise`` or the
+    draw of ``bias_noise_key``.  The 16-bit kernels form it from the operand
+    fragments they hold, in the same call; fp32 operands run the column-sum
+    kernel after the weight gradient.  With ``return_stats`` the bias's norms
+    and factors follow the weight's.
     """
     simple = (clip_args is None and noise is None and out is None and not return_stats
               and not check and bias_noise is None)
@@ -251,7 +254,7 @@ def wgrad_clip(a: torch.Tensor, b: torch.Tensor, C: float = 1.0, clamp_value: fl
         fkey = (a.shape, a.stride(), b.shape, b.stride(), a.dtype, b.dtype, a.device, b.device,
                 layout, out_dtype, noclip, two_pass, launch or _launch_mode, single_pass,
                 None if bias_out is None else (bias_out.shape, bias_out.dtype, bias_out.device,
-                                               bias_out.is_contiguous()))
+                                               bias_out.is_contiguous(), bias_operand))
         prep = _prepared.get(fkey)
         if prep is not None:
             return prep.call(a, b, C, clamp_value, out_scale, noise_scale, noise_key, bias_out,
@@ -264,8 +267,13 @@ def wgrad_clip(a: torch.Tensor, b: torch.Tensor, C: float = 1.0, clamp_value: fl
     a, b = _inner_contig(a), _inner_contig(b)
     if bias_out is not None:
         if layout != "tn" or noclip:
-            raise ValueError("the bias of a needs layout 'tn' and a clip")
-        a = a.contiguous()
+            raise ValueError("the bias of an operand needs layout 'tn' and a clip")
+        if bias_operand == "a":
+            a = a.contiguous()
+        elif bias_operand == "b":
+            b = b.contiguous()
+        else:
+            raise ValueError(f"bias_operand must be 'a' or 'b', got {bias_operand!r}")
     if layout == "tn":
         Bn, K, M = a.shape
         lay = _lib.LAYOUT_TN
@@ -299,12 +307,13 @@ def wgrad_clip(a: torch.Tensor, b: torch.Tensor, C: float = 1.0, clamp_value: fl
         norms = None if noclip else torch.empty(Bn, dtype=torch.float32, device=dev)
     bias_arg = bnorms = bfactors = None
     if bias_out is not None:
-        if bias_out.shape != (M,) or not bias_out.is_contiguous():
-            raise ValueError(f"bias_out must be a contiguous [{M}] tensor")
+        blen = M if bias_operand == "a" else N
+        if bias_out.shape != (blen,) or not bias_out.is_contiguous():
+            raise ValueError(f"bias_out must be a contiguous [{blen}] tensor")
         if bias_noise is not None:
-            if bias_noise.numel() != M:
-                raise ValueError(f"bias_noise must have {M} elements")
-            bias_noise = bias_noise.reshape(M).to(bias_out.dtype).contiguous()
+            if bias_noise.numel() != blen:
+                raise ValueError(f"bias_noise must have {blen} elements")
+            bias_noise = bias_noise.reshape(blen).to(bias_out.dtype).contiguous()
         if return_stats:
             bnorms = torch.empty(Bn, dtype=torch.float32, device=dev)
             bfactors = torch.empty(Bn, dtype=torch.float32, device=dev)
@@ -319,7 +328,8 @@ def wgrad_clip(a: torch.Tensor, b: torch.Tensor, C: float = 1.0, clamp_value: fl
         raise ValueError(f"single_pass must be one of {tuple(_SINGLE_PASS)}, got {single_pass!r}")
     flags = ((_lib.WGRAD_NOCLIP if noclip else 0) | (_lib.WGRAD_TWO_PASS if two_pass else 0)
              | (_lib.WGRAD_PLAIN_LAUNCH if mode == "plain" else 0) | _lib.WGRAD_CLEAN_WORKSPACE
-             | _SINGLE_PASS[single_pass])
+             | _SINGLE_PASS[single_pass]
+             | (_lib.WGRAD_BIAS_OF_B if bias_out is not None and bias_operand == "b" else 0))
     L = _lib.lib()
     key = (dev.index, Bn, K, M, N, dt, flags, bias_arg is not None)
     nbytes = _ws_sizes.get(key)

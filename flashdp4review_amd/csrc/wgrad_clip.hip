@@ -410,7 +410,7 @@ int fdp::wgrad_check_args(const void* a, const void* b, int64_t B, int64_t K, in
   if ((K > 0 && (a == nullptr || b == nullptr)) || out == nullptr) return FDP_ERR_ARG;
   if ((flags & ~(FDP_WGRAD_NOCLIP | FDP_WGRAD_TWO_PASS | FDP_WGRAD_PLAIN_LAUNCH |
                  FDP_WGRAD_CLEAN_WORKSPACE | FDP_WGRAD_WIDE | FDP_WGRAD_NARROW)) != 0)
-    return FDP_ERR_ARG;
+    return FDP_ERR_ARG;  // (FDP_WGRAD_BIAS_OF_B only with fdp_wgrad_bias_clip)
   if ((flags & FDP_WGRAD_WIDE) && (flags & FDP_WGRAD_NARROW)) return FDP_ERR_ARG;
   if ((flags & FDP_WGRAD_NOCLIP) != 0 && norms != nullptr) return FDP_ERR_ARG;
   return FDP_OK;
@@ -418,15 +418,18 @@ int fdp::wgrad_check_args(const void* a, const void* b, int64_t B, int64_t K, in
 
 namespace {
 
-// fdp_wgrad_clip; with `bias`, the wide kernel also forms the bias of operand
-// a when it runs (*bias_done = true), and otherwise leaves it to the caller.
+// fdp_wgrad_clip; with `bias`, the 16-bit TN kernels (wide, grouped and
+// streamed) also form the bias of operand a (bias_op 1) or b (bias_op 2) from
+// the fragments they hold, with its partials in bias_part / bias_sq
+// (*bias_done = true); the generic two-pass schedule leaves it to the caller.
 int wgrad_clip_impl(const void* a, const void* b, int64_t B, int64_t K, int64_t M, int64_t N,
                     int64_t stride_ab, int64_t lda, int64_t stride_bb, int64_t ldb, int layout,
                     int dtype, float C, float clamp, const float* clip_args_dev, float out_scale,
                     const void* noise, float noise_scale, const fdp_noise_key* noise_key,
                     void* out, int64_t ldo, int out_dtype, float* norms, float* factors,
                     int flags, void* workspace, size_t workspace_bytes, void* stream,
-                    const fdp_bias_out* bias, bool* bias_done) {
+                    const fdp_bias_out* bias, int bias_op, float* bias_part, float* bias_sq,
+                    bool* bias_done) {
   const int bad = fdp::wgrad_check_args(a, b, B, K, M, N, lda, ldb, layout, dtype, out, ldo,
                                         out_dtype, norms, flags);
   if (bad != FDP_OK) return bad;
@@ -482,6 +485,21 @@ int wgrad_clip_impl(const void* a, const void* b, int64_t B, int64_t K, int64_t 
   args.clip_args_dev = clip_args_dev;
   args.norms_out = norms;
   args.factors_out = factors;
+  if (bias != nullptr) {
+    args.bias_op = bias_op;
+    args.bias_P = bias_op == 1 ? pl.tiles_n : pl.tiles_m;  // the grouped kernel's tiles
+    args.bias_len = bias_op == 1 ? M : N;
+    args.bias_part = bias_part;
+    args.bias_sq = bias_sq;
+    args.bias_out = bias->out;
+    args.bias_dtype = bias->out_dtype;
+    args.bias_scale = bias->out_scale;
+    args.bias_noise = make_noise(bias->noise, bias->out_dtype,
+                                 bias->noise_scale != 0.f ? bias->noise_key : nullptr, 0);
+    args.bias_noise_scale = bias->noise_scale;
+    args.bias_norms = bias->norms;
+    args.bias_factors = bias->factors;
+  }
 
   // 16-byte vector loads need 16-byte aligned rows of every sample.
   const int esz = dtype == FDP_F32 ? 4 : 2;
@@ -529,6 +547,7 @@ int wgrad_clip_impl(const void* a, const void* b, int64_t B, int64_t K, int64_t 
     w.norms_out = norms;
     w.factors_out = factors;
     if (bias != nullptr) {
+      w.bias_op = bias_op;
       w.bias_part = reinterpret_cast<float*>(ws + pl.off_wide_bias_part);
       w.bias_sq = reinterpret_cast<float*>(ws + pl.off_wide_bias_sq);
       w.bias_out = bias->out;
@@ -567,9 +586,17 @@ int wgrad_clip_impl(const void* a, const void* b, int64_t B, int64_t K, int64_t 
       dtype != FDP_F32 && pl.total_fused > 0) {
     const bool plain = (flags & FDP_WGRAD_PLAIN_LAUNCH) != 0;
     const bool clean = (flags & FDP_WGRAD_CLEAN_WORKSPACE) != 0;
-    const hipError_t e = dtype == FDP_BF16 ? launch_grouped_bf16(args, cus, plain, clean, s)
-                                           : launch_grouped_f16(args, cus, plain, clean, s);
-    if (e == hipSuccess) return FDP_OK;
+    hipError_t e;
+    if (bias != nullptr)
+      e = dtype == FDP_BF16 ? launch_grouped_bias_bf16(args, cus, plain, clean, s)
+                            : launch_grouped_bias_f16(args, cus, plain, clean, s);
+    else
+      e = dtype == FDP_BF16 ? launch_grouped_bf16(args, cus, plain, clean, s)
+                            : launch_grouped_f16(args, cus, plain, clean, s);
+    if (e == hipSuccess) {
+      if (bias_done != nullptr) *bias_done = bias != nullptr;
+      return FDP_OK;
+    }
     if (e != hipErrorNotSupported && e != hipErrorCooperativeLaunchTooLarge) {
       (void)hipGetLastError();
       return FDP_ERR_HIP;
@@ -584,8 +611,11 @@ int wgrad_clip_impl(const void* a, const void* b, int64_t B, int64_t K, int64_t 
                                                 factors, fac_ws, s)
                           : launch_stream<F16>(args, pl, noclip, C, clamp, clip_args_dev, norms,
                                                factors, fac_ws, s);
-    return e == hipSuccess ? FDP_OK : FDP_ERR_HIP;
+    if (e != hipSuccess) return FDP_ERR_HIP;
+    if (bias_done != nullptr) *bias_done = bias != nullptr;
+    return FDP_OK;
   }
+  args.bias_op = 0;  // the generic schedule: the caller forms the bias
   if (dtype == FDP_BF16) {
     e = dispatch_layout<Core16<BF16>>(layout, vec, args, pl, noclip, C, clamp, clip_args_dev,
                                       norms, factors, fac_ws, s);
@@ -612,20 +642,52 @@ extern "C" int fdp_wgrad_clip(const void* a, const void* b, int64_t B, int64_t K
   return wgrad_clip_impl(a, b, B, K, M, N, stride_ab, lda, stride_bb, ldb, layout, dtype, C, clamp,
                          clip_args_dev, out_scale, noise, noise_scale, noise_key, out, ldo,
                          out_dtype, norms, factors, flags, workspace, workspace_bytes, stream,
-                         nullptr, nullptr);
+                         nullptr, 0, nullptr, nullptr, nullptr);
 }
 
-// The weight gradient's workspace, then (256-aligned) the column sums' for the
-// bias when the wide kernel does not form it.
+namespace {
+
+// Workspace of fdp_wgrad_bias_clip (every part 256-aligned): the weight
+// gradient's workspace, the column-sum kernel's (the bias when the generic
+// schedule runs), then the bias partials of the grouped and streamed kernels
+// (bias_part [len, B, P], bias_sq [B, tiles], sized for both tile grids).
+struct BiasLayout {
+  size_t wspan, col_off, part_off, sq_off, total;
+};
+int bias_layout(int64_t B, int64_t K, int64_t M, int64_t N, int dtype, int wflags, int bias_op,
+                BiasLayout* l) {
+  size_t w = 0, c = 0;
+  int st = fdp_wgrad_clip_workspace_size(B, K, M, N, dtype, wflags, &w);
+  if (st != FDP_OK) return st;
+  st = fdp_colsum_clip_workspace_size(B, K, bias_op == 1 ? M : N, dtype, &c);
+  if (st != FDP_OK) return st;
+  const int gm = static_cast<int>((M + BM - 1) / BM), gn = static_cast<int>((N + BN - 1) / BN);
+  const StreamPlan sp = stream_plan(B, K, M, N, num_cus());
+  const int64_t P_group = bias_op == 1 ? gn : gm, P_stream = stream_bias_P(sp, bias_op);
+  const int64_t tiles_group = int64_t(gm) * gn, tiles_stream = int64_t(sp.sum_tiles_m) * sp.sum_tiles_n;
+  const int64_t P = P_group > P_stream ? P_group : P_stream;
+  const int64_t tiles = tiles_group > tiles_stream ? tiles_group : tiles_stream;
+  const int64_t len = bias_op == 1 ? M : N;
+  l->wspan = align_up(w);
+  l->col_off = l->wspan;
+  l->part_off = l->col_off + align_up(c);
+  l->sq_off = l->part_off + align_up(sizeof(float) * size_t(len) * size_t(B) * size_t(P));
+  l->total = l->sq_off + sizeof(float) * size_t(B) * size_t(tiles);
+  return FDP_OK;
+}
+
+}  // namespace
+
 extern "C" int fdp_wgrad_bias_clip_workspace_size(int64_t B, int64_t K, int64_t M, int64_t N,
                                                   int dtype, int flags, size_t* bytes) {
   if (bytes == nullptr) return FDP_ERR_ARG;
-  size_t w = 0, c = 0;
-  int st = fdp_wgrad_clip_workspace_size(B, K, M, N, dtype, flags, &w);
+  if (!valid_dtype(dtype)) return FDP_ERR_DTYPE;
+  if (B < 1 || M < 1 || N < 1 || K < 0) return FDP_ERR_SHAPE;
+  const int bias_op = (flags & FDP_WGRAD_BIAS_OF_B) ? 2 : 1;
+  BiasLayout l{};
+  const int st = bias_layout(B, K, M, N, dtype, flags & ~FDP_WGRAD_BIAS_OF_B, bias_op, &l);
   if (st != FDP_OK) return st;
-  st = fdp_colsum_clip_workspace_size(B, K, M, dtype, &c);
-  if (st != FDP_OK) return st;
-  *bytes = align_up(w) + c;
+  *bytes = l.total;
   return FDP_OK;
 }
 
@@ -637,30 +699,34 @@ extern "C" int fdp_wgrad_bias_clip(const void* a, const void* b, int64_t B, int6
                                    int64_t ldo, int out_dtype, float* norms, float* factors,
                                    int flags, const fdp_bias_out* bias, void* workspace,
                                    size_t workspace_bytes, void* stream) {
+  const int bias_op = (flags & FDP_WGRAD_BIAS_OF_B) ? 2 : 1;
+  flags &= ~FDP_WGRAD_BIAS_OF_B;
   const int bad = fdp::wgrad_check_args(a, b, B, K, M, N, lda, ldb, layout, dtype, out, ldo,
                                         out_dtype, norms, flags);
   if (bad != FDP_OK) return bad;
   if (bias == nullptr || bias->out == nullptr) return FDP_ERR_ARG;
   if (!valid_dtype(bias->out_dtype)) return FDP_ERR_DTYPE;
-  // the bias is of a = [B, K, M] over K, contiguous (the column-sum kernel
-  // reads it that way when the wide kernel does not run); the clip is not
+  // the bias operand is [B, K, len] over K, contiguous (the column-sum kernel
+  // reads it that way when the generic schedule runs); the clip is not
   // optional
   if (layout != FDP_LAYOUT_TN || (flags & FDP_WGRAD_NOCLIP) != 0) return FDP_ERR_ARG;
-  if (lda != M || stride_ab != K * M) return FDP_ERR_SHAPE;
-  size_t wbytes = 0, cbytes = 0;
-  int st = fdp_wgrad_clip_workspace_size(B, K, M, N, dtype, flags, &wbytes);
+  if (bias_op == 1 && (lda != M || stride_ab != K * M)) return FDP_ERR_SHAPE;
+  if (bias_op == 2 && (ldb != N || stride_bb != K * N)) return FDP_ERR_SHAPE;
+  BiasLayout l{};
+  int st = bias_layout(B, K, M, N, dtype, flags, bias_op, &l);
   if (st != FDP_OK) return st;
-  st = fdp_colsum_clip_workspace_size(B, K, M, dtype, &cbytes);
-  if (st != FDP_OK) return st;
-  const size_t wspan = align_up(wbytes);
-  if (workspace == nullptr || workspace_bytes < wspan + cbytes) return FDP_ERR_WORKSPACE;
+  if (workspace == nullptr || workspace_bytes < l.total) return FDP_ERR_WORKSPACE;
+  char* ws = static_cast<char*>(workspace);
   bool done = false;
   st = wgrad_clip_impl(a, b, B, K, M, N, stride_ab, lda, stride_bb, ldb, layout, dtype, C, clamp,
                        clip_args_dev, out_scale, noise, noise_scale, noise_key, out, ldo,
-                       out_dtype, norms, factors, flags, workspace, wspan, stream, bias, &done);
+                       out_dtype, norms, factors, flags, workspace, l.wspan, stream, bias, bias_op,
+                       reinterpret_cast<float*>(ws + l.part_off),
+                       reinterpret_cast<float*>(ws + l.sq_off), &done);
   if (st != FDP_OK || done) return st;
-  return fdp_colsum_clip(a, nullptr, B, K, M, dtype, FDP_NORM_FROB, C, clamp, clip_args_dev,
-                         bias->out_scale, bias->noise, bias->noise_scale, bias->noise_key,
-                         bias->out, bias->out_dtype, bias->norms, bias->factors,
-                         static_cast<char*>(workspace) + wspan, workspace_bytes - wspan, stream);
+  return fdp_colsum_clip(bias_op == 1 ? a : b, nullptr, B, K, bias_op == 1 ? M : N, dtype,
+                         FDP_NORM_FROB, C, clamp, clip_args_dev, bias->out_scale, bias->noise,
+                         bias->noise_scale, bias->noise_key, bias->out, bias->out_dtype,
+                         bias->norms, bias->factors, ws + l.col_off, l.part_off - l.col_off,
+                         stream);
 }

@@ -63,6 +63,22 @@ struct Args {
   uint32_t helper_mask[kPermMax / 32];
   unsigned* pair_flag;    // [kPairMax] helper -> owner hand-over flags
   int split_k1;
+  // The bias of operand a (bias_op 1) or b (bias_op 2), formed by the grouped
+  // single-pass and the streamed clipped-sum kernels (see bias_finish):
+  //   bias[c] = bias_scale * sum_b c'_b sum_k op_b[k, c] + bias_noise_scale * zb[c],
+  //   c'_b = clip(||op_b||_F) with the weight's C and clamp.
+  int bias_op;            // 0: no bias
+  int bias_P;             // tiles along the other axis: partials per (column, sample)
+  int64_t bias_len;       // M (bias_op 1) or N (bias_op 2)
+  float* bias_part;       // [bias_len, B, bias_P] column sums over a tile's counted k-tiles
+  float* bias_sq;         // [B, tiles] sums of squares over a tile's counted k-tiles
+  void* bias_out;
+  int bias_dtype;
+  float bias_scale;
+  NoiseSrc bias_noise;
+  float bias_noise_scale;
+  float* bias_norms;      // optional [B]: ||op_b||_F
+  float* bias_factors;    // optional [B]: c'_b
 };
 
 // ------------------------------------------------------------------ 16-bit
@@ -390,6 +406,187 @@ __device__ __forceinline__ void tile_coords(const Args& p, int tile, int64_t& m0
   const int band_rows = rows_left < kBandRows ? rows_left : kBandRows;
   m0 = int64_t(band * kBandRows + in_band % band_rows) * BM;
   n0 = int64_t(in_band / band_rows) * BN;
+}
+
+// ============================================================ bias of an operand
+// The bias gradient of a DP layer is a clipped sum of the column sums of one
+// operand of the weight gradient's product (grad_output: operand a of a
+// Linear, G_b = g_b^T x_b; operand b of a Conv1D, G_b = x_b^T g_b):
+//   bias[c] = bias_scale * sum_b c'_b sum_k op_b[k, c] + bias_noise_scale * zb[c],
+//   c'_b = clip(||op_b||_F)           (flashdp/core/linear_clip.py:116-123).
+// The product kernels take it from the operand fragments their MFMAs already
+// hold, so grad_output is read once.  A 16-bit fragment pair gives its column
+// sum and its square in two v_dot2 (with ones, and with itself).  Each element
+// is counted once: in the tile grid, k-tile kt of a sample is counted by the
+// tile whose index along the other axis is kt % P (P tiles there), and k-step
+// ks by the wave with (ks & 1) == its index among the two waves that share the
+// fragment.  A tile's column sums go to bias_part[c][b][other] (an output's
+// B * P partials are contiguous), its sum of squares to bias_sq[b][tile].
+
+// acc + x.lo + x.hi and acc + x.lo^2 + x.hi^2 for two packed 16-bit values.
+template <class DT>
+__device__ __forceinline__ float dot2_ones(uint32_t x, float acc) {
+  if constexpr (DT::code == FDP_BF16) {
+    typedef __attribute__((ext_vector_type(2))) __bf16 v2;
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2, x),
+                                           __builtin_bit_cast(v2, 0x3f803f80u), acc, false);
+  } else {
+    typedef __attribute__((ext_vector_type(2))) _Float16 v2;
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(v2, x), __builtin_bit_cast(v2, 0x3c003c00u),
+                                  acc, false);
+  }
+}
+template <class DT>
+__device__ __forceinline__ float dot2_self(uint32_t x, float acc) {
+  if constexpr (DT::code == FDP_BF16) {
+    typedef __attribute__((ext_vector_type(2))) __bf16 v2;
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2, x), __builtin_bit_cast(v2, x),
+                                           acc, false);
+  } else {
+    typedef __attribute__((ext_vector_type(2))) _Float16 v2;
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(v2, x), __builtin_bit_cast(v2, x), acc, false);
+  }
+}
+
+// One fragment (8 consecutive k-values of the tile's column `col`) into a
+// lane's column sum cs and sum of squares sq; the tile's columns at or past
+// `lim` (past the operand's width: they may hold the next row's values) are
+// left out of the squares.
+template <class DT>
+__device__ __forceinline__ void bias_frag(const uint4& f, float& cs, float& sq, int col, int lim) {
+  const uint32_t w4[4] = {f.x, f.y, f.z, f.w};
+  float c = cs, q = 0.f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    c = dot2_ones<DT>(w4[e], c);
+    q = dot2_self<DT>(w4[e], q);
+  }
+  cs = c;
+  sq += col < lim ? q : 0.f;
+}
+// Columns of the bias operand left in a tile that starts at column c0
+// (clamped to 2^30: a tile is narrower).
+__device__ __forceinline__ int bias_limit(int64_t len, int64_t c0) {
+  const int64_t l = len - c0;
+  return l < (int64_t(1) << 30) ? static_cast<int>(l) : (1 << 30);
+}
+
+// End of one sample's product in a 4-wave workgroup: a wave's column sums
+// (lanes l and l + 32 hold the two k halves of one column) go to bcol[ws][.]
+// at local columns cl0 + 32 f + lane (f < NF), its sum of squares to
+// bred[wave]; both are cleared.  The caller then synchronises and calls
+// bias_store.
+template <int NF, int W>
+__device__ __forceinline__ void bias_fold(float (&cs)[NF], float& sq, float* bcol, float* bred,
+                                          int ws, int cl0) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int f = 0; f < NF; ++f) {
+    const float v = cs[f] + __shfl_xor(cs[f], 32, kWave);
+    if (lane < 32) bcol[ws * W + cl0 + 32 * f + lane] = v;
+    cs[f] = 0.f;
+  }
+  const float q = wave_sum(sq);
+  if (lane == 0) bred[wave] = q;
+  sq = 0.f;
+}
+// The folded partials of sample b in tile `tile` (local columns [0, W) from
+// column c0; the two waves sharing a fragment added in wave order).
+template <int W>
+__device__ __forceinline__ void bias_store(const Args& p, const float* bcol, const float* bred,
+                                           int64_t b, int tile, int tiles, int64_t c0, int other) {
+  for (int t = threadIdx.x; t < W; t += NT) {
+    const int64_t c = c0 + t;
+    if (c < p.bias_len)
+      st_coherent(p.bias_part + (c * p.B + b) * p.bias_P + other, bcol[t] + bcol[W + t]);
+  }
+  if (threadIdx.x == 0)
+    st_coherent(p.bias_sq + b * tiles + tile, (bred[0] + bred[1]) + (bred[2] + bred[3]));
+}
+
+// Outputs [wg * kBiasCols, ...) (and every nwg * kBiasCols after) of the bias
+// from the partials of all B samples: per output, the samples in four
+// contiguous quarters (thread q of the output), each the fixed-order sum of
+// c'_b times the sample's P partials, then the quarters in order -- a fixed
+// summation order, so the result is deterministic.  The clip factors are
+// formed kBiasFacBlock at a time into LDS (wave w: samples w, w + 4, ...).
+// Workgroup 0 writes bias_norms / bias_factors.  Every thread of the
+// workgroup calls it.
+constexpr int kBiasCols = 64;
+constexpr int kBiasFacBlock = 256;
+struct BiasSmem {
+  float fac[kBiasFacBlock];
+  float red[NT];
+};
+__device__ inline void bias_finish(const Args& p, int tiles, int wg, int nwg, bool poisoned,
+                                   BiasSmem& sm) {
+  static_assert(NT == 4 * kBiasCols, "four threads per output");
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int q = threadIdx.x / kBiasCols, cl = threadIdx.x % kBiasCols;
+  float C = p.C, clamp = p.clamp;
+  if (p.clip_args_dev != nullptr) {
+    C = p.clip_args_dev[0];
+    clamp = p.clip_args_dev[1];
+  }
+  const int64_t B = p.B;
+  const int P = p.bias_P;
+  for (int64_t c0 = int64_t(wg) * kBiasCols; c0 < p.bias_len; c0 += int64_t(nwg) * kBiasCols) {
+    const int64_t c = c0 + cl;
+    float acc = 0.f;
+    for (int64_t fb = 0; fb < B; fb += kBiasFacBlock) {
+      const int nb = B - fb < kBiasFacBlock ? static_cast<int>(B - fb) : kBiasFacBlock;
+      for (int s = wave; s < nb; s += NT / kWave) {
+        const float* sq = p.bias_sq + (fb + s) * tiles;
+        float v = 0.f;
+        for (int t = lane; t < tiles; t += kWave) v += ld_coherent(sq + t);
+        v = wave_sum(v);
+        if (lane == 0) {
+          const float n = poisoned ? __builtin_nanf("") : sqrtf(v);
+          const float cf = poisoned ? n : clip_factor(n, C, clamp);
+          sm.fac[s] = cf;
+          if (wg == 0 && c0 == 0) {
+            if (p.bias_norms) p.bias_norms[fb + s] = n;
+            if (p.bias_factors) p.bias_factors[fb + s] = cf;
+          }
+        }
+      }
+      __syncthreads();
+      const int s0 = (q * nb) / 4, s1 = ((q + 1) * nb) / 4;
+      if (c < p.bias_len) {
+        const float* src = p.bias_part + (c * B + fb) * P;
+        for (int s = s0; s < s1; ++s) {
+          float v = 0.f;
+          for (int u0 = 0; u0 < P; u0 += 8) {
+            float x[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x[e] = u0 + e < P ? ld_coherent(src + s * P + u0 + e) : 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v += x[e];
+          }
+          acc += sm.fac[s] * v;
+        }
+      }
+      __syncthreads();  // the factors are read before the next block replaces them
+    }
+    sm.red[threadIdx.x] = acc;
+    __syncthreads();
+    if (q == 0 && c < p.bias_len) {
+      float v = ((sm.red[cl] + sm.red[kBiasCols + cl]) + sm.red[2 * kBiasCols + cl]) +
+                sm.red[3 * kBiasCols + cl];
+      v *= p.bias_scale;
+      if (p.bias_noise.on()) v += p.bias_noise_scale * p.bias_noise.at(c);
+      if (poisoned) v = __builtin_nanf("");
+      store_from_f32(p.bias_out, c, p.bias_dtype, v);
+    }
+    __syncthreads();
+  }
+}
+
+// The bias from the partials of a completed launch (the streamed schedule).
+template <int kUnused = 0>
+__global__ __launch_bounds__(NT) void bias_finish_kernel(Args p, int tiles) {
+  __shared__ BiasSmem sm;
+  bias_finish(p, tiles, blockIdx.x, gridDim.x, false, sm);
 }
 
 // ============================================================ single pass
@@ -864,9 +1061,14 @@ __device__ inline void take_over(const float* slot, f32x16 (&acc)[2][2]) {
 // finish, waits for the tile's other groups, and finishes rows
 // [g*128/ng, (g+1)*128/ng) itself (output, or the running sum carried to the
 // next launch in chunk_acc).
+// BOP 1 / 2: also the bias of operand a / b (bias_finish): every product's
+// column sums and squares are taken from its fragments and stored at the
+// product's end; after the last launch's grid barrier and the row finish,
+// workgroups [0, ceil(bias_len / kBiasCols)) finish the bias.  Split products
+// are not used then (the host sets split_k1 = 0).
 constexpr int kStages = 2;  // LDS ring depth of the single-pass kernel (64-deep k-tiles)
 
-template <class DT, int U>
+template <class DT, int U, int BOP = 0>
 __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
   using G = dma::Geom<BM, BN, 64>;
   static_assert(kStages * G::STAGE == BM * BN * 4, "the output staging reuses the ring");
@@ -876,6 +1078,8 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
   __shared__ float red[NT / kWave];
   __shared__ float fac[U];
   __shared__ int flag;
+  __shared__ float bcol[BOP != 0 ? 2 * BM : 1];  // a product's folded bias column sums
+  __shared__ float bred[NT / kWave];
   const dma::Stages stages{{(FDP_LDS char*)(st0), (FDP_LDS char*)(st1),
                             (FDP_LDS char*)(st0), (FDP_LDS char*)(st1)}};
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -923,6 +1127,17 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
   int iu = 0, ik = 0;
   int64_t m0, n0;
   tile_coords(p, as.tile, m0, n0);
+  // bias: the tile's index along the other axis, this wave's index among the
+  // two that share its fragments, and its lane's columns (bias_frag)
+  const int bother = BOP == 1 ? static_cast<int>(n0 / BN) : static_cast<int>(m0 / BM);
+  const int bws = BOP == 1 ? (wave & 1) : (wave >> 1);
+  const int bcl = BOP == 1 ? wm : wn;  // the wave's first column in the tile
+  const int blim = bias_limit(p.bias_len, BOP == 1 ? m0 : n0);
+  float bcs[2] = {0.f, 0.f}, bsq = 0.f;
+  (void)bother;
+  (void)bws;
+  (void)bcl;
+  (void)blim;
   // rows [r0, r1) of the tile are finished by this group; their noise (VALU
   // work independent of the data) is drawn ahead into zpre: by workgroups with
   // fewer products than the most loaded ones while they wait at the grid
@@ -983,7 +1198,20 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
         dma::wait_tiles<G::LOADS>(ahead < kStages - 2 ? ahead : kStages - 2);
         dma::barrier();
         if (q + kStages - 1 < nq) issue_next(stages.get((s + kStages - 1) % kStages));
-        dma::compute_stage<DT, G>(stages.get(s), fo, acc);
+        if constexpr (BOP == 0) {
+          dma::compute_stage<DT, G>(stages.get(s), fo, acc);
+        } else {
+          const bool cnt = ck % p.bias_P == bother;
+          dma::compute_stage_fh<DT, G>(
+              stages.get(s), fo, acc, true, [&](int ks, const dma::Frags<G>& f) {
+                if (cnt && (ks & 1) == bws) {
+#pragma unroll
+                  for (int i = 0; i < 2; ++i)
+                    bias_frag<DT>(BOP == 1 ? f.a[i] : f.b[i], bcs[i], bsq,
+                                  bcl + 32 * i + (lane & 31), blim);
+                }
+              });
+        }
         if (++ck == unit_nk(cu)) {
           {
             const int own = cu;
@@ -1003,10 +1231,14 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
               }
             sq = wave_sum(sq);
             if (lane == 0) red[wave] = sq;
+            if constexpr (BOP != 0) bias_fold<2, BM>(bcs, bsq, bcol, bred, bws, BOP == 1 ? wm : wn);
             __syncthreads();
             if (threadIdx.x == 0)
               st_coherent(p.partials + (as.b0 + own) * tiles + as.tile,
                           (red[0] + red[1]) + (red[2] + red[3]));
+            if constexpr (BOP != 0)
+              bias_store<BM>(p, bcol, bred, as.b0 + own, as.tile, tiles, BOP == 1 ? m0 : n0,
+                             bother);
             if (own + 1 < nb) {  // park it and start the next product
 #pragma unroll
               for (int j = 0; j < U - 1; ++j)
@@ -1176,6 +1408,14 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
   if (p.out_dtype == FDP_BF16) finish_rows<BF16>(p, as, m0, n0, r0, r1, q4, poisoned, zpre);
   else if (p.out_dtype == FDP_F16) finish_rows<F16>(p, as, m0, n0, r0, r1, q4, poisoned, zpre);
   else finish_rows<F32>(p, as, m0, n0, r0, r1, q4, poisoned, zpre);
+  if constexpr (BOP != 0) {
+    // every sample's partials are visible: this launch's since the grid
+    // barrier, earlier launches' by stream order
+    if (p.chunk_last && int64_t(blockIdx.x) * kBiasCols < p.bias_len) {
+      __syncthreads();  // the staged rows in the ring are read
+      bias_finish(p, tiles, blockIdx.x, p.nwg, poisoned, *reinterpret_cast<BiasSmem*>(st0));
+    }
+  }
 }
 
 // Clears the barrier / ticket words at the head of the workspace.
@@ -1369,15 +1609,15 @@ inline host::ShapeCache<WorkMapKey, WorkMap>& work_map_cache() {
 // grid, sized to the computed occupancy, is resident at once).  `clean`: the
 // control words are already zero (every launch of the kernel leaves them so),
 // which makes the clearing kernel unnecessary.
-template <class DT>
+template <class DT, int BOP = 0>
 hipError_t try_grouped(Args a, int cus, bool plain, bool clean, hipStream_t s) {
   const int tiles = a.tiles_m * a.tiles_n;
   if (a.K * a.lda * 2 >= (int64_t(1) << 31) || a.K * a.ldb * 2 >= (int64_t(1) << 31))
     return hipErrorNotSupported;
   const GroupPlan gp = group_plan(a.B, tiles, 2 * cus);
   if (gp.chunk == 0) return hipErrorNotSupported;
-  KernelFn grouped[kGroupUnits] = {&wgrad_group_kernel<DT, 1>, &wgrad_group_kernel<DT, 2>,
-                                   &wgrad_group_kernel<DT, 3>, &wgrad_group_kernel<DT, 4>};
+  KernelFn grouped[kGroupUnits] = {&wgrad_group_kernel<DT, 1, BOP>, &wgrad_group_kernel<DT, 2, BOP>,
+                                   &wgrad_group_kernel<DT, 3, BOP>, &wgrad_group_kernel<DT, 4, BOP>};
   const int64_t words = int64_t(kWsHead / sizeof(unsigned));
   for (int64_t b0 = 0; b0 < a.B; b0 += gp.chunk) {
     Args c = a;
@@ -1406,6 +1646,10 @@ hipError_t try_grouped(Args a, int cus, bool plain, bool clean, hipStream_t s) {
     std::memcpy(c.owner_mask, wm.owner_mask, sizeof(wm.owner_mask));
     std::memcpy(c.helper_mask, wm.helper_mask, sizeof(wm.helper_mask));
     c.split_k1 = wm.split_k1;
+    if (BOP != 0) {  // the bias counts k-tiles per (sample, tile): no split products
+      c.split_k1 = 0;
+      for (int w = 0; w < kPermMax / 32; ++w) c.owner_mask[w] = c.helper_mask[w] = 0u;
+    }
     KernelFn fn = grouped[ls.units - 1];
     if (host::occupancy(reinterpret_cast<const void*>(fn), NT, 0) < 2) return hipErrorNotSupported;
     if (b0 == 0 && !clean)
@@ -1422,9 +1666,12 @@ hipError_t try_grouped(Args a, int cus, bool plain, bool clean, hipStream_t s) {
   return hipSuccess;
 }
 
-// Per-dtype launchers (wgrad_group_{bf16,f16}.hip).
+// Per-dtype launchers (wgrad_group_{bf16,f16}.hip; with the bias of operand
+// a.bias_op, wgrad_group_bias_{bf16,f16}.hip).
 hipError_t launch_grouped_bf16(Args a, int cus, bool plain, bool clean, hipStream_t s);
 hipError_t launch_grouped_f16(Args a, int cus, bool plain, bool clean, hipStream_t s);
+hipError_t launch_grouped_bias_bf16(Args a, int cus, bool plain, bool clean, hipStream_t s);
+hipError_t launch_grouped_bias_f16(Args a, int cus, bool plain, bool clean, hipStream_t s);
 
 }  // namespace wg
 }  // namespace fdp

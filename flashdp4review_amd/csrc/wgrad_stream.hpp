@@ -306,11 +306,19 @@ __device__ inline void store_half(const Args& p, int64_t m0, int64_t n0, int h,
 
 // Grid: tiles x groups workgroups (XCD-aware numbering; group-major).  Group g
 // sums samples [g*spg, min(B, (g+1)*spg)) of one output tile.
-template <class DT, class G, int S>
+// BOP 1 / 2: also the column sums and squares of operand a / b for its bias
+// (bias_finish, run by bias_finish_kernel after this kernel): taken from the
+// fragments of every sample, also of a sample whose clip factor is zero
+// (its fragments are then read for the bias only).
+template <class DT, class G, int S, int BOP = 0>
 __global__ __launch_bounds__(NT, 2) void clipsum_kernel(Args p) {
   static_assert(S >= 2 && S <= 4, "ring depth");
   static_assert(S * G::STAGE >= G::WM * G::BN * 4, "output staging reuses the ring");
+  constexpr int BW = BOP == 1 ? G::BM : G::BN;  // the tile's extent along the bias axis
+  constexpr int NF = BOP == 1 ? G::FI : G::FJ;  // fragments of the bias operand per wave
   __shared__ __attribute__((aligned(16))) char ring[S * G::STAGE];
+  __shared__ float bcol[BOP != 0 ? 2 * BW : 1];
+  __shared__ float bred[NT / kWave];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = (wave >> 1) * G::WM, wn = (wave & 1) * G::WN;
   (void)lane;
@@ -326,6 +334,17 @@ __global__ __launch_bounds__(NT, 2) void clipsum_kernel(Args p) {
   const int nq = nsamp * nk;
   const uint16_t* pa = static_cast<const uint16_t*>(p.a);
   const uint16_t* pb = static_cast<const uint16_t*>(p.b);
+  // bias: the tile's index along the other axis, this wave's index among the
+  // two that share its fragments, and its lane's columns (bias_frag)
+  const int bother = BOP == 1 ? static_cast<int>(n0 / G::BN) : static_cast<int>(m0 / G::BM);
+  const int bws = BOP == 1 ? (wave & 1) : (wave >> 1);
+  const int bcl = BOP == 1 ? wm : wn;  // the wave's first column in the tile
+  const int blim = bias_limit(p.bias_len, BOP == 1 ? m0 : n0);
+  float bcs[NF] = {}, bsq = 0.f;
+  (void)bother;
+  (void)bws;
+  (void)bcl;
+  (void)blim;
 
   dma::FragOffsets<G> fo;
   fo.init(wm, wn);
@@ -384,8 +403,27 @@ __global__ __launch_bounds__(NT, 2) void clipsum_kernel(Args p) {
             any = true;
           }
         }
-        if (live) dma::compute_stage<DT, G>(stage(s), fo, acc);
+        if constexpr (BOP == 0) {
+          if (live) dma::compute_stage<DT, G>(stage(s), fo, acc);
+        } else {
+          const bool cnt = ck % p.bias_P == bother;
+          if (live || cnt)
+            dma::compute_stage_fh<DT, G>(
+                stage(s), fo, acc, live, [&](int ks, const dma::Frags<G>& f) {
+                  if (cnt && (ks & 1) == bws) {
+#pragma unroll
+                    for (int i = 0; i < NF; ++i)
+                      bias_frag<DT>(BOP == 1 ? f.a[i] : f.b[i], bcs[i], bsq,
+                                    bcl + 32 * i + (lane & 31), blim);
+                  }
+                });
+        }
         if (++ck == nk) {
+          if constexpr (BOP != 0) {  // the sample's bias partials
+            bias_fold<NF, BW>(bcs, bsq, bcol, bred, bws, BOP == 1 ? wm : wn);
+            dma::barrier();
+            bias_store<BW>(p, bcol, bred, b0 + cu, tile, tiles, BOP == 1 ? m0 : n0, bother);
+          }
           ck = 0;
           ++cu;
         }
@@ -449,14 +487,36 @@ hipError_t launch_gram_norm(const GramArgs& g, hipStream_t s) {
   return hipGetLastError();
 }
 
+// Partials per bias output of the clipped-sum pass (tiles along the other axis).
+inline int stream_bias_P(const StreamPlan& sp, int bias_op) {
+  return bias_op == 1 ? sp.sum_tiles_n : sp.sum_tiles_m;
+}
+
+// The clipped-sum pass; with a.bias_op, also the bias (bias_finish_kernel
+// after the pass, one workgroup per kBiasCols outputs).
 template <class DT>
 hipError_t launch_clipsum(Args a, const StreamPlan& sp, hipStream_t s) {
   a.tiles_m = sp.sum_tiles_m;
   a.tiles_n = sp.sum_tiles_n;
   a.groups = sp.sum_groups;
   a.spg = sp.sum_spg;
-  const unsigned grid = static_cast<unsigned>(a.tiles_m * a.tiles_n * a.groups);
-  hipLaunchKernelGGL((clipsum_kernel<DT, SumGeom, kSumStages>), dim3(grid), dim3(NT), 0, s, a);
+  const int tiles = a.tiles_m * a.tiles_n;
+  const unsigned grid = static_cast<unsigned>(tiles * a.groups);
+  if (a.bias_op == 0) {
+    hipLaunchKernelGGL((clipsum_kernel<DT, SumGeom, kSumStages, 0>), dim3(grid), dim3(NT), 0, s, a);
+    return hipGetLastError();
+  }
+  a.bias_P = stream_bias_P(sp, a.bias_op);
+  if (a.bias_op == 1)
+    hipLaunchKernelGGL((clipsum_kernel<DT, SumGeom, kSumStages, 1>), dim3(grid), dim3(NT), 0, s, a);
+  else
+    hipLaunchKernelGGL((clipsum_kernel<DT, SumGeom, kSumStages, 2>), dim3(grid), dim3(NT), 0, s, a);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  int64_t nfin = (a.bias_len + kBiasCols - 1) / kBiasCols;
+  if (nfin > 1024) nfin = 1024;
+  hipLaunchKernelGGL(bias_finish_kernel<0>, dim3(static_cast<unsigned>(nfin)), dim3(NT), 0, s, a,
+                     tiles);
   return hipGetLastError();
 }
 

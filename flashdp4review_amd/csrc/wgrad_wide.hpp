@@ -69,12 +69,14 @@ struct WideArgs {
   float* norms_out;
   float* factors_out;
   int vec_out;  // out rows hold whole aligned quads: 4 outputs per vector store
-  // The bias of operand a (kernel's BIAS = true):
-  //   bias[m] = bias_scale * sum_b c'_b sum_k a_b[k, m] + bias_noise_scale * zb[m],
-  //   c'_b = clip(||a_b||_F) with the weight's C and clamp.
-  float* bias_part;  // [tiles_m, BM, B, tiles_n]: column sums over a workgroup's k-tiles
-                     // (an output's B * tiles_n partials are contiguous)
-  float* bias_sq;    // [B, tiles]: sums of squares of a over a workgroup's (m-block, k-tiles)
+  // The bias of operand a (bias_op 1, rows m) or b (bias_op 2, columns n):
+  //   bias[c] = bias_scale * sum_b c'_b sum_k op_b[k, c] + bias_noise_scale * zb[c],
+  //   c'_b = clip(||op_b||_F) with the weight's C and clamp.
+  int bias_op;       // 0: no bias
+  float* bias_part;  // [tiles_own, W, B, tiles_other] (W = the tile's extent along the
+                     // bias axis): column sums over a workgroup's k-tiles (an output's
+                     // B * tiles_other partials are contiguous)
+  float* bias_sq;    // [B, tiles]: sums of squares of the operand over a workgroup's k-tiles
   void* bias_out;
   int bias_dtype;
   float bias_scale;
@@ -114,37 +116,15 @@ __device__ __forceinline__ void quad_transpose(const float (&in)[4], float (&out
   }
 }
 
-// BIAS: also the bias of operand a.  The column sums and squares of a come from
-// the A fragments the MFMAs already hold: k-tile kt of an m-block is counted by
-// the tile with n-index kt % tiles_n, k-step ks by the wave of the row group
-// with column index ks (two v_dot2 per 2 elements: with ones, and with itself).
-// acc + x.lo + x.hi and acc + x.lo^2 + x.hi^2 for two packed 16-bit values.
-template <class DT>
-__device__ __forceinline__ float dot2_ones(uint32_t x, float acc) {
-  if constexpr (DT::code == FDP_BF16) {
-    typedef __attribute__((ext_vector_type(2))) __bf16 v2;
-    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2, x),
-                                           __builtin_bit_cast(v2, 0x3f803f80u), acc, false);
-  } else {
-    typedef __attribute__((ext_vector_type(2))) _Float16 v2;
-    return __builtin_amdgcn_fdot2(__builtin_bit_cast(v2, x), __builtin_bit_cast(v2, 0x3c003c00u),
-                                  acc, false);
-  }
-}
-template <class DT>
-__device__ __forceinline__ float dot2_self(uint32_t x, float acc) {
-  if constexpr (DT::code == FDP_BF16) {
-    typedef __attribute__((ext_vector_type(2))) __bf16 v2;
-    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2, x), __builtin_bit_cast(v2, x),
-                                           acc, false);
-  } else {
-    typedef __attribute__((ext_vector_type(2))) _Float16 v2;
-    return __builtin_amdgcn_fdot2(__builtin_bit_cast(v2, x), __builtin_bit_cast(v2, x), acc, false);
-  }
-}
-
-template <class DT, int WGM, int WGN, bool BIAS>
+// BOP 1 / 2: also the bias of operand a / b, from the fragments the MFMAs
+// already hold (bias_frag): k-tile kt is counted by the tile whose index along
+// the other axis is kt % (tiles there), k-step ks by the wave with index ks
+// among the waves that share the fragment; the workgroup folds its waves'
+// column sums through LDS and publishes them, and after the barrier workgroup
+// L finishes bias outputs [L * ceil(len / nwg), ...).
+template <class DT, int WGM, int WGN, int BOP>
 __global__ __launch_bounds__(kWideThreads, 1) void wgrad_wide_kernel(WideArgs p) {
+  constexpr bool BIAS = BOP != 0;
   using G = dma::Geom<96 * WGM, 96 * WGN, 32, WGM, WGN>;
   static_assert(G::NW == 8 && G::FI == 3 && G::FJ == 3, "8 waves of 3x3 blocks");
   constexpr int S = kWideStages;
@@ -223,25 +203,23 @@ __global__ __launch_bounds__(kWideThreads, 1) void wgrad_wide_kernel(WideArgs p)
     }
   };
 
-  // bias of a: this lane's rows (wm + 32 i + lane % 32, k half lane / 32)
+  // bias: this lane's columns of the bias operand (wm + 32 i + lane % 32 of a,
+  // or wn + 32 j + lane % 32 of b; k half lane / 32)
   const int tile_m = static_cast<int>(m0 / G::BM), tile_n = static_cast<int>(n0 / G::BN);
+  const int blim = bias_limit(BOP == 1 ? p.M : p.N, BOP == 1 ? m0 : n0);
   float bcs[3] = {0.f, 0.f, 0.f}, bsq = 0.f;
   auto fhook = [&](int kt, int ks, const dma::Frags<G>& f) {
-    if constexpr (BIAS) {
+    if constexpr (BOP == 1) {
       if (kt % p.tiles_n == tile_n && (wave % WGN) == ks) {
 #pragma unroll
-        for (int i = 0; i < 3; ++i) {
-          const uint32_t w4[4] = {f.a[i].x, f.a[i].y, f.a[i].z, f.a[i].w};
-          float cs = bcs[i], q = 0.f;
+        for (int i = 0; i < 3; ++i)
+          bias_frag<DT>(f.a[i], bcs[i], bsq, wm + 32 * i + (lane & 31), blim);
+      }
+    } else if constexpr (BOP == 2) {
+      if (kt % p.tiles_m == tile_m && (wave / WGN) == ks) {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            cs = dot2_ones<DT>(w4[e], cs);
-            q = dot2_self<DT>(w4[e], q);
-          }
-          bcs[i] = cs;
-          // rows past M may hold the next row's values: left out of the norm
-          bsq += m0 + wm + 32 * i + (lane & 31) < p.M ? q : 0.f;
-        }
+        for (int j = 0; j < 3; ++j)
+          bias_frag<DT>(f.b[j], bcs[j], bsq, wn + 32 * j + (lane & 31), blim);
       }
     }
   };
@@ -275,25 +253,31 @@ __global__ __launch_bounds__(kWideThreads, 1) void wgrad_wide_kernel(WideArgs p)
     }
   }
   if constexpr (BIAS) {
-    // lanes l and l + 32 hold one row's two k halves; the WGN waves of a row
-    // group (one k-step each) are added in wave order through LDS (st2 is
+    // lanes l and l + 32 hold one column's two k halves; the NS waves sharing
+    // a fragment (one k-step each) are added in wave order through LDS (st2 is
     // free: gemm_pipe ended on a barrier, and the own region never reaches it)
+    constexpr int W = BOP == 1 ? G::BM : G::BN;  // the tile's extent along the bias axis
+    constexpr int NS = BOP == 1 ? WGN : WGM;     // waves sharing a fragment
     __shared__ float bred[8];
-    float* colp = reinterpret_cast<float*>(st2);  // [WGN][BM]
+    float* colp = reinterpret_cast<float*>(st2);  // [NS][W]
+    const int ws = BOP == 1 ? wave % WGN : wave / WGN;
+    const int cl0 = BOP == 1 ? wm : wn;
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
       const float v = bcs[i] + __shfl_xor(bcs[i], 32, kWave);
-      if (lane < 32) colp[(wave % WGN) * G::BM + wm + 32 * i + lane] = v;
+      if (lane < 32) colp[ws * W + cl0 + 32 * i + lane] = v;
     }
     const float q = wave_sum_dpp(bsq);
     if (lane == 0) bred[wave] = q;
     __syncthreads();
-    const int J = ng * p.tiles_n;  // partials per output
-    float* part = p.bias_part + int64_t(tile_m) * G::BM * J + sample * p.tiles_n + tile_n;
-    for (int r = threadIdx.x; r < G::BM; r += kWideThreads) {
+    const int tiles_o = BOP == 1 ? p.tiles_n : p.tiles_m;
+    const int own = BOP == 1 ? tile_m : tile_n, oth = BOP == 1 ? tile_n : tile_m;
+    const int J = ng * tiles_o;  // partials per output
+    float* part = p.bias_part + int64_t(own) * W * J + sample * tiles_o + oth;
+    for (int r = threadIdx.x; r < W; r += kWideThreads) {
       float v = colp[r];
 #pragma unroll
-      for (int q2 = 1; q2 < WGN; ++q2) v += colp[q2 * G::BM + r];
+      for (int q2 = 1; q2 < NS; ++q2) v += colp[q2 * W + r];
       st_coherent(part + int64_t(r) * J, v);
     }
     if (threadIdx.x == 0)
@@ -418,12 +402,16 @@ __global__ __launch_bounds__(kWideThreads, 1) void wgrad_wide_kernel(WideArgs p)
   // c'_s * part[s][q]; an output's partials are contiguous, loaded as 16-byte
   // agent-coherent vectors, 8 in flight at a time
   if constexpr (BIAS) {
-    const int64_t per = (p.M + p.nwg - 1) / p.nwg;
-    const int J = ng * p.tiles_n;
-    const uint32_t pbytes = static_cast<uint32_t>(int64_t(p.tiles_m) * G::BM * J * 4);
+    constexpr int W = BOP == 1 ? G::BM : G::BN;
+    const int64_t len = BOP == 1 ? p.M : p.N;
+    const int tiles_o = BOP == 1 ? p.tiles_n : p.tiles_m;
+    const int64_t per = (len + p.nwg - 1) / p.nwg;
+    const int J = ng * tiles_o;
+    const uint32_t pbytes =
+        static_cast<uint32_t>(int64_t(BOP == 1 ? p.tiles_m : p.tiles_n) * W * J * 4);
     const CoherentSpan span(p.bias_part, pbytes);
     for (int64_t m = int64_t(L) * per + threadIdx.x;
-         m < p.M && m < (int64_t(L) + 1) * per; m += kWideThreads) {
+         m < len && m < (int64_t(L) + 1) * per; m += kWideThreads) {
       const uint32_t base = static_cast<uint32_t>(m * J * 4);
       float v = 0.f;
       if (J % 4 == 0) {
@@ -437,11 +425,11 @@ __global__ __launch_bounds__(kWideThreads, 1) void wgrad_wide_kernel(WideArgs p)
           for (int u = 0; u < 8; ++u)
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-              if (j0 + 4 * u + e < J) v += bfac[(j0 + 4 * u + e) / p.tiles_n] * x[u][e];
+              if (j0 + 4 * u + e < J) v += bfac[(j0 + 4 * u + e) / tiles_o] * x[u][e];
         }
       } else {
 #pragma unroll 1
-        for (int j = 0; j < J; ++j) v += bfac[j / p.tiles_n] * ld_coherent(p.bias_part + m * J + j);
+        for (int j = 0; j < J; ++j) v += bfac[j / tiles_o] * ld_coherent(p.bias_part + m * J + j);
       }
       v *= p.bias_scale;
       if (p.bias_noise.on()) v += p.bias_noise_scale * p.bias_noise.at(m);
@@ -619,15 +607,13 @@ __global__ __launch_bounds__(kWideThreads, 1) void wgrad_wide_kernel(WideArgs p)
 // outputs; applicable when every product gets a CU of its own, the products
 // fill at least `min_fill` of the device, and the row strides keep a
 // sample's operand under 2^31 bytes (32-bit buffer records).
-// Rows of a 384x192 (wgm 4) or 192x384 (wgm 2) tile, in units of 96.
-constexpr int wgm_rows(int wgm) { return wgm; }
 
 struct WidePlan {
   int wgm;  // 4: 384x192, 2: 192x384, 0: not applicable
   int tiles_m, tiles_n, tiles, nwg;
   int slot_blocks;
   size_t partial_bytes, slot_bytes;
-  size_t bias_part_bytes, bias_sq_bytes;  // the bias of a (reserved whether asked or not)
+  size_t bias_part_bytes, bias_sq_bytes;  // the bias of a or b (reserved whether asked or not)
 };
 inline WidePlan wide_plan(int64_t B, int64_t K, int64_t M, int64_t N, int64_t lda, int64_t ldb,
                           int cus, double min_fill) {
@@ -655,19 +641,23 @@ inline WidePlan wide_plan(int64_t B, int64_t K, int64_t M, int64_t N, int64_t ld
   w.slot_blocks = kWideBlocks - static_cast<int>(kWideBlocks / B);
   w.partial_bytes = sizeof(float) * size_t(units);
   w.slot_bytes = size_t(units) * size_t(w.slot_blocks) * kWideBlockBytes;
-  w.bias_part_bytes = sizeof(float) * size_t(B) * w.tiles_m * w.tiles_n * (96 * wgm_rows(w.wgm));
+  // [tiles_own, W, B, tiles_other] with W <= 384 for either operand
+  w.bias_part_bytes = sizeof(float) * size_t(B) * w.tiles_m * w.tiles_n * 384;
   w.bias_sq_bytes = sizeof(float) * size_t(units);
   return w;
 }
 
 template <class DT>
 hipError_t launch_wide_t(const WideArgs& a, int wgm, bool plain, hipStream_t s) {
-  const bool bias = a.bias_out != nullptr;
-  const void* fn =
-      wgm == 4 ? (bias ? reinterpret_cast<const void*>(&wgrad_wide_kernel<DT, 4, 2, true>)
-                       : reinterpret_cast<const void*>(&wgrad_wide_kernel<DT, 4, 2, false>))
-               : (bias ? reinterpret_cast<const void*>(&wgrad_wide_kernel<DT, 2, 4, true>)
-                       : reinterpret_cast<const void*>(&wgrad_wide_kernel<DT, 2, 4, false>));
+  const void* fns[2][3] = {
+      {reinterpret_cast<const void*>(&wgrad_wide_kernel<DT, 4, 2, 0>),
+       reinterpret_cast<const void*>(&wgrad_wide_kernel<DT, 4, 2, 1>),
+       reinterpret_cast<const void*>(&wgrad_wide_kernel<DT, 4, 2, 2>)},
+      {reinterpret_cast<const void*>(&wgrad_wide_kernel<DT, 2, 4, 0>),
+       reinterpret_cast<const void*>(&wgrad_wide_kernel<DT, 2, 4, 1>),
+       reinterpret_cast<const void*>(&wgrad_wide_kernel<DT, 2, 4, 2>)}};
+  if (a.bias_op < 0 || a.bias_op > 2) return hipErrorInvalidValue;
+  const void* fn = fns[wgm == 4 ? 0 : 1][a.bias_op];
   if (host::occupancy(fn, kWideThreads, 0) < 1) return hipErrorNotSupported;
   WideArgs c = a;
   void* params[] = {&c};

@@ -9,8 +9,8 @@ selects sigma*C/B.)
 with clip(n) = min(clamp_value, C/(n + 1e-10)).  dW and db run as one HIP call
 (fdp_wgrad_bias_clip; fdp_wgrad_clip / fdp_colsum_clip when only one of them
 is needed): norm, clip, 1/B and noise add happen on the device, and
-grad_output is never modified.  Where the wide single-pass kernel runs, the
-bias comes from the grad_output fragments it already holds (no second pass).
+grad_output is never modified.  For 16-bit operands the product kernels take
+the bias from the grad_output fragments they already hold (no second pass).
 """
 from __future__ import annotations
 

@@ -10,7 +10,10 @@ so that dX and dW see the scaled grad_output.  Here:
   db = (1/(B*T)) sum_b clip(||g_b||_F) sum_t g_bt  + (sigma/sqrt(B)) z_b
 (sigma/sqrt(B) is the reference's noise std; set_noise_convention("dpsgd")
 selects sigma*C/B.)
-so DPConv1D(W) computes exactly DPLinear(W^T)'s gradients, transposed.
+so DPConv1D(W) computes exactly DPLinear(W^T)'s gradients, transposed.  dW and
+db run as one HIP call (fdp_wgrad_bias_clip with the bias of operand b = g):
+the product kernels take the bias's column sums and squares from the
+grad_output fragments they already hold, so grad_output is read once.
 """
 from __future__ import annotations
 
@@ -95,16 +98,28 @@ class _DPConv1DFunction(Function):
         if ctx.needs_input_grad[0]:
             w = weight if weight.dtype == g3.dtype else weight.to(g3.dtype)
             grad_input = (g3 @ w.t()).reshape(input.shape)
+        want_bias = ctx.needs_input_grad[2]
         if ctx.needs_input_grad[1]:
             z, key = noise_args(std, gen, nstream, weight.shape, weight.dtype, weight.device)
-            r = wgrad_clip(x3.to(g3.dtype), g3, C, clamp_value, layout="tn", out_scale=1.0 / B,
-                           noise=z, noise_scale=std, noise_key=key, out_dtype=weight.dtype,
-                           return_stats=stats is not None)
+            extra = {}
+            if want_bias:  # both in one call (noise drawn in the same order: weight, bias)
+                O = g3.shape[-1]
+                zb, keyb = noise_args(std, gen, nstream, (O,), ctx.bias_dtype, g3.device)
+                grad_bias = torch.empty(O, dtype=ctx.bias_dtype, device=g3.device)
+                extra = dict(bias_out=grad_bias, bias_scale=1.0 / (B * T), bias_noise=zb,
+                             bias_noise_scale=std, bias_noise_key=keyb, bias_operand="b")
+            r = wgrad_clip(x3.to(g3.dtype), g3.contiguous() if want_bias else g3, C, clamp_value,
+                           layout="tn", out_scale=1.0 / B, noise=z, noise_scale=std,
+                           noise_key=key, out_dtype=weight.dtype,
+                           return_stats=stats is not None, **extra)
             if stats is not None:
-                grad_weight, stats["norms_w"], stats["fac_w"] = r
+                grad_weight, stats["norms_w"], stats["fac_w"] = r[:3]
+                if want_bias:
+                    stats["norms_b"], stats["fac_b"] = r[3], r[4]
             else:
                 grad_weight = r
-        if ctx.needs_input_grad[2]:
+            want_bias = False
+        if want_bias:
             z, key = noise_args(std, gen, nstream, (g3.shape[-1],), ctx.bias_dtype, g3.device)
             r = colsum_clip(g3, None, C, clamp_value, norm="frob", out_scale=1.0 / (B * T),
                             noise=z, noise_scale=std, noise_key=key, out_dtype=ctx.bias_dtype,

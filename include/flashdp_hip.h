@@ -178,29 +178,37 @@ int fdp_wgrad_clip(const void* a, const void* b, int64_t B, int64_t K, int64_t M
                    void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
- * The weight and bias gradients of a DP Linear layer in one call
+ * The weight and bias gradients of a DP Linear or Conv1D layer in one call
  * (replaces the pair linear_weight_flashdp + linear_bias_grad_clip in the
  * reference's DPLinear backward, flashdp/layers/linear.py:72-92, with
- * flashdp/core/linear_clip.py:107-123):
+ * flashdp/core/linear_clip.py:107-123; and conv1d_weight_flashdp +
+ * conv1d_bias_grad_clip, flashdp/core/transformers_conv1d_clip.py:22-39, as
+ * DPConv1D's backward intends them, flashdp/layers/transformers_conv1d.py:59-66):
  *
- *   out  = as fdp_wgrad_clip (layout FDP_LAYOUT_TN, a = grad_output [B,K,M],
- *          b = input [B,K,N]),
- *   bias[m] = bias->out_scale * sum_b c'_b sum_k a_b[k,m] + bias->noise_scale * zb[m],
- *   c'_b = min(clamp, C / (||a_b||_F + 1e-10))   (the weight's C, clamp),
+ *   out  = as fdp_wgrad_clip (layout FDP_LAYOUT_TN),
+ *   bias[c] = bias->out_scale * sum_b c'_b sum_k op_b[k,c] + bias->noise_scale * zb[c],
+ *   c'_b = min(clamp, C / (||op_b||_F + 1e-10))   (the weight's C, clamp),
  *
- * i.e. linear_bias_grad_clip with out_scale = 1/(B*K) (its mean over B*T)
- * and noise_scale = sigma/sqrt(B).  zb is bias->noise (M values of
- * bias->out_dtype) or, without one, the in-kernel draw of bias->noise_key
- * (stream 0, as fdp_colsum_clip).  a must be contiguous (stride_ab = K*M,
- * lda = M); FDP_WGRAD_NOCLIP is not accepted.  When the wide single-pass
- * kernel runs, it forms the bias from the operand fragments it already holds
- * (no second pass over a); otherwise the call runs fdp_colsum_clip
- * (FDP_NORM_FROB) after the weight gradient.  bias->norms / bias->factors
- * (optional, B floats) receive ||a_b||_F and c'_b.
- * Workspace: fdp_wgrad_bias_clip_workspace_size bytes; its first
- * fdp_wgrad_clip_workspace_size bytes (rounded up to 256) are the weight
- * gradient's workspace, with the same rules (FDP_WGRAD_CLEAN_WORKSPACE).
+ * where op is operand a ([B,K,M]: a Linear's grad_output, G_b = g_b^T x_b),
+ * or, with flags bit 6 (FDP_WGRAD_BIAS_OF_B), operand b ([B,K,N]: a Conv1D's
+ * grad_output, G_b = x_b^T g_b).  This is linear_bias_grad_clip with
+ * out_scale = 1/(B*K) (its mean over B*T) and noise_scale = sigma/sqrt(B).
+ * zb is bias->noise (len values of bias->out_dtype, len = M or N) or, without
+ * one, the in-kernel draw of bias->noise_key (stream 0, as fdp_colsum_clip).
+ * The bias operand must be contiguous (stride K*len, row stride len);
+ * FDP_WGRAD_NOCLIP is not accepted.  The 16-bit TN kernels (wide, grouped and
+ * streamed schedules) form the bias from the operand fragments they already
+ * hold, so grad_output is read once; the generic schedule (fp32 operands,
+ * unaligned rows) runs fdp_colsum_clip (FDP_NORM_FROB) after the weight
+ * gradient.  bias->norms / bias->factors (optional, B floats) receive
+ * ||op_b||_F and c'_b.
+ * Workspace: fdp_wgrad_bias_clip_workspace_size bytes (pass the same flags,
+ * FDP_WGRAD_BIAS_OF_B included); its first fdp_wgrad_clip_workspace_size
+ * bytes (rounded up to 256) are the weight gradient's workspace, with the
+ * same rules (FDP_WGRAD_CLEAN_WORKSPACE); the rest needs no clearing.
  * ---------------------------------------------------------------------- */
+#define FDP_WGRAD_BIAS_OF_B 64
+
 typedef struct fdp_bias_out {
   void* out;
   int out_dtype;
