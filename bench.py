@@ -93,21 +93,31 @@ def cfg3_inputs(dev):
     return x, go
 
 
-def run_wgrad(x, go, out_dtype, sigma=1.0, transpose=False, launch=None, single_pass="auto"):
+def run_wgrad(x, go, out_dtype, sigma=1.0, transpose=False, launch=None, single_pass="auto",
+              bias=False):
     """One DP weight-gradient step: the fused clipped product sum with its noise
-    drawn in the epilogue (a fresh Philox counter range every step)."""
+    drawn in the epilogue (a fresh Philox counter range every step).  With
+    `bias`, the layer's bias gradient (column sums of grad_output, clipped by
+    ||g_b||, mean over B*T, noise) in the same call, as the DP layers run it
+    (transpose: the Conv1D orientation x^T g, whose bias is of operand b)."""
     from flashdp4review_amd.core import wgrad_clip
     from flashdp4review_amd.layers.utils import NoiseStream
-    B = x.shape[0]
+    B, T = x.shape[0], x.shape[1]
     a, b = (x, go) if transpose else (go, x)
     M, N = a.shape[2], b.shape[2]
     std = sigma / math.sqrt(B)
     keys = NoiseStream()
+    O = go.shape[2]
+    bias_out = torch.empty(O, dtype=go.dtype, device=go.device) if bias else None
 
     def step():
+        kw = {}
+        if bias:
+            kw = dict(bias_out=bias_out, bias_scale=1.0 / (B * T), bias_noise_scale=std,
+                      bias_noise_key=keys.next(O), bias_operand="b" if transpose else "a")
         return wgrad_clip(a, b, 1.0, 1.0, layout="tn", out_scale=1.0 / B, noise_scale=std,
                           noise_key=keys.next(M * N), out_dtype=out_dtype, launch=launch,
-                          single_pass=single_pass)
+                          single_pass=single_pass, **kw)
 
     return step, step
 
@@ -227,7 +237,19 @@ def cpu_baseline_cfg2():
                       f"fp32 {t32:.4f} s/step over {n32} steps",
             "fp32_value": round(F / t32 / 1e12, 4),
             "machine_cores": machine,
-            "cpu_model": platform.processor() or platform.machine()}
+            "cpu_model": cpu_model()}
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), else the machine type."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
 
 
 # ------------------------------------------------------------------------ cfg5
@@ -250,7 +272,9 @@ def _attention(q, k, v):
 
 
 def gpt_model(n_layer=24, d=2048, n_head=16, ffn=8192, vocab=50257, ctx=1024):
-    """GPT-2-style decoder (pre-LN, no Linear bias, GELU MLP), random init."""
+    """GPT-2-style decoder (pre-LN, no Linear bias, GELU MLP, lm_head tied to the
+    token embedding as in the reference's example model, example/gpt2/model.py:111-114),
+    random init: 1.313 B parameters at the defaults."""
     import torch.nn as nn
     import torch.nn.functional as F
 
@@ -283,6 +307,7 @@ def gpt_model(n_layer=24, d=2048, n_head=16, ffn=8192, vocab=50257, ctx=1024):
             for m in self.modules():
                 if isinstance(m, (nn.Linear, nn.Embedding)):
                     nn.init.normal_(m.weight, std=0.02)
+            self.lm_head.weight = self.wte.weight  # weight tying
 
         def forward(self, idx):
             pos = torch.arange(idx.shape[1], device=idx.device)
@@ -294,7 +319,7 @@ def gpt_model(n_layer=24, d=2048, n_head=16, ffn=8192, vocab=50257, ctx=1024):
     return GPT()
 
 
-def cfg5_training(dev, steps=10, warmup=3, n_layer=24):
+def cfg5_training(dev, steps=10, warmup=3, n_layer=24, fused_adam=True):
     """Tokens/s of full training steps (fwd, bwd, Adam) of the cfg5 decoder, plain and
     with every Linear/LayerNorm except lm_head wrapped by wrap_with_flashdp_layers
     (C=1, sigma=1), bf16 weights, B=8, T=1024, uniform random token ids."""
@@ -307,12 +332,19 @@ def cfg5_training(dev, steps=10, warmup=3, n_layer=24):
     torch.manual_seed(0)
     with torch.device(dev):
         base = gpt_model(n_layer=n_layer).to(torch.bfloat16)
+    n_params = sum(p.numel() for p in base.parameters())  # (the tied head counted once)
     g = torch.Generator(device=dev).manual_seed(0)
     idx = torch.randint(0, V, (B, T + 1), device=dev, generator=g)
     x, y = idx[:, :-1].contiguous(), idx[:, 1:].contiguous()
 
     def run(model):
-        opt = torch.optim.Adam(model.parameters(), lr=1e-5, foreach=True)
+        # fused Adam (one multi-tensor kernel per parameter group) where the
+        # build has it, else the foreach implementation; the same for both legs
+        try:
+            opt = torch.optim.Adam(model.parameters(), lr=1e-5, fused=fused_adam,
+                                   foreach=None if fused_adam else True)
+        except (RuntimeError, ValueError):
+            opt = torch.optim.Adam(model.parameters(), lr=1e-5, foreach=True)
 
         def step():
             logits = model(x)
@@ -347,7 +379,8 @@ def cfg5_training(dev, steps=10, warmup=3, n_layer=24):
     torch.cuda.empty_cache()
     tok = B * T
     return {"workload": f"cfg5: GPT-2-style decoder {n_layer}L d=2048 h=16 ffn=8192 V=50257, "
-                        "B=8 T=1024 bf16, Adam, C=1 sigma=1",
+                        f"tied lm_head, {n_params / 1e9:.3f} B params, B=8 T=1024 bf16, Adam, "
+                        "C=1 sigma=1",
             "dp_tokens_per_s": round(tok / ms_dp * 1e3, 1),
             "non_dp_tokens_per_s": round(tok / ms_plain * 1e3, 1),
             "dp_over_non_dp_throughput": round(ms_plain / ms_dp, 4),
@@ -477,13 +510,30 @@ def extra_measurements(dev, steps, warmup):
                                           "dp_over_non_dp_throughput": round(t_linb / t_dpb, 4)}
     out["cfg2_weight_and_bias"] = weight_and_bias_cost(dev, steps, warmup)
     out["cfg2_dx_overlap"] = dx_overlap(dev, steps, warmup)
-    # cfg3: Conv1D orientation (x^T g, [768, 2304]) with partially active clipping
+    # cfg3: Conv1D orientation (x^T g, [768, 2304]) with partially active clipping:
+    # the layer's weight and bias gradients in one call (what DPConv1D runs, and
+    # what cpu_cfg3 times), the weight alone, and the weight followed by the
+    # separate column-sum kernel over grad_output for the bias
+    from flashdp4review_amd.core import colsum_clip
     x3, g3 = cfg3_inputs(dev)
+    F3 = 2.0 * 16 * 1024 * 768 * 2304
+    _, wb3 = run_wgrad(x3, g3, torch.bfloat16, transpose=True, bias=True)
+    t3b = median_cuda_time(wb3, steps, warmup, reps=3)
     _, gemm3 = run_wgrad(x3, g3, torch.bfloat16, transpose=True)
     t3 = median_cuda_time(gemm3, steps, warmup, reps=3)
-    F3 = 2.0 * 16 * 1024 * 768 * 2304
-    out["cfg3_conv1d_clipped_wgrad"] = {"ms": round(t3, 4), "tflops": round(F3 / t3 / 1e9, 2),
-                                        "frac_bf16_peak": round(F3 / t3 / 1e9 / PEAK_BF16_TFLOPS, 4)}
+
+    def two_calls():
+        gemm3()
+        colsum_clip(g3, None, 1.0, 1.0, norm="frob", out_scale=1.0 / (16 * 1024),
+                    noise_scale=0.25, noise_key=(7, 0), out_dtype=torch.bfloat16)
+    t3s = median_cuda_time(two_calls, steps, warmup, reps=3)
+    out["cfg3_conv1d_clipped_wgrad"] = {
+        "ms": round(t3b, 4), "tflops": round(F3 / t3b / 1e9, 2),
+        "frac_bf16_peak": round(F3 / t3b / 1e9 / PEAK_BF16_TFLOPS, 4),
+        "what": "dW and db in one fdp_wgrad_bias_clip call (the bias from the grouped "
+                "kernel's grad_output fragments)",
+        "weight_only_ms": round(t3, 4),
+        "weight_then_column_sum_kernel_ms": round(t3s, 4)}
     # cfg4: LayerNorm H=1024, bf16 I/O, per-sample gamma/beta clip (backward incl. dx)
     g4 = torch.Generator(device=dev).manual_seed(5)
     xl = torch.randn(16, 1024, 1024, device=dev, generator=g4).to(torch.bfloat16)
@@ -559,9 +609,11 @@ def main():
     elif args.workload == "cfg3":
         x, go = cfg3_inputs(dev)
         B, T, I, O = 16, 1024, 768, 2304
-        step, _ = run_wgrad(x, go, torch.bfloat16, transpose=True)
-        step_coop, _ = run_wgrad(x, go, torch.bfloat16, transpose=True, launch="cooperative")
-        workload = "cfg3: DP Conv1D 768->2304 clipped per-sample weight grad, B=16 T=1024"
+        step, _ = run_wgrad(x, go, torch.bfloat16, transpose=True, bias=True)
+        step_coop, _ = run_wgrad(x, go, torch.bfloat16, transpose=True, launch="cooperative",
+                                 bias=True)
+        workload = ("cfg3: DP Conv1D 768->2304 clipped per-sample weight and bias grads in one "
+                    "call, B=16 T=1024, norms 0.1C..10C")
     else:
         from flashdp4review_amd.core import layernorm_bwd_clip, layernorm_fwd
         g4 = torch.Generator(device=dev).manual_seed(5)

@@ -39,9 +39,10 @@ _c_sz_p = ctypes.POINTER(ctypes.c_size_t)
 
 
 class NoiseKey(ctypes.Structure):
-    """fdp_noise_key: the Philox4x32-10 key (seed) and first counter block of an
-    in-kernel Gaussian draw (include/flashdp_hip.h)."""
-    _fields_ = [("seed", ctypes.c_uint64), ("offset", ctypes.c_uint64)]
+    """fdp_noise_key: the Philox4x32-10 key (seed), first counter block and
+    optional device counter of an in-kernel Gaussian draw (include/flashdp_hip.h)."""
+    _fields_ = [("seed", ctypes.c_uint64), ("offset", ctypes.c_uint64),
+                ("counter", ctypes.c_void_p)]
 
 
 _c_key = ctypes.POINTER(NoiseKey)
@@ -60,17 +61,27 @@ _c_bias = ctypes.POINTER(BiasOut)
 
 
 def noise_key(key) -> "ctypes._Pointer | None":
-    """(seed, offset) -> a fdp_noise_key pointer for the call (None -> NULL)."""
+    """(seed, offset) or (seed, offset, device counter address) -> a fdp_noise_key
+    pointer for the call (None -> NULL)."""
     if key is None:
         return None
-    seed, offset = key
-    return ctypes.pointer(NoiseKey(int(seed) & (2**64 - 1), int(offset) & (2**64 - 1)))
+    seed, offset = key[0], key[1]
+    counter = key[2] if len(key) > 2 else None
+    return ctypes.pointer(NoiseKey(int(seed) & (2**64 - 1), int(offset) & (2**64 - 1), counter))
+
+
+def noise_advance(counter: torch.Tensor, blocks: int) -> None:
+    """Stream-ordered ``counter += blocks`` on the device (fdp_noise_advance): the
+    advance of a graph-captured draw's counter (``counter`` an int64 [1] tensor)."""
+    check(lib().fdp_noise_advance(counter.data_ptr(), int(blocks),
+                                  stream_handle(counter.device)), "fdp_noise_advance")
 
 # Every exported symbol with its (restype, argtypes); tests check this list
 # against include/flashdp_hip.h.
 SIGNATURES = {
     "fdp_strerror": (ctypes.c_char_p, [_c_int]),
     "fdp_version": (_c_int, []),
+    "fdp_noise_advance": (_c_int, [_c_p, ctypes.c_uint64, _c_p]),
     "fdp_wgrad_clip_workspace_size": (_c_int, [_c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int,
                                                _c_sz_p]),
     "fdp_wgrad_clip": (_c_int, [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,

@@ -9,6 +9,7 @@ from .wgrad import (
     wgrad_clip,
     wgrad_status,
     set_wgrad_launch,
+    set_expiry_check,
     bmtm_clip,
     bmm_clip,
     mm_clip,
@@ -33,7 +34,7 @@ from .layernorm import (
 from .utils import RuntimeAutoTuner, supported_acc_dtypes
 
 __all__ = [
-    "wgrad_clip", "wgrad_status", "set_wgrad_launch", "bmtm_clip", "bmm_clip", "mm_clip", "mm_fused", "linear_weight_flashdp",
+    "wgrad_clip", "wgrad_status", "set_wgrad_launch", "set_expiry_check", "bmtm_clip", "bmm_clip", "mm_clip", "mm_fused", "linear_weight_flashdp",
     "conv1d_weight_flashdp", "colsum_clip", "linear_bias_grad_clip", "conv1d_bias_grad_clip",
     "layernorm_dw_clip", "layernorm_db_clip", "layernorm_fwd", "layernorm_bwd_clip",
     "layernorm_fwd_fused", "layernorm_bwd_clip_fused", "layernorm_dwdb_fused",

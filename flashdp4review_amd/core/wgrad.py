@@ -44,20 +44,25 @@ class _Workspace:
         self.status_host = torch.zeros(1, dtype=torch.int32, pin_memory=True)
         self.event = None
         self.calls = 0
+        self.unchecked = False  # calls since the last check before an optimizer step
+        self.guard_event = None  # status copy behind a step guarded on the device
 
     def status_word(self) -> torch.Tensor:
         return self.buf[:4].view(torch.int32)
 
     def take_probe(self) -> int:
-        """Status seen by a completed probe (0 if none has completed)."""
-        if self.event is None or not self.event.query():
+        """Status seen by a completed probe (0 if none has completed, or while
+        the stream is being captured into a graph)."""
+        if self.event is None or torch.cuda.is_current_stream_capturing() or not self.event.query():
             return 0
         self.event = None
         return int(self.status_host[0])
 
     def queue_probe(self) -> None:
         self.calls += 1
-        if self.event is None and self.calls % STATUS_PERIOD == 0:
+        self.unchecked = True
+        if (self.event is None and self.calls % STATUS_PERIOD == 0
+                and not torch.cuda.is_current_stream_capturing()):
             self.status_host.copy_(self.status_word(), non_blocking=True)
             self.event = torch.cuda.Event()
             self.event.record()
@@ -75,7 +80,109 @@ def _persistent_workspace(nbytes: int, dev: torch.device, stream: int) -> _Works
                 _ws_cache.clear()
             ws = _Workspace(nbytes, dev)
             _ws_cache[key] = ws
+        _install_step_check()
         return ws
+
+
+# Before every optimizer step (a global torch.optim pre-step hook, installed with
+# the first workspace), the status words of the workspaces used since the last
+# step are checked, so that no step consumes the NaN gradients of a call whose
+# bounded wait expired:
+#   - optimizers that can skip a step on the device (torch's fused ones, which
+#     honour a `found_inf` tensor as GradScaler uses it) get found_inf = 1 when
+#     a status word is set, without a host synchronisation; the expiry is then
+#     raised at the next step (or the next call that reads a completed probe);
+#   - every other optimizer: one device synchronisation, and the step raises
+#     before it runs.
+# "async" leaves only the periodic asynchronous probe (no check before steps).
+_EXPIRY_CHECKS = ("optimizer_step", "async")
+_expiry_check = os.environ.get("FDP_EXPIRY_CHECK", "optimizer_step")
+if _expiry_check not in _EXPIRY_CHECKS:
+    raise ValueError(f"FDP_EXPIRY_CHECK must be one of {_EXPIRY_CHECKS}, got {_expiry_check!r}")
+_step_hook = None
+_guarded: dict = {}  # id(optimizer) -> its found_inf before the guard (restored after the step)
+
+
+def set_expiry_check(mode: str) -> str:
+    """When an expired bounded wait is reported; returns the previous mode.
+
+    "optimizer_step" (default): before every optimizer step the status words
+    of the workspaces used since the last step are checked.  An optimizer that
+    can skip a step on the device (torch's fused optimizers) skips it when a
+    word is set, with no host synchronisation, and the next step raises
+    FlashDPError; any other optimizer synchronises once per step and raises
+    before the step runs.  "async": only the asynchronous probe every
+    STATUS_PERIOD calls (a later call raises; no check before steps).
+    """
+    global _expiry_check
+    if mode not in _EXPIRY_CHECKS:
+        raise ValueError(f"expiry check must be one of {_EXPIRY_CHECKS}, got {mode!r}")
+    prev, _expiry_check = _expiry_check, mode
+    return prev
+
+
+def _check_before_step(optimizer, args, kwargs):
+    if _expiry_check != "optimizer_step":
+        return
+    wss = list(_ws_cache.values())
+    for ws in wss:  # an expiry that an earlier guarded step skipped on the device
+        if ws.guard_event is not None and ws.guard_event.query():
+            ws.guard_event = None
+            if int(ws.status_host[0]) != 0:
+                _raise_expired(ws, "an earlier optimizer step was skipped on the device for it")
+    dirty = [ws for ws in wss if ws.unchecked]
+    if not dirty:
+        return
+    devs = {ws.buf.device for ws in dirty}
+    if getattr(optimizer, "_step_supports_amp_scaling", False) and len(devs) == 1:
+        dev = devs.pop()
+        with torch.cuda.device(dev):
+            if torch.cuda.is_current_stream_capturing():
+                return
+            flag = torch.zeros((), dtype=torch.float32, device=dev)  # (a scalar, as GradScaler's)
+            for ws in dirty:
+                ws.unchecked = False
+                flag = torch.maximum(flag, ws.status_word().ne(0).float().reshape(()))
+                if ws.guard_event is None:  # report it at the next step
+                    ws.status_host.copy_(ws.status_word(), non_blocking=True)
+                    ws.guard_event = torch.cuda.Event()
+                    ws.guard_event.record()
+        prev = getattr(optimizer, "found_inf", None)
+        _guarded[id(optimizer)] = prev
+        optimizer.found_inf = (flag if prev is None else
+                               torch.maximum(flag, prev.to(dev).float().reshape(())))
+        return
+    for ws in dirty:
+        dev = ws.buf.device
+        with torch.cuda.device(dev):
+            if torch.cuda.is_current_stream_capturing():
+                return
+            torch.cuda.synchronize(dev)
+        ws.unchecked = False
+        status = int(ws.status_word().item())
+        if status != 0:
+            _raise_expired(ws, "found before optimizer.step(); the step did not run", status)
+
+
+def _restore_after_step(optimizer, args, kwargs):
+    key = id(optimizer)
+    if key not in _guarded:
+        return
+    prev = _guarded.pop(key)
+    if prev is None:
+        if hasattr(optimizer, "found_inf"):
+            del optimizer.found_inf
+    else:
+        optimizer.found_inf = prev
+
+
+def _install_step_check() -> None:
+    global _step_hook
+    if _step_hook is None:
+        from torch.optim.optimizer import (register_optimizer_step_post_hook,
+                                           register_optimizer_step_pre_hook)
+        _step_hook = (register_optimizer_step_pre_hook(_check_before_step),
+                      register_optimizer_step_post_hook(_restore_after_step))
 
 
 def release_workspaces() -> None:
@@ -174,14 +281,12 @@ class _Prepared:
                 _lib.check(st, self.name)
             ws.queue_probe()
             return out
-        key = None if noise_key is None else ctypes.byref(
-            _lib.NoiseKey(noise_key[0] & _U64, noise_key[1] & _U64))
+        key = None if noise_key is None else _lib.noise_key(noise_key)
         args = (a.data_ptr(), b.data_ptr(), *self.dims, float(C), float(clamp), None,
                 float(out_scale), None, float(noise_scale), key, out.data_ptr(),
                 self.out_shape[1], self.odt, None, None, self.flags)
         if self.bias:
-            bkey = None if bias_noise_key is None else ctypes.pointer(
-                _lib.NoiseKey(bias_noise_key[0] & _U64, bias_noise_key[1] & _U64))
+            bkey = _lib.noise_key(bias_noise_key)
             bias = _lib.BiasOut(bias_out.data_ptr(), _lib.dtype_code(bias_out.dtype),
                                 float(bias_scale), None, float(bias_noise_scale), bkey, None, None)
             st = self.fn(*args, ctypes.byref(bias), ws.buf.data_ptr(), ws.buf.numel(), stream)
@@ -193,7 +298,6 @@ class _Prepared:
         return out
 
 
-_U64 = 2**64 - 1
 _prepared: dict = {}
 
 

@@ -120,17 +120,29 @@ __device__ __forceinline__ void box_muller(uint32_t a, uint32_t b, float& z0, fl
 }
 
 // Noise of one output: an injected tensor z (row-major, dtype `dtype`) or, when
-// `draw`, the Philox stream of fdp_noise_key (counter block offset + e/4,
-// counter word 2 = stream).
+// `draw`, the Philox stream of fdp_noise_key (counter block offset (+ *ctr) +
+// e/4, counter word 2 = stream).  ctr: the key's device counter (read when the
+// kernel runs; nullptr: none).
 struct NoiseSrc {
   const void* z;
   int dtype;
   bool draw;
   uint32_t k0, k1, stream;
   uint64_t offset;
+  const uint64_t* ctr;
   __device__ __forceinline__ bool on() const { return z != nullptr || draw; }
+  // A copy with the device counter added to the offset (one read per copy:
+  // kernels take it once for their main output).
+  __device__ __forceinline__ NoiseSrc resolved() const {
+    NoiseSrc n = *this;
+    if (n.draw && n.ctr != nullptr) {
+      n.offset += *n.ctr;
+      n.ctr = nullptr;
+    }
+    return n;
+  }
   __device__ __forceinline__ void block(int64_t q, float (&o)[4]) const {
-    const uint64_t c = offset + static_cast<uint64_t>(q);
+    const uint64_t c = offset + (ctr != nullptr ? *ctr : 0ull) + static_cast<uint64_t>(q);
     const U32x4 r = philox4x32_10(static_cast<uint32_t>(c), static_cast<uint32_t>(c >> 32), stream,
                                   0u, k0, k1);
     box_muller(r.w[0], r.w[1], o[0], o[1]);
@@ -226,6 +238,7 @@ inline NoiseSrc make_noise(const void* z, int dtype, const fdp_noise_key* key, u
     n.k0 = static_cast<uint32_t>(key->seed);
     n.k1 = static_cast<uint32_t>(key->seed >> 32);
     n.offset = key->offset;
+    n.ctr = key->counter;
   }
   return n;
 }

@@ -39,18 +39,22 @@ inline bool get_f32(PyObject* o, float* f) {
   *f = static_cast<float>(d);
   return true;
 }
-// (seed, offset) or None
+// (seed, offset), (seed, offset, device counter address) or None
 inline bool get_key(PyObject* o, fdp_noise_key* k, bool* has) {
   *has = false;
   if (o == Py_None) return true;
-  if (!PyTuple_Check(o) || PyTuple_GET_SIZE(o) != 2) {
-    PyErr_SetString(PyExc_TypeError, "noise key must be (seed, offset) or None");
+  const Py_ssize_t n = PyTuple_Check(o) ? PyTuple_GET_SIZE(o) : 0;
+  if (n != 2 && n != 3) {
+    PyErr_SetString(PyExc_TypeError, "noise key must be (seed, offset[, counter]) or None");
     return false;
   }
   uint64_t s = 0, off = 0;
+  void* ctr = nullptr;
   if (!get_u64(PyTuple_GET_ITEM(o, 0), &s) || !get_u64(PyTuple_GET_ITEM(o, 1), &off)) return false;
+  if (n == 3 && !get_ptr(PyTuple_GET_ITEM(o, 2), &ctr)) return false;
   k->seed = s;
   k->offset = off;
+  k->counter = static_cast<const uint64_t*>(ctr);
   *has = true;
   return true;
 }

@@ -2254,4 +2254,4 @@ extern "C" const char* fdp_strerror(int status) {
   }
 }
 
-extern "C" int fdp_version(void) { return 100; }
+extern "C" int fdp_version(void) { return 200; }

@@ -146,7 +146,7 @@ __global__ __launch_bounds__(NT) void wgrad_sum_kernel(Args p) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
   const bool single = p.groups == 1;
-  const NoiseSrc nz = p.noise;
+  const NoiseSrc nz = p.noise.resolved();
   const float scale = any ? c_prev * (single ? p.out_scale : 1.f) : 0.f;
 #pragma unroll
   for (int i = 0; i < 2; ++i)
@@ -172,7 +172,7 @@ __global__ __launch_bounds__(NT) void wgrad_sum_kernel(Args p) {
 // out = out_scale * sum_g group_out[g] + noise_scale * noise, fixed order in g.
 __global__ __launch_bounds__(NT) void wgrad_finalize_kernel(Args p) {
   const int64_t MN = p.M * p.N;
-  const NoiseSrc nz = p.noise;
+  const NoiseSrc nz = p.noise.resolved();
   for (int64_t e = int64_t(blockIdx.x) * NT + threadIdx.x; e < MN; e += int64_t(gridDim.x) * NT) {
     float s = 0.f;
     for (int g = 0; g < p.groups; ++g) s += p.group_out[int64_t(g) * MN + e];
@@ -650,7 +650,7 @@ namespace {
 // Workspace of fdp_wgrad_bias_clip (every part 256-aligned): the weight
 // gradient's workspace, the column-sum kernel's (the bias when the generic
 // schedule runs), then the bias partials of the grouped and streamed kernels
-// (bias_part [len, B, P], bias_sq [B, tiles], sized for both tile grids).
+// (bias_part [B, P, len], bias_sq [B, tiles], sized for both tile grids).
 struct BiasLayout {
   size_t wspan, col_off, part_off, sq_off, total;
 };

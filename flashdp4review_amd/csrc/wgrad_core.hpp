@@ -70,7 +70,7 @@ struct Args {
   int bias_op;            // 0: no bias
   int bias_P;             // tiles along the other axis: partials per (column, sample)
   int64_t bias_len;       // M (bias_op 1) or N (bias_op 2)
-  float* bias_part;       // [bias_len, B, bias_P] column sums over a tile's counted k-tiles
+  float* bias_part;       // [B, bias_P, bias_len] column sums over a tile's counted k-tiles
   float* bias_sq;         // [B, tiles] sums of squares over a tile's counted k-tiles
   void* bias_out;
   int bias_dtype;
@@ -420,8 +420,8 @@ __device__ __forceinline__ void tile_coords(const Args& p, int tile, int64_t& m0
 // is counted once: in the tile grid, k-tile kt of a sample is counted by the
 // tile whose index along the other axis is kt % P (P tiles there), and k-step
 // ks by the wave with (ks & 1) == its index among the two waves that share the
-// fragment.  A tile's column sums go to bias_part[c][b][other] (an output's
-// B * P partials are contiguous), its sum of squares to bias_sq[b][tile].
+// fragment.  A tile's column sums go to bias_part[b][other][c] (a row of
+// the tile's columns is contiguous), its sum of squares to bias_sq[b][tile].
 
 // acc + x.lo + x.hi and acc + x.lo^2 + x.hi^2 for two packed 16-bit values.
 template <class DT>
@@ -491,88 +491,102 @@ __device__ __forceinline__ void bias_fold(float (&cs)[NF], float& sq, float* bco
   sq = 0.f;
 }
 // The folded partials of sample b in tile `tile` (local columns [0, W) from
-// column c0; the two waves sharing a fragment added in wave order).
+// column c0; the two waves sharing a fragment added in wave order): one row
+// of bias_part [B][P][len] (coalesced stores) and one bias_sq entry.
 template <int W>
 __device__ __forceinline__ void bias_store(const Args& p, const float* bcol, const float* bred,
                                            int64_t b, int tile, int tiles, int64_t c0, int other) {
+  float* row = p.bias_part + (b * p.bias_P + other) * p.bias_len + c0;
   for (int t = threadIdx.x; t < W; t += NT) {
-    const int64_t c = c0 + t;
-    if (c < p.bias_len)
-      st_coherent(p.bias_part + (c * p.B + b) * p.bias_P + other, bcol[t] + bcol[W + t]);
+    if (c0 + t < p.bias_len) st_coherent(row + t, bcol[t] + bcol[W + t]);
   }
   if (threadIdx.x == 0)
     st_coherent(p.bias_sq + b * tiles + tile, (bred[0] + bred[1]) + (bred[2] + bred[3]));
 }
 
 // Outputs [wg * kBiasCols, ...) (and every nwg * kBiasCols after) of the bias
-// from the partials of all B samples: per output, the samples in four
-// contiguous quarters (thread q of the output), each the fixed-order sum of
-// c'_b times the sample's P partials, then the quarters in order -- a fixed
-// summation order, so the result is deterministic.  The clip factors are
-// formed kBiasFacBlock at a time into LDS (wave w: samples w, w + 4, ...).
+// from the partials of all B samples.  A workgroup first forms the clip
+// factors of up to kBiasFacBlock samples into LDS (L = NT / samples threads
+// per sample, each summing a strided part of the sample's tiles, then a
+// butterfly over the L lanes), then kBiasLanes threads per output each add
+// c'_b * partial over a contiguous range of the (sample, partial) pairs, and
+// the ranges are added in order: a fixed summation order for a given shape,
+// so the result is deterministic.  Every load of a round is issued before
+// any is used (one round trip for the factors, one for the partials).
 // Workgroup 0 writes bias_norms / bias_factors.  Every thread of the
 // workgroup calls it.
-constexpr int kBiasCols = 64;
-constexpr int kBiasFacBlock = 256;
+constexpr int kBiasCols = 16;
+constexpr int kBiasLanes = NT / kBiasCols;  // threads per output
+constexpr int kBiasFacBlock = NT;
 struct BiasSmem {
   float fac[kBiasFacBlock];
   float red[NT];
 };
+__device__ inline void bias_factors(const Args& p, int tiles, int64_t fb, int nb, bool writer,
+                                    bool poisoned, float C, float clamp, float* fac) {
+  int L = kWave;
+  while (L > 1 && L * nb > NT) L >>= 1;  // power of two: a sample's lanes lie in one wavefront
+  const int s = threadIdx.x / L, r = threadIdx.x % L;
+  float v = 0.f;
+  if (s < nb) {
+    const float* sq = p.bias_sq + (fb + s) * tiles;
+    for (int t0 = r; t0 < tiles; t0 += 8 * L) {
+      float x[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = t0 + e * L < tiles ? ld_coherent(sq + t0 + e * L) : 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v += x[e];
+    }
+  }
+  for (int off = L >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  if (s < nb && r == 0) {
+    const float n = poisoned ? __builtin_nanf("") : sqrtf(v);
+    const float cf = poisoned ? n : clip_factor(n, C, clamp);
+    fac[s] = cf;
+    if (writer) {
+      if (p.bias_norms) p.bias_norms[fb + s] = n;
+      if (p.bias_factors) p.bias_factors[fb + s] = cf;
+    }
+  }
+}
 __device__ inline void bias_finish(const Args& p, int tiles, int wg, int nwg, bool poisoned,
                                    BiasSmem& sm) {
-  static_assert(NT == 4 * kBiasCols, "four threads per output");
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int q = threadIdx.x / kBiasCols, cl = threadIdx.x % kBiasCols;
   float C = p.C, clamp = p.clamp;
   if (p.clip_args_dev != nullptr) {
     C = p.clip_args_dev[0];
     clamp = p.clip_args_dev[1];
   }
-  const int64_t B = p.B;
+  const int64_t B = p.B, len = p.bias_len;
   const int P = p.bias_P;
-  for (int64_t c0 = int64_t(wg) * kBiasCols; c0 < p.bias_len; c0 += int64_t(nwg) * kBiasCols) {
+  for (int64_t c0 = int64_t(wg) * kBiasCols; c0 < len; c0 += int64_t(nwg) * kBiasCols) {
     const int64_t c = c0 + cl;
     float acc = 0.f;
     for (int64_t fb = 0; fb < B; fb += kBiasFacBlock) {
       const int nb = B - fb < kBiasFacBlock ? static_cast<int>(B - fb) : kBiasFacBlock;
-      for (int s = wave; s < nb; s += NT / kWave) {
-        const float* sq = p.bias_sq + (fb + s) * tiles;
-        float v = 0.f;
-        for (int t = lane; t < tiles; t += kWave) v += ld_coherent(sq + t);
-        v = wave_sum(v);
-        if (lane == 0) {
-          const float n = poisoned ? __builtin_nanf("") : sqrtf(v);
-          const float cf = poisoned ? n : clip_factor(n, C, clamp);
-          sm.fac[s] = cf;
-          if (wg == 0 && c0 == 0) {
-            if (p.bias_norms) p.bias_norms[fb + s] = n;
-            if (p.bias_factors) p.bias_factors[fb + s] = cf;
-          }
-        }
-      }
+      bias_factors(p, tiles, fb, nb, wg == 0 && c0 == 0, poisoned, C, clamp, sm.fac);
       __syncthreads();
-      const int s0 = (q * nb) / 4, s1 = ((q + 1) * nb) / 4;
-      if (c < p.bias_len) {
-        const float* src = p.bias_part + (c * B + fb) * P;
-        for (int s = s0; s < s1; ++s) {
-          float v = 0.f;
-          for (int u0 = 0; u0 < P; u0 += 8) {
-            float x[8];
+      const int npair = nb * P;
+      const int j0 = (q * npair) / kBiasLanes, j1 = ((q + 1) * npair) / kBiasLanes;
+      if (c < len) {
+        const float* src = p.bias_part + fb * P * len + c;  // pair j = (sample, partial) at j * len
+        for (int j = j0; j < j1; j += 8) {
+          float x[8];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) x[e] = u0 + e < P ? ld_coherent(src + s * P + u0 + e) : 0.f;
+          for (int e = 0; e < 8; ++e) x[e] = j + e < j1 ? ld_coherent(src + (j + e) * len) : 0.f;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) v += x[e];
-          }
-          acc += sm.fac[s] * v;
+          for (int e = 0; e < 8; ++e)
+            if (j + e < j1) acc += sm.fac[(j + e) / P] * x[e];
         }
       }
       __syncthreads();  // the factors are read before the next block replaces them
     }
     sm.red[threadIdx.x] = acc;
     __syncthreads();
-    if (q == 0 && c < p.bias_len) {
-      float v = ((sm.red[cl] + sm.red[kBiasCols + cl]) + sm.red[2 * kBiasCols + cl]) +
-                sm.red[3 * kBiasCols + cl];
+    if (q == 0 && c < len) {
+      float v = 0.f;
+#pragma unroll
+      for (int k = 0; k < kBiasLanes; ++k) v += sm.red[k * kBiasCols + cl];
       v *= p.bias_scale;
       if (p.bias_noise.on()) v += p.bias_noise_scale * p.bias_noise.at(c);
       if (poisoned) v = __builtin_nanf("");
@@ -822,7 +836,7 @@ __device__ __attribute__((noinline)) Z8 noise8_draw(NoiseSrc nz, int64_t N, int6
 }
 // Only the last launch of a batch adds noise.
 __device__ inline void noise8(const Args& p, int64_t m, int64_t n, float (&z)[8]) {
-  const NoiseSrc nz = p.noise;  // a value copy: no address of the kernel argument is taken
+  const NoiseSrc nz = p.noise.resolved();  // a value copy: no address of the kernel argument is taken
   if (!p.chunk_last || !nz.on()) return;
   const Z8 d = noise8_draw(nz, p.N, m, n);
 #pragma unroll

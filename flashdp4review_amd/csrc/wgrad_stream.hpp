@@ -265,7 +265,7 @@ __device__ inline void store_half(const Args& p, int64_t m0, int64_t n0, int h,
     constexpr int CPR = G::BN / E;
     S* out = static_cast<S*>(p.out);
     const bool vec = (reinterpret_cast<uintptr_t>(out) % 16 == 0) && (p.ldo % E == 0);
-    const NoiseSrc nz = p.noise;  // a value copy: no address of the kernel argument is taken
+    const NoiseSrc nz = p.noise.resolved();  // a value copy: no address of the kernel argument is taken
   const int zvec = noise_chunks<E>(nz, p.N);
 #pragma unroll 1
     for (int q = threadIdx.x; q < G::WM * CPR; q += NT) {
@@ -514,7 +514,7 @@ hipError_t launch_clipsum(Args a, const StreamPlan& sp, hipStream_t s) {
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   int64_t nfin = (a.bias_len + kBiasCols - 1) / kBiasCols;
-  if (nfin > 1024) nfin = 1024;
+  if (nfin > 2048) nfin = 2048;
   hipLaunchKernelGGL(bias_finish_kernel<0>, dim3(static_cast<unsigned>(nfin)), dim3(NT), 0, s, a,
                      tiles);
   return hipGetLastError();

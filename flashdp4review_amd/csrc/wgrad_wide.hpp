@@ -187,7 +187,7 @@ __global__ __launch_bounds__(kWideThreads, 1) void wgrad_wide_kernel(WideArgs p)
   // most 9 blocks) and whole blocks per row (N % 4 == 0, no injected tensor)
   // the draws happen during the product phase, one per k-tile while the
   // matrix cores work, into LDS; otherwise in the finish.
-  const NoiseSrc nz = p.noise;
+  const NoiseSrc nz = p.noise.resolved();
   const bool noisy = nz.on();
   const bool pre_noise = noisy && nz.z == nullptr && p.N % 4 == 0 && rb1 - rb0 <= kPreNoiseBlocks;
   __shared__ f32x4 zpre[kPreNoiseBlocks * 128 * 2];

@@ -28,7 +28,7 @@ from torch.autograd.function import Function
 from ..core import layernorm_bwd_clip, layernorm_fwd
 from ..core.layernorm import check_fused_row
 from .utils import DPParameter as Parameter
-from .utils import NoiseStream, draw_noise, noise_std
+from .utils import NoiseStream, advance_noise, draw_noise, noise_counter, noise_std
 
 
 class DPLayerNorm(nn.LayerNorm):
@@ -63,6 +63,7 @@ class DPLayerNorm(nn.LayerNorm):
         self.reset_parameters()
         self.noise_generator = None
         self.noise_stream = NoiseStream()
+        self.register_buffer("noise_counter", noise_counter(device), persistent=False)
         self.record_stats = False
         self.last_stats = None
 
@@ -96,32 +97,35 @@ class _DPLayerNormFunction(Function):
         ctx.param_dtype = None if weight is None else weight.dtype
         ctx.has_bias = bias is not None
         ctx.cfg = (float(module.C), float(module.clamp_value), float(module.noise_multiplier),
-                   module.noise_generator, module.noise_stream)
+                   module.noise_generator, module.noise_stream, module.noise_counter)
         ctx.module = module if module.record_stats else None
         return y.reshape(input.shape)
 
     @staticmethod
     def backward(ctx, grad_output):
         x, w, mean, rstd = ctx.saved_tensors
-        C, clamp_value, sigma, gen, nstream = ctx.cfg
+        C, clamp_value, sigma, gen, nstream, counter = ctx.cfg
         H = x.shape[-1]
         B = x.shape[0] if x.dim() > 1 else 1
         std = noise_std(sigma, B, C)
         need_dw = w is not None and ctx.needs_input_grad[1]
         need_db = ctx.has_bias and ctx.needs_input_grad[2]
         zw = zb = key = None
+        adv = 0
         if std > 0 and (need_dw or need_db):
             if gen is not None:
                 zw = draw_noise((H,), ctx.param_dtype, x.device, gen) if need_dw else None
                 zb = draw_noise((H,), ctx.param_dtype, x.device, gen) if need_db else None
             else:  # one key: dgamma draws counter stream 0, dbeta stream 1
-                key = nstream.next(H)
+                keys, adv = nstream.keys([H], counter)
+                key = keys[0]
         r = layernorm_bwd_clip(grad_output.reshape(x.shape), x, w, mean, rstd, C, clamp_value,
                                out_scale=1.0 / B, noise_w=zw, noise_b=zb, noise_scale=std,
                                noise_key=key,
                                need_dw=need_dw, need_db=need_db,
                                param_dtype=ctx.param_dtype or x.dtype,
                                return_stats=ctx.module is not None)
+        advance_noise(counter, adv)
         if ctx.module is not None:
             dx, dw, db, norms, factors = r
             ctx.module.last_stats = {"norms_w": norms[:B], "fac_w": factors[:B],

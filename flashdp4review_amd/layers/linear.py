@@ -22,7 +22,7 @@ from torch.autograd.function import Function
 from ..core import colsum_clip, wgrad_clip
 from ..core.utils import RuntimeAutoTuner
 from .utils import DPParameter as Parameter
-from .utils import NoiseStream, as_btf, noise_args, noise_std
+from .utils import NoiseStream, advance_noise, as_btf, noise_counter, noise_draws, noise_std
 
 
 class DPLinear(nn.Linear):
@@ -49,6 +49,7 @@ class DPLinear(nn.Linear):
         # torch.Generator is set here, drawn with it (z_W first, then z_b).
         self.noise_generator = None
         self.noise_stream = NoiseStream()
+        self.register_buffer("noise_counter", noise_counter(device), persistent=False)
         # When True, backward stores per-sample norms / clip factors in last_stats.
         self.record_stats = False
         self.last_stats = None
@@ -65,7 +66,7 @@ class _DPLinearFunction(Function):
         ctx.has_bias = bias is not None
         ctx.bias_dtype = bias.dtype if bias is not None else None
         ctx.cfg = (float(module.C), float(module.clamp_value), float(module.noise_multiplier),
-                   module.noise_generator, module.noise_stream)
+                   module.noise_generator, module.noise_stream, module.noise_counter)
         ctx.module = module if module.record_stats else None
         w = weight if weight.dtype == input.dtype else weight.to(input.dtype)
         b = None if bias is None else (bias if bias.dtype == input.dtype else bias.to(input.dtype))
@@ -74,7 +75,7 @@ class _DPLinearFunction(Function):
     @staticmethod
     def backward(ctx, grad_output):
         input, weight = ctx.saved_tensors
-        C, clamp_value, sigma, gen, nstream = ctx.cfg
+        C, clamp_value, sigma, gen, nstream, counter = ctx.cfg
         x3, g3 = as_btf(input), as_btf(grad_output)
         B, T = x3.shape[0], x3.shape[1]
         std = noise_std(sigma, B, C)
@@ -84,19 +85,24 @@ class _DPLinearFunction(Function):
             w = weight if weight.dtype == g3.dtype else weight.to(g3.dtype)
             grad_input = (g3 @ w).reshape(input.shape)
         want_bias = ctx.has_bias and ctx.needs_input_grad[2]
+        O = g3.shape[-1]
         if ctx.needs_input_grad[1]:
-            z, key = noise_args(std, gen, nstream, weight.shape, weight.dtype, weight.device)
+            # both in one call when the bias is needed (noise in the order weight, bias)
+            shapes, dts = [tuple(weight.shape)], [weight.dtype]
+            if want_bias:
+                shapes.append((O,))
+                dts.append(ctx.bias_dtype)
+            zs, keys, adv = noise_draws(std, gen, nstream, shapes, dts, g3.device, counter)
             extra = {}
-            if want_bias:  # both in one call (noise drawn in the same order: weight, bias)
-                O = g3.shape[-1]
-                zb, keyb = noise_args(std, gen, nstream, (O,), ctx.bias_dtype, g3.device)
+            if want_bias:
                 grad_bias = torch.empty(O, dtype=ctx.bias_dtype, device=g3.device)
-                extra = dict(bias_out=grad_bias, bias_scale=1.0 / (B * T), bias_noise=zb,
-                             bias_noise_scale=std, bias_noise_key=keyb)
+                extra = dict(bias_out=grad_bias, bias_scale=1.0 / (B * T), bias_noise=zs[1],
+                             bias_noise_scale=std, bias_noise_key=keys[1])
             r = wgrad_clip(g3.contiguous() if want_bias else g3, x3.to(g3.dtype), C, clamp_value,
-                           layout="tn", out_scale=1.0 / B, noise=z, noise_scale=std,
-                           noise_key=key, out_dtype=weight.dtype,
+                           layout="tn", out_scale=1.0 / B, noise=zs[0], noise_scale=std,
+                           noise_key=keys[0], out_dtype=weight.dtype,
                            return_stats=stats is not None, **extra)
+            advance_noise(counter, adv)
             if stats is not None:
                 grad_weight, stats["norms_w"], stats["fac_w"] = r[:3]
                 if want_bias:
@@ -105,11 +111,12 @@ class _DPLinearFunction(Function):
                 grad_weight = r
             want_bias = False
         if want_bias:
-            O = g3.shape[-1]
-            z, key = noise_args(std, gen, nstream, (O,), ctx.bias_dtype, g3.device)
+            zs, keys, adv = noise_draws(std, gen, nstream, [(O,)], [ctx.bias_dtype], g3.device,
+                                        counter)
             r = colsum_clip(g3, None, C, clamp_value, norm="frob", out_scale=1.0 / (B * T),
-                            noise=z, noise_scale=std, noise_key=key, out_dtype=ctx.bias_dtype,
-                            return_stats=stats is not None)
+                            noise=zs[0], noise_scale=std, noise_key=keys[0],
+                            out_dtype=ctx.bias_dtype, return_stats=stats is not None)
+            advance_noise(counter, adv)
             if stats is not None:
                 grad_bias, stats["norms_b"], stats["fac_b"] = r
             else:

@@ -24,7 +24,7 @@ from torch.autograd.function import Function
 from ..core import colsum_clip, wgrad_clip
 from ..core.utils import RuntimeAutoTuner
 from .utils import DPParameter as Parameter
-from .utils import NoiseStream, as_btf, noise_args, noise_std
+from .utils import NoiseStream, advance_noise, as_btf, noise_counter, noise_draws, noise_std
 
 try:  # the HF module type is what wrap_with_flashdp_layers replaces
     from transformers.pytorch_utils import Conv1D as _HFConv1D
@@ -63,6 +63,7 @@ class DPConv1D(_Base):
         nn.init.normal_(self.weight, std=0.02)
         self.noise_generator = None
         self.noise_stream = NoiseStream()
+        self.register_buffer("noise_counter", noise_counter(), persistent=False)
         self.record_stats = False
         self.last_stats = None
 
@@ -79,7 +80,7 @@ class _DPConv1DFunction(Function):
         ctx.save_for_backward(input, weight)
         ctx.bias_dtype = bias.dtype
         ctx.cfg = (float(module.C), float(module.clamp_value), float(module.noise_multiplier),
-                   module.noise_generator, module.noise_stream)
+                   module.noise_generator, module.noise_stream, module.noise_counter)
         ctx.module = module if module.record_stats else None
         w = weight if weight.dtype == input.dtype else weight.to(input.dtype)
         b = bias if bias.dtype == input.dtype else bias.to(input.dtype)
@@ -89,7 +90,7 @@ class _DPConv1DFunction(Function):
     @staticmethod
     def backward(ctx, grad_output):
         input, weight = ctx.saved_tensors
-        C, clamp_value, sigma, gen, nstream = ctx.cfg
+        C, clamp_value, sigma, gen, nstream, counter = ctx.cfg
         x3, g3 = as_btf(input), as_btf(grad_output)
         B, T = x3.shape[0], x3.shape[1]
         std = noise_std(sigma, B, C)
@@ -99,19 +100,24 @@ class _DPConv1DFunction(Function):
             w = weight if weight.dtype == g3.dtype else weight.to(g3.dtype)
             grad_input = (g3 @ w.t()).reshape(input.shape)
         want_bias = ctx.needs_input_grad[2]
+        O = g3.shape[-1]
         if ctx.needs_input_grad[1]:
-            z, key = noise_args(std, gen, nstream, weight.shape, weight.dtype, weight.device)
+            # both in one call when the bias is needed (noise in the order weight, bias)
+            shapes, dts = [tuple(weight.shape)], [weight.dtype]
+            if want_bias:
+                shapes.append((O,))
+                dts.append(ctx.bias_dtype)
+            zs, keys, adv = noise_draws(std, gen, nstream, shapes, dts, g3.device, counter)
             extra = {}
-            if want_bias:  # both in one call (noise drawn in the same order: weight, bias)
-                O = g3.shape[-1]
-                zb, keyb = noise_args(std, gen, nstream, (O,), ctx.bias_dtype, g3.device)
+            if want_bias:
                 grad_bias = torch.empty(O, dtype=ctx.bias_dtype, device=g3.device)
-                extra = dict(bias_out=grad_bias, bias_scale=1.0 / (B * T), bias_noise=zb,
-                             bias_noise_scale=std, bias_noise_key=keyb, bias_operand="b")
+                extra = dict(bias_out=grad_bias, bias_scale=1.0 / (B * T), bias_noise=zs[1],
+                             bias_noise_scale=std, bias_noise_key=keys[1], bias_operand="b")
             r = wgrad_clip(x3.to(g3.dtype), g3.contiguous() if want_bias else g3, C, clamp_value,
-                           layout="tn", out_scale=1.0 / B, noise=z, noise_scale=std,
-                           noise_key=key, out_dtype=weight.dtype,
+                           layout="tn", out_scale=1.0 / B, noise=zs[0], noise_scale=std,
+                           noise_key=keys[0], out_dtype=weight.dtype,
                            return_stats=stats is not None, **extra)
+            advance_noise(counter, adv)
             if stats is not None:
                 grad_weight, stats["norms_w"], stats["fac_w"] = r[:3]
                 if want_bias:
@@ -120,10 +126,12 @@ class _DPConv1DFunction(Function):
                 grad_weight = r
             want_bias = False
         if want_bias:
-            z, key = noise_args(std, gen, nstream, (g3.shape[-1],), ctx.bias_dtype, g3.device)
+            zs, keys, adv = noise_draws(std, gen, nstream, [(O,)], [ctx.bias_dtype], g3.device,
+                                        counter)
             r = colsum_clip(g3, None, C, clamp_value, norm="frob", out_scale=1.0 / (B * T),
-                            noise=z, noise_scale=std, noise_key=key, out_dtype=ctx.bias_dtype,
-                            return_stats=stats is not None)
+                            noise=zs[0], noise_scale=std, noise_key=keys[0],
+                            out_dtype=ctx.bias_dtype, return_stats=stats is not None)
+            advance_noise(counter, adv)
             if stats is not None:
                 grad_bias, stats["norms_b"], stats["fac_b"] = r
             else:

@@ -72,32 +72,82 @@ def draw_noise(shape, dtype, device, generator) -> torch.Tensor:
     return torch.randn(shape, dtype=dtype, device=device, generator=generator)
 
 
+def noise_blocks(numel: int) -> int:
+    """Philox counter blocks of an output of numel elements (four normals each)."""
+    return (int(numel) + 3) // 4
+
+
 class NoiseStream:
-    """Keys of one DP module's in-kernel Gaussian draws (fdp_noise_key): a 64-bit
-    Philox seed taken from torch's default CPU generator at the first draw (so
-    torch.manual_seed makes a run reproducible) and a counter offset advanced
-    past every draw (an output of n elements uses ceil(n / 4) counter blocks).
-    The reference draws the same N(0, 1) noise with torch.normal
-    (flashdp/layers/linear.py:74-80); drawing it in the output epilogue saves
-    writing and re-reading a noise tensor per parameter."""
+    """Keys of one DP module's in-kernel Gaussian draws (fdp_noise_key).
+
+    Eager calls: a 64-bit Philox seed taken from torch's default CPU generator
+    at the first draw (so torch.manual_seed makes a run reproducible) and a
+    counter offset advanced on the host past every draw (an output of n
+    elements uses ceil(n / 4) counter blocks).
+    Calls captured into a HIP graph: a second seed, the module's device counter
+    (``counter``, an int64 [1] buffer) read by the kernels when they run, and a
+    device-side advance of that counter after the call (fdp_noise_advance), so
+    that every replay of the graph draws fresh noise.  The two seeds keep eager
+    and replayed draws apart.
+    The reference draws the same N(0, 1) noise with torch.normal on the device
+    generator (flashdp/layers/linear.py:74-80), whose offset torch's graphs
+    also advance per replay; drawing it in the output epilogue saves writing
+    and re-reading a noise tensor per parameter."""
 
     def __init__(self):
         self.seed = None
+        self.graph_seed = None
         self.offset = 0
 
-    def next(self, numel: int) -> tuple[int, int]:
+    def _seeds(self):
         if self.seed is None:
-            self.seed = int(torch.randint(0, 2**62, (1,), dtype=torch.int64).item())
+            s = torch.randint(0, 2**62, (2,), dtype=torch.int64)
+            self.seed, self.graph_seed = int(s[0]), int(s[1])
+
+    def next(self, numel: int) -> tuple[int, int]:
+        """The eager key of one output of numel elements."""
+        self._seeds()
         key = (self.seed, self.offset)
-        self.offset += (int(numel) + 3) // 4
+        self.offset += noise_blocks(numel)
         return key
 
+    def keys(self, sizes, counter: torch.Tensor | None = None):
+        """Keys of one call's outputs (sizes in elements, in draw order) and the
+        counter blocks to advance ``counter`` by after the call (0: none).
+        Under graph capture (with a device counter) the keys read the counter;
+        otherwise they are the next eager keys."""
+        if counter is not None and counter.is_cuda and torch.cuda.is_current_stream_capturing():
+            self._seeds()
+            keys, off = [], 0
+            for n in sizes:
+                keys.append((self.graph_seed, off, counter.data_ptr()))
+                off += noise_blocks(n)
+            return keys, off
+        return [self.next(n) for n in sizes], 0
 
-def noise_args(std: float, generator, stream: NoiseStream, shape, dtype, device):
-    """(z, key) for one noisy output: nothing at std == 0; an explicit torch draw
-    when the module has a noise_generator; else the next in-kernel key."""
+
+def noise_counter(device=None) -> torch.Tensor:
+    """A DP module's device noise counter (int64 [1], zero): registered as a
+    non-persistent buffer so that it moves with the module."""
+    return torch.zeros(1, dtype=torch.int64, device=device)
+
+
+def noise_draws(std: float, generator, stream: NoiseStream, shapes, dtypes, device,
+                counter: torch.Tensor | None = None):
+    """(z list, key list, counter blocks to advance) for one call's noisy outputs:
+    nothing at std == 0; explicit torch draws (in order) when the module has a
+    noise_generator; else in-kernel keys (NoiseStream.keys)."""
+    n = len(shapes)
     if std <= 0:
-        return None, None
+        return [None] * n, [None] * n, 0
     if generator is not None:
-        return draw_noise(shape, dtype, device, generator), None
-    return None, stream.next(math.prod(shape))
+        return [draw_noise(s, dt, device, generator) for s, dt in zip(shapes, dtypes)], [None] * n, 0
+    keys, adv = stream.keys([math.prod(s) for s in shapes], counter)
+    return [None] * n, keys, adv
+
+
+def advance_noise(counter: torch.Tensor | None, blocks: int) -> None:
+    """The device-side advance after a call whose keys read ``counter``."""
+    if blocks:
+        from .. import _lib
+        _lib.noise_advance(counter, blocks)

@@ -67,19 +67,32 @@ typedef enum fdp_layout {
 /* In-kernel Gaussian noise.  Output k of a call (k = 0; the LayerNorm entry
  * point's db is k = 1) gets, at its row-major element e, the (e mod 4)-th of
  * four normals made from the Philox4x32-10 block (Salmon et al., SC'11)
- *   counter {lo32(offset + e/4), hi32(offset + e/4), k, 0}, key {lo32(seed), hi32(seed)}
+ *   counter {lo32(q), hi32(q), k, 0}, key {lo32(seed), hi32(seed)},
+ *   q = offset + e/4 (+ *counter when `counter` is set)
  * whose words (w0, w1) and (w2, w3) each give two normals by Box-Muller:
  *   r = sqrt(-2 ln u_first), z = (r cos 2 pi u_second, r sin 2 pi u_second),
  *   u_first = (w_first + 0.5) / 2^32, u_second = ((w_second >> 8) + 0.5) / 2^24,
  * so |z| <= sqrt(-2 ln 2^-33) = 6.76 (the tail beyond holds about 1.4e-11 of
  * a normal's mass).
- * A call uses counter blocks [offset, offset + ceil(numel / 4)) of each output;
- * callers advance `offset` (or change `seed`) between calls.  The struct is
- * read on the host during the call. */
+ * A call uses counter blocks [offset, offset + ceil(numel / 4)) of each output
+ * (shifted by *counter); callers advance `offset` (or change `seed`) between
+ * calls.  The struct is read on the host during the call.
+ * counter: NULL, or a device pointer to a 64-bit block count that the kernels
+ * read when they run (not when the call is made).  Work captured once into a
+ * HIP graph and replayed then draws fresh noise on every replay if the
+ * caller enqueues fdp_noise_advance(counter, blocks) after the call, in the
+ * same capture (the reference's torch.normal on the device generator does the
+ * same through the generator's offset, flashdp/layers/linear.py:74-80). */
 typedef struct fdp_noise_key {
   uint64_t seed;
   uint64_t offset;
+  const uint64_t* counter;
 } fdp_noise_key;
+
+/* *counter += blocks, stream-ordered (a one-thread kernel; no memset, so it
+ * may be captured into a HIP graph).  No counterpart in the reference: the
+ * device-side advance of a noise key's counter (see fdp_noise_key). */
+int fdp_noise_advance(uint64_t* counter, uint64_t blocks, void* stream);
 
 /* Which per-sample norm drives the clip of a column-sum reduction.
  *   FDP_NORM_SUM:  || sum_t u_bt (.* v_bt) ||_2       (LayerNorm dgamma/dbeta,

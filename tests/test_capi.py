@@ -26,7 +26,7 @@ def header_functions():
 
 def test_library_loads():
     L = _lib.lib()
-    assert L.fdp_version() == 100
+    assert L.fdp_version() == 200
     assert L.fdp_strerror(0) == b"ok"
     assert L.fdp_strerror(4).startswith(b"workspace")
 
@@ -148,3 +148,18 @@ def test_status_to_exception_mapping():
         _lib.check(2, "x")
     with pytest.raises(RuntimeError):
         _lib.check(5, "x")
+
+
+def test_noise_advance_rejects_null_counter():
+    assert _lib.lib().fdp_noise_advance(None, 4, None) == 3
+
+
+def test_bias_of_b_flag_only_with_the_bias_entry_point():
+    """FDP_WGRAD_BIAS_OF_B selects the bias operand of fdp_wgrad_bias_clip;
+    fdp_wgrad_clip rejects it as an unknown flag."""
+    assert _wgrad(flags=_lib.WGRAD_BIAS_OF_B) == 3
+    L = _lib.lib()
+    n_a = _lib.size_query(L.fdp_wgrad_bias_clip_workspace_size, 4, 64, 512, 2048, 2, 0)
+    n_b = _lib.size_query(L.fdp_wgrad_bias_clip_workspace_size, 4, 64, 512, 2048, 2,
+                          _lib.WGRAD_BIAS_OF_B)
+    assert n_a > 0 and n_b > n_a  # the bias partials scale with the bias length (512 vs 2048)

@@ -13,8 +13,12 @@ bf16 models and under autocast.
         every wrapped gradient is the non-DP gradient / B (a property the
         per-sample clipping math fixes: clip factors are all 1, the sum over
         samples is the batch gradient, then 1/B; flashdp/layers/linear.py:72-92,
-        flashdp/layers/layernorm.py:128-165); with C = 1 the recorded per-sample
-        norms of two layers match fp32 per-sample products.
+        flashdp/layers/layernorm.py:128-165); with C at half the smallest
+        per-sample norm (every sample clipped) and sigma = 0, the per-sample
+        norms, clip factors and the clipped dW of
+        c_fc (2048 -> 8192) and mlp_proj (8192 -> 2048) -- the streamed
+        Gram-norm + clipped-sum schedule at B=8, T=1024 -- match fp32
+        per-sample products on the GPU (flashdp/core/linear_clip.py:94-104).
   AMP   an fp32 model wrapped and run under torch.autocast(bfloat16), as the
         reference's example trains (example/gpt2/train.py:77-79), and a bf16
         model: every DP layer's gradients match the oracle on the bf16 tensors
@@ -117,23 +121,31 @@ def test_cfg5_decoder_dp_grads_equal_non_dp_over_batch():
     assert dp.h[0].c_fc.weight.dtype == torch.bfloat16          # the wrap keeps the dtype
     idx = torch.randint(0, 50257, (B, 1025), device=DEV,
                         generator=torch.Generator(device=DEV).manual_seed(0))
+    checked = ("h.0.c_fc", "h.1.mlp_proj")
+    for name in checked:
+        dp.get_submodule(name).record_stats = True
     _loss(base, idx).backward()
     _loss(dp, idx).backward()
+    # a C below every per-sample norm of the two checked layers: all samples clip
+    C = 0.5 * min(float(dp.get_submodule(n).last_stats["norms_w"].min()) for n in checked)
     dp_params = {id(p) for m in dp.modules() if isinstance(m, (DPLinear, DPLayerNorm))
                  for p in m.parameters(recurse=False)}
-    worst = 0.0
+    worst, worst_name = 0.0, ""
     for (name, p), (_, q) in zip(base.named_parameters(), dp.named_parameters()):
         expect = p.grad.float() / B if id(q) in dp_params else p.grad.float()
         e = assert_close(q.grad, expect.double().cpu().numpy(), torch.bfloat16, name)
-        worst = max(worst, e)
+        if e > worst:
+            worst, worst_name = e, name
     from tests._tol import report
-    report("cfg5 decoder (2 blocks, d=2048): DP grad vs non-DP/B, worst tensor", worst, 2e-2)
+    report(f"cfg5 decoder (2 blocks, d=2048), C=inf: DP grad vs non-DP/B, worst ({worst_name})",
+           worst, 2e-2)
 
-    # C = 1: the recorded per-sample norms of two layers against fp32 products
+    # every sample clipped, sigma = 0: norms, factors and the clipped dW of two
+    # layers against fp32 per-sample products
     torch.manual_seed(0)
-    dp1 = _wrapped(copy.deepcopy(base), C=1.0, sigma=1.0)
+    dp1 = _wrapped(copy.deepcopy(base), C=C, sigma=0.0)
     seen = {}
-    for name in ("h.0.c_fc", "h.1.mlp_proj"):
+    for name in checked:
         mod = dp1.get_submodule(name)
         mod.record_stats = True
 
@@ -144,14 +156,21 @@ def test_cfg5_decoder_dp_grads_equal_non_dp_over_batch():
         mod.register_forward_hook(fwd_hook)
     _loss(dp1, idx).backward()
     for name, (x, g) in seen.items():
-        G = per_sample_products(g, x)  # g_b^T x_b
+        G = per_sample_products(g, x)  # g_b^T x_b, fp32
         n_ref = G.flatten(1).norm(dim=1)
-        st = dp1.get_submodule(name).last_stats
+        mod = dp1.get_submodule(name)
+        st = mod.last_stats
         assert_elementwise(st["norms_w"], n_ref.double().cpu().numpy(), torch.bfloat16,
                            f"{name} norms", margin=f"cfg5 {name}: per-sample norms")
-        c_ref = torch.clamp(1.0 / (n_ref + 1e-10), max=1.0)
+        c_ref = torch.clamp(C / (n_ref + 1e-10), max=1.0)
+        assert bool((c_ref < 1.0).all()), f"{name}: every sample clips"
         assert_elementwise(st["fac_w"], c_ref.double().cpu().numpy(), torch.bfloat16,
-                           f"{name} factors")
+                           f"{name} factors", margin=f"cfg5 {name}: clip factors (all clipped)")
+        dw_ref = (c_ref[:, None, None] * G).sum(0) / B
+        del G
+        assert_close(mod.weight.grad, dw_ref.double().cpu().numpy(), torch.bfloat16,
+                     f"{name} clipped dW",
+                     margin=f"cfg5 {name}: clipped dW (all clipped, bf16 out)")
 
 
 # ------------------------------------------------------------------- AMP, bf16

@@ -235,3 +235,127 @@ def test_layers_in_kernel_noise(dtype):
     lin.weight.grad = None
     lin(x).backward(g)
     assert not torch.equal(w1, lin.weight.grad)
+
+
+def test_graph_captured_backward_draws_fresh_noise():
+    """A DPLinear backward (weight and bias, in-kernel noise) captured once into
+    a HIP graph and replayed three times, with eager DP work and
+    synchronisations between the replays: the kernels read the module's device
+    noise counter when they run and fdp_noise_advance (captured with them)
+    moves it on, so every replay draws the next range of the module's graph
+    seed -- the replays differ, and each equals the oracle with the Philox
+    stream at that replay's counter (the reference's torch.normal on the device
+    generator, flashdp/layers/linear.py:74-80, also advances per replay)."""
+    from oracle import philox as PX
+    torch.manual_seed(11)
+    B, T, I, Od = 4, 64, 256, 384
+    dtype = torch.bfloat16
+    lin = DPLinear(I, Od, bias=True, C=1.0, noise_multiplier=1.0).to(DEV, dtype)
+    other = DPLinear(I, Od, bias=True, C=1.0, noise_multiplier=1.0).to(DEV, dtype)
+    x = torch.randn(B, T, I, device=DEV).to(dtype).requires_grad_(True)
+    g = (torch.randn(B, T, Od, device=DEV) * 0.01).to(dtype)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):  # warm-up on the capture stream (its workspace exists)
+        for _ in range(2):
+            lin.weight.grad = lin.bias.grad = x.grad = None
+            lin(x).backward(g)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    lin.weight.grad = lin.bias.grad = x.grad = None
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        lin(x).backward(g)
+    torch.cuda.synchronize()
+    seed = lin.noise_stream.graph_seed
+    assert seed is not None and seed != lin.noise_stream.seed
+    nw = Od * I
+    bw, bb = (nw + 3) // 4, (Od + 3) // 4
+    prev = None
+    for rep in range(3):
+        ctr = int(lin.noise_counter.item())
+        graph.replay()
+        torch.cuda.synchronize()
+        dw, db = lin.weight.grad.clone(), lin.bias.grad.clone()
+        assert int(lin.noise_counter.item()) == ctr + bw + bb
+        zw = torch.tensor(PX.normals(nw, seed, ctr).reshape(Od, I))
+        zb = torch.tensor(PX.normals(Od, seed, ctr + bw))
+        ref = O.linear_backward(x.detach(), g, lin.weight.detach(), 1.0, 1.0, 1.0, zw, zb)
+        assert_close(dw, ref["dw"], dtype, f"replay {rep}: dW")
+        assert_close(db, ref["db"], dtype, f"replay {rep}: db")
+        if prev is not None:
+            assert not torch.equal(prev, dw)
+        prev = dw
+        other.weight.grad = None
+        other(x.detach()).backward(g)  # eager DP work between the replays
+        torch.cuda.synchronize()
+
+
+def test_expired_wait_raises_before_optimizer_step(monkeypatch):
+    """An expired bounded wait in a DP layer's backward (forced from the host:
+    FDP_WGRAD_SPIN_LIMIT=0, every kernel still runs to completion) is reported
+    by the optimizer pre-step check, before the step runs: the parameters stay
+    as they were, and the next step (normal limit) goes through."""
+    from flashdp4review_amd import _lib
+    from flashdp4review_amd.core import wgrad as W
+    assert W._expiry_check == "optimizer_step"
+    torch.manual_seed(12)
+    lin = DPLinear(384, 512, bias=False, C=0.5, noise_multiplier=0.0).to(DEV, torch.bfloat16)
+    opt = torch.optim.SGD(lin.parameters(), lr=0.1)
+    x = torch.randn(8, 1024, 384, device=DEV).to(torch.bfloat16)
+    g = (torch.randn(8, 1024, 512, device=DEV) * 0.02).to(torch.bfloat16)
+    core_status = __import__("flashdp4review_amd.core", fromlist=["wgrad_status"]).wgrad_status
+    core_status()  # start from a clear status word
+    w0 = lin.weight.detach().clone()
+    monkeypatch.setenv("FDP_WGRAD_SPIN_LIMIT", "0")
+    lin(x).backward(g)
+    monkeypatch.delenv("FDP_WGRAD_SPIN_LIMIT")
+    with pytest.raises(_lib.FlashDPError):
+        opt.step()
+    torch.cuda.synchronize()
+    assert torch.isnan(lin.weight.grad.float()).any()
+    assert torch.equal(lin.weight.detach(), w0), "the step ran on NaN gradients"
+    opt.zero_grad(set_to_none=True)
+    lin(x).backward(g)
+    opt.step()
+    assert torch.isfinite(lin.weight.float()).all() and not torch.equal(lin.weight.detach(), w0)
+
+
+def test_expired_wait_skips_a_fused_optimizer_step_on_the_device(monkeypatch):
+    """With an optimizer that can skip a step on the device (fused Adam), the
+    pre-step check sets its found_inf from the status word instead of
+    synchronising: the step on NaN gradients changes neither the parameters
+    nor Adam's state, the next step raises, and training then continues."""
+    from flashdp4review_amd import _lib
+    from flashdp4review_amd.core import wgrad_status
+    torch.manual_seed(13)
+    lin = DPLinear(384, 512, bias=False, C=0.5, noise_multiplier=0.0).to(DEV, torch.bfloat16)
+    opt = torch.optim.Adam(lin.parameters(), lr=1e-2, fused=True)
+    x = torch.randn(8, 1024, 384, device=DEV).to(torch.bfloat16)
+    g = (torch.randn(8, 1024, 512, device=DEV) * 0.02).to(torch.bfloat16)
+    wgrad_status()  # start from a clear status word
+    lin(x).backward(g)
+    opt.step()  # a good step: Adam's state exists
+    opt.zero_grad(set_to_none=True)
+    w = lin.weight
+    w0, st0 = w.detach().clone(), {k: v.clone() for k, v in opt.state[w].items()}
+    monkeypatch.setenv("FDP_WGRAD_SPIN_LIMIT", "0")
+    lin(x).backward(g)
+    monkeypatch.delenv("FDP_WGRAD_SPIN_LIMIT")
+    opt.step()  # skipped on the device
+    torch.cuda.synchronize()
+    assert torch.isnan(w.grad.float()).any()
+    assert torch.equal(w.detach(), w0), "the step ran on NaN gradients"
+    for k, v in opt.state[w].items():
+        assert torch.equal(v, st0[k]), f"Adam state {k} changed"
+    assert not hasattr(opt, "found_inf")
+    opt.zero_grad(set_to_none=True)
+    lin(x).backward(g)
+    with pytest.raises(_lib.FlashDPError):
+        opt.step()
+    assert torch.equal(w.detach(), w0)
+    opt.zero_grad(set_to_none=True)
+    lin(x).backward(g)
+    opt.step()
+    torch.cuda.synchronize()
+    assert torch.isfinite(w.float()).all() and not torch.equal(w.detach(), w0)

@@ -202,3 +202,18 @@ def test_layernorm_fused_row_limit():
     with pytest.raises(RuntimeError) as e:
         DPLayerNorm(40000, use_fused=False)(torch.zeros(1, 2, 40000))
     assert "64KB" not in str(e.value)
+
+
+def test_optimizer_pre_step_check_installs_and_passes_without_workspaces():
+    """The expiry check before optimizer steps installs as a global torch.optim
+    pre-step hook; with no workspace in use it lets every step through."""
+    import torch
+    from flashdp4review_amd.core import wgrad as W
+    W._install_step_check()
+    assert W._step_hook is not None
+    p = torch.nn.Parameter(torch.ones(3))
+    p.grad = torch.ones(3)
+    torch.optim.SGD([p], lr=0.5).step()
+    assert torch.equal(p.detach(), torch.full((3,), 0.5))
+    assert W.set_expiry_check("async") == "optimizer_step"
+    assert W.set_expiry_check("optimizer_step") == "async"
