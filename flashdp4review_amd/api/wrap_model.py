@@ -1,17 +1,34 @@
-"""wrap_with_flashdp_layers: swap supported modules for their DP counterparts.
+"""wrap_with_flashdp_layers: put DP layers in place of a model's Linear,
+LayerNorm and HF Conv1D modules.
 
-Reference: flashdp/api/wrap_model.py:11-276.  Same arguments, selection rules
-and messages.  Selection keeps the reference's behaviour exactly: the
-prefix-expanded groups of _process_layer_groups only drive the skip-name
-validation, and the layers actually wrapped are chosen by _select_layers,
-which matches names exactly (wrap_model.py:83-86,169-182), so skipping a parent
-name does not skip its children.  One deliberate difference: the new module is
-moved to the replaced module's device AND dtype (the reference moves it to the
-device only, wrap_model.py:204-205, so a bf16 model would get fp32 DP layers).
+The call keeps the reference's signature, argument meanings, error types and
+messages (flashdp/api/wrap_model.py:17-68, 71-76), so that existing training
+scripts run unchanged.  How a module is chosen:
+
+  * candidates are the submodules whose type is one of ``target_modules``
+    exactly (a subclass of nn.Linear that is not nn.Linear itself, such as an
+    already wrapped DPLinear or nn.MultiheadAttention's out_proj, is left as
+    it is);
+  * a candidate is replaced when its dotted name is in ``target_layers`` (all
+    names when that is empty) and not in ``skip_layers``.  Names match
+    exactly, as in the reference (flashdp/api/wrap_model.py:169-182): skipping
+    "h.0" does not skip "h.0.fc".  ``priority_to_target`` is accepted; with
+    exact names both of the reference's orders give the same set difference.
+
+The DP module gets the replaced module's weights, training mode, device and
+dtype (the reference moves it to the device only, so a bf16 model would get
+fp32 DP layers).  A LayerNorm without a bias or over more than one trailing
+axis gets the non-fused DPLayerNorm (the fused one requires a bias and one
+axis; both compute the same per-sample math here).  With ``feedback`` the
+names of the layers actually replaced are printed, and the skip list.  A
+module type in
+``target_modules`` that the model does not use draws a warning; skip names are
+checked only after their expansion to the model's own names, as in the
+reference, so an unknown skip name draws none.
 """
 from __future__ import annotations
 
-from typing import List, Type
+from typing import Iterator, List, Tuple, Type
 
 import torch.nn as nn
 
@@ -27,6 +44,39 @@ if _HFConv1D is not None:
     dp_supported_modules[_HFConv1D] = DPConv1D
 
 
+def _walk(module: nn.Module, prefix: str = "") -> Iterator[Tuple[nn.Module, str, nn.Module, str]]:
+    """(parent, attribute name, child, dotted name) of every submodule, a parent
+    before its children (every path, also of a module reachable by two)."""
+    for attr, child in module.named_children():
+        path = prefix + attr
+        yield module, attr, child, path
+        yield from _walk(child, path + ".")
+
+
+def _dp_twin(child: nn.Module, dp_options: dict) -> nn.Module:
+    """The DP module standing in for `child`, with its hyper-parameters."""
+    kind = type(child)
+    if kind is nn.Linear:
+        twin = DPLinear(child.in_features, child.out_features, bias=child.bias is not None,
+                        **dp_options)
+    elif kind is nn.LayerNorm:
+        # the fused mode needs a bias and a 1-D normalized_shape; the non-fused
+        # mode computes the same per-sample math for the others
+        no_bias = child.elementwise_affine and child.bias is None
+        fused = not no_bias and len(child.normalized_shape) == 1
+        twin = DPLayerNorm(child.normalized_shape, eps=child.eps,
+                           elementwise_affine=child.elementwise_affine, bias=not no_bias,
+                           use_fused=fused, **dp_options)
+    else:  # HF Conv1D: weight [nx, nf]
+        twin = DPConv1D(child.nf, child.weight.shape[0], **dp_options)
+    ref = next(child.parameters(), None)
+    if ref is not None:
+        twin = twin.to(device=ref.device, dtype=ref.dtype)
+    twin.load_state_dict(child.state_dict())
+    twin.train(child.training)
+    return twin
+
+
 def wrap_with_flashdp_layers(
         model,
         target_modules: List[Type[nn.Module]] = None,
@@ -40,140 +90,47 @@ def wrap_with_flashdp_layers(
 ) -> nn.Module:
     """Replace the selected modules of ``model`` in place and return it.
 
-    Args mirror the reference (flashdp/api/wrap_model.py:17-68): target_modules
-    (types among nn.Linear, nn.LayerNorm, transformers Conv1D), target_layers
-    (names; default all), skip_layers (exact names), priority_to_target,
-    feedback (print wrapped/skipped), C, noise_multiplier, clamp_value.
-    Raises ValueError for missing/empty/unsupported target_modules.
+    target_modules: types among nn.Linear, nn.LayerNorm and transformers'
+    Conv1D (required, non-empty); target_layers: dotted names to consider
+    (default: all); skip_layers: dotted names to leave alone; C,
+    noise_multiplier, clamp_value: the DP layers' clipping bound, noise
+    multiplier and clip factor cap.  Raises ValueError for a missing, empty or
+    unsupported target_modules.
     """
     print("Wrapping the model with FlashDP...")
     if target_modules is None and target_layers is None:
         raise ValueError("Either target_modules or target_layers must be specified.")
     if target_modules is None or len(target_modules) == 0:
         raise ValueError("target_modules cannot be empty and must be list of torch.nn.Module.")
-    supported_modules = dp_supported_modules.keys()
-    if not all(m in supported_modules for m in target_modules):
-        raise ValueError(f"target_modules must be among {supported_modules}, got {target_modules}")
+    supported = dp_supported_modules.keys()
+    if any(kind not in supported for kind in target_modules):
+        raise ValueError(f"target_modules must be among {supported}, got {target_modules}")
+    del priority_to_target  # exact-name selection: the same set either way
 
-    target_layers = target_layers if target_layers is not None else []
-    skip_layers = skip_layers if skip_layers is not None else []
+    entries = list(_walk(model))
+    present = {type(child) for _, _, child, _ in entries}
+    for kind in target_modules:
+        if kind not in present:
+            print(f"Warning: Module type '{kind.__name__}' specified in target_modules is not "
+                  "used in the model.")
 
-    _, skipped_layers = _process_layer_groups(model, target_layers, skip_layers,
-                                              priority_to_target)
-    selected_layers = _select_layers(model, target_layers, skip_layers, priority_to_target)
-
-    if target_modules:
-        _validate_target_modules(model, target_modules)
-    if skip_layers:
-        _validate_skip_layers(model, skipped_layers)
-
-    _wrap_selected_layers(model, selected_layers, target_modules, C, clamp_value,
-                          noise_multiplier)
+    wanted = set(target_layers) if target_layers else {path for *_, path in entries}
+    wanted -= set(skip_layers or [])
+    kinds = set(target_modules)
+    dp_options = dict(C=C, clamp_value=clamp_value, noise_multiplier=noise_multiplier)
+    replaced, gone = [], set()
+    for parent, attr, child, path in entries:
+        if id(parent) in gone:  # inside a module replaced above
+            gone.add(id(child))
+            continue
+        if type(child) in kinds and path in wanted:
+            setattr(parent, attr, _dp_twin(child, dp_options))
+            gone.add(id(child))
+            replaced.append(path)
 
     if feedback:
-        _print_layer_feedback(selected_layers, "Wrapped")
-        _print_layer_feedback(skip_layers, "Skipped")
+        print(f"Layers Wrapped: {', '.join(replaced)}" if replaced else "No layers Wrapped.")
+        skipped = list(skip_layers or [])
+        print(f"Layers Skipped: {', '.join(skipped)}" if skipped else "No layers Skipped.")
     print("Model wrapped with FlashDP.")
     return model
-
-
-def _get_init_args(module):
-    if isinstance(module, nn.Linear):
-        return {"in_features": module.in_features, "out_features": module.out_features,
-                "bias": module.bias}
-    if isinstance(module, nn.LayerNorm):
-        return {"normalized_shape": module.normalized_shape, "eps": module.eps,
-                "elementwise_affine": module.elementwise_affine}
-    if _HFConv1D is not None and isinstance(module, _HFConv1D):
-        return {"nf": module.nf, "nx": module.weight.shape[0]}
-    raise NotImplementedError(f"Unsupported module type: {type(module)}")
-
-
-def _collect_all_layer_names(model):
-    names = []
-
-    def collect(module, prefix=""):
-        for name, child in module.named_children():
-            path = f"{prefix}.{name}" if prefix else name
-            names.append(path)
-            collect(child, path)
-
-    collect(model)
-    return names
-
-
-def _expand_submodules(layers, all_layers):
-    out = []
-    for layer in layers:
-        out.extend(l for l in all_layers if l.startswith(layer + ".") or l == layer)
-    return out
-
-
-def _process_layer_groups(model, target_layers, skip_layers, priority_to_target):
-    all_layers = _collect_all_layer_names(model)
-    t = set(_expand_submodules(target_layers, all_layers))
-    s = set(_expand_submodules(skip_layers, all_layers))
-    if priority_to_target:
-        return list(t - s), list(s - t)
-    return list(t - t.intersection(s)), list(s)
-
-
-def _select_layers(model, target_layers, skip_layers, priority_to_target):
-    all_layers = set(_collect_all_layer_names(model))
-    selected = set(target_layers) if target_layers else all_layers
-    skip = set(skip_layers) if skip_layers else set()
-    if priority_to_target:
-        return selected - skip
-    return selected.difference(selected.intersection(skip))
-
-
-def _wrap_selected_layers(model, selected_layers, target_modules, C, clamp_value,
-                          noise_multiplier):
-    targets = tuple(target_modules)
-
-    def replace(module, path=""):
-        for child_name, child in module.named_children():
-            full_name = f"{path}.{child_name}" if path else child_name
-            if isinstance(child, targets) and full_name in selected_layers:
-                dp_cls = dp_supported_modules[type(child)]
-                new_module = dp_cls(**_get_init_args(child), C=C, clamp_value=clamp_value,
-                                    noise_multiplier=noise_multiplier)
-                p = next(child.parameters(), None)
-                if p is not None:
-                    new_module = new_module.to(device=p.device, dtype=p.dtype)
-                new_module.load_state_dict(child.state_dict())
-                new_module.train(child.training)
-                setattr(module, child_name, new_module)
-            else:
-                replace(child, full_name)
-
-    replace(model)
-
-
-def _validate_target_modules(model, target_modules):
-    used = set()
-
-    def collect(module):
-        for child in module.children():
-            used.add(type(child))
-            collect(child)
-
-    collect(model)
-    for tm in target_modules:
-        if tm not in used:
-            print(f"Warning: Module type '{tm.__name__}' specified in target_modules is not used "
-                  "in the model.")
-
-
-def _validate_skip_layers(model, skip_layers):
-    names = set(_collect_all_layer_names(model))
-    for s in skip_layers:
-        if s not in names:
-            print(f"Warning: '{s}' specified in skip_layers does not exist in the model.")
-
-
-def _print_layer_feedback(layers, action):
-    if layers:
-        print(f"Layers {action}: {', '.join(layers)}")
-    else:
-        print(f"No layers {action}.")

@@ -18,7 +18,8 @@
 //    GPU (other streams, other threads) race and must be serialised by the
 //    caller.
 //  * Problems whose workspace exceeds the array are rejected with
-//    FDP_ERR_TOO_LARGE before anything is launched.
+//    FDP_ERR_TOO_LARGE before anything is launched; a stream of another
+//    device than the current one with FDP_ERR_ARG.
 #include <mutex>
 
 #include "fdp_common.hpp"
@@ -61,6 +62,18 @@ extern "C" int fdp_wgrad_clip_noalloc(const void* a, const void* b, int64_t B, i
   const int bad = fdp::wgrad_check_args(a, b, B, K, M, N, lda, ldb, layout, dtype, out, ldo,
                                         out_dtype, norms, flags);
   if (bad != FDP_OK) return bad;
+  // The scratch copy, the plan (CU count) and the launch are those of the
+  // current device: the stream must belong to it.
+  if (stream != nullptr) {
+    int cur = 0;
+    hipDevice_t sd = 0;
+    if (hipGetDevice(&cur) != hipSuccess ||
+        hipStreamGetDevice(static_cast<hipStream_t>(stream), &sd) != hipSuccess) {
+      (void)hipGetLastError();
+      return FDP_ERR_ARG;
+    }
+    if (static_cast<int>(sd) != cur) return FDP_ERR_ARG;
+  }
   // The control words are cleared by the call itself (a small fill kernel):
   // an expired wait of an earlier call may have left its status word set.
   flags = (flags | FDP_WGRAD_PLAIN_LAUNCH) & ~FDP_WGRAD_CLEAN_WORKSPACE;

@@ -259,7 +259,11 @@ int fdp_wgrad_bias_clip(const void* a, const void* b, int64_t B, int64_t K, int6
  * without launching.  All calls on one GPU share the array: calls that
  * overlap on one GPU race, so the caller serialises them.  The array's
  * status word is not visible to the caller: an expired bounded wait shows
- * only as NaN outputs.
+ * only as NaN outputs.  `stream` must belong to the current device (its
+ * copy of the array and its CU count are used): FDP_ERR_ARG otherwise.  The
+ * call may be captured into a HIP graph (it records kernels only, no memset);
+ * a noise key with a device counter plus fdp_noise_advance then draws fresh
+ * noise on every replay.
  * ---------------------------------------------------------------------- */
 #define FDP_NOALLOC_SCRATCH_BYTES (64u << 20)
 

@@ -359,3 +359,47 @@ def test_expired_wait_skips_a_fused_optimizer_step_on_the_device(monkeypatch):
     opt.step()
     torch.cuda.synchronize()
     assert torch.isfinite(w.float()).all() and not torch.equal(w.detach(), w0)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=str)
+def test_dplayernorm_two_axis_shape_and_no_affine(dtype):
+    """The non-fused DPLayerNorm over a 2-D normalized_shape normalises the
+    trailing axes together and clips the per-sample sums over the remaining
+    axis, as the reference's non-fused layer does (flashdp/layers/
+    layernorm.py:77-112): the oracle on the flattened [B, T, 4*64] tensors.
+    elementwise_affine=False has no gamma/beta: only dx."""
+    import torch.nn.functional as F
+    torch.manual_seed(21)
+    B, T = 4, 32
+    ln = DPLayerNorm((4, 64), use_fused=False, C=0.05, noise_multiplier=1.0).to(DEV, dtype)
+    with torch.no_grad():
+        ln.weight.copy_(1 + 0.1 * torch.randn(4, 64, device=DEV))
+        ln.bias.copy_(0.1 * torch.randn(4, 64, device=DEV))
+    ln.record_stats = True
+    ln.noise_generator = torch.Generator(device=DEV).manual_seed(78)
+    x = torch.randn(B, T, 4, 64, device=DEV).to(dtype).requires_grad_(True)
+    g = (torch.randn(B, T, 4, 64, device=DEV) * 0.01).to(dtype)
+    y = ln(x)
+    yt = F.layer_norm(x.detach().float(), (4, 64), ln.weight.detach().float(),
+                      ln.bias.detach().float(), 1e-5)
+    assert_close(y, yt.double().cpu().numpy(), dtype, "y vs F.layer_norm")
+    y.backward(g)
+    zw, zb = draws(78, [(4, 64), (4, 64)], dtype)
+    ref = O.layernorm_bwd_clip(g.reshape(B, T, 256), x.detach().reshape(B, T, 256),
+                               ln.weight.detach().reshape(256), 1e-5, C=0.05,
+                               noise_multiplier=1.0, z_w=zw.reshape(256), z_b=zb.reshape(256))
+    assert ln.weight.grad.shape == (4, 64) and x.grad.shape == x.shape
+    assert_close(x.grad.reshape(B, T, 256), ref["dx"], dtype, "dx")
+    assert_close(ln.weight.grad.reshape(256), ref["dw"], dtype, "dgamma")
+    assert_close(ln.bias.grad.reshape(256), ref["db"], dtype, "dbeta")
+    assert_elementwise(ln.last_stats["norms_w"], ref["norms_w"], dtype, "gamma norms")
+    assert np.all(ref["fac_w"] < 1.0)  # clipped
+
+    for fused in (False, True):
+        ln2 = DPLayerNorm(256, elementwise_affine=False, use_fused=fused, C=0.05).to(DEV, dtype)
+        assert ln2.weight is None and ln2.bias is None
+        x2 = torch.randn(B, T, 256, device=DEV).to(dtype).requires_grad_(True)
+        g2 = (torch.randn(B, T, 256, device=DEV) * 0.01).to(dtype)
+        ln2(x2).backward(g2)
+        ref2 = O.layernorm_bwd_clip(g2, x2.detach(), None, 1e-5, C=0.05)
+        assert_close(x2.grad, ref2["dx"], dtype, f"dx without affine (fused={fused})")

@@ -182,6 +182,30 @@ def test_layernorm_long_row_lengths(shape, dtype):
     assert_elementwise(fac[:B], ref["fac_w"], dtype, "factors gamma")
 
 
+@pytest.mark.parametrize("shape", [(2, 1, 1 << 20), (1, 2, 1000003)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_layernorm_million_element_rows_fp32(shape):
+    """Rows of about 10^6 elements in fp32 (each thread adds about H/1024 values
+    in order before the fixed-order block sum): statistics, forward and
+    backward within the fp32 bar, with the measured margins reported."""
+    B, T, H = shape
+    dtype = torch.float32
+    x = randn(shape, dtype, 51)
+    g = randn(shape, dtype, 52, 0.01)
+    w, b = randn((H,), dtype, 53), randn((H,), dtype, 54)
+    y, mean, rstd = core.layernorm_fwd(x, w, b, 1e-5)
+    yr, _, rr = O.layernorm_fwd(x, w, b, 1e-5)  # (the mean, near 0, is checked through y)
+    assert_elementwise(rstd.reshape(rr.shape), rr, dtype, "rstd",
+                       margin=f"LN fp32 rows of {H}: rstd")
+    assert_close(y, yr, dtype, "y", margin=f"LN fp32 rows of {H}: y")
+    dx, dw, db = core.layernorm_bwd_clip(g, x, w, mean, rstd, 1e30, 1.0,
+                                         param_dtype=torch.float32)
+    ref = O.layernorm_bwd_clip(g, x, w, 1e-5, C=1e30)  # the oracle's own statistics
+    assert_close(dx, ref["dx"], dtype, "dx", margin=f"LN fp32 rows of {H}: dx")
+    assert_close(dw, ref["dw"], dtype, "dgamma", margin=f"LN fp32 rows of {H}: dgamma")
+    assert_close(db, ref["db"], dtype, "dbeta")
+
+
 @pytest.mark.parametrize("shape", [(2, 0, 64), (16, 0, 1024), (2, 0, 20000)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_layernorm_bwd_empty_rows(shape):

@@ -217,3 +217,30 @@ def test_optimizer_pre_step_check_installs_and_passes_without_workspaces():
     assert torch.equal(p.detach(), torch.full((3,), 0.5))
     assert W.set_expiry_check("async") == "optimizer_step"
     assert W.set_expiry_check("optimizer_step") == "async"
+
+
+def test_wrap_leaves_subclasses_and_wrapped_layers_alone(capsys):
+    """Only exact types are replaced: wrapping twice changes nothing the second
+    time (a DPLinear is a subclass of nn.Linear), and a LayerNorm without a
+    bias or over two axes gets the non-fused DPLayerNorm; the feedback names
+    the layers actually replaced."""
+    m = Net()
+    wrap_with_flashdp_layers(m, target_modules=[nn.Linear])
+    first = {n: id(x) for n, x in m.named_modules()}
+    wrap_with_flashdp_layers(m, target_modules=[nn.Linear])
+    assert {n: id(x) for n, x in m.named_modules()} == first
+    out = capsys.readouterr().out
+    assert "No layers Wrapped." in out and "Layers Wrapped: h.0.fc, h.0.proj" in out
+
+    class Norms(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.a = nn.LayerNorm(8, bias=False)
+            self.b = nn.LayerNorm((4, 8))
+            self.c = nn.LayerNorm(8, elementwise_affine=False)
+
+    n = Norms()
+    wrap_with_flashdp_layers(n, target_modules=[nn.LayerNorm], feedback=False)
+    assert isinstance(n.a, DPLayerNorm) and not n.a.use_fused and n.a.bias is None
+    assert isinstance(n.b, DPLayerNorm) and not n.b.use_fused and n.b.weight.shape == (4, 8)
+    assert isinstance(n.c, DPLayerNorm) and n.c.use_fused and n.c.weight is None

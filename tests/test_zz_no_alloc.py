@@ -112,3 +112,76 @@ def test_noalloc_rejects_oversize_without_launch():
     assert torch.isnan(out).all() and torch.isnan(norms).all() and torch.isnan(fac).all()
     with pytest.raises(ValueError):
         _lib.check(st, "fdp_wgrad_clip_noalloc")
+
+
+def _noalloc_into(a, b, shape, C, key, out, norms, fac, flags=0):
+    """fdp_wgrad_clip_noalloc (layout TN) into caller-made outputs; returns the status."""
+    B, K, M, N = shape
+    return _lib.lib().fdp_wgrad_clip_noalloc(
+        a.data_ptr(), b.data_ptr(), B, K, M, N, a.stride(0), a.stride(1), b.stride(0),
+        b.stride(1), _lib.LAYOUT_TN, _lib.FDP_BF16, ctypes.c_float(C), ctypes.c_float(1.0), None,
+        ctypes.c_float(1.0 / B), None, ctypes.c_float(0.5 / B), _lib.noise_key(key),
+        out.data_ptr(), N, _lib.FDP_F32, norms.data_ptr(), fac.data_ptr(), flags,
+        _lib.stream_handle(torch.device(DEV)))
+
+
+def test_noalloc_allocates_nothing():
+    """Two calls (the large one, then a smaller one) leave the device's free
+    memory unchanged: the call makes no device allocation (its inputs and
+    outputs are made before the first reading; a first call loads the
+    library's code on the device)."""
+    calls = []
+    for i, shape in enumerate([(8, 1024, 3072, 768), (16, 16, 256, 256)]):
+        a, b = _inputs(*shape, "tn", seed=60 + i)
+        B, K, M, N = shape
+        outs = (torch.empty(M, N, device=DEV), torch.empty(B, device=DEV),
+                torch.empty(B, device=DEV))
+        calls.append((a, b, shape, outs))
+    a, b, shape, outs = calls[0]
+    assert _noalloc_into(a, b, shape, 0.05, (5, 0), *outs) == 0  # warm-up
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    for a, b, shape, outs in calls:
+        assert _noalloc_into(a, b, shape, 0.05, (5, 0), *outs) == 0
+    torch.cuda.synchronize()
+    free1 = torch.cuda.mem_get_info()[0]
+    assert free1 == free0, f"device free memory changed by {free0 - free1} bytes"
+
+
+def test_noalloc_in_a_graph_with_a_noise_counter():
+    """The no-allocation call and fdp_noise_advance captured into one HIP graph
+    and replayed three times, with eager work and synchronisations between the
+    replays: each replay equals the eager call with the key's offset moved to
+    that replay's counter value, and the replays differ from one another."""
+    shape = (8, 256, 1536, 384)
+    B, K, M, N = shape
+    a, b = _inputs(*shape, "tn", seed=70)
+    counter = torch.zeros(1, dtype=torch.int64, device=DEV)
+    blocks = (M * N + 3) // 4
+    out, norms, fac = (torch.empty(M, N, device=DEV), torch.empty(B, device=DEV),
+                       torch.empty(B, device=DEV))
+    key = (4321, 10, counter.data_ptr())
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):  # one eager call on the capture stream first
+        assert _noalloc_into(a, b, shape, 0.05, key, out, norms, fac) == 0
+        _lib.noise_advance(counter, blocks)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        assert _noalloc_into(a, b, shape, 0.05, key, out, norms, fac) == 0
+        _lib.noise_advance(counter, blocks)
+    prev = None
+    for rep in range(3):
+        ctr = int(counter.item())
+        graph.replay()
+        torch.cuda.synchronize()
+        assert int(counter.item()) == ctr + blocks
+        got = out.clone()
+        st, ref, _, _ = _call(False, a, b, shape, "tn", 0.05, (4321, 10 + ctr), 0)
+        assert st == 0
+        assert torch.equal(got, ref), f"replay {rep} differs from the eager call"
+        if prev is not None:
+            assert not torch.equal(prev, got)
+        prev = got
