@@ -21,10 +21,9 @@ fp32 DP layers).  A LayerNorm without a bias or over more than one trailing
 axis gets the non-fused DPLayerNorm (the fused one requires a bias and one
 axis; both compute the same per-sample math here).  With ``feedback`` the
 names of the layers actually replaced are printed, and the skip list.  A
-module type in
-``target_modules`` that the model does not use draws a warning; skip names are
-checked only after their expansion to the model's own names, as in the
-reference, so an unknown skip name draws none.
+module type in ``target_modules`` that the model does not use draws a
+warning; skip names are checked only after their expansion to the model's own
+names, as in the reference, so an unknown skip name draws none.
 """
 from __future__ import annotations
 

@@ -229,27 +229,6 @@ __device__ __forceinline__ void compute_stage(const FDP_LDS char* st, const Frag
   }
 }
 
-// compute_stage with fhook(ks, frags) after the MFMAs of each k-step (VALU work
-// on the fragments overlaps the MFMAs in flight).  mfma = false reads the
-// fragments and runs the hook only (acc is left as it is).
-template <class DT, class G, class FragHook>
-__device__ __forceinline__ void compute_stage_fh(const FDP_LDS char* st, const FragOffsets<G>& fo,
-                                                 f32x16 (&acc)[G::FI][G::FJ], bool mfma,
-                                                 const FragHook& fhook) {
-#pragma unroll
-  for (int ks = 0; ks < G::KS; ++ks) {
-    Frags<G> f;
-    f.load(st, fo, ks);
-    if (mfma) {
-#pragma unroll
-      for (int i = 0; i < G::FI; ++i)
-#pragma unroll
-        for (int j = 0; j < G::FJ; ++j) acc[i][j] = mfma16<DT>(f.a[i], f.b[j], acc[i][j]);
-    }
-    fhook(ks, f);
-  }
-}
-
 // s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding).
 template <int N>
 __device__ __forceinline__ void wait_vm() {

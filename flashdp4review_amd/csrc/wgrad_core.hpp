@@ -418,10 +418,14 @@ __device__ __forceinline__ void tile_coords(const Args& p, int tile, int64_t& m0
 // hold, so grad_output is read once.  A 16-bit fragment pair gives its column
 // sum and its square in two v_dot2 (with ones, and with itself).  Each element
 // is counted once: in the tile grid, k-tile kt of a sample is counted by the
-// tile whose index along the other axis is kt % P (P tiles there), and k-step
-// ks by the wave with (ks & 1) == its index among the two waves that share the
-// fragment.  A tile's column sums go to bias_part[b][other][c] (a row of
-// the tile's columns is contiguous), its sum of squares to bias_sq[b][tile].
+// tile whose index along the other axis is kt % P (P tiles there), and of the
+// two waves that share a row (or column) of fragments, each sums half of them
+// over every k-step of a counted k-tile.  The kernels pick the k-tile code
+// with or without this work per k-tile: a branch inside the unrolled k-steps
+// would keep the next step's LDS reads from being scheduled among this step's
+// MFMAs, and VALU work on every k-tile competes with the MFMAs for issue.  A
+// tile's column sums go to bias_part[b][other][c] (a row of the tile's columns
+// is contiguous), its sum of squares to bias_sq[b][tile].
 
 // acc + x.lo + x.hi and acc + x.lo^2 + x.hi^2 for two packed 16-bit values.
 template <class DT>
@@ -464,6 +468,30 @@ __device__ __forceinline__ void bias_frag(const uint4& f, float& cs, float& sq, 
   cs = c;
   sq += col < lim ? q : 0.f;
 }
+// A counted k-tile's bias work, after its MFMAs are issued: this wave reads
+// its NF fragments (f0 .. f0 + NF - 1 of its row of A fragments, or column
+// of B fragments, from tile row / column w0) of every k-step again from the
+// LDS stage -- the stage stays valid until the next k-tile's barrier -- and
+// adds them to cs / sq.  The MFMA code of the k-tile is left as it is.
+template <class DT, class G, int BOP, int NF>
+__device__ inline void bias_from_stage(const FDP_LDS char* st, int w0, int f0, float (&cs)[NF],
+                                       float& sq, int col0, int lim) {
+  constexpr int R = BOP == 1 ? G::BM : G::BN;
+  constexpr int ROW = BOP == 1 ? G::ROW_A : G::ROW_B;
+  constexpr uint32_t base = BOP == 1 ? 0u : static_cast<uint32_t>(G::TILE_A);
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int i = 0; i < NF; ++i) {
+    const uint32_t o0 = dma::frag_off<R>(w0, f0 + i, 0) + base;
+    const uint32_t o1 = dma::frag_off<R>(w0, f0 + i, 1) + base;
+    uint4 fr[G::KS];
+#pragma unroll
+    for (int ks = 0; ks < G::KS; ++ks)
+      fr[ks] = dma::read_frag(st, o0 + ks * 16 * ROW, o1 + ks * 16 * ROW);
+#pragma unroll
+    for (int ks = 0; ks < G::KS; ++ks) bias_frag<DT>(fr[ks], cs[i], sq, col0 + 32 * i + (lane & 31), lim);
+  }
+}
 // Columns of the bias operand left in a tile that starts at column c0
 // (clamped to 2^30: a tile is narrower).
 __device__ __forceinline__ int bias_limit(int64_t len, int64_t c0) {
@@ -472,36 +500,43 @@ __device__ __forceinline__ int bias_limit(int64_t len, int64_t c0) {
 }
 
 // End of one sample's product in a 4-wave workgroup: a wave's column sums
-// (lanes l and l + 32 hold the two k halves of one column) go to bcol[ws][.]
-// at local columns cl0 + 32 f + lane (f < NF), its sum of squares to
-// bred[wave]; both are cleared.  The caller then synchronises and calls
+// (lanes l and l + 32 hold the two k halves of one column) go to bcol at its
+// columns cl0 + 32 f + lane (f < NF), its sum of squares to bred[wave]; both
+// are cleared.  The caller then synchronises and calls bias_park or
 // bias_store.
-template <int NF, int W>
+template <int NF>
 __device__ __forceinline__ void bias_fold(float (&cs)[NF], float& sq, float* bcol, float* bred,
-                                          int ws, int cl0) {
+                                          int cl0) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
   for (int f = 0; f < NF; ++f) {
     const float v = cs[f] + __shfl_xor(cs[f], 32, kWave);
-    if (lane < 32) bcol[ws * W + cl0 + 32 * f + lane] = v;
+    if (lane < 32) bcol[cl0 + 32 * f + lane] = v;
     cs[f] = 0.f;
   }
-  const float q = wave_sum(sq);
+  const float q = wave_sum_dpp(sq);
   if (lane == 0) bred[wave] = q;
   sq = 0.f;
 }
-// The folded partials of sample b in tile `tile` (local columns [0, W) from
-// column c0; the two waves sharing a fragment added in wave order): one row
-// of bias_part [B][P][len] (coalesced stores) and one bias_sq entry.
+// After the synchronisation that follows bias_fold: one product's partials
+// into vals[0, W) and *sq (LDS, where they wait until the k-loop is over).
 template <int W>
-__device__ __forceinline__ void bias_store(const Args& p, const float* bcol, const float* bred,
-                                           int64_t b, int tile, int tiles, int64_t c0, int other) {
+__device__ __forceinline__ void bias_park(const float* bcol, const float* bred, float* vals,
+                                          float* sq) {
+  for (int t = threadIdx.x; t < W; t += NT) vals[t] = bcol[t];
+  if (threadIdx.x == 0) *sq = (bred[0] + bred[1]) + (bred[2] + bred[3]);
+}
+// The partials of sample b in tile `tile` (local columns [0, W) from column
+// c0): one row of bias_part [B][P][len] (coalesced stores) and one bias_sq
+// entry.
+template <int W>
+__device__ __forceinline__ void bias_store(const Args& p, const float* vals, float sq, int64_t b,
+                                           int tile, int tiles, int64_t c0, int other) {
   float* row = p.bias_part + (b * p.bias_P + other) * p.bias_len + c0;
   for (int t = threadIdx.x; t < W; t += NT) {
-    if (c0 + t < p.bias_len) st_coherent(row + t, bcol[t] + bcol[W + t]);
+    if (c0 + t < p.bias_len) st_coherent(row + t, vals[t]);
   }
-  if (threadIdx.x == 0)
-    st_coherent(p.bias_sq + b * tiles + tile, (bred[0] + bred[1]) + (bred[2] + bred[3]));
+  if (threadIdx.x == 0) st_coherent(p.bias_sq + b * tiles + tile, sq);
 }
 
 // Outputs [wg * kBiasCols, ...) (and every nwg * kBiasCols after) of the bias
@@ -1092,8 +1127,14 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
   __shared__ float red[NT / kWave];
   __shared__ float fac[U];
   __shared__ int flag;
-  __shared__ float bcol[BOP != 0 ? 2 * BM : 1];  // a product's folded bias column sums
+  __shared__ float bcol[BOP != 0 ? BM : 1];  // a product's folded bias column sums
   __shared__ float bred[NT / kWave];
+  // every product's partials (sum of squares; the bias's column sums and sum
+  // of squares) wait here until the k-loop is over: a store issued inside the
+  // loop would make the ring's vmcnt waits wait for the next k-tile's loads
+  __shared__ float wsq[U];
+  __shared__ float bpend[BOP != 0 ? U * BM : 1];
+  __shared__ float bsqp[U];
   const dma::Stages stages{{(FDP_LDS char*)(st0), (FDP_LDS char*)(st1),
                             (FDP_LDS char*)(st0), (FDP_LDS char*)(st1)}};
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -1141,13 +1182,14 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
   int iu = 0, ik = 0;
   int64_t m0, n0;
   tile_coords(p, as.tile, m0, n0);
-  // bias: the tile's index along the other axis, this wave's index among the
-  // two that share its fragments, and its lane's columns (bias_frag)
+  // bias: the tile's index along the other axis; of the two waves sharing a
+  // row (column) of fragments, this one sums fragment bws: its tile columns
+  // from bcl (bias_frag)
   const int bother = BOP == 1 ? static_cast<int>(n0 / BN) : static_cast<int>(m0 / BM);
   const int bws = BOP == 1 ? (wave & 1) : (wave >> 1);
-  const int bcl = BOP == 1 ? wm : wn;  // the wave's first column in the tile
+  const int bcl = (BOP == 1 ? wm : wn) + 32 * bws;
   const int blim = bias_limit(p.bias_len, BOP == 1 ? m0 : n0);
-  float bcs[2] = {0.f, 0.f}, bsq = 0.f;
+  float bcs[1] = {0.f}, bsq = 0.f;
   (void)bother;
   (void)bws;
   (void)bcl;
@@ -1212,20 +1254,11 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
         dma::wait_tiles<G::LOADS>(ahead < kStages - 2 ? ahead : kStages - 2);
         dma::barrier();
         if (q + kStages - 1 < nq) issue_next(stages.get((s + kStages - 1) % kStages));
-        if constexpr (BOP == 0) {
-          dma::compute_stage<DT, G>(stages.get(s), fo, acc);
-        } else {
-          const bool cnt = ck % p.bias_P == bother;
-          dma::compute_stage_fh<DT, G>(
-              stages.get(s), fo, acc, true, [&](int ks, const dma::Frags<G>& f) {
-                if (cnt && (ks & 1) == bws) {
-#pragma unroll
-                  for (int i = 0; i < 2; ++i)
-                    bias_frag<DT>(BOP == 1 ? f.a[i] : f.b[i], bcs[i], bsq,
-                                  bcl + 32 * i + (lane & 31), blim);
-                }
-              });
-        }
+        dma::compute_stage<DT, G>(stages.get(s), fo, acc);
+        // (a counter in place of the modulo adds a live register and spills)
+        if (BOP != 0 && ck % p.bias_P == bother)  // a counted k-tile
+          bias_from_stage<DT, G, BOP, 1>(stages.get(s), BOP == 1 ? wm : wn, bws, bcs, bsq, bcl,
+                                         blim);
         if (++ck == unit_nk(cu)) {
           {
             const int own = cu;
@@ -1245,14 +1278,10 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
               }
             sq = wave_sum(sq);
             if (lane == 0) red[wave] = sq;
-            if constexpr (BOP != 0) bias_fold<2, BM>(bcs, bsq, bcol, bred, bws, BOP == 1 ? wm : wn);
+            if constexpr (BOP != 0) bias_fold<1>(bcs, bsq, bcol, bred, bcl);
             __syncthreads();
-            if (threadIdx.x == 0)
-              st_coherent(p.partials + (as.b0 + own) * tiles + as.tile,
-                          (red[0] + red[1]) + (red[2] + red[3]));
-            if constexpr (BOP != 0)
-              bias_store<BM>(p, bcol, bred, as.b0 + own, as.tile, tiles, BOP == 1 ? m0 : n0,
-                             bother);
+            if (threadIdx.x == 0) wsq[own] = (red[0] + red[1]) + (red[2] + red[3]);
+            if constexpr (BOP != 0) bias_park<BM>(bcol, bred, bpend + own * BM, bsqp + own);
             if (own + 1 < nb) {  // park it and start the next product
 #pragma unroll
               for (int j = 0; j < U - 1; ++j)
@@ -1284,7 +1313,14 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
       }
     }
   }
-  dma::barrier();  // every wave is done reading the ring
+  dma::barrier();  // every wave is done reading the ring (and the parked partials are written)
+  if (threadIdx.x < nb)
+    st_coherent(p.partials + (as.b0 + threadIdx.x) * tiles + as.tile, wsq[threadIdx.x]);
+  if constexpr (BOP != 0) {
+    for (int u = 0; u < nb; ++u)
+      bias_store<BM>(p, bpend + u * BM, bsqp[u], as.b0 + u, as.tile, tiles, BOP == 1 ? m0 : n0,
+                     bother);
+  }
 
   // The tile's exchange ticket starts at zero in every launch: group 0 clears
   // it before the grid barrier, every ticket is taken after it.  (A ticket

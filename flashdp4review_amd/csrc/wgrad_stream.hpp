@@ -314,10 +314,11 @@ template <class DT, class G, int S, int BOP = 0>
 __global__ __launch_bounds__(NT, 2) void clipsum_kernel(Args p) {
   static_assert(S >= 2 && S <= 4, "ring depth");
   static_assert(S * G::STAGE >= G::WM * G::BN * 4, "output staging reuses the ring");
-  constexpr int BW = BOP == 1 ? G::BM : G::BN;  // the tile's extent along the bias axis
-  constexpr int NF = BOP == 1 ? G::FI : G::FJ;  // fragments of the bias operand per wave
+  constexpr int BW = BOP == 1 ? G::BM : G::BN;      // the tile's extent along the bias axis
+  constexpr int NF = (BOP == 1 ? G::FI : G::FJ) / 2;  // bias fragments summed per wave
+  static_assert(BOP == 0 || NF >= 1, "two waves share each row (column) of fragments");
   __shared__ __attribute__((aligned(16))) char ring[S * G::STAGE];
-  __shared__ float bcol[BOP != 0 ? 2 * BW : 1];
+  __shared__ float bcol[BOP != 0 ? BW : 1];
   __shared__ float bred[NT / kWave];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = (wave >> 1) * G::WM, wn = (wave & 1) * G::WN;
@@ -334,13 +335,14 @@ __global__ __launch_bounds__(NT, 2) void clipsum_kernel(Args p) {
   const int nq = nsamp * nk;
   const uint16_t* pa = static_cast<const uint16_t*>(p.a);
   const uint16_t* pb = static_cast<const uint16_t*>(p.b);
-  // bias: the tile's index along the other axis, this wave's index among the
-  // two that share its fragments, and its lane's columns (bias_frag)
+  // bias: the tile's index along the other axis; of the two waves sharing a
+  // row (column) of fragments, this one sums fragments bws * NF .. + NF - 1:
+  // its tile columns from bcl (bias_frag)
   const int bother = BOP == 1 ? static_cast<int>(n0 / G::BN) : static_cast<int>(m0 / G::BM);
   const int bws = BOP == 1 ? (wave & 1) : (wave >> 1);
-  const int bcl = BOP == 1 ? wm : wn;  // the wave's first column in the tile
+  const int bcl = (BOP == 1 ? wm : wn) + 32 * NF * bws;
   const int blim = bias_limit(p.bias_len, BOP == 1 ? m0 : n0);
-  float bcs[NF] = {}, bsq = 0.f;
+  float bcs[NF > 0 ? NF : 1] = {}, bsq = 0.f;
   (void)bother;
   (void)bws;
   (void)bcl;
@@ -373,6 +375,7 @@ __global__ __launch_bounds__(NT, 2) void clipsum_kernel(Args p) {
   float c_prev = 0.f;
   bool any = false, live = false;
   int cu = 0, ck = 0;
+  int bk = 0;  // ck % bias_P (the bias counts k-tile ck when bk == bother)
   dma::wait_vm<0>();
 #pragma unroll
   for (int s = 0; s < S - 1; ++s)
@@ -403,26 +406,20 @@ __global__ __launch_bounds__(NT, 2) void clipsum_kernel(Args p) {
             any = true;
           }
         }
-        if constexpr (BOP == 0) {
-          if (live) dma::compute_stage<DT, G>(stage(s), fo, acc);
-        } else {
-          const bool cnt = ck % p.bias_P == bother;
-          if (live || cnt)
-            dma::compute_stage_fh<DT, G>(
-                stage(s), fo, acc, live, [&](int ks, const dma::Frags<G>& f) {
-                  if (cnt && (ks & 1) == bws) {
-#pragma unroll
-                    for (int i = 0; i < NF; ++i)
-                      bias_frag<DT>(BOP == 1 ? f.a[i] : f.b[i], bcs[i], bsq,
-                                    bcl + 32 * i + (lane & 31), blim);
-                  }
-                });
+        if (live) dma::compute_stage<DT, G>(stage(s), fo, acc);
+        if constexpr (BOP != 0) {
+          if (bk == bother)  // a counted k-tile
+            bias_from_stage<DT, G, BOP, NF>(stage(s), BOP == 1 ? wm : wn, NF * bws, bcs, bsq,
+                                            bcl, blim);
+          bk = bk + 1 == p.bias_P ? 0 : bk + 1;
         }
         if (++ck == nk) {
+          bk = 0;
           if constexpr (BOP != 0) {  // the sample's bias partials
-            bias_fold<NF, BW>(bcs, bsq, bcol, bred, bws, BOP == 1 ? wm : wn);
+            bias_fold<NF>(bcs, bsq, bcol, bred, bcl);
             dma::barrier();
-            bias_store<BW>(p, bcol, bred, b0 + cu, tile, tiles, BOP == 1 ? m0 : n0, bother);
+            bias_store<BW>(p, bcol, (bred[0] + bred[1]) + (bred[2] + bred[3]), b0 + cu, tile,
+                           tiles, BOP == 1 ? m0 : n0, bother);
           }
           ck = 0;
           ++cu;
