@@ -22,7 +22,8 @@ from torch.autograd.function import Function
 from ..core import colsum_clip, wgrad_clip
 from ..core.utils import RuntimeAutoTuner
 from .utils import DPParameter as Parameter
-from .utils import NoiseStream, advance_noise, as_btf, noise_counter, noise_draws, noise_std
+from .utils import (NoiseStream, advance_noise, as_btf, exact_fp32, noise_counter, noise_draws,
+                    noise_std)
 
 
 class DPLinear(nn.Linear):
@@ -101,7 +102,8 @@ class _DPLinearFunction(Function):
             r = wgrad_clip(g3.contiguous() if want_bias else g3, x3.to(g3.dtype), C, clamp_value,
                            layout="tn", out_scale=1.0 / B, noise=zs[0], noise_scale=std,
                            noise_key=keys[0], out_dtype=weight.dtype,
-                           return_stats=stats is not None, **extra)
+                           two_pass=exact_fp32(weight.dtype), return_stats=stats is not None,
+                           **extra)
             advance_noise(counter, adv)
             if stats is not None:
                 grad_weight, stats["norms_w"], stats["fac_w"] = r[:3]

@@ -24,7 +24,8 @@ from torch.autograd.function import Function
 from ..core import colsum_clip, wgrad_clip
 from ..core.utils import RuntimeAutoTuner
 from .utils import DPParameter as Parameter
-from .utils import NoiseStream, advance_noise, as_btf, noise_counter, noise_draws, noise_std
+from .utils import (NoiseStream, advance_noise, as_btf, exact_fp32, noise_counter, noise_draws,
+                    noise_std)
 
 try:  # the HF module type is what wrap_with_flashdp_layers replaces
     from transformers.pytorch_utils import Conv1D as _HFConv1D
@@ -116,7 +117,8 @@ class _DPConv1DFunction(Function):
             r = wgrad_clip(x3.to(g3.dtype), g3.contiguous() if want_bias else g3, C, clamp_value,
                            layout="tn", out_scale=1.0 / B, noise=zs[0], noise_scale=std,
                            noise_key=keys[0], out_dtype=weight.dtype,
-                           return_stats=stats is not None, **extra)
+                           two_pass=exact_fp32(weight.dtype), return_stats=stats is not None,
+                           **extra)
             advance_noise(counter, adv)
             if stats is not None:
                 grad_weight, stats["norms_w"], stats["fac_w"] = r[:3]

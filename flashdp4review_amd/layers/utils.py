@@ -58,6 +58,36 @@ def get_noise_convention() -> str:
     return _noise_convention
 
 
+# Accumulation of the DP layers' fp32 weight gradients from 16-bit operands
+# (an fp32 model under autocast, the reference's AMP training):
+#   "fast": the single-pass kernels, which hold or exchange each per-sample
+#           product once in bf16 before the fp32 sum (about 2e-3 relative error
+#           at the config shapes; the reference's own autocast einsum forms the
+#           per-sample products in bf16);
+#   "fp32": the streamed two-pass schedule, which sums every sample's product
+#           in fp32 in one accumulator (about 1e-6), at the cost of a norm pass.
+WGRAD_PRECISIONS = ("fast", "fp32")
+_wgrad_precision = "fast"
+
+
+def set_wgrad_precision(mode: str) -> None:
+    """Select how the DP layers form fp32 weight gradients from 16-bit operands
+    (process-wide): "fast" (the default) or "fp32"."""
+    global _wgrad_precision
+    if mode not in WGRAD_PRECISIONS:
+        raise ValueError(f"wgrad precision must be one of {WGRAD_PRECISIONS}, got {mode!r}")
+    _wgrad_precision = mode
+
+
+def get_wgrad_precision() -> str:
+    return _wgrad_precision
+
+
+def exact_fp32(out_dtype: torch.dtype) -> bool:
+    """Whether a weight gradient of out_dtype takes the fp32-accumulating schedule."""
+    return _wgrad_precision == "fp32" and out_dtype == torch.float32
+
+
 def noise_std(noise_multiplier: float, batch: int, C: float = 1.0) -> float:
     """Standard deviation of the Gaussian noise added after the 1/B average under
     the selected convention: noise_multiplier / sqrt(B) ("reference",

@@ -22,7 +22,8 @@ bf16 models and under autocast.
   AMP   an fp32 model wrapped and run under torch.autocast(bfloat16), as the
         reference's example trains (example/gpt2/train.py:77-79), and a bf16
         model: every DP layer's gradients match the oracle on the bf16 tensors
-        its kernels saw.
+        its kernels saw; with set_wgrad_precision("fp32") the fp32 weight and
+        bias gradients meet the fp32 tolerance.
 """
 import copy
 
@@ -230,6 +231,39 @@ def test_autocast_bf16_wrapped_fp32_model():
     w0 = model[0].weight.detach().clone()
     torch.optim.Adam(model.parameters(), lr=1e-3).step()
     assert not torch.equal(w0, model[0].weight)
+
+
+def test_autocast_fp32_precision_mode():
+    """set_wgrad_precision("fp32"): fp32 weight gradients from bf16 operands
+    are summed in fp32 (streamed schedule) and meet the fp32 tolerance against
+    the float64 oracle on the same bf16 tensors."""
+    import flashdp4review_amd as fdp
+    model = _wrapped(_mlp(torch.float32), C=0.05, sigma=0.0)
+    seen = _capture(model)
+    x = torch.randn(4, 64, 256, device=DEV)
+    fdp.set_wgrad_precision("fp32")
+    try:
+        with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+            loss = (model(x).float() ** 2).mean()
+        loss.backward()
+    finally:
+        fdp.set_wgrad_precision("fast")
+    assert fdp.get_wgrad_precision() == "fast"
+    with pytest.raises(ValueError):
+        fdp.set_wgrad_precision("fp64")
+    checked = 0
+    for m, xin, g in seen:
+        if not isinstance(m, DPLinear):
+            continue
+        assert g.dtype == torch.bfloat16 and m.weight.grad.dtype == torch.float32
+        ref = O.linear_backward(xin.to(g.dtype), g, m.weight.detach(), 0.05, 1.0)
+        assert float(ref["fac_w"].min()) < 1.0, "some samples clip"
+        assert_close(m.weight.grad, ref["dw"], torch.float32, "fp32 mode dW",
+                     margin=f"autocast fp32 mode: Linear {tuple(m.weight.shape)} dW")
+        assert_close(m.bias.grad, ref["db"], torch.float32, "fp32 mode db",
+                     margin=f"autocast fp32 mode: Linear {tuple(m.weight.shape)} db")
+        checked += 1
+    assert checked == 2
 
 
 def test_wrapped_bf16_model():

@@ -183,6 +183,23 @@ def test_noise_convention():
         clip_args_of(torch.tensor([1.0, 2.0, 3.0]), torch.device("cpu"))
 
 
+def test_wgrad_precision_mode():
+    """fp32 accumulation is opt-in and applies to fp32 weight gradients only."""
+    from flashdp4review_amd.layers.utils import exact_fp32
+    assert fdp.get_wgrad_precision() == "fast"
+    assert not exact_fp32(torch.float32)
+    try:
+        fdp.set_wgrad_precision("fp32")
+        assert exact_fp32(torch.float32)
+        assert not exact_fp32(torch.bfloat16) and not exact_fp32(torch.float16)
+        with pytest.raises(ValueError):
+            fdp.set_wgrad_precision("exact")
+        assert fdp.get_wgrad_precision() == "fp32"
+    finally:
+        fdp.set_wgrad_precision("fast")
+    assert not exact_fp32(torch.float32)
+
+
 def test_layernorm_fused_row_limit():
     """Fused mode keeps the reference's limit of 64 KB rows and its error
     (flashdp/core/layernorm_clip.py:217-221); rows at the limit pass the check
