@@ -46,9 +46,9 @@ PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 # factor the same counter reads on a plain copy of known size.  None = not
 # measured for that workload.
 TRAFFIC_BYTES = {
-    "cfg2": 134206210,   # profiles/wgrad_wide_kernel_cfg2.md
-    "cfg3": 229735374,   # profiles/wgrad_group_kernel_cfg3.md
-    "cfg4": 105568579,   # profiles/layernorm_bwd_clip_cfg4.md (one launch per call)
+    "cfg2": 134224748,   # profiles/wgrad_wide_kernel_cfg2.md
+    "cfg3": 234360493,   # profiles/wgrad_group_kernel_cfg3.md (weight and bias in one launch)
+    "cfg4": 105565315,   # profiles/layernorm_bwd_clip_cfg4.md (one launch per call)
 }
 
 
