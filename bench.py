@@ -680,8 +680,10 @@ def main():
                 "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(F / call_ms / 1e9 / PEAK_BF16_TFLOPS, 4),
                 "traffic": TRAFFIC_BYTES[args.workload],
-                "kernel": "single-pass clipped weight-gradient kernel: one launch per "
-                          "fdp_wgrad_clip call, HIP events around the timed region",
+                "kernel": ("wgrad_pair_kernel (two samples' 192x192 tiles per CU)"
+                           if args.workload == "cfg2" else "wgrad_group_kernel (weight and bias)")
+                          + ": one launch per fdp_wgrad_clip call, HIP events around the timed "
+                            "region",
                 "flops_per_launch": F, "avg_ms": round(call_ms, 4)}
     out = {"metric": res["metric"], "value": res["value"], "unit": res["unit"], "n_gpus": 1,
            "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
@@ -696,6 +698,10 @@ def main():
         F = 2.0 * B * T * I * O
         extra["cfg2_step_cooperative_launch"] = {"ms": round(t_coop, 4),
                                                  "tflops": round(F / t_coop / 1e9, 2)}
+        step_one, _ = run_wgrad(x, go, torch.bfloat16, single_pass="unpaired")
+        t_one = median_cuda_time(step_one, args.steps, 3, reps=3)
+        extra["cfg2_step_one_sample_per_cu"] = {"ms": round(t_one, 4),
+                                                "tflops": round(F / t_one / 1e9, 2)}
         step_narrow, _ = run_wgrad(x, go, torch.bfloat16, single_pass="narrow")
         t_nar = median_cuda_time(step_narrow, args.steps, 3, reps=3)
         extra["cfg2_step_grouped_kernel"] = {"ms": round(t_nar, 4),

@@ -27,6 +27,7 @@ WGRAD_CLEAN_WORKSPACE = 8
 WGRAD_WIDE = 16
 WGRAD_NARROW = 32
 WGRAD_BIAS_OF_B = 64  # fdp_wgrad_bias_clip: the bias of operand b instead of a
+WGRAD_UNPAIRED = 128  # the wide schedule with one sample per workgroup only
 WGRAD_CONTROL_BYTES = 2048  # control words at the head of an fdp_wgrad_clip workspace
 
 _DTYPE_CODES = {torch.float32: FDP_F32, torch.float16: FDP_F16, torch.bfloat16: FDP_BF16}

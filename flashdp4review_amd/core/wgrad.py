@@ -20,7 +20,8 @@ from .utils import RuntimeAutoTuner
 
 
 _LAUNCH_MODES = ("cooperative", "plain")
-_SINGLE_PASS = {"auto": 0, "wide": _lib.WGRAD_WIDE, "narrow": _lib.WGRAD_NARROW}
+_SINGLE_PASS = {"auto": 0, "wide": _lib.WGRAD_WIDE,
+                "unpaired": _lib.WGRAD_WIDE | _lib.WGRAD_UNPAIRED, "narrow": _lib.WGRAD_NARROW}
 _launch_mode = os.environ.get("FDP_WGRAD_LAUNCH", "plain")
 if _launch_mode not in _LAUNCH_MODES:
     raise ValueError(f"FDP_WGRAD_LAUNCH must be one of {_LAUNCH_MODES}, got {_launch_mode!r}")
@@ -330,10 +331,14 @@ def wgrad_clip(a: torch.Tensor, b: torch.Tensor, C: float = 1.0, clamp_value: fl
     With ``return_stats`` also returns the fp32 per-sample norms and factors.
     ``two_pass`` forces the norm-pass + clipped-sum-pass schedule instead of the
     single-pass kernels; ``single_pass`` picks between those: "auto" (the wide
-    kernel, one 384x192 tile of one sample per CU, when the layer's products
-    fill at least 70% of the CUs, else the grouped 128x128 kernel), "wide"
-    (whenever the products fit the CUs) or "narrow" (grouped only); ``launch`` ("cooperative" / "plain", default: the
-    mode of ``set_wgrad_launch``) picks how that kernel is dispatched.
+    schedule when the layer's products fill at least 70% of the CUs, else the
+    grouped 128x128 kernel), "wide" (the wide schedule whenever the products
+    fit the CUs), "unpaired" (as "wide", one sample per CU only) or "narrow"
+    (grouped only).  The wide schedule holds two samples' 192x192 tiles per CU
+    where the batch is even (6..72), the contraction a multiple of 32 and no
+    bias is formed, else one sample's 384x192 tile.  ``launch``
+    ("cooperative" / "plain", default: the mode of ``set_wgrad_launch``) picks
+    how that kernel is dispatched.
     ``check`` synchronises and raises if a bounded inter-workgroup wait of the
     single-pass kernel expired (in this call or an earlier one on the stream
     whose expiry was not reported yet).  Without it, expiries are reported by a

@@ -114,6 +114,31 @@ struct Operand {
     retile(r0);
     step = static_cast<uint32_t>(BK * ld * 2);
   }
+  // Two samples' R-wide tiles side by side in one LDS row of 2R values: logical
+  // chunks [0, R/8) from the sample at `base`, [R/8, R/4) from the one `ds`
+  // elements further on (one buffer record over both).  Rows past K of the
+  // first sample would read the second's rows: callers need K % BK == 0.
+  template <int R>
+  __device__ inline void init_pair(const uint16_t* base, int64_t ld, int64_t K, int64_t r0,
+                                   int64_t ds) {
+    constexpr int CPR = R / 8;
+    constexpr int RS = row_chunks(2 * R);
+    static_assert(RS == 2 * CPR, "the two samples fill the LDS row");
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    rsrc = u32x4{static_cast<uint32_t>(a), static_cast<uint32_t>(a >> 32) & 0xffffu,
+                 static_cast<uint32_t>((ds + K * ld) * 2), kRsrcWord3};
+#pragma unroll
+    for (int j = 0; j < L; ++j) {
+      const int slot = (wave * L + j) * 64 + lane;
+      const int k = slot / RS;
+      const int c = (slot % RS) ^ swz(k);
+      const int64_t e = (c < CPR ? 0 : ds) + int64_t(k) * ld + 8 * (c < CPR ? c : c - CPR);
+      voff[j] = static_cast<uint32_t>(e * 2);
+    }
+    retile(r0);
+    step = static_cast<uint32_t>(BK * ld * 2);
+  }
   // The same tile of another sample (same ld, K and columns).  Records past
   // K*ld*2 bytes read as zero.
   __device__ __forceinline__ void retarget(const uint16_t* base, int64_t ld, int64_t K) {
@@ -294,6 +319,26 @@ struct Job {
   }
 };
 
+// Per-thread state of two samples' products of one output tile, loaded side
+// by side (Operand::init_pair): the A tile's rows hold both samples' BM/2
+// columns, the B tile's both samples' BN/2.
+template <class G>
+struct PairJob {
+  Operand<G::LOADS_A, G::BK> a;
+  Operand<G::LOADS_B, G::BK> b;
+  // pa/pb: the first sample's operands; dsa/dsb: elements to the second's
+  __device__ __forceinline__ void init(const uint16_t* pa, int64_t lda, int64_t dsa,
+                                       const uint16_t* pb, int64_t ldb, int64_t dsb, int64_t K,
+                                       int64_t m0, int64_t n0) {
+    a.template init_pair<G::BM / 2>(pa, lda, K, m0, dsa);
+    b.template init_pair<G::BN / 2>(pb, ldb, K, n0, dsb);
+  }
+  __device__ __forceinline__ void issue(FDP_LDS char* stage, int kt) const {
+    a.issue(stage, kt);
+    b.issue(stage + G::TILE_A, kt);
+  }
+};
+
 // acc += A_tile^T B_tile over nk k-tiles with an S-stage ring (S in {2, 3, 4}).
 template <class DT, class G, int S>
 __device__ inline void gemm(const Job<G>& job, int nk, const FragOffsets<G>& fo, const Stages& st,
@@ -341,8 +386,9 @@ struct NoFragHook {
 // the SIMD.  fhook(kt, ks, frags) runs after the MFMAs of k-step ks are
 // issued, with that step's operand fragments (VALU work on them overlaps
 // the MFMAs in flight).
-template <class DT, class G, int S, class Hook = NoHook, class FragHook = NoFragHook>
-__device__ inline void gemm_pipe(const Job<G>& job, int nk, const FragOffsets<G>& fo,
+// J: Job<G> (one sample) or PairJob<G> (two samples side by side).
+template <class DT, class G, int S, class J, class Hook = NoHook, class FragHook = NoFragHook>
+__device__ inline void gemm_pipe(const J& job, int nk, const FragOffsets<G>& fo,
                                  const Stages& st, f32x16 (&acc)[G::FI][G::FJ],
                                  const Hook& hook = Hook(), const FragHook& fhook = FragHook()) {
   static_assert(S >= 2 && S <= 4, "stages");

@@ -272,7 +272,8 @@ Plan make_plan(int64_t B, int64_t K, int64_t M, int64_t N, int cus, int flags, i
   if ((flags & FDP_WGRAD_NARROW) == 0 && K > 0) {
     pl.wp = wide_plan(B, K, M, N, lda > 0 ? lda : M, ldb > 0 ? ldb : N, cus,
                       (flags & FDP_WGRAD_WIDE) ? 0.0 : kWideMinFill);
-    if (pl.wp.wgm != 0) {
+    if (flags & FDP_WGRAD_UNPAIRED) pl.wp.pair = 0;
+    if (pl.wp.any()) {
       pl.off_wide_partials = kWsHead;
       pl.off_wide_slots = pl.off_wide_partials + align_up(pl.wp.partial_bytes);
       pl.off_wide_bias_part = pl.off_wide_slots + align_up(pl.wp.slot_bytes);
@@ -409,7 +410,8 @@ int fdp::wgrad_check_args(const void* a, const void* b, int64_t B, int64_t K, in
   if (M * N > (int64_t(1) << 40) || B > (int64_t(1) << 31)) return FDP_ERR_SHAPE;
   if ((K > 0 && (a == nullptr || b == nullptr)) || out == nullptr) return FDP_ERR_ARG;
   if ((flags & ~(FDP_WGRAD_NOCLIP | FDP_WGRAD_TWO_PASS | FDP_WGRAD_PLAIN_LAUNCH |
-                 FDP_WGRAD_CLEAN_WORKSPACE | FDP_WGRAD_WIDE | FDP_WGRAD_NARROW)) != 0)
+                 FDP_WGRAD_CLEAN_WORKSPACE | FDP_WGRAD_WIDE | FDP_WGRAD_NARROW |
+                 FDP_WGRAD_UNPAIRED)) != 0)
     return FDP_ERR_ARG;  // (FDP_WGRAD_BIAS_OF_B only with fdp_wgrad_bias_clip)
   if ((flags & FDP_WGRAD_WIDE) && (flags & FDP_WGRAD_NARROW)) return FDP_ERR_ARG;
   if ((flags & FDP_WGRAD_NOCLIP) != 0 && norms != nullptr) return FDP_ERR_ARG;
@@ -441,7 +443,7 @@ int wgrad_clip_impl(const void* a, const void* b, int64_t B, int64_t K, int64_t 
   const Plan pl0 = cached_plan(B, K, M, N, cus, flags);
   if (workspace == nullptr || workspace_bytes < pl0.total) return FDP_ERR_WORKSPACE;
   Plan pl = cached_plan(B, K, M, N, cus, flags, lda, ldb);
-  if (pl.total > workspace_bytes) pl.wp.wgm = 0;
+  if (pl.total > workspace_bytes) pl.wp.wgm = pl.wp.pair = 0;
   if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0) return FDP_ERR_ALIGN;
 
   char* ws = static_cast<char*>(workspace);
@@ -509,9 +511,12 @@ int wgrad_clip_impl(const void* a, const void* b, int64_t B, int64_t K, int64_t 
                    ldb % vel == 0 && stride_ab % vel == 0 && stride_bb % vel == 0;
 
   hipStream_t s = static_cast<hipStream_t>(stream);
-  // Wide single pass: 16-bit TN inputs, aligned rows, one product per CU.
+  // Wide single pass: 16-bit TN inputs, aligned rows, two samples' products
+  // per CU (paired) or one.
+  const bool pair = pl.wp.pair != 0 && bias == nullptr && pair_records_fit(K, lda, stride_ab) &&
+                    pair_records_fit(K, ldb, stride_bb);
   if (!noclip && (flags & FDP_WGRAD_TWO_PASS) == 0 && layout == FDP_LAYOUT_TN && vec && K > 0 &&
-      dtype != FDP_F32 && pl.wp.wgm != 0) {
+      dtype != FDP_F32 && (pair || pl.wp.wgm != 0)) {
     WideArgs w{};
     w.a = static_cast<const uint16_t*>(a);
     w.b = static_cast<const uint16_t*>(b);
@@ -523,13 +528,15 @@ int wgrad_clip_impl(const void* a, const void* b, int64_t B, int64_t K, int64_t 
     w.lda = lda;
     w.sbb = stride_bb;
     w.ldb = ldb;
-    w.tiles_m = pl.wp.tiles_m;
-    w.tiles_n = pl.wp.tiles_n;
-    w.tiles = pl.wp.tiles;
-    w.nwg = pl.wp.nwg;
+    w.tiles_m = pair ? pl.wp.pair_tiles_m : pl.wp.tiles_m;
+    w.tiles_n = pair ? pl.wp.pair_tiles_n : pl.wp.tiles_n;
+    w.tiles = pair ? pl.wp.pair_tiles : pl.wp.tiles;
+    w.nwg = pair ? pl.wp.pair_nwg : pl.wp.nwg;
     w.partials = reinterpret_cast<float*>(ws + pl.off_wide_partials);
     w.slots = ws + pl.off_wide_slots;
-    w.slot_blocks = pl.wp.slot_blocks;
+    w.slot_blocks = pair ? pl.wp.pair_slot_blocks : pl.wp.slot_blocks;
+    w.group_cnt = reinterpret_cast<unsigned*>(ws) + kGroupWord0;
+    w.tagged = reinterpret_cast<uint64_t*>(ws + pl.off_wide_partials);
     w.out = out;
     w.ldo = ldo;
     w.out_dtype = out_dtype;
@@ -569,8 +576,9 @@ int wgrad_clip_impl(const void* a, const void* b, int64_t B, int64_t K, int64_t 
       hipLaunchKernelGGL(clear_words_kernel<0>, dim3(static_cast<unsigned>((words + NT - 1) / NT)),
                          dim3(NT), 0, s, reinterpret_cast<unsigned*>(ws), words);
     }
-    const hipError_t e = dtype == FDP_BF16 ? launch_wide_bf16(w, pl.wp.wgm, plain, s)
-                                           : launch_wide_f16(w, pl.wp.wgm, plain, s);
+    const int wgm = pair ? 1 : pl.wp.wgm;
+    const hipError_t e = dtype == FDP_BF16 ? launch_wide_bf16(w, wgm, plain, s)
+                                           : launch_wide_f16(w, wgm, plain, s);
     if (e == hipSuccess) {
       if (bias_done != nullptr) *bias_done = bias != nullptr;
       return FDP_OK;

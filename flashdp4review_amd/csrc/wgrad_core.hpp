@@ -682,7 +682,10 @@ constexpr int kXcds = 8;
 // its CU; callers pass an estimate of when the slowest workgroup arrives.
 //
 // Split in two: grid_arrive() (every thread; thread 0 gets the arrival index)
-// and grid_wait(); a workgroup may do work of its own in between.
+// and grid_wait(); a workgroup may do work of its own in between.  With
+// epoch == nullptr the same pair waits for the n workgroups that share one
+// counter (a part of the grid, all of which arrive once per launch); the
+// launch epoch is then left alone.
 __device__ inline unsigned grid_arrive(unsigned* bar) {
   wait_stores();
   __syncthreads();
@@ -703,7 +706,8 @@ __device__ inline bool grid_wait(unsigned* bar, unsigned n, unsigned i, int* err
     int bad = 0;
     if (i + 1 == n) {
       __hip_atomic_store(bar, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_fetch_add(epoch, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (epoch != nullptr)
+        __hip_atomic_fetch_add(epoch, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     } else {
       while (wall_clock64() < quiet_until) __builtin_amdgcn_s_sleep(32);
       // at most `limit` polls (0: none -- the wait expires at once, which
@@ -1485,6 +1489,10 @@ using KernelFn = void (*)(Args);
 constexpr size_t kWsHead = 2048;
 constexpr int kPairFlag0 = 64;
 static_assert((kPairFlag0 + kPairMax) * sizeof(unsigned) <= kWsHead, "control words");
+// Words [kGroupWord0, kGroupWord0 + kGroupMax): the paired wide kernel's
+// per-tile counters (zero between launches).
+constexpr int kGroupWord0 = kPairFlag0 + kPairMax;
+constexpr int kGroupMax = static_cast<int>(kWsHead / sizeof(unsigned)) - kGroupWord0;
 constexpr int kGroupUnits = 4;    // samples held by one workgroup at most
 
 // Single-pass schedule for B samples over `tiles` 128x128 tiles on `slots`

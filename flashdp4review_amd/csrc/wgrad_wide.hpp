@@ -69,6 +69,9 @@ struct WideArgs {
   float* norms_out;
   float* factors_out;
   int vec_out;  // out rows hold whole aligned quads: 4 outputs per vector store
+  unsigned* group_cnt;  // paired kernel: [tiles] per-tile counters, then one start
+                        // counter (zero between launches)
+  uint64_t* tagged;     // paired kernel: [B, tiles] partials, each with its launch tag
   // The bias of operand a (bias_op 1, rows m) or b (bias_op 2, columns n):
   //   bias[c] = bias_scale * sum_b c'_b sum_k op_b[k, c] + bias_noise_scale * zb[c],
   //   c'_b = clip(||op_b||_F) with the weight's C and clamp.
@@ -113,6 +116,82 @@ __device__ __forceinline__ void quad_transpose(const float (&in)[4], float (&out
     out[1] = d == 1 ? r : out[1];
     out[2] = d == 2 ? r : out[2];
     out[3] = d == 3 ? r : out[3];
+  }
+}
+
+// Stores one finish item: the 8 sums v of rows mr + {0..3, 8..11} of column
+// nc (registers 8h..8h+7 of one lane of a 32x32 block), as
+// out = out_scale * v + noise_scale * z.  Each 4-row group is transposed in
+// its quad of lanes: lane k then holds row k's 4 consecutive outputs, one
+// vector store (and the row layout of the Philox draw).  zpre: the item's two
+// early draws (row groups 0 and 1), or nullptr to draw them here.
+__device__ __forceinline__ void store_item(const WideArgs& p, const NoiseSrc& nz, const f32x4* zpre,
+                                           int64_t mr, int64_t nc, const float (&v)[8],
+                                           bool poisoned) {
+  const int lane = threadIdx.x & 63;
+  const int64_t n4 = nc & ~int64_t(3);
+#pragma unroll 1
+  for (int grp = 0; grp < 2; ++grp) {
+    float src[4], o[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) src[k] = (grp == 0 ? v[k] : v[4 + k]) * p.out_scale;
+    quad_transpose(src, o);
+    const int64_t row = mr + 8 * grp + (lane & 3);
+    if (nz.on()) {
+      float z[4];
+      if (zpre != nullptr) {
+        const f32x4 zz = zpre[grp];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) z[c] = zz[c];
+      } else if (nz.z == nullptr && p.N % 4 == 0) {
+        nz.block((row * p.N + n4) / 4, z);
+      } else {
+        // an injected tensor, or rows of N % 4 != 0 outputs: element by
+        // element (rolled: one copy of the element draw, placed by selects)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) z[c] = 0.f;
+#pragma unroll 1
+        for (int c = 0; c < 4; ++c) {
+          const float zc = (row < p.M && n4 + c < p.N) ? nz.at(row * p.N + n4 + c) : 0.f;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) z[q] = q == c ? zc : z[q];
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c) o[c] += p.noise_scale * z[c];
+    }
+    if (poisoned) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) o[c] = __builtin_nanf("");
+    }
+    if (row < p.M) {
+      const int64_t e = row * p.ldo + n4;
+      if (p.out_dtype == FDP_F32) {
+        float* out = static_cast<float*>(p.out) + e;
+        if (p.vec_out && n4 + 4 <= p.N) {
+          *reinterpret_cast<f32x4*>(out) = f32x4{o[0], o[1], o[2], o[3]};
+        } else {
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            if (n4 + c < p.N) out[c] = o[c];
+        }
+      } else {
+        uint16_t h16[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          h16[c] = p.out_dtype == FDP_BF16 ? BF16::from_f32(o[c]) : F16::from_f32(o[c]);
+        uint16_t* out = static_cast<uint16_t*>(p.out) + e;
+        if (p.vec_out && n4 + 4 <= p.N) {
+          *reinterpret_cast<uint2*>(out) =
+              make_uint2(uint32_t(h16[0]) | (uint32_t(h16[1]) << 16),
+                         uint32_t(h16[2]) | (uint32_t(h16[3]) << 16));
+        } else {
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            if (n4 + c < p.N) out[c] = h16[c];
+        }
+      }
+    }
   }
 }
 
@@ -461,76 +540,10 @@ __global__ __launch_bounds__(kWideThreads, 1) void wgrad_wide_kernel(WideArgs p)
       v[2 * e + 1] += c * __uint_as_float(w[e] & 0xffff0000u);
     }
   };
-  // out_scale, noise, store.  Each 4-row group of the item is transposed in
-  // its quad of lanes: lane k then holds row k's 4 consecutive outputs, one
-  // vector store (and the row layout of the Philox draw).
   auto finish = [&](int it, const float (&v)[8]) {
     int64_t mr, nc;
     item_pos(it, mr, nc);
-    const int64_t n4 = nc & ~int64_t(3);
-#pragma unroll 1
-    for (int grp = 0; grp < 2; ++grp) {
-      float src[4], o[4];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) src[k] = (grp == 0 ? v[k] : v[4 + k]) * p.out_scale;
-      quad_transpose(src, o);
-      const int64_t row = mr + 8 * grp + (lane & 3);
-      if (noisy) {
-        float z[4];
-        if (pre_noise) {
-          const f32x4 zz = zpre[it * 2 + grp];
-#pragma unroll
-          for (int c = 0; c < 4; ++c) z[c] = zz[c];
-        } else if (nz.z == nullptr && p.N % 4 == 0) {
-          nz.block((row * p.N + n4) / 4, z);
-        } else {
-          // an injected tensor, or rows of N % 4 != 0 outputs: element by
-          // element (rolled: one copy of the element draw, placed by selects)
-#pragma unroll
-          for (int c = 0; c < 4; ++c) z[c] = 0.f;
-#pragma unroll 1
-          for (int c = 0; c < 4; ++c) {
-            const float zc = (row < p.M && n4 + c < p.N) ? nz.at(row * p.N + n4 + c) : 0.f;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) z[q] = q == c ? zc : z[q];
-          }
-        }
-#pragma unroll
-        for (int c = 0; c < 4; ++c) o[c] += p.noise_scale * z[c];
-      }
-      if (poisoned) {
-#pragma unroll
-        for (int c = 0; c < 4; ++c) o[c] = __builtin_nanf("");
-      }
-      if (row < p.M) {
-        const int64_t e = row * p.ldo + n4;
-        if (p.out_dtype == FDP_F32) {
-          float* out = static_cast<float*>(p.out) + e;
-          if (p.vec_out && n4 + 4 <= p.N) {
-            *reinterpret_cast<f32x4*>(out) = f32x4{o[0], o[1], o[2], o[3]};
-          } else {
-#pragma unroll
-            for (int c = 0; c < 4; ++c)
-              if (n4 + c < p.N) out[c] = o[c];
-          }
-        } else {
-          uint16_t h16[4];
-#pragma unroll
-          for (int c = 0; c < 4; ++c)
-            h16[c] = p.out_dtype == FDP_BF16 ? BF16::from_f32(o[c]) : F16::from_f32(o[c]);
-          uint16_t* out = static_cast<uint16_t*>(p.out) + e;
-          if (p.vec_out && n4 + 4 <= p.N) {
-            *reinterpret_cast<uint2*>(out) =
-                make_uint2(uint32_t(h16[0]) | (uint32_t(h16[1]) << 16),
-                           uint32_t(h16[2]) | (uint32_t(h16[3]) << 16));
-          } else {
-#pragma unroll
-            for (int c = 0; c < 4; ++c)
-              if (n4 + c < p.N) out[c] = h16[c];
-          }
-        }
-      }
-    }
+    store_item(p, nz, pre_noise ? zpre + it * 2 : nullptr, mr, nc, v, poisoned);
   };
   if (ng >= 8 && ng <= kFastGroups) {
     // at most 3 items per thread (regions of 8 or 9 blocks): every chunk of
@@ -602,6 +615,391 @@ __global__ __launch_bounds__(kWideThreads, 1) void wgrad_wide_kernel(WideArgs p)
   }
 }
 
+// ================================================================ paired
+// Two samples' products of one 192x192 output tile per CU, added inside the
+// CU.  For the wide schedule's shapes with an even batch (6 <= B <= 72) and
+// whole 32-deep k-tiles: a GPT-2-small MLP weight gradient at B = 8 is
+// 64 tiles x 4 sample pairs = 256 workgroups on 256 CUs.  Waves 0-3 hold the
+// first sample's 2 x 2 wave tiles of 96 x 96 (3 x 3 blocks of 32x32 MFMA
+// accumulators, as in the wide kernel), waves 4-7 the second sample's; one
+// LDS stage holds both samples' k-tiles side by side (rows of 384 values, no
+// padding), 3 stages in 144 KB.  Per workgroup:
+//
+//   1. the two products, their masked sums of squares -> partials[b, tile],
+//      each stored with the launch's tag in one 64-bit word;
+//   2. the noise of the workgroup's outputs is drawn (into LDS) while the
+//      pair's other workgroups finish; two waves then poll the pair's
+//      partials (all tiles of its two samples) until every one carries the
+//      tag, and form the two clip factors c;
+//   3. S = c_2q G_2q + c_2q+1 G_2q+1 in fp32 (for each block one of the two
+//      waves holding it hands its scaled block to the other through LDS);
+//   4. the tile's 36 blocks are split into ng = B/2 regions, one per pair; the
+//      workgroup keeps its own region of S in LDS (fp32) and publishes every
+//      other block (bf16, agent-coherent) to its exchange slot;
+//   5. the ng workgroups of the tile wait for each other;
+//   6. finish: out = out_scale * sum_q S_q (q in pair order) + noise.
+//
+// The tile's wait uses a self-resetting counter per tile (grid_wait) at the
+// head of the workspace.  No grid-wide barrier: a pair's clip factors depend
+// on its own workgroups only.
+//
+// Against the wide kernel's one product per CU this loads a third more
+// operand bytes per flop (each k-tile carries 4 x 192 columns for 2 x 192^2
+// outputs instead of 576 for 384 x 192), and exchanges (ng-1)/ng of one
+// clipped pair sum per CU instead of of every product: 14 MB instead of
+// 33 MB at B = 8.  Sums are formed in fixed orders: deterministic.
+struct PairGeom {
+  static constexpr int BM = 384, BN = 384;  // LDS rows: both samples' 192 columns
+  static constexpr int BK = 32;
+  static constexpr int NW = 8, KS = BK / 16;
+  static constexpr int WM = 96, WN = 96, FI = 3, FJ = 3;
+  static constexpr int ROW_A = dma::row_chunks(BM) * 16;
+  static constexpr int ROW_B = dma::row_chunks(BN) * 16;
+  static constexpr int TILE_A = BK * ROW_A;
+  static constexpr int TILE_B = BK * ROW_B;
+  static constexpr int STAGE = TILE_A + TILE_B;
+  static constexpr int LOADS_A = TILE_A / (NW * 64 * 16);
+  static constexpr int LOADS_B = TILE_B / (NW * 64 * 16);
+  static constexpr int LOADS = LOADS_A + LOADS_B;
+  static_assert(LOADS_A * NW * 64 * 16 == TILE_A && LOADS_B * NW * 64 * 16 == TILE_B,
+                "each wave issues whole 1 KB loads");
+};
+constexpr int kPairTile = 192;
+constexpr int kPairBlocks = 36;      // 32x32 blocks per 192x192 tile
+constexpr int kPairMinB = 6;         // regions of at most 12 blocks (48 KB in fp32)
+constexpr int kPairRegionMax = 12;
+constexpr int kPairFast = 8;         // pairs up to which a round's chunks load at once
+
+__device__ __forceinline__ int pair_region_first(int q, int ng) {
+  return (q * kPairBlocks + ng - 1) / ng;
+}
+
+template <class DT>
+__global__ __launch_bounds__(kWideThreads, 1) void wgrad_pair_kernel(WideArgs p) {
+  using G = PairGeom;
+  constexpr int S = kWideStages;
+  __shared__ __attribute__((aligned(16))) char st0[G::STAGE];
+  __shared__ __attribute__((aligned(16))) char st1[G::STAGE];
+  __shared__ __attribute__((aligned(16))) char st2[G::STAGE];
+  __shared__ float red[8];
+  __shared__ float fac[2];
+  __shared__ int bad2[2];
+  __shared__ unsigned tag_s;
+  __shared__ int flag;
+  static_assert(4 * 3 * 16 * 64 * 4 <= G::STAGE, "a row of scaled blocks fits a stage");
+  static_assert(kPairRegionMax * 16 * 64 * 4 <= G::STAGE, "the own region fits a stage");
+  static_assert(kPairRegionMax * 128 * 2 * 16 <= G::STAGE, "the region's noise fits a stage");
+  const dma::Stages stages{{(FDP_LDS char*)(st0), (FDP_LDS char*)(st1), (FDP_LDS char*)(st2),
+                            (FDP_LDS char*)(st0)}};
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int half = wave >> 2, wl = wave & 3;  // sample of the pair, wave within the sample
+  const int wm = (wl >> 1) * 96, wn = (wl & 1) * 96;
+
+  // hardware workgroup -> (pair, tile), pair-major: the workgroups of one XCD
+  // (logical_wg) contract one pair's operands over a band of tiles
+  const int L = logical_wg(blockIdx.x, p.nwg);
+  const int ng = static_cast<int>(p.B / 2);
+  const int q = L / p.tiles, tile = L % p.tiles;
+  const int64_t s0 = 2 * int64_t(q);
+  int64_t m0, n0;
+  {
+    const int per_band = kBandRows * p.tiles_n;
+    const int band = tile / per_band, in_band = tile % per_band;
+    const int rows_left = p.tiles_m - band * kBandRows;
+    const int band_rows = rows_left < kBandRows ? rows_left : kBandRows;
+    m0 = int64_t(band * kBandRows + in_band % band_rows) * kPairTile;
+    n0 = int64_t(in_band / band_rows) * kPairTile;
+  }
+  unsigned tag = 0;
+  if (threadIdx.x == 0)
+    tag = __hip_atomic_load(p.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+  const int rb0 = pair_region_first(q, ng), rb1 = pair_region_first(q + 1, ng);
+  const int nitems = (rb1 - rb0) * 128;
+
+  // ---- 1. the two products
+  f32x16 acc[3][3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i)
+#pragma unroll
+    for (int j = 0; j < 3; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+  {
+    dma::FragOffsets<G> fo;
+    fo.init(half * kPairTile + wm, half * kPairTile + wn);
+    dma::PairJob<G> job;
+    job.init(p.a + s0 * p.sab, p.lda, p.sab, p.b + s0 * p.sbb, p.ldb, p.sbb, p.K, m0, n0);
+    dma::gemm_pipe<DT, G, S>(job, static_cast<int>(p.K / G::BK), fo, stages, acc);
+  }
+  {
+    // rows/columns past M/N may hold the next row's values: left out of the norm
+    const int64_t rl = p.M - m0, cl = p.N - n0;
+    const int rlim = rl < kPairTile ? static_cast<int>(rl) : kPairTile;
+    const int clim = cl < kPairTile ? static_cast<int>(cl) : kPairTile;
+    float sq = 0.f;
+    if (rlim == kPairTile && clim == kPairTile) {
+#pragma unroll
+      for (int i = 0; i < 3; ++i)
+#pragma unroll
+        for (int j = 0; j < 3; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) sq = __builtin_fmaf(acc[i][j][r], acc[i][j][r], sq);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 3; ++i)
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+          const bool ncol = acc_col(wn, j, lane) < clim;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const float v = ncol && acc_row(wm, i, lane, r) < rlim ? acc[i][j][r] : 0.f;
+            sq = __builtin_fmaf(v, v, sq);
+          }
+        }
+    }
+    sq = wave_sum_dpp(sq);
+    if (lane == 0) red[wave] = sq;
+    if (threadIdx.x == 0) tag_s = tag;
+    __syncthreads();
+    tag = tag_s;
+    // the two samples' partials of this tile, each one 64-bit store of the
+    // value and the launch's tag (complemented: a pattern no fp32 or bf16 data
+    // left in the workspace carries), so that both become visible together
+    if (threadIdx.x < 2) {
+      const float* r4 = red + 4 * threadIdx.x;
+      const float v = (r4[0] + r4[1]) + (r4[2] + r4[3]);
+      __hip_atomic_store(p.tagged + (s0 + threadIdx.x) * p.tiles + tile,
+                         (uint64_t(~tag) << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  // The launch epoch (the next launch's tags) advances once every workgroup
+  // has read it: the last one to count itself here advances it and resets the
+  // self-clearing counter.
+  unsigned* const start_cnt = p.group_cnt + p.tiles;
+  unsigned started = 0;
+  if (threadIdx.x == 0)
+    started = __hip_atomic_fetch_add(start_cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+  // item it of the region: block rb0 + it/128, half (it/64)%2, lane it%64 --
+  // rows mr + {0..3, 8..11} of column nc
+  auto item_pos = [&](int it, int64_t& mr, int64_t& nc) {
+    const int bid = rb0 + (it >> 7), h = (it >> 6) & 1, l = it & 63;
+    const int w = bid / 9, ij = bid % 9;
+    mr = m0 + (w >> 1) * 96 + 32 * (ij / 3) + 16 * h + 4 * (l >> 5);
+    nc = n0 + (w & 1) * 96 + 32 * (ij % 3) + (l & 31);
+  };
+  // ---- 2. the noise of the region, drawn while the pair's other workgroups
+  // finish their products (st2: [item][row group])
+  const NoiseSrc nz = p.noise.resolved();
+  const bool pre_noise = nz.on() && nz.z == nullptr && p.N % 4 == 0;
+  f32x4* zpre = reinterpret_cast<f32x4*>(st2);
+  if (pre_noise) {
+#pragma unroll 1
+    for (int it = threadIdx.x; it < nitems; it += kWideThreads) {
+      int64_t mr, nc;
+      item_pos(it, mr, nc);
+#pragma unroll 1
+      for (int grp = 0; grp < 2; ++grp) {
+        const int64_t row = mr + 8 * grp + (lane & 3);
+        float blk[4];
+        nz.block((row * p.N + (nc & ~int64_t(3))) / 4, blk);
+        zpre[it * 2 + grp] = f32x4{blk[0], blk[1], blk[2], blk[3]};
+      }
+    }
+  }
+  if (threadIdx.x == 0 && started + 1 == unsigned(p.nwg)) {
+    __hip_atomic_store(start_cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_fetch_add(p.epoch, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  // the clip factors: wave w < 2 polls sample s0 + w's partials (all tiles,
+  // written by the pair's workgroups) until each carries this launch's tag,
+  // then sums them in tile order; a bounded wait
+  if (wave < 2) {
+    float C = p.C, clamp = p.clamp;
+    if (p.clip_args_dev != nullptr) {
+      C = p.clip_args_dev[0];
+      clamp = p.clip_args_dev[1];
+    }
+    const int64_t s = s0 + wave;
+    const uint64_t* part = p.tagged + s * p.tiles;
+    const uint32_t want = ~tag;
+    float a = 0.f;
+    bool bad = false;
+    for (int t0 = 0; t0 < p.tiles && !bad; t0 += kWave) {
+      const int t = t0 + lane;
+      uint64_t v = uint64_t(want) << 32;
+      for (unsigned spins = 0;; ++spins) {
+        if (spins >= p.spin_limit) {
+          bad = true;
+          break;
+        }
+        if (t < p.tiles) v = __hip_atomic_load(part + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (__all(uint32_t(v >> 32) == want)) break;
+        __builtin_amdgcn_s_sleep(2);
+      }
+      a += __uint_as_float(uint32_t(v));
+    }
+    a = wave_sum_dpp(a);
+    if (lane == 0) {
+      if (bad) expire(p.err, p.poison, tag);
+      const float n = bad ? __builtin_nanf("") : sqrtf(a);
+      const float cf = bad ? n : clip_factor(n, C, clamp);
+      fac[wave] = cf;
+      bad2[wave] = bad;
+      if (tile == 0) {  // one writer per sample
+        if (p.norms_out) p.norms_out[s] = n;
+        if (p.factors_out) p.factors_out[s] = cf;
+      }
+    }
+  }
+  __syncthreads();
+  bool poisoned = bad2[0] != 0 || bad2[1] != 0;
+
+  // ---- 3./4. S = c0 G0 + c1 G1, one row i of blocks at a time.  Waves w and
+  // w + 4 hold the same blocks; for block (i, j) one of them (the stager)
+  // puts its scaled block in st0 ([wave][j][register][lane]) and the other
+  // (the adder, alternating with the block index) adds its own, then keeps
+  // the sum (own region, st1: [block][half][lane][8]) or publishes it (bf16).
+  const float cmine = fac[half];
+  float* stg = reinterpret_cast<float*>(st0);
+  f32x4* own = reinterpret_cast<f32x4*>(st1);
+  const int slot_bytes = p.slot_blocks * kWideBlockBytes;
+  {
+    const CoherentSpan slot(reinterpret_cast<const float*>(p.slots + int64_t(L) * slot_bytes),
+                            static_cast<uint32_t>(slot_bytes));
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+#pragma unroll
+      for (int j = 0; j < 3; ++j)
+        if (((i * 3 + j) & 1) != half) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            stg[((wl * 3 + j) * 16 + r) * 64 + lane] = cmine * acc[i][j][r];
+        }
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < 3; ++j) {
+        if (((i * 3 + j) & 1) != half) continue;
+        const int bid = wl * 9 + i * 3 + j;
+        float v[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          v[r] = __builtin_fmaf(cmine, acc[i][j][r], stg[((wl * 3 + j) * 16 + r) * 64 + lane]);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          if (bid >= rb0 && bid < rb1) {
+            f32x4* o = own + (((bid - rb0) * 2 + h) * 64 + lane) * 2;
+            o[0] = f32x4{v[8 * h], v[8 * h + 1], v[8 * h + 2], v[8 * h + 3]};
+            o[1] = f32x4{v[8 * h + 4], v[8 * h + 5], v[8 * h + 6], v[8 * h + 7]};
+          } else {
+            u32x4 w;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) w[e] = BF16::pack2(v[8 * h + 2 * e], v[8 * h + 2 * e + 1]);
+            slot.store4(
+                static_cast<uint32_t>((slot_block(bid, rb0, rb1) * 2 + h) * 1024 + lane * 16),
+                __builtin_bit_cast(f32x4, w));
+          }
+        }
+      }
+      __syncthreads();  // st0 is rewritten by the next row
+    }
+  }
+
+
+  // ---- 5. the tile's workgroups wait for each other
+  unsigned* cnt = p.group_cnt + tile;
+  const unsigned garr = grid_arrive(cnt);
+  poisoned = grid_wait(cnt, unsigned(ng), garr, p.err, nullptr, p.poison, tag, p.spin_limit, &flag,
+                       0, 2) || poisoned;
+
+  // ---- 6. finish: out = out_scale * sum of the pairs' chunks of each item (in
+  // pair order) + noise
+  const int64_t slot_stride = int64_t(p.tiles) * slot_bytes;  // between pairs of one tile
+  const char* const slots_tile = p.slots + int64_t(tile) * slot_bytes;
+  auto slot_load = [&](int qq, int it) -> u32x4 {
+    const int bid = rb0 + (it >> 7), h = (it >> 6) & 1, l = it & 63;
+    const CoherentSpan sl(reinterpret_cast<const float*>(slots_tile + qq * slot_stride),
+                          static_cast<uint32_t>(slot_bytes));
+    const int sb = slot_block(bid, pair_region_first(qq, ng), pair_region_first(qq + 1, ng));
+    return __builtin_bit_cast(u32x4, sl.load4(static_cast<uint32_t>((sb * 2 + h) * 1024 + l * 16)));
+  };
+  auto add_own = [&](float (&v)[8], int it) {
+    const int lb = it >> 7, h = (it >> 6) & 1, l = it & 63;
+    const f32x4* o = own + ((lb * 2 + h) * 64 + l) * 2;
+    const f32x4 lo = o[0], hi = o[1];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[e] += lo[e];
+      v[4 + e] += hi[e];
+    }
+  };
+  auto add_bf16 = [&](float (&v)[8], const u32x4& w) {
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      v[2 * e] += __uint_as_float(w[e] << 16);
+      v[2 * e + 1] += __uint_as_float(w[e] & 0xffff0000u);
+      v[4 + 2 * e] += __uint_as_float(w[2 + e] << 16);
+      v[4 + 2 * e + 1] += __uint_as_float(w[2 + e] & 0xffff0000u);
+    }
+  };
+  auto finish = [&](int it, const float (&v)[8]) {
+    int64_t mr, nc;
+    item_pos(it, mr, nc);
+    store_item(p, nz, pre_noise ? zpre + it * 2 : nullptr, mr, nc, v, poisoned);
+  };
+  constexpr int R = (kPairRegionMax * 128 + kWideThreads - 1) / kWideThreads;
+  static_assert(R == 3, "three rounds of items per thread at most");
+  if (ng <= kPairFast) {
+    // every chunk of every item of this thread in flight at once (at most
+    // R x (kPairFast - 1) loads), then the sums
+    u32x4 w[R][kPairFast];
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+      const int it = threadIdx.x + k * kWideThreads;
+      if (it < nitems) {
+#pragma unroll
+        for (int qq = 0; qq < kPairFast; ++qq)
+          if (qq < ng && qq != q) w[k][qq] = slot_load(qq, it);
+      }
+    }
+#pragma unroll 1
+    for (int k = 0; k < R; ++k) {
+      const int it = threadIdx.x + k * kWideThreads;
+      if (it >= nitems) break;
+      float v[8] = {};
+      // (round k's chunks through selects: the register arrays stay static)
+#pragma unroll
+      for (int qq = 0; qq < kPairFast; ++qq) {
+        if (qq >= ng) break;
+        if (qq == q) add_own(v, it);
+        else add_bf16(v, k == 0 ? w[0][qq] : k == 1 ? w[1][qq] : w[2][qq]);
+      }
+      finish(it, v);
+    }
+  } else {
+#pragma unroll 1
+    for (int it = threadIdx.x; it < nitems; it += kWideThreads) {
+      float v[8] = {};
+      // chunks in pair order, kPairFast loads in flight at a time
+#pragma unroll 1
+      for (int qb = 0; qb < ng; qb += kPairFast) {
+        u32x4 w[kPairFast];
+#pragma unroll
+        for (int u = 0; u < kPairFast; ++u)
+          if (qb + u < ng && qb + u != q) w[u] = slot_load(qb + u, it);
+#pragma unroll
+        for (int u = 0; u < kPairFast; ++u) {
+          if (qb + u >= ng) break;
+          if (qb + u == q) add_own(v, it);
+          else add_bf16(v, w[u]);
+        }
+      }
+      finish(it, v);
+    }
+  }
+}
+
 // Tile orientation and workspace of the wide schedule for a problem: 384x192
 // (WGM = 4) or 192x384 (WGM = 2) output tiles, whichever wastes fewer
 // outputs; applicable when every product gets a CU of its own, the products
@@ -609,16 +1007,31 @@ __global__ __launch_bounds__(kWideThreads, 1) void wgrad_wide_kernel(WideArgs p)
 // sample's operand under 2^31 bytes (32-bit buffer records).
 
 struct WidePlan {
-  int wgm;  // 4: 384x192, 2: 192x384, 0: not applicable
+  // one sample per workgroup: wgm 4 (384x192 tiles), 2 (192x384), 0 (not applicable)
+  int wgm;
   int tiles_m, tiles_n, tiles, nwg;
   int slot_blocks;
-  size_t partial_bytes, slot_bytes;
-  size_t bias_part_bytes, bias_sq_bytes;  // the bias of a or b (reserved whether asked or not)
+  // two samples per workgroup (192x192 tiles, wgrad_pair_kernel): pair 0 = not applicable
+  int pair;
+  int pair_tiles_m, pair_tiles_n, pair_tiles, pair_nwg;
+  int pair_slot_blocks;
+  size_t partial_bytes, slot_bytes;       // the larger of the two layouts'
+  size_t bias_part_bytes, bias_sq_bytes;  // the bias of a or b (one sample per workgroup only;
+                                          // reserved whether asked or not)
+  bool any() const { return wgm != 0 || pair != 0; }
 };
+// The paired layout also needs whole k-tiles and both samples of a pair
+// inside one 32-bit buffer record ((sab + K * lda) * 2 bytes): checked here for
+// contiguous operands, by the caller for the strides of the call.
+inline bool pair_records_fit(int64_t K, int64_t ld, int64_t ds) {
+  return ds >= 0 && (ds + K * ld) * 2 < (int64_t(1) << 31);
+}
 inline WidePlan wide_plan(int64_t B, int64_t K, int64_t M, int64_t N, int64_t lda, int64_t ldb,
                           int cus, double min_fill) {
   WidePlan w{};
   if (K * lda * 2 >= (int64_t(1) << 31) || K * ldb * 2 >= (int64_t(1) << 31)) return w;
+  const double fill = double(M) * double(N) * double(B) / (double(cus) * 73728.0);
+  if (fill < min_fill) return w;
   int64_t best_tiles = 0;
   for (int wgm : {4, 2}) {
     const int64_t tm = 96 * wgm, tn = 96 * (8 / wgm);
@@ -632,21 +1045,39 @@ inline WidePlan wide_plan(int64_t B, int64_t K, int64_t M, int64_t N, int64_t ld
   }
   w.tiles = static_cast<int>(best_tiles);
   const int64_t units = best_tiles * B;
-  const double fill = double(M) * double(N) * double(B) / (double(cus) * 73728.0);
-  if (units > cus || fill < min_fill || B < 2 || B > kWideBlocks) {
+  if (units > cus || B < 2 || B > kWideBlocks) {
     w.wgm = 0;
-    return w;
+  } else {
+    w.nwg = static_cast<int>(units);
+    w.slot_blocks = kWideBlocks - static_cast<int>(kWideBlocks / B);
+    w.partial_bytes = sizeof(float) * size_t(units);
+    w.slot_bytes = size_t(units) * size_t(w.slot_blocks) * kWideBlockBytes;
+    // [tiles_own, W, B, tiles_other] with W <= 384 for either operand
+    w.bias_part_bytes = sizeof(float) * size_t(B) * w.tiles_m * w.tiles_n * 384;
+    w.bias_sq_bytes = sizeof(float) * size_t(units);
   }
-  w.nwg = static_cast<int>(units);
-  w.slot_blocks = kWideBlocks - static_cast<int>(kWideBlocks / B);
-  w.partial_bytes = sizeof(float) * size_t(units);
-  w.slot_bytes = size_t(units) * size_t(w.slot_blocks) * kWideBlockBytes;
-  // [tiles_own, W, B, tiles_other] with W <= 384 for either operand
-  w.bias_part_bytes = sizeof(float) * size_t(B) * w.tiles_m * w.tiles_n * 384;
-  w.bias_sq_bytes = sizeof(float) * size_t(units);
+  const int64_t ptm = (M + kPairTile - 1) / kPairTile, ptn = (N + kPairTile - 1) / kPairTile;
+  const int64_t punits = ptm * ptn * (B / 2);
+  if (B % 2 == 0 && B >= kPairMinB && B <= 2 * kPairBlocks && K % PairGeom::BK == 0 &&
+      ptm * ptn + 1 <= kGroupMax && punits <= cus && pair_records_fit(K, lda, K * lda) &&
+      pair_records_fit(K, ldb, K * ldb)) {
+    w.pair = 1;
+    w.pair_tiles_m = static_cast<int>(ptm);
+    w.pair_tiles_n = static_cast<int>(ptn);
+    w.pair_tiles = static_cast<int>(ptm * ptn);
+    w.pair_nwg = static_cast<int>(punits);
+    const int ng = static_cast<int>(B / 2);
+    w.pair_slot_blocks = kPairBlocks - kPairBlocks / ng;
+    const size_t pb = sizeof(uint64_t) * size_t(B) * w.pair_tiles;
+    const size_t sb = size_t(punits) * size_t(w.pair_slot_blocks) * kWideBlockBytes;
+    if (pb > w.partial_bytes) w.partial_bytes = pb;
+    if (sb > w.slot_bytes) w.slot_bytes = sb;
+  }
   return w;
 }
 
+// wgm 4 / 2: the one-sample kernel in that orientation; wgm 1: the paired
+// kernel (no bias).
 template <class DT>
 hipError_t launch_wide_t(const WideArgs& a, int wgm, bool plain, hipStream_t s) {
   const void* fns[2][3] = {
@@ -656,8 +1087,9 @@ hipError_t launch_wide_t(const WideArgs& a, int wgm, bool plain, hipStream_t s) 
       {reinterpret_cast<const void*>(&wgrad_wide_kernel<DT, 2, 4, 0>),
        reinterpret_cast<const void*>(&wgrad_wide_kernel<DT, 2, 4, 1>),
        reinterpret_cast<const void*>(&wgrad_wide_kernel<DT, 2, 4, 2>)}};
-  if (a.bias_op < 0 || a.bias_op > 2) return hipErrorInvalidValue;
-  const void* fn = fns[wgm == 4 ? 0 : 1][a.bias_op];
+  if (a.bias_op < 0 || a.bias_op > 2 || (wgm == 1 && a.bias_op != 0)) return hipErrorInvalidValue;
+  const void* fn = wgm == 1 ? reinterpret_cast<const void*>(&wgrad_pair_kernel<DT>)
+                            : fns[wgm == 4 ? 0 : 1][a.bias_op];
   if (host::occupancy(fn, kWideThreads, 0) < 1) return hipErrorNotSupported;
   WideArgs c = a;
   void* params[] = {&c};

@@ -155,7 +155,11 @@ int fdp_version(void);
  *            least 70% of them, and the grouped kernel (128x128 tiles, several
  *            samples per workgroup) otherwise; bit 4 (FDP_WGRAD_WIDE) takes the
  *            wide kernel whenever the products fit the CUs at all, bit 5
- *            (FDP_WGRAD_NARROW) never takes it;
+ *            (FDP_WGRAD_NARROW) never takes it.  Where the batch is even
+ *            (6 <= B <= 72), K is a multiple of 32 and no bias is asked for,
+ *            the wide schedule holds two samples' 192x192 tiles per CU and
+ *            adds them inside the CU (a quarter to a half of the exchanged
+ *            bytes); bit 7 (FDP_WGRAD_UNPAIRED) keeps one sample per CU;
  *            bit 3 (FDP_WGRAD_CLEAN_WORKSPACE) states that the workspace's
  *            control words (its first 2048 bytes) are valid -- a zero-filled
  *            buffer, or one whose last use was a completed fdp_wgrad_clip call
@@ -178,6 +182,7 @@ int fdp_version(void);
 #define FDP_WGRAD_CLEAN_WORKSPACE 8
 #define FDP_WGRAD_WIDE 16
 #define FDP_WGRAD_NARROW 32
+#define FDP_WGRAD_UNPAIRED 128
 
 int fdp_wgrad_clip_workspace_size(int64_t B, int64_t K, int64_t M, int64_t N,
                                   int dtype, int flags, size_t* bytes);

@@ -110,12 +110,13 @@ def test_wgrad_bias_fused(shape, sched, operand):
     assert_close(bo, ref_b, dtype, "bias", margin=tag)
     assert_elementwise(bn, ref_bn, dtype, "bias norms")
     assert_elementwise(bf, ref_bf, dtype, "bias factors")
-    # the weight gradient is the one fdp_wgrad_clip gives on the same schedule:
+    # the weight gradient is the one fdp_wgrad_clip gives on the same schedule
+    # (for the wide schedule its one-sample kernel, the one that forms biases):
     # bit for bit, except on the grouped schedule, which splits no products when
     # it also forms a bias (a split product is handed over in bf16)
     w_only = core.wgrad_clip(a, b, C, 1.0, out_scale=1.0 / B, noise=zw, noise_scale=0.25,
                              out_dtype=torch.float32, two_pass=sched == "stream",
-                             single_pass={"wide": "wide", "narrow": "narrow",
+                             single_pass={"wide": "unpaired", "narrow": "narrow",
                                           "stream": "auto"}[sched], check=True)
     if sched == "narrow":
         assert_close(out, w_only.double().cpu().numpy(), dtype, "weight vs weight-only call")

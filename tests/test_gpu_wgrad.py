@@ -329,12 +329,13 @@ def test_operator_api():
     assert_close(core.conv1d_weight_flashdp(x, g, 0.2, 1.0), ref, dtype, "conv1d_weight_flashdp")
 
 
-@pytest.mark.parametrize("single_pass", ["auto", "narrow"])
+@pytest.mark.parametrize("single_pass", ["auto", "unpaired", "narrow"])
 @pytest.mark.parametrize("dtype", [torch.bfloat16], ids=str)
 def test_wgrad_cfg2_full_size(dtype, single_pass):
     """cfg2 (Linear 768->3072, B=8, T=1024): norms and the clipped sum against an fp32
     torch reference on the GPU (per-sample bmm in fp32), all samples clipped; the
-    default kernel (the wide one at this shape) and the grouped one."""
+    default kernel (the paired wide one at this shape), the one-sample wide
+    kernel and the grouped one."""
     torch.manual_seed(0)
     x = torch.randn(8, 1024, 768, device=DEV).to(dtype)
     g = (torch.randn(8, 1024, 3072, device=DEV) * 0.02).to(dtype)
@@ -432,17 +433,22 @@ WIDE_SHAPES = [
     (2, 32, 384, 192),      # one tile, two samples: regions of 36 blocks
     (72, 16, 96, 96),       # 72 samples of one (mostly empty) tile: one block per region
     (3, 1, 200, 400),       # K = 1
-    (6, 256, 576, 768),     # 192x384 tiles (6 against 8 of 384x192)
+    (6, 256, 576, 768),     # 192x384 tiles (6 against 8 of 384x192); paired: regions of 12
+    (10, 64, 1000, 704),    # paired: ragged tiles, 5 pairs (regions of 7-8 blocks)
+    (18, 32, 384, 384),     # paired: 9 pairs, chunks loaded in two batches
+    (72, 32, 96, 96),       # paired: 36 pairs, one block per region
 ]
 
 
+@pytest.mark.parametrize("kernel", ["wide", "unpaired"])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=str)
 @pytest.mark.parametrize("shape", WIDE_SHAPES, ids=lambda s: "x".join(map(str, s)))
-def test_wgrad_wide_parity(shape, dtype):
-    """The wide single-pass kernel (one tile of one sample per CU), forced on
-    shapes it fits: clipped sum, norms and factors against the fp64 oracle, in
-    fp32 and the input dtype, both launch modes, bitwise-equal repeats, and the
-    grouped kernel within the same tolerance."""
+def test_wgrad_wide_parity(shape, dtype, kernel):
+    """The wide schedule, forced on shapes it fits ("wide": two samples per CU
+    where the batch is even, 6..72, and K % 32 == 0, else one; "unpaired": one
+    tile of one sample per CU): clipped sum, norms and factors against the fp64
+    oracle, in fp32 and the input dtype, both launch modes, bitwise-equal
+    repeats, and the grouped kernel within the same tolerance."""
     B, K, M, N = shape
     a, b = make(B, K, M, N, dtype, "tn", seed=50)
     _, n0, _ = O.wgrad_clip(a, b, 1.0, 1.0, "tn")
@@ -451,14 +457,14 @@ def test_wgrad_wide_parity(shape, dtype):
     outs = []
     for launch in ("plain", "cooperative"):
         out, n, f = core.wgrad_clip(a, b, C, 1.0, out_dtype=torch.float32, return_stats=True,
-                                    launch=launch, single_pass="wide", check=True)
+                                    launch=launch, single_pass=kernel, check=True)
         assert_close(out, ref, dtype, "out", margin=None if shape != WIDE_SHAPES[0] else
-                     f"wide kernel cfg2 shape: clipped sum, fp32 out ({dtype})")
+                     f"{kernel} kernel cfg2 shape: clipped sum, fp32 out ({dtype})")
         assert_elementwise(n, nref, dtype, "norms")
         assert_elementwise(f, fref, dtype, "factors")
         outs.append(out)
     assert torch.equal(outs[0], outs[1])
-    out16 = core.wgrad_clip(a, b, C, 1.0, single_pass="wide", check=True)
+    out16 = core.wgrad_clip(a, b, C, 1.0, single_pass=kernel, check=True)
     assert out16.dtype == dtype
     assert_close(out16, ref, dtype, "out (input dtype)")
     narrow = core.wgrad_clip(a, b, C, 1.0, out_dtype=torch.float32, single_pass="narrow",
@@ -466,16 +472,17 @@ def test_wgrad_wide_parity(shape, dtype):
     assert_close(narrow, ref, dtype, "grouped kernel")
 
 
+@pytest.mark.parametrize("kernel", ["wide", "unpaired"])
 @pytest.mark.parametrize("shape", [(8, 64, 392, 520), (8, 1024, 3072, 768), (5, 40, 200, 96)],
                          ids=lambda s: "x".join(map(str, s)))
-def test_wgrad_wide_noise(shape):
+def test_wgrad_wide_noise(shape, kernel):
     """Noise in the wide kernel's finish: the in-kernel Philox draw (each quad of
     lanes draws four rows' blocks and transposes them) equals the oracle's
     stream element for element; an injected tensor is added as given."""
     B, K, M, N = shape
     a, b = make(B, K, M, N, torch.bfloat16, "tn", seed=51)
     ref, _, _ = O.wgrad_clip(a, b, 0.5, 1.0, "tn")
-    kw = dict(out_scale=0.5, out_dtype=torch.float32, single_pass="wide", check=True)
+    kw = dict(out_scale=0.5, out_dtype=torch.float32, single_pass=kernel, check=True)
     out0 = core.wgrad_clip(a, b, 0.5, 1.0, noise_scale=0.25, **kw)
     out = core.wgrad_clip(a, b, 0.5, 1.0, noise_scale=0.25, noise_key=NOISE_KEY, **kw)
     z = PX.normals(M * N, *NOISE_KEY).reshape(M, N)
@@ -487,21 +494,23 @@ def test_wgrad_wide_noise(shape):
     assert_close(out2, 0.5 * ref + 0.25 * zt.double().cpu().numpy(), torch.bfloat16, "injected")
 
 
-def test_wgrad_wide_expired_wait(monkeypatch):
-    """A forced expiry of the wide kernel's grid wait: NaN outputs and a raised
-    check; the next call on the same workspace is exact."""
+@pytest.mark.parametrize("kernel", ["wide", "unpaired"])
+def test_wgrad_wide_expired_wait(monkeypatch, kernel):
+    """A forced expiry of the wide kernels' waits (the grid barrier, and the
+    paired kernel's per-tile wait): NaN outputs and a raised check; the next
+    call on the same workspace is exact."""
     from flashdp4review_amd import _lib
     a, b = make(8, 256, 3072, 768, torch.bfloat16, "tn", seed=52)
     ref, _, _ = O.wgrad_clip(a, b, 0.5, 1.0, "tn")
     core.wgrad_status()
     monkeypatch.setenv("FDP_WGRAD_SPIN_LIMIT", "0")
     with pytest.raises(_lib.FlashDPError):
-        core.wgrad_clip(a, b, 0.5, 1.0, out_dtype=torch.float32, single_pass="wide", check=True)
-    out = core.wgrad_clip(a, b, 0.5, 1.0, out_dtype=torch.float32, single_pass="wide")
+        core.wgrad_clip(a, b, 0.5, 1.0, out_dtype=torch.float32, single_pass=kernel, check=True)
+    out = core.wgrad_clip(a, b, 0.5, 1.0, out_dtype=torch.float32, single_pass=kernel)
     torch.cuda.synchronize()
     assert torch.isnan(out).any()
     monkeypatch.delenv("FDP_WGRAD_SPIN_LIMIT")
-    out = core.wgrad_clip(a, b, 0.5, 1.0, out_dtype=torch.float32, single_pass="wide")
+    out = core.wgrad_clip(a, b, 0.5, 1.0, out_dtype=torch.float32, single_pass=kernel)
     assert_close(out, ref, torch.bfloat16, "after expiry")
     assert core.wgrad_status() != 0
 
@@ -569,7 +578,10 @@ def test_wgrad_bias_fused_in_wide_kernel(shape, dtype):
 
     out, norms, fac, bo, bn, bf, untouched = run(_lib.WGRAD_WIDE, canary=True)
     assert untouched, "the bias took the column-sum fallback instead of the wide kernel"
-    w_only = run(_lib.WGRAD_WIDE, with_bias=False)
+    # the weight as the one-sample wide kernel forms it without a bias (the
+    # paired kernel, which takes weight-only calls where it applies, sums in
+    # another order)
+    w_only = run(_lib.WGRAD_WIDE | _lib.WGRAD_UNPAIRED, with_bias=False)
     assert torch.equal(out, w_only[0]) and torch.equal(norms, w_only[1])
     ref_b, ref_bn, ref_bf = O.colsum_clip(a, None, C, 1.0, "frob", 1.0 / (B * K), zb, 0.5)
     tag = f"bias fused in the wide kernel {shape} ({dtype})" if shape == BIAS_SHAPES[0] else None
