@@ -20,7 +20,12 @@ Conv1D (cfg3) and LayerNorm (cfg4) paths, and DP vs non-DP training tokens/s of
 the cfg5 decoder.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload cfg2|cfg3|cfg4]
-                       [--no-cpu-baseline] [--no-extra] [--copy-calibration MiB]
+                       [--single-pass auto|unpaired|narrow] [--no-cpu-baseline]
+                       [--no-extra] [--copy-calibration MiB]
+
+--single-pass picks the kernel of the cfg2/cfg3 step as wgrad_clip's argument
+of that name does (default auto: at cfg2 the paired wide kernel); the
+profiles of the other kernels are made with it.
 """
 from __future__ import annotations
 
@@ -45,10 +50,19 @@ PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 # and WRITE_SIZE runs of this script (the HBM traffic sections of profiles/*.md), each scaled by the
 # factor the same counter reads on a plain copy of known size.  None = not
 # measured for that workload.
-TRAFFIC_BYTES = {
-    "cfg2": 134224748,   # profiles/wgrad_wide_kernel_cfg2.md
-    "cfg3": 234360493,   # profiles/wgrad_group_kernel_cfg3.md (weight and bias in one launch)
-    "cfg4": 105565315,   # profiles/layernorm_bwd_clip_cfg4.md (one launch per call)
+TRAFFIC_BYTES = {  # (workload, --single-pass)
+    ("cfg2", "auto"): 109076755,      # profiles/wgrad_pair_kernel_cfg2.md
+    ("cfg2", "unpaired"): 134239518,  # profiles/wgrad_wide_kernel_cfg2.md
+    ("cfg3", "auto"): 234360493,     # profiles/wgrad_group_kernel_cfg3.md (weight and bias)
+    ("cfg4", "auto"): 105565315,     # profiles/layernorm_bwd_clip_cfg4.md (one launch per call)
+}
+# the dominant kernel of each (workload, --single-pass)
+KERNELS = {
+    ("cfg2", "auto"): "wgrad_pair_kernel (two samples' 192x192 tiles per CU)",
+    ("cfg2", "unpaired"): "wgrad_wide_kernel (one sample's 384x192 tile per CU)",
+    ("cfg2", "narrow"): "wgrad_group_kernel (128x128 tiles)",
+    ("cfg3", "auto"): "wgrad_group_kernel (weight and bias)",
+    ("cfg3", "narrow"): "wgrad_group_kernel (weight and bias)",
 }
 
 
@@ -558,6 +572,7 @@ def main():
                     help="untimed warm-up steps (default 100, enough for the clocks to settle; "
                          "cfg5: 2)")
     ap.add_argument("--workload", default="cfg2", choices=["cfg2", "cfg3", "cfg4", "cfg5"])
+    ap.add_argument("--single-pass", default="auto", choices=["auto", "unpaired", "narrow"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MiB",
@@ -602,16 +617,18 @@ def main():
     if args.workload == "cfg2":
         x, go, _ = cfg2_inputs(dev)
         B, T, I, O = 8, 1024, 768, 3072
-        step, _ = run_wgrad(x, go, torch.bfloat16)
-        step_coop, _ = run_wgrad(x, go, torch.bfloat16, launch="cooperative")
+        step, _ = run_wgrad(x, go, torch.bfloat16, single_pass=args.single_pass)
+        step_coop, _ = run_wgrad(x, go, torch.bfloat16, launch="cooperative",
+                                 single_pass=args.single_pass)
         workload = ("cfg2: DP Linear 768->3072 clipped per-sample weight grad, B=8 T=1024, "
                     "C=1, sigma=1")
     elif args.workload == "cfg3":
         x, go = cfg3_inputs(dev)
         B, T, I, O = 16, 1024, 768, 2304
-        step, _ = run_wgrad(x, go, torch.bfloat16, transpose=True, bias=True)
+        step, _ = run_wgrad(x, go, torch.bfloat16, transpose=True, bias=True,
+                            single_pass=args.single_pass)
         step_coop, _ = run_wgrad(x, go, torch.bfloat16, transpose=True, launch="cooperative",
-                                 bias=True)
+                                 bias=True, single_pass=args.single_pass)
         workload = ("cfg3: DP Conv1D 768->2304 clipped per-sample weight and bias grads in one "
                     "call, B=16 T=1024, norms 0.1C..10C")
     else:
@@ -668,7 +685,7 @@ def main():
         roof = {"bound": "hbm", "achieved": round(nbytes / call_ms / 1e6, 1),
                 "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(nbytes / call_ms / 1e6 / PEAK_HBM_GBS, 4),
-                "traffic": TRAFFIC_BYTES["cfg4"],
+                "traffic": TRAFFIC_BYTES[("cfg4", "auto")],
                 "kernel": "ln_bwd_fused_kernel: one launch per fdp_layernorm_bwd_clip call, "
                           "HIP events around the timed region",
                 "bytes_per_launch": nbytes, "avg_ms": round(call_ms, 4)}
@@ -679,9 +696,8 @@ def main():
         roof = {"bound": "mfma", "achieved": round(F / call_ms / 1e9, 2),
                 "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(F / call_ms / 1e9 / PEAK_BF16_TFLOPS, 4),
-                "traffic": TRAFFIC_BYTES[args.workload],
-                "kernel": ("wgrad_pair_kernel (two samples' 192x192 tiles per CU)"
-                           if args.workload == "cfg2" else "wgrad_group_kernel (weight and bias)")
+                "traffic": TRAFFIC_BYTES.get((args.workload, args.single_pass)),
+                "kernel": KERNELS.get((args.workload, args.single_pass), "single-pass kernel")
                           + ": one launch per fdp_wgrad_clip call, HIP events around the timed "
                             "region",
                 "flops_per_launch": F, "avg_ms": round(call_ms, 4)}
