@@ -29,6 +29,8 @@
 // and the outputs are NaN (the kernel still runs to completion).
 #pragma once
 
+#include <type_traits>
+
 #include "wgrad_core.hpp"
 
 namespace fdp {
@@ -627,15 +629,14 @@ __global__ __launch_bounds__(kWideThreads, 1) void wgrad_wide_kernel(WideArgs p)
 //
 //   1. the two products, their masked sums of squares -> partials[b, tile],
 //      each stored with the launch's tag in one 64-bit word;
-//   2. the noise of the workgroup's outputs is drawn (into LDS) while the
-//      pair's other workgroups finish; two waves then poll the pair's
-//      partials (all tiles of its two samples) until every one carries the
-//      tag, and form the two clip factors c;
+//   2. two waves poll the pair's partials (all tiles of its two samples)
+//      until every one carries the tag, and form the two clip factors c;
 //   3. S = c_2q G_2q + c_2q+1 G_2q+1 in fp32 (for each block one of the two
 //      waves holding it hands its scaled block to the other through LDS);
 //   4. the tile's 36 blocks are split into ng = B/2 regions, one per pair; the
 //      workgroup keeps its own region of S in LDS (fp32) and publishes every
-//      other block (bf16, agent-coherent) to its exchange slot;
+//      other block (bf16, agent-coherent) to its exchange slot, then draws
+//      the noise of its region (into LDS) while those stores drain;
 //   5. the ng workgroups of the tile wait for each other;
 //   6. finish: out = out_scale * sum_q S_q (q in pair order) + noise.
 //
@@ -689,6 +690,7 @@ __global__ __launch_bounds__(kWideThreads, 1) void wgrad_pair_kernel(WideArgs p)
   static_assert(4 * 3 * 16 * 64 * 4 <= G::STAGE, "a row of scaled blocks fits a stage");
   static_assert(kPairRegionMax * 16 * 64 * 4 <= G::STAGE, "the own region fits a stage");
   static_assert(kPairRegionMax * 128 * 2 * 16 <= G::STAGE, "the region's noise fits a stage");
+  static_assert(kPairRegionMax * 1024 * 4 <= G::STAGE, "the region's sums fit a stage");
   const dma::Stages stages{{(FDP_LDS char*)(st0), (FDP_LDS char*)(st1), (FDP_LDS char*)(st2),
                             (FDP_LDS char*)(st0)}};
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -781,38 +783,25 @@ __global__ __launch_bounds__(kWideThreads, 1) void wgrad_pair_kernel(WideArgs p)
   if (threadIdx.x == 0)
     started = __hip_atomic_fetch_add(start_cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
-  // item it of the region: block rb0 + it/128, half (it/64)%2, lane it%64 --
-  // rows mr + {0..3, 8..11} of column nc
-  auto item_pos = [&](int it, int64_t& mr, int64_t& nc) {
-    const int bid = rb0 + (it >> 7), h = (it >> 6) & 1, l = it & 63;
+  // The finish stores chunks of 8 consecutive outputs of one row: chunk ch
+  // of the region is row (ch / 4) % 32, columns 8 * (ch % 4) .. + 7 of block
+  // rb0 + ch / 128; chunk_pos gives its first output.
+  const int nchunks = (rb1 - rb0) * 128;
+  auto chunk_pos = [&](int ch, int64_t& row, int64_t& col) {
+    const int bid = rb0 + (ch >> 7), r = (ch >> 2) & 31;
     const int w = bid / 9, ij = bid % 9;
-    mr = m0 + (w >> 1) * 96 + 32 * (ij / 3) + 16 * h + 4 * (l >> 5);
-    nc = n0 + (w & 1) * 96 + 32 * (ij % 3) + (l & 31);
+    row = m0 + (w >> 1) * 96 + 32 * (ij / 3) + r;
+    col = n0 + (w & 1) * 96 + 32 * (ij % 3) + 8 * (ch & 3);
   };
-  // ---- 2. the noise of the region, drawn while the pair's other workgroups
-  // finish their products (st2: [item][row group])
   const NoiseSrc nz = p.noise.resolved();
   const bool pre_noise = nz.on() && nz.z == nullptr && p.N % 4 == 0;
-  f32x4* zpre = reinterpret_cast<f32x4*>(st2);
-  if (pre_noise) {
-#pragma unroll 1
-    for (int it = threadIdx.x; it < nitems; it += kWideThreads) {
-      int64_t mr, nc;
-      item_pos(it, mr, nc);
-#pragma unroll 1
-      for (int grp = 0; grp < 2; ++grp) {
-        const int64_t row = mr + 8 * grp + (lane & 3);
-        float blk[4];
-        nz.block((row * p.N + (nc & ~int64_t(3))) / 4, blk);
-        zpre[it * 2 + grp] = f32x4{blk[0], blk[1], blk[2], blk[3]};
-      }
-    }
-  }
+  f32x4* zpre = reinterpret_cast<f32x4*>(st2);  // the two Philox blocks of each chunk
+
   if (threadIdx.x == 0 && started + 1 == unsigned(p.nwg)) {
     __hip_atomic_store(start_cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __hip_atomic_fetch_add(p.epoch, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  // the clip factors: wave w < 2 polls sample s0 + w's partials (all tiles,
+  // ---- 2. the clip factors: wave w < 2 polls sample s0 + w's partials (all tiles,
   // written by the pair's workgroups) until each carries this launch's tag,
   // then sums them in tile order; a bounded wait
   if (wave < 2) {
@@ -858,34 +847,44 @@ __global__ __launch_bounds__(kWideThreads, 1) void wgrad_pair_kernel(WideArgs p)
 
   // ---- 3./4. S = c0 G0 + c1 G1, one row i of blocks at a time.  Waves w and
   // w + 4 hold the same blocks; for block (i, j) one of them (the stager)
-  // puts its scaled block in st0 ([wave][j][register][lane]) and the other
-  // (the adder, alternating with the block index) adds its own, then keeps
-  // the sum (own region, st1: [block][half][lane][8]) or publishes it (bf16).
+  // puts its scaled block in LDS ([wave][j][register quad][lane], 16-byte
+  // words; rows alternate between st0 and st2) and the other (the adder,
+  // alternating with the block index) adds its own, then keeps the sum (own
+  // region, st1: [block][half][lane][8]) or publishes it (bf16).  Row i + 1
+  // is staged while row i is added.
   const float cmine = fac[half];
-  float* stg = reinterpret_cast<float*>(st0);
+  f32x4* const stg[2] = {reinterpret_cast<f32x4*>(st0), reinterpret_cast<f32x4*>(st2)};
   f32x4* own = reinterpret_cast<f32x4*>(st1);
   const int slot_bytes = p.slot_blocks * kWideBlockBytes;
   {
     const CoherentSpan slot(reinterpret_cast<const float*>(p.slots + int64_t(L) * slot_bytes),
                             static_cast<uint32_t>(slot_bytes));
-#pragma unroll
-    for (int i = 0; i < 3; ++i) {
+    auto stage = [&](auto i_c, f32x4* buf) {
+      constexpr int i = decltype(i_c)::value;
 #pragma unroll
       for (int j = 0; j < 3; ++j)
         if (((i * 3 + j) & 1) != half) {
 #pragma unroll
-          for (int r = 0; r < 16; ++r)
-            stg[((wl * 3 + j) * 16 + r) * 64 + lane] = cmine * acc[i][j][r];
+          for (int r4 = 0; r4 < 4; ++r4)
+            buf[((wl * 3 + j) * 4 + r4) * 64 + lane] =
+                f32x4{cmine * acc[i][j][4 * r4], cmine * acc[i][j][4 * r4 + 1],
+                      cmine * acc[i][j][4 * r4 + 2], cmine * acc[i][j][4 * r4 + 3]};
         }
-      __syncthreads();
+    };
+    auto add = [&](auto i_c, const f32x4* buf) {
+      constexpr int i = decltype(i_c)::value;
 #pragma unroll
       for (int j = 0; j < 3; ++j) {
         if (((i * 3 + j) & 1) != half) continue;
         const int bid = wl * 9 + i * 3 + j;
         float v[16];
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          v[r] = __builtin_fmaf(cmine, acc[i][j][r], stg[((wl * 3 + j) * 16 + r) * 64 + lane]);
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const f32x4 o = buf[((wl * 3 + j) * 4 + r4) * 64 + lane];
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            v[4 * r4 + e] = __builtin_fmaf(cmine, acc[i][j][4 * r4 + e], o[e]);
+        }
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           if (bid >= rb0 && bid < rb1) {
@@ -902,10 +901,36 @@ __global__ __launch_bounds__(kWideThreads, 1) void wgrad_pair_kernel(WideArgs p)
           }
         }
       }
-      __syncthreads();  // st0 is rewritten by the next row
-    }
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    stage(I0{}, stg[0]);
+    __syncthreads();
+    stage(I1{}, stg[1]);
+    add(I0{}, stg[0]);
+    __syncthreads();
+    stage(I2{}, stg[0]);
+    add(I1{}, stg[1]);
+    __syncthreads();
+    add(I2{}, stg[0]);
   }
 
+  // the noise of the region (st2 is free again), drawn while the published
+  // blocks drain
+  if (pre_noise) {
+#pragma unroll 1
+    for (int ch = threadIdx.x; ch < nchunks; ch += kWideThreads) {
+      int64_t row, col;
+      chunk_pos(ch, row, col);
+#pragma unroll 1
+      for (int u = 0; u < 2; ++u) {
+        float blk[4];
+        nz.block((row * p.N + col) / 4 + u, blk);
+        zpre[ch * 2 + u] = f32x4{blk[0], blk[1], blk[2], blk[3]};
+      }
+    }
+  }
 
   // ---- 5. the tile's workgroups wait for each other
   unsigned* cnt = p.group_cnt + tile;
@@ -913,10 +938,15 @@ __global__ __launch_bounds__(kWideThreads, 1) void wgrad_pair_kernel(WideArgs p)
   poisoned = grid_wait(cnt, unsigned(ng), garr, p.err, nullptr, p.poison, tag, p.spin_limit, &flag,
                        0, 2) || poisoned;
 
-  // ---- 6. finish: out = out_scale * sum of the pairs' chunks of each item (in
-  // pair order) + noise
+  // ---- 6. finish.  Item it of the region (block rb0 + it/128, half
+  // (it/64)%2, lane it%64: rows {0..3, 8..11} + 16 half + 4 (lane/32) of
+  // column lane%32 of the block) is the sum of the pairs' chunks in pair
+  // order; the sums go to st0 in row-major blocks ([block][32 rows][32]),
+  // from which each thread stores chunks of 8 consecutive outputs of a row:
+  // out = out_scale * sum + noise_scale * z.
   const int64_t slot_stride = int64_t(p.tiles) * slot_bytes;  // between pairs of one tile
   const char* const slots_tile = p.slots + int64_t(tile) * slot_bytes;
+  float* const rows = reinterpret_cast<float*>(st0);
   auto slot_load = [&](int qq, int it) -> u32x4 {
     const int bid = rb0 + (it >> 7), h = (it >> 6) & 1, l = it & 63;
     const CoherentSpan sl(reinterpret_cast<const float*>(slots_tile + qq * slot_stride),
@@ -943,10 +973,14 @@ __global__ __launch_bounds__(kWideThreads, 1) void wgrad_pair_kernel(WideArgs p)
       v[4 + 2 * e + 1] += __uint_as_float(w[2 + e] & 0xffff0000u);
     }
   };
-  auto finish = [&](int it, const float (&v)[8]) {
-    int64_t mr, nc;
-    item_pos(it, mr, nc);
-    store_item(p, nz, pre_noise ? zpre + it * 2 : nullptr, mr, nc, v, poisoned);
+  auto put_rows = [&](int it, const float (&v)[8]) {
+    const int lb = it >> 7, h = (it >> 6) & 1, l = it & 63;
+    float* b = rows + lb * 1024 + (16 * h + 4 * (l >> 5)) * 32 + (l & 31);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      b[e * 32] = v[e];
+      b[(8 + e) * 32] = v[4 + e];
+    }
   };
   constexpr int R = (kPairRegionMax * 128 + kWideThreads - 1) / kWideThreads;
   static_assert(R == 3, "three rounds of items per thread at most");
@@ -975,7 +1009,7 @@ __global__ __launch_bounds__(kWideThreads, 1) void wgrad_pair_kernel(WideArgs p)
         if (qq == q) add_own(v, it);
         else add_bf16(v, k == 0 ? w[0][qq] : k == 1 ? w[1][qq] : w[2][qq]);
       }
-      finish(it, v);
+      put_rows(it, v);
     }
   } else {
 #pragma unroll 1
@@ -995,7 +1029,68 @@ __global__ __launch_bounds__(kWideThreads, 1) void wgrad_pair_kernel(WideArgs p)
           else add_bf16(v, w[u]);
         }
       }
-      finish(it, v);
+      put_rows(it, v);
+    }
+  }
+  __syncthreads();
+  const int oes = p.out_dtype == FDP_F32 ? 4 : 2;
+  const bool vec8 = reinterpret_cast<uintptr_t>(p.out) % (8 * oes) == 0 && p.ldo % 8 == 0;
+#pragma unroll 1
+  for (int ch = threadIdx.x; ch < nchunks; ch += kWideThreads) {
+    int64_t row, col;
+    chunk_pos(ch, row, col);
+    const f32x4* src = reinterpret_cast<const f32x4*>(rows + (ch >> 7) * 1024 + ((ch >> 2) & 31) * 32 +
+                                                      8 * (ch & 3));
+    float o[8];
+    {
+      const f32x4 lo = src[0], hi = src[1];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        o[e] = lo[e] * p.out_scale;
+        o[4 + e] = hi[e] * p.out_scale;
+      }
+    }
+    if (nz.on()) {
+      if (pre_noise) {
+        const f32x4 z0 = zpre[ch * 2], z1 = zpre[ch * 2 + 1];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          o[e] += p.noise_scale * z0[e];
+          o[4 + e] += p.noise_scale * z1[e];
+        }
+      } else {
+        // an injected tensor, or rows of N % 4 != 0 outputs: element by element
+#pragma unroll 1
+        for (int e = 0; e < 8; ++e) {
+          const float ze = (row < p.M && col + e < p.N) ? nz.at(row * p.N + col + e) : 0.f;
+#pragma unroll
+          for (int d = 0; d < 8; ++d) o[d] += d == e ? p.noise_scale * ze : 0.f;
+        }
+      }
+    }
+    if (poisoned) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = __builtin_nanf("");
+    }
+    if (row >= p.M) continue;
+    const int64_t at = row * p.ldo + col;
+    if (vec8 && col + 8 <= p.N) {
+      if (p.out_dtype == FDP_F32) {
+        f32x4* d = reinterpret_cast<f32x4*>(static_cast<float*>(p.out) + at);
+        d[0] = f32x4{o[0], o[1], o[2], o[3]};
+        d[1] = f32x4{o[4], o[5], o[6], o[7]};
+      } else {
+        u32x4 pk;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          pk[e] = p.out_dtype == FDP_BF16 ? BF16::pack2(o[2 * e], o[2 * e + 1])
+                                          : F16::pack2(o[2 * e], o[2 * e + 1]);
+        *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(p.out) + at) = pk;
+      }
+    } else {
+#pragma unroll 1
+      for (int e = 0; e < 8; ++e)
+        if (col + e < p.N) store_from_f32(p.out, at + e, p.out_dtype, o[e]);
     }
   }
 }
