@@ -51,7 +51,7 @@ PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 # factor the same counter reads on a plain copy of known size.  None = not
 # measured for that workload.
 TRAFFIC_BYTES = {  # (workload, --single-pass)
-    ("cfg2", "auto"): 109076755,      # profiles/wgrad_pair_kernel_cfg2.md
+    ("cfg2", "auto"): 109053575,      # profiles/wgrad_pair_kernel_cfg2.md
     ("cfg2", "unpaired"): 134239518,  # profiles/wgrad_wide_kernel_cfg2.md
     ("cfg3", "auto"): 234360493,     # profiles/wgrad_group_kernel_cfg3.md (weight and bias)
     ("cfg4", "auto"): 105565315,     # profiles/layernorm_bwd_clip_cfg4.md (one launch per call)
