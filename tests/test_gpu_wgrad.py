@@ -494,6 +494,32 @@ def test_wgrad_wide_noise(shape, kernel):
     assert_close(out2, 0.5 * ref + 0.25 * zt.double().cpu().numpy(), torch.bfloat16, "injected")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=str)
+def test_wgrad_paired_strided_operands(dtype):
+    """The paired wide kernel reads both samples of a pair through one buffer
+    record (sample stride sab apart): samples taken every other one from a
+    larger batch (sab = 2 * K * lda), rows padded past N (ldb > N) with
+    N % 4 != 0 (the noise is then drawn element by element and the outputs
+    stored one by one), against the fp64 oracle and the oracle's Philox stream."""
+    B, K, M, N = 8, 64, 576, 390
+    ga, gb = make(2 * B, K, M, 400, dtype, "tn", seed=53)
+    a = ga[::2]                   # [8, 64, 576], sample stride 2 * K * M
+    b = gb[::2, :, :N]            # [8, 64, 390], sample stride 2 * K * 400, ldb = 400
+    assert a.stride(0) == 2 * K * M and b.stride(1) == 400
+    ref, nref, fref = O.wgrad_clip(a, b, 0.5, 1.0, "tn")
+    kw = dict(out_scale=0.5, out_dtype=torch.float32, single_pass="wide", check=True)
+    out, n, f = core.wgrad_clip(a, b, 0.5, 1.0, return_stats=True, **kw)
+    assert_close(out, 0.5 * ref, dtype, "paired, strided operands")
+    assert_elementwise(n, nref, dtype, "norms")
+    assert_elementwise(f, fref, dtype, "factors")
+    unpaired = core.wgrad_clip(a, b, 0.5, 1.0, **{**kw, "single_pass": "unpaired"})
+    assert_close(unpaired, 0.5 * ref, dtype, "one sample per CU, same operands")
+    noisy = core.wgrad_clip(a, b, 0.5, 1.0, noise_scale=0.25, noise_key=NOISE_KEY, **kw)
+    z = PX.normals(M * N, *NOISE_KEY).reshape(M, N)
+    got = (noisy.double() - out.double()).cpu().numpy() / 0.25
+    assert np.max(np.abs(got - z)) < 1e-4, np.max(np.abs(got - z))
+
+
 @pytest.mark.parametrize("kernel", ["wide", "unpaired"])
 def test_wgrad_wide_expired_wait(monkeypatch, kernel):
     """A forced expiry of the wide kernels' waits (the grid barrier, and the
