@@ -80,13 +80,15 @@ def test_layernorm_fwd_parity(H, dtype):
                                    (1, 1, 64), (20, 8, 4096), (70, 3, 1000), (3, 9, 1001),
                                    (4, 128, 8192), (2, 40, 16384), (3, 17, 5000), (1, 3, 4100),
                                    (4, 1024, 512), (2, 9, 32768), (3, 17, 16385), (5, 8, 20000),
-                                   (2, 70, 40000)],
+                                   (2, 70, 40000), (8, 1024, 2048), (270, 2, 64), (300, 2, 256)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_layernorm_bwd_parity(shape, dtype):
     """Paths: B*H <= 65536 with at most 16 row chunks per sample runs in one
-    launch (cfg4 and the small shapes); 4x1024x512 (32 chunks per sample) runs
-    the rows, then the one-workgroup-per-stream reduction; 20x8x4096 and
-    70x3x1000 (B*H > 65536) the rows, then the two reduction kernels.  Rows of
+    launch (cfg4, the small shapes, 270x2x64 with more workgroups than CUs);
+    4x1024x512 and 8x1024x2048 (cfg5's LayerNorm; 32 chunks per sample) run
+    the rows, then the one-workgroup-per-stream reduction; 20x8x4096,
+    70x3x1000 and 300x2x256 (B*H > 65536) the rows, then the two reduction
+    kernels.  Rows of
     1025..4096 elements share a row among 2 or 4 wavefronts; above 4096 among
     16 (8192, 16384, 5000, 4100; 5000 and 4100 leave threads without columns,
     4100 is also unaligned in 16-bit).  Longer rows take the per-row statistics
