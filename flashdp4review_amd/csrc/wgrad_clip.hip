@@ -513,7 +513,7 @@ int wgrad_clip_impl(const void* a, const void* b, int64_t B, int64_t K, int64_t 
   hipStream_t s = static_cast<hipStream_t>(stream);
   // Wide single pass: 16-bit TN inputs, aligned rows, two samples' products
   // per CU (paired) or one.
-  const bool pair = pl.wp.pair != 0 && bias == nullptr && pair_records_fit(K, lda, stride_ab) &&
+  const bool pair = pl.wp.pair != 0 && pair_records_fit(K, lda, stride_ab) &&
                     pair_records_fit(K, ldb, stride_bb);
   if (!noclip && (flags & FDP_WGRAD_TWO_PASS) == 0 && layout == FDP_LAYOUT_TN && vec && K > 0 &&
       dtype != FDP_F32 && (pair || pl.wp.wgm != 0)) {
@@ -557,6 +557,8 @@ int wgrad_clip_impl(const void* a, const void* b, int64_t B, int64_t K, int64_t 
       w.bias_op = bias_op;
       w.bias_part = reinterpret_cast<float*>(ws + pl.off_wide_bias_part);
       w.bias_sq = reinterpret_cast<float*>(ws + pl.off_wide_bias_sq);
+      w.bias_tagged = reinterpret_cast<uint64_t*>(ws + pl.off_wide_bias_part);
+      w.bias_sq_tagged = reinterpret_cast<uint64_t*>(ws + pl.off_wide_bias_sq);
       w.bias_out = bias->out;
       w.bias_dtype = bias->out_dtype;
       w.bias_scale = bias->out_scale;

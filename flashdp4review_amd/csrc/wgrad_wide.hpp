@@ -74,6 +74,10 @@ struct WideArgs {
   unsigned* group_cnt;  // paired kernel: [tiles] per-tile counters, then one start
                         // counter (zero between launches)
   uint64_t* tagged;     // paired kernel: [B, tiles] partials, each with its launch tag
+  // paired kernel, bias of a (bias_op 1) or b (bias_op 2), tagged like `tagged`:
+  uint64_t* bias_tagged;     // [len rounded up to 192][B][P] column sums over a tile's
+                             // counted k-tiles (P: tiles along the other axis)
+  uint64_t* bias_sq_tagged;  // [B, tiles] their sums of squares
   // The bias of operand a (bias_op 1, rows m) or b (bias_op 2, columns n):
   //   bias[c] = bias_scale * sum_b c'_b sum_k op_b[k, c] + bias_noise_scale * zb[c],
   //   c'_b = clip(||op_b||_F) with the weight's C and clamp.
@@ -675,8 +679,16 @@ __device__ __forceinline__ int pair_region_first(int q, int ng) {
   return (q * kPairBlocks + ng - 1) / ng;
 }
 
-template <class DT>
+// BOP 1 / 2: also the bias of operand a / b (the counting rule of the wide
+// kernel: k-tile kt is counted by the tile whose index along the other axis is
+// kt % (tiles there), k-step ks by the sample's wave with index ks among the
+// two that share the fragment).  Each workgroup publishes its two samples'
+// column sums and squares as tagged words right after the products, and
+// finishes bias outputs [L * ceil(len / nwg), ...) at the end, when they have
+// long been visible.
+template <class DT, int BOP>
 __global__ __launch_bounds__(kWideThreads, 1) void wgrad_pair_kernel(WideArgs p) {
+  constexpr bool BIAS = BOP != 0;
   using G = PairGeom;
   constexpr int S = kWideStages;
   __shared__ __attribute__((aligned(16))) char st0[G::STAGE];
@@ -685,6 +697,9 @@ __global__ __launch_bounds__(kWideThreads, 1) void wgrad_pair_kernel(WideArgs p)
   __shared__ float red[8];
   __shared__ float fac[2];
   __shared__ int bad2[2];
+  __shared__ float bred[8];
+  __shared__ float bfac[BIAS ? kWideBlocks : 1];  // bias clip factors (B <= 72)
+  __shared__ int bbad;
   __shared__ unsigned tag_s;
   __shared__ int flag;
   static_assert(4 * 3 * 16 * 64 * 4 <= G::STAGE, "a row of scaled blocks fits a stage");
@@ -718,6 +733,27 @@ __global__ __launch_bounds__(kWideThreads, 1) void wgrad_pair_kernel(WideArgs p)
   const int rb0 = pair_region_first(q, ng), rb1 = pair_region_first(q + 1, ng);
   const int nitems = (rb1 - rb0) * 128;
 
+  // bias: this lane's columns of the bias operand (rows wm + 32 i + lane % 32
+  // of a, or columns wn + 32 j + lane % 32 of b; k half lane / 32)
+  const int tile_m = static_cast<int>(m0 / kPairTile), tile_n = static_cast<int>(n0 / kPairTile);
+  const int blim = bias_limit(BOP == 1 ? p.M : p.N, BOP == 1 ? m0 : n0);
+  float bcs[3] = {0.f, 0.f, 0.f}, bsq = 0.f;
+  auto fhook = [&](int kt, int ks, const dma::Frags<G>& f) {
+    if constexpr (BOP == 1) {
+      if (kt % p.tiles_n == tile_n && (wl & 1) == ks) {
+#pragma unroll
+        for (int i = 0; i < 3; ++i)
+          bias_frag<DT>(f.a[i], bcs[i], bsq, wm + 32 * i + (lane & 31), blim);
+      }
+    } else if constexpr (BOP == 2) {
+      if (kt % p.tiles_m == tile_m && (wl >> 1) == ks) {
+#pragma unroll
+        for (int j = 0; j < 3; ++j)
+          bias_frag<DT>(f.b[j], bcs[j], bsq, wn + 32 * j + (lane & 31), blim);
+      }
+    }
+  };
+
   // ---- 1. the two products
   f32x16 acc[3][3];
 #pragma unroll
@@ -731,7 +767,8 @@ __global__ __launch_bounds__(kWideThreads, 1) void wgrad_pair_kernel(WideArgs p)
     fo.init(half * kPairTile + wm, half * kPairTile + wn);
     dma::PairJob<G> job;
     job.init(p.a + s0 * p.sab, p.lda, p.sab, p.b + s0 * p.sbb, p.ldb, p.sbb, p.K, m0, n0);
-    dma::gemm_pipe<DT, G, S>(job, static_cast<int>(p.K / G::BK), fo, stages, acc);
+    dma::gemm_pipe<DT, G, S>(job, static_cast<int>(p.K / G::BK), fo, stages, acc, dma::NoHook(),
+                             fhook);
   }
   {
     // rows/columns past M/N may hold the next row's values: left out of the norm
@@ -761,7 +798,10 @@ __global__ __launch_bounds__(kWideThreads, 1) void wgrad_pair_kernel(WideArgs p)
     }
     sq = wave_sum_dpp(sq);
     if (lane == 0) red[wave] = sq;
-    if (threadIdx.x == 0) tag_s = tag;
+    if (threadIdx.x == 0) {
+      tag_s = tag;
+      bbad = 0;
+    }
     __syncthreads();
     tag = tag_s;
     // the two samples' partials of this tile, each one 64-bit store of the
@@ -775,6 +815,42 @@ __global__ __launch_bounds__(kWideThreads, 1) void wgrad_pair_kernel(WideArgs p)
                          __HIP_MEMORY_SCOPE_AGENT);
     }
   }
+  if constexpr (BIAS) {
+    // the bias's column sums: lanes l and l + 32 hold one column's two k
+    // halves; the two waves of a sample that share a fragment (one k-step
+    // each) are added in wave order through st0 ([sample][wave][192], free:
+    // gemm_pipe ended on a barrier).  Then one tagged word per (column,
+    // sample) and one per (sample, tile) for the squares.
+    float* colp = reinterpret_cast<float*>(st0);
+    const int ws = BOP == 1 ? (wl & 1) : (wl >> 1);
+    const int cl0 = BOP == 1 ? wm : wn;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      const float v = bcs[i] + __shfl_xor(bcs[i], 32, kWave);
+      if (lane < 32) colp[(half * 2 + ws) * kPairTile + cl0 + 32 * i + lane] = v;
+    }
+    const float q = wave_sum_dpp(bsq);
+    if (lane == 0) bred[wave] = q;
+    __syncthreads();
+    const int own = BOP == 1 ? tile_m : tile_n, oth = BOP == 1 ? tile_n : tile_m;
+    const int P = BOP == 1 ? p.tiles_n : p.tiles_m;
+    for (int r = threadIdx.x; r < 2 * kPairTile; r += kWideThreads) {
+      const int h = r / kPairTile, c = r % kPairTile;
+      const float v = colp[(h * 2) * kPairTile + c] + colp[(h * 2 + 1) * kPairTile + c];
+      const int64_t word = ((int64_t(own) * kPairTile + c) * p.B + s0 + h) * P + oth;
+      __hip_atomic_store(p.bias_tagged + word, (uint64_t(~tag) << 32) | __float_as_uint(v),
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (threadIdx.x < 2) {
+      const float* q4 = bred + 4 * threadIdx.x;
+      const float v = (q4[0] + q4[1]) + (q4[2] + q4[3]);
+      __hip_atomic_store(p.bias_sq_tagged + (s0 + threadIdx.x) * p.tiles + tile,
+                         (uint64_t(~tag) << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();  // (st0 is staged into next)
+  }
+
   // The launch epoch (the next launch's tags) advances once every workgroup
   // has read it: the last one to count itself here advances it and resets the
   // self-clearing counter.
@@ -1093,6 +1169,114 @@ __global__ __launch_bounds__(kWideThreads, 1) void wgrad_pair_kernel(WideArgs p)
         if (col + e < p.N) store_from_f32(p.out, at + e, p.out_dtype, o[e]);
     }
   }
+
+  // ---- 7. the bias: outputs [L * per, (L + 1) * per) of len, eight threads
+  // each.  Output c is the sum over the J = B * P partials (sample s, partial
+  // q; word j = s * P + q) of c'_s * part[c][s][q]: thread u of the eight takes
+  // words u, u + 8, ... in that order, and the eight sums are added in a fixed
+  // tree.  The clip factors c'_s are formed by every workgroup from all
+  // samples' squares (wave w: samples w, w + 8, ...).  Every word was published
+  // right after the products; the first words are requested before the
+  // squares, so that one round trip brings both.  The polls are bounded like
+  // the others.
+  if constexpr (BIAS) {
+    const int64_t len = BOP == 1 ? p.M : p.N;
+    const int P = BOP == 1 ? p.tiles_n : p.tiles_m;
+    const int nb = static_cast<int>(p.B);
+    const int J = nb * P;
+    const uint32_t want = ~tag;
+    const int64_t per = (len + p.nwg - 1) / p.nwg;
+    const int64_t lo = int64_t(L) * per, hi = lo + per < len ? lo + per : len;
+    const int sub = threadIdx.x & 7;
+    uint64_t w8[8];
+    auto issue = [&](int64_t m, int j0) {
+      const uint64_t* words = p.bias_tagged + m * J;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int j = j0 + sub + 8 * u;
+        w8[u] = m < hi && j < J
+                    ? __hip_atomic_load(words + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                    : uint64_t(want) << 32;
+      }
+    };
+    issue(lo + (threadIdx.x >> 3), 0);
+    {
+      float C = p.C, clamp = p.clamp;
+      if (p.clip_args_dev != nullptr) {
+        C = p.clip_args_dev[0];
+        clamp = p.clip_args_dev[1];
+      }
+      for (int sm = wave; sm < nb; sm += kWideThreads / kWave) {
+        const uint64_t* part = p.bias_sq_tagged + int64_t(sm) * p.tiles;
+        float a = 0.f;
+        bool bad = false;
+        for (int t0 = 0; t0 < p.tiles && !bad; t0 += kWave) {
+          const int t = t0 + lane;
+          uint64_t v = uint64_t(want) << 32;
+          for (unsigned spins = 0;; ++spins) {
+            if (spins >= p.spin_limit) {
+              bad = true;
+              break;
+            }
+            if (t < p.tiles) v = __hip_atomic_load(part + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (__all(uint32_t(v >> 32) == want)) break;
+            __builtin_amdgcn_s_sleep(2);
+          }
+          a += __uint_as_float(uint32_t(v));
+        }
+        a = wave_sum_dpp(a);
+        if (lane == 0) {
+          const float n = bad || poisoned ? __builtin_nanf("") : sqrtf(a);
+          const float cf = bad || poisoned ? n : clip_factor(n, C, clamp);
+          bfac[sm] = cf;
+          if (bad) {
+            bbad = 1;
+            expire(p.err, p.poison, tag);
+          }
+          if (L == 0) {  // one writer
+            if (p.bias_norms) p.bias_norms[sm] = n;
+            if (p.bias_factors) p.bias_factors[sm] = cf;
+          }
+        }
+      }
+    }
+    __syncthreads();
+    for (int64_t mb = lo; mb < hi; mb += kWideThreads / 8) {
+      const int64_t m = mb + (threadIdx.x >> 3);
+      const uint64_t* words = p.bias_tagged + m * J;
+      float v = 0.f;
+      bool bad = false;
+#pragma unroll 1
+      for (int j0 = 0; j0 < J; j0 += 64) {
+        if (mb != lo || j0 != 0) issue(m, j0);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int j = j0 + sub + 8 * u;
+          // (a word not yet visible is polled again, boundedly)
+          for (unsigned spins = 0; uint32_t(w8[u] >> 32) != want; ++spins) {
+            if (spins >= p.spin_limit) {
+              bad = true;
+              w8[u] = uint64_t(want) << 32;
+              break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+            w8[u] = __hip_atomic_load(words + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+          if (m < hi && j < J) v += bfac[j / P] * __uint_as_float(uint32_t(w8[u]));
+        }
+      }
+      if (bad && bbad == 0 && !poisoned) expire(p.err, p.poison, tag);
+      if (bad || bbad != 0 || poisoned) v = __builtin_nanf("");
+      v += __shfl_xor(v, 1, kWave);
+      v += __shfl_xor(v, 2, kWave);
+      v += __shfl_xor(v, 4, kWave);
+      if (sub == 0 && m < hi) {
+        v *= p.bias_scale;
+        if (p.bias_noise.on()) v += p.bias_noise_scale * p.bias_noise.at(m);
+        store_from_f32(p.bias_out, m, p.bias_dtype, v);
+      }
+    }
+  }
 }
 
 // Tile orientation and workspace of the wide schedule for a problem: 384x192
@@ -1111,8 +1295,8 @@ struct WidePlan {
   int pair_tiles_m, pair_tiles_n, pair_tiles, pair_nwg;
   int pair_slot_blocks;
   size_t partial_bytes, slot_bytes;       // the larger of the two layouts'
-  size_t bias_part_bytes, bias_sq_bytes;  // the bias of a or b (one sample per workgroup only;
-                                          // reserved whether asked or not)
+  size_t bias_part_bytes, bias_sq_bytes;  // the bias of a or b, the larger of the two
+                                          // layouts' (reserved whether asked or not)
   bool any() const { return wgm != 0 || pair != 0; }
 };
 // The paired layout also needs whole k-tiles and both samples of a pair
@@ -1165,14 +1349,19 @@ inline WidePlan wide_plan(int64_t B, int64_t K, int64_t M, int64_t N, int64_t ld
     w.pair_slot_blocks = kPairBlocks - kPairBlocks / ng;
     const size_t pb = sizeof(uint64_t) * size_t(B) * w.pair_tiles;
     const size_t sb = size_t(punits) * size_t(w.pair_slot_blocks) * kWideBlockBytes;
+    // bias: [tiles_own * 192][B][P] words with tiles_own * P = the tile count
+    const size_t bp = sizeof(uint64_t) * size_t(kPairTile) * size_t(B) * w.pair_tiles;
+    const size_t bq = sizeof(uint64_t) * size_t(B) * w.pair_tiles;
     if (pb > w.partial_bytes) w.partial_bytes = pb;
     if (sb > w.slot_bytes) w.slot_bytes = sb;
+    if (bp > w.bias_part_bytes) w.bias_part_bytes = bp;
+    if (bq > w.bias_sq_bytes) w.bias_sq_bytes = bq;
   }
   return w;
 }
 
 // wgm 4 / 2: the one-sample kernel in that orientation; wgm 1: the paired
-// kernel (no bias).
+// kernel.
 template <class DT>
 hipError_t launch_wide_t(const WideArgs& a, int wgm, bool plain, hipStream_t s) {
   const void* fns[2][3] = {
@@ -1182,9 +1371,11 @@ hipError_t launch_wide_t(const WideArgs& a, int wgm, bool plain, hipStream_t s) 
       {reinterpret_cast<const void*>(&wgrad_wide_kernel<DT, 2, 4, 0>),
        reinterpret_cast<const void*>(&wgrad_wide_kernel<DT, 2, 4, 1>),
        reinterpret_cast<const void*>(&wgrad_wide_kernel<DT, 2, 4, 2>)}};
-  if (a.bias_op < 0 || a.bias_op > 2 || (wgm == 1 && a.bias_op != 0)) return hipErrorInvalidValue;
-  const void* fn = wgm == 1 ? reinterpret_cast<const void*>(&wgrad_pair_kernel<DT>)
-                            : fns[wgm == 4 ? 0 : 1][a.bias_op];
+  const void* pairs[3] = {reinterpret_cast<const void*>(&wgrad_pair_kernel<DT, 0>),
+                          reinterpret_cast<const void*>(&wgrad_pair_kernel<DT, 1>),
+                          reinterpret_cast<const void*>(&wgrad_pair_kernel<DT, 2>)};
+  if (a.bias_op < 0 || a.bias_op > 2) return hipErrorInvalidValue;
+  const void* fn = wgm == 1 ? pairs[a.bias_op] : fns[wgm == 4 ? 0 : 1][a.bias_op];
   if (host::occupancy(fn, kWideThreads, 0) < 1) return hipErrorNotSupported;
   WideArgs c = a;
   void* params[] = {&c};

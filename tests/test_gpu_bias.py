@@ -23,7 +23,8 @@ from flashdp4review_amd import _lib, core
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
-SCHEDULES = {"wide": _lib.WGRAD_WIDE, "narrow": _lib.WGRAD_NARROW, "stream": _lib.WGRAD_TWO_PASS}
+SCHEDULES = {"wide": _lib.WGRAD_WIDE, "unpaired": _lib.WGRAD_WIDE | _lib.WGRAD_UNPAIRED,
+             "narrow": _lib.WGRAD_NARROW, "stream": _lib.WGRAD_TWO_PASS}
 
 
 def make(B, K, M, N, dtype, seed=0):
@@ -73,9 +74,11 @@ def run_bias_call(a, b, C, flags, operand, zw, zb, canary):
 
 # (shape B, K, M, N; the schedules that take it)
 CASES = [
-    ((8, 1024, 3072, 768), ("wide", "narrow", "stream")),  # cfg2 (wide by default)
+    # cfg2 (paired wide kernel by default; the one-sample wide kernel unpaired)
+    ((8, 1024, 3072, 768), ("wide", "unpaired", "narrow", "stream")),
     ((16, 1024, 768, 2304), ("narrow", "stream")),        # cfg3: Conv1D x^T g (grouped by default)
-    ((12, 64, 1000, 704), ("wide", "narrow", "stream")),  # ragged tiles both ways
+    ((12, 64, 1000, 704), ("wide", "unpaired", "narrow", "stream")),  # ragged tiles both ways
+    ((6, 96, 392, 1160), ("wide",)),                      # paired, 3 x 7 tiles of 192
     ((5, 40, 520, 392), ("wide", "narrow", "stream")),    # one partial k-tile: idle partial slots
     ((4, 200, 1536, 384), ("wide", "narrow", "stream")),  # partial last k-tile
     ((20, 32, 3072, 1536), ("narrow", "stream")),         # grouped: five launches of 4 samples
@@ -111,13 +114,13 @@ def test_wgrad_bias_fused(shape, sched, operand):
     assert_elementwise(bn, ref_bn, dtype, "bias norms")
     assert_elementwise(bf, ref_bf, dtype, "bias factors")
     # the weight gradient is the one fdp_wgrad_clip gives on the same schedule
-    # (for the wide schedule its one-sample kernel, the one that forms biases):
-    # bit for bit, except on the grouped schedule, which splits no products when
-    # it also forms a bias (a split product is handed over in bf16)
+    # and kernel: bit for bit, except on the grouped schedule, which splits no
+    # products when it also forms a bias (a split product is handed over in bf16)
     w_only = core.wgrad_clip(a, b, C, 1.0, out_scale=1.0 / B, noise=zw, noise_scale=0.25,
                              out_dtype=torch.float32, two_pass=sched == "stream",
-                             single_pass={"wide": "unpaired", "narrow": "narrow",
-                                          "stream": "auto"}[sched], check=True)
+                             single_pass={"wide": "wide", "unpaired": "unpaired",
+                                          "narrow": "narrow", "stream": "auto"}[sched],
+                             check=True)
     if sched == "narrow":
         assert_close(out, w_only.double().cpu().numpy(), dtype, "weight vs weight-only call")
     else:
@@ -149,7 +152,7 @@ def test_wgrad_bias_fp32_takes_column_sums(operand):
     assert_close(out, ref_w, torch.float32, "weight")
 
 
-@pytest.mark.parametrize("sched", ["wide", "narrow", "stream"])
+@pytest.mark.parametrize("sched", ["wide", "unpaired", "narrow", "stream"])
 def test_wgrad_bias_of_b_in_kernel_noise(sched):
     """The bias noise drawn in the product kernels is the column-sum kernel's
     draw for the same key (Philox stream 0, element n)."""

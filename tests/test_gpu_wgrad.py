@@ -541,6 +541,34 @@ def test_wgrad_wide_expired_wait(monkeypatch, kernel):
     assert core.wgrad_status() != 0
 
 
+@pytest.mark.parametrize("kernel", ["wide", "unpaired"])
+def test_wgrad_wide_bias_expired_wait(monkeypatch, kernel):
+    """A forced expiry with a bias in the same launch (the paired kernel's
+    bias polls expire too): a raised check and NaN in both outputs; the next
+    call on the same workspace gives both exactly again."""
+    from flashdp4review_amd import _lib
+    B, K, M, N = 8, 256, 3072, 768
+    a, b = make(B, K, M, N, torch.bfloat16, "tn", seed=53)
+    kw = dict(out_dtype=torch.float32, bias_scale=1.0 / (B * K), single_pass=kernel)
+    ref_w, _, _ = O.wgrad_clip(a, b, 0.5, 1.0, "tn")
+    ref_b, _, _ = O.colsum_clip(a, None, 0.5, 1.0, "frob", 1.0 / (B * K), None, 0.0)
+    core.wgrad_status()
+    monkeypatch.setenv("FDP_WGRAD_SPIN_LIMIT", "0")
+    bo = torch.empty(M, dtype=torch.float32, device=DEV)
+    with pytest.raises(_lib.FlashDPError):
+        core.wgrad_clip(a, b, 0.5, 1.0, bias_out=bo, check=True, **kw)
+    bo = torch.empty(M, dtype=torch.float32, device=DEV)
+    out = core.wgrad_clip(a, b, 0.5, 1.0, bias_out=bo, **kw)
+    torch.cuda.synchronize()
+    assert torch.isnan(out).any() and torch.isnan(bo).any()
+    monkeypatch.delenv("FDP_WGRAD_SPIN_LIMIT")
+    bo = torch.empty(M, dtype=torch.float32, device=DEV)
+    out = core.wgrad_clip(a, b, 0.5, 1.0, bias_out=bo, **kw)
+    assert_close(out, ref_w, torch.bfloat16, "weight after expiry")
+    assert_close(bo, ref_b, torch.bfloat16, "bias after expiry")
+    assert core.wgrad_status() != 0
+
+
 # ------------------------------------------------- weight and bias in one call
 BIAS_SHAPES = [
     (8, 1024, 3072, 768),  # cfg2: the DP Linear 768 -> 3072 layer, B=8, T=1024
@@ -549,19 +577,23 @@ BIAS_SHAPES = [
 ]
 
 
+@pytest.mark.parametrize("kernel", ["wide", "unpaired"])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=str)
 @pytest.mark.parametrize("shape", BIAS_SHAPES, ids=lambda s: "x".join(map(str, s)))
-def test_wgrad_bias_fused_in_wide_kernel(shape, dtype):
-    """fdp_wgrad_bias_clip through the C ABI: with the wide kernel the bias of a
-    comes from the same launch -- the column-sum half of the workspace (filled
-    with a canary) is never touched -- and matches the float64 oracle
+def test_wgrad_bias_fused_in_wide_kernel(shape, dtype, kernel):
+    """fdp_wgrad_bias_clip through the C ABI: with the wide kernels (paired
+    where B allows, or the one-sample kernel) the bias of a comes from the same
+    launch -- the column-sum half of the workspace (filled with a canary) is
+    never touched -- and matches the float64 oracle
     (flashdp/core/linear_clip.py:116-123: norm of the whole a_b, mean over
     B*K) and the column-sum kernel's result (FDP_WGRAD_NARROW: the fallback);
-    the weight gradient is the one fdp_wgrad_clip gives, bit for bit."""
+    the weight gradient is the one fdp_wgrad_clip gives with the same kernel,
+    bit for bit."""
     import ctypes
     from flashdp4review_amd import _lib
     B, K, M, N = shape
-    print(f"bias fused: shape={shape} dtype={dtype}", flush=True)
+    flags = _lib.WGRAD_WIDE | (_lib.WGRAD_UNPAIRED if kernel == "unpaired" else 0)
+    print(f"bias fused: shape={shape} dtype={dtype} kernel={kernel}", flush=True)
     a, b = make(B, K, M, N, dtype, "tn", seed=21)
     L = _lib.lib()
     dt = _lib.dtype_code(dtype)
@@ -602,15 +634,14 @@ def test_wgrad_bias_fused_in_wide_kernel(shape, dtype):
         untouched = bool(torch.all(ws[span:] == 0xA5)) if canary else None
         return out, norms, fac, bo, bn, bf, untouched
 
-    out, norms, fac, bo, bn, bf, untouched = run(_lib.WGRAD_WIDE, canary=True)
+    out, norms, fac, bo, bn, bf, untouched = run(flags, canary=True)
     assert untouched, "the bias took the column-sum fallback instead of the wide kernel"
-    # the weight as the one-sample wide kernel forms it without a bias (the
-    # paired kernel, which takes weight-only calls where it applies, sums in
-    # another order)
-    w_only = run(_lib.WGRAD_WIDE | _lib.WGRAD_UNPAIRED, with_bias=False)
+    # the weight as the same kernel forms it without a bias
+    w_only = run(flags, with_bias=False)
     assert torch.equal(out, w_only[0]) and torch.equal(norms, w_only[1])
     ref_b, ref_bn, ref_bf = O.colsum_clip(a, None, C, 1.0, "frob", 1.0 / (B * K), zb, 0.5)
-    tag = f"bias fused in the wide kernel {shape} ({dtype})" if shape == BIAS_SHAPES[0] else None
+    tag = (f"bias fused in the {kernel} wide kernel {shape} ({dtype})"
+           if shape == BIAS_SHAPES[0] else None)
     assert_close(bo, ref_b, dtype, "bias", margin=tag)
     assert_elementwise(bn, ref_bn, dtype, "bias norms")
     assert_elementwise(bf, ref_bf, dtype, "bias factors")
@@ -631,7 +662,7 @@ def test_wgrad_bias_in_kernel_noise_matches_fallback():
     B, K, M, N = 8, 256, 3072, 768
     a, b = make(B, K, M, N, torch.bfloat16, "tn", seed=22)
     outs = []
-    for sp in ("wide", "narrow"):
+    for sp in ("wide", "unpaired", "narrow"):
         bo = torch.empty(M, dtype=torch.float32, device=DEV)
         core.wgrad_clip(a, b, 0.05, 1.0, out_dtype=torch.float32, bias_out=bo,
                         bias_scale=1.0 / (B * K), bias_noise_key=(777, 12), bias_noise_scale=0.5,
@@ -639,8 +670,9 @@ def test_wgrad_bias_in_kernel_noise_matches_fallback():
         outs.append(bo)
     z = torch.from_numpy(PX.normals(M, 777, 12, 0)).float()
     ref, _, _ = O.colsum_clip(a, None, 0.05, 1.0, "frob", 1.0 / (B * K), z, 0.5)
-    assert_close(outs[0], ref, torch.bfloat16, "bias with in-kernel noise (wide)")
-    assert_close(outs[1], ref, torch.bfloat16, "bias with in-kernel noise (column sums)")
+    assert_close(outs[0], ref, torch.bfloat16, "bias with in-kernel noise (paired wide)")
+    assert_close(outs[1], ref, torch.bfloat16, "bias with in-kernel noise (one-sample wide)")
+    assert_close(outs[2], ref, torch.bfloat16, "bias with in-kernel noise (column sums)")
 
 
 def test_wgrad_bias_argument_checks():
