@@ -405,10 +405,10 @@ def cfg5_training(dev, steps=10, warmup=3, n_layer=24, fused_adam=True):
 
 # ---------------------------------------------------------------------- extras
 def weight_and_bias_cost(dev, steps, warmup):
-    """cfg2 with a bias: the clipped weight gradient alone (the default, paired
-    kernel, and the one-sample wide kernel, the one that forms biases), with
-    the bias formed in the same launch (fdp_wgrad_bias_clip), and the bias by
-    the separate column-sum kernel (what a call without the fused path adds)."""
+    """cfg2 with a bias: the clipped weight gradient alone and with the bias
+    formed in the same launch (fdp_wgrad_bias_clip), each with the default,
+    paired kernel and the one-sample wide kernel, and the bias by the separate
+    column-sum kernel (what a call without the fused path adds)."""
     from flashdp4review_amd.core import colsum_clip, wgrad_clip
     from flashdp4review_amd.layers.utils import NoiseStream
     x, go, _ = cfg2_inputs(dev)
@@ -425,10 +425,10 @@ def weight_and_bias_cost(dev, steps, warmup):
         wgrad_clip(go, x, 1.0, 1.0, out_scale=1.0 / B, noise_scale=std,
                    noise_key=keys.next(O * x.shape[2]), single_pass="unpaired")
 
-    def w_and_b():
+    def w_and_b(single_pass="auto"):
         wgrad_clip(go, x, 1.0, 1.0, out_scale=1.0 / B, noise_scale=std,
                    noise_key=keys.next(O * x.shape[2]), bias_out=bo, bias_scale=1.0 / (B * T),
-                   bias_noise_scale=std, bias_noise_key=keys.next(O))
+                   bias_noise_scale=std, bias_noise_key=keys.next(O), single_pass=single_pass)
 
     def b_only():
         colsum_clip(go, None, 1.0, 1.0, norm="frob", out_scale=1.0 / (B * T), noise_scale=std,
@@ -437,13 +437,14 @@ def weight_and_bias_cost(dev, steps, warmup):
     tw = median_cuda_time(w_only, steps, warmup, reps=3)
     tw1 = median_cuda_time(w_only_one_sample, steps, warmup, reps=3)
     twb = median_cuda_time(w_and_b, steps, warmup, reps=3)
+    twb1 = median_cuda_time(lambda: w_and_b("unpaired"), steps, warmup, reps=3)
     tb = median_cuda_time(b_only, steps, warmup, reps=3)
     return {"weight_ms": round(tw, 4), "weight_one_sample_kernel_ms": round(tw1, 4),
             "weight_and_bias_one_launch_ms": round(twb, 4),
+            "weight_and_bias_one_sample_kernel_ms": round(twb1, 4),
             "bias_column_sum_kernel_ms": round(tb, 4),
-            "bias_cost_in_launch_us": round((twb - tw1) * 1e3, 2),
-            "what": "the bias is formed by the one-sample wide kernel; its cost is against "
-                    "that kernel's weight-only call"}
+            "bias_cost_in_launch_us": round((twb - tw) * 1e3, 2),
+            "bias_cost_in_one_sample_kernel_us": round((twb1 - tw1) * 1e3, 2)}
 
 
 def dx_overlap(dev, steps, warmup):

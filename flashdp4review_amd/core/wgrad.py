@@ -335,8 +335,9 @@ def wgrad_clip(a: torch.Tensor, b: torch.Tensor, C: float = 1.0, clamp_value: fl
     grouped 128x128 kernel), "wide" (the wide schedule whenever the products
     fit the CUs), "unpaired" (as "wide", one sample per CU only) or "narrow"
     (grouped only).  The wide schedule holds two samples' 192x192 tiles per CU
-    where the batch is even (6..72), the contraction a multiple of 32 and no
-    bias is formed, else one sample's 384x192 tile.  ``launch``
+    where the batch is even (6..72) and the contraction a multiple of 32 (a
+    bias is formed in the same launch either way), else one sample's 384x192
+    tile.  ``launch``
     ("cooperative" / "plain", default: the mode of ``set_wgrad_launch``) picks
     how that kernel is dispatched.
     ``check`` synchronises and raises if a bounded inter-workgroup wait of the

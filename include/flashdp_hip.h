@@ -156,10 +156,11 @@ int fdp_version(void);
  *            samples per workgroup) otherwise; bit 4 (FDP_WGRAD_WIDE) takes the
  *            wide kernel whenever the products fit the CUs at all, bit 5
  *            (FDP_WGRAD_NARROW) never takes it.  Where the batch is even
- *            (6 <= B <= 72), K is a multiple of 32 and no bias is asked for,
- *            the wide schedule holds two samples' 192x192 tiles per CU and
- *            adds them inside the CU (a quarter to a half of the exchanged
- *            bytes); bit 7 (FDP_WGRAD_UNPAIRED) keeps one sample per CU;
+ *            (6 <= B <= 72) and K is a multiple of 32, the wide schedule
+ *            holds two samples' 192x192 tiles per CU and adds them inside
+ *            the CU (a quarter to a half of the exchanged bytes), with or
+ *            without a bias; bit 7 (FDP_WGRAD_UNPAIRED) keeps one sample per
+ *            CU;
  *            bit 3 (FDP_WGRAD_CLEAN_WORKSPACE) states that the workspace's
  *            control words (its first 2048 bytes) are valid -- a zero-filled
  *            buffer, or one whose last use was a completed fdp_wgrad_clip call
