@@ -254,6 +254,22 @@ __device__ __forceinline__ void compute_stage(const FDP_LDS char* st, const Frag
   }
 }
 
+// The same, handing each k-step's fragments to fh(ks, frags) after its MFMAs.
+template <class DT, class G, class FH>
+__device__ __forceinline__ void compute_stage_f(const FDP_LDS char* st, const FragOffsets<G>& fo,
+                                                f32x16 (&acc)[G::FI][G::FJ], const FH& fh) {
+#pragma unroll
+  for (int ks = 0; ks < G::KS; ++ks) {
+    Frags<G> f;
+    f.load(st, fo, ks);
+#pragma unroll
+    for (int i = 0; i < G::FI; ++i)
+#pragma unroll
+      for (int j = 0; j < G::FJ; ++j) acc[i][j] = mfma16<DT>(f.a[i], f.b[j], acc[i][j]);
+    fh(ks, f);
+  }
+}
+
 // s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding).
 template <int N>
 __device__ __forceinline__ void wait_vm() {

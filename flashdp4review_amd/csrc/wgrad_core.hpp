@@ -1258,11 +1258,17 @@ __global__ __launch_bounds__(NT, 2) void wgrad_group_kernel(Args p) {
         dma::wait_tiles<G::LOADS>(ahead < kStages - 2 ? ahead : kStages - 2);
         dma::barrier();
         if (q + kStages - 1 < nq) issue_next(stages.get((s + kStages - 1) % kStages));
-        dma::compute_stage<DT, G>(stages.get(s), fo, acc);
-        // (a counter in place of the modulo adds a live register and spills)
-        if (BOP != 0 && ck % p.bias_P == bother)  // a counted k-tile
-          bias_from_stage<DT, G, BOP, 1>(stages.get(s), BOP == 1 ? wm : wn, bws, bcs, bsq, bcl,
-                                         blim);
+        if constexpr (BOP != 0) {
+          const bool counted = ck % p.bias_P == bother;
+          dma::compute_stage_f<DT, G>(stages.get(s), fo, acc, [&](int, const dma::Frags<G>& f) {
+            if (counted) {
+              const uint4 fr = BOP == 1 ? (bws == 0 ? f.a[0] : f.a[1]) : (bws == 0 ? f.b[0] : f.b[1]);
+              bias_frag<DT>(fr, bcs[0], bsq, bcl + (lane & 31), blim);
+            }
+          });
+        } else {
+          dma::compute_stage<DT, G>(stages.get(s), fo, acc);
+        }
         if (++ck == unit_nk(cu)) {
           {
             const int own = cu;
