@@ -168,7 +168,7 @@ def test_wgrad_bias_of_b_in_kernel_noise(sched):
     assert_close(bo, ref, torch.bfloat16, f"bias of b with in-kernel noise ({sched})")
 
 
-@pytest.mark.parametrize("sched", ["narrow", "stream"])
+@pytest.mark.parametrize("sched", ["wide", "unpaired", "narrow", "stream"])
 def test_wgrad_bias_deterministic_and_zero_factors(sched):
     """Repeated calls are bitwise equal; with C = 0 every factor (weight and
     bias) is zero and so are both outputs, while the bias norms are still
@@ -177,7 +177,7 @@ def test_wgrad_bias_deterministic_and_zero_factors(sched):
     B, K, M, N = 6, 96, 640, 896
     a, b = make(B, K, M, N, torch.bfloat16, seed=25)
     kw = dict(out_dtype=torch.float32, bias_operand="b", bias_scale=1.0 / (B * K),
-              two_pass=sched == "stream", single_pass="narrow" if sched == "narrow" else "auto",
+              two_pass=sched == "stream", single_pass="auto" if sched == "stream" else sched,
               check=True, return_stats=True)
     outs = []
     for _ in range(2):
