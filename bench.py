@@ -53,7 +53,7 @@ PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 TRAFFIC_BYTES = {  # (workload, --single-pass)
     ("cfg2", "auto"): 109053575,      # profiles/wgrad_pair_kernel_cfg2.md
     ("cfg2", "unpaired"): 134239518,  # profiles/wgrad_wide_kernel_cfg2.md
-    ("cfg3", "auto"): 234360493,     # profiles/wgrad_group_kernel_cfg3.md (weight and bias)
+    ("cfg3", "auto"): 233419812,     # profiles/wgrad_group_kernel_cfg3.md (weight and bias)
     ("cfg4", "auto"): 105565315,     # profiles/layernorm_bwd_clip_cfg4.md (one launch per call)
 }
 # the dominant kernel of each (workload, --single-pass)
