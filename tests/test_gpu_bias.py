@@ -168,6 +168,45 @@ def test_wgrad_bias_of_b_in_kernel_noise(sched):
     assert_close(bo, ref, torch.bfloat16, f"bias of b with in-kernel noise ({sched})")
 
 
+WIDE_BIAS_SHAPES = [
+    (72, 32, 96, 96),     # paired: 36 pairs of one tile, one block per region
+    (18, 32, 384, 384),   # paired: 9 pairs over 2 x 2 tiles
+    (6, 256, 576, 768),   # paired: 3 pairs over 3 x 4 tiles, regions of 12 blocks
+]
+
+
+@pytest.mark.parametrize("operand", ["a", "b"])
+@pytest.mark.parametrize("kernel", ["wide", "unpaired"])
+@pytest.mark.parametrize("shape", WIDE_BIAS_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_wgrad_bias_wide_device_clip_args(shape, kernel, operand):
+    """The wide kernels with a bias, C and clamp read from a device tensor
+    (clamp 0.9), fp16 operands and bf16 outputs: weight, bias, both norms and
+    both factors against the float64 oracle."""
+    B, K, M, N = shape
+    dtype = torch.float16
+    print(f"wide bias, device clip args: shape={shape} kernel={kernel} operand={operand}",
+          flush=True)
+    a, b = make(B, K, M, N, dtype, seed=26)
+    wn = [float((a[i].float().t() @ b[i].float()).norm()) for i in range(B)]
+    C = float(np.median(wn))
+    op = a if operand == "a" else b
+    blen = op.shape[2]
+    clip_args = torch.tensor([C, 0.9], device=DEV)
+    bo = torch.empty(blen, dtype=torch.bfloat16, device=DEV)
+    out, n, f, bn, bf = core.wgrad_clip(
+        a, b, clip_args=clip_args, out_scale=1.0 / B, out_dtype=torch.bfloat16,
+        return_stats=True, single_pass=kernel, check=True, bias_out=bo,
+        bias_operand=operand, bias_scale=1.0 / (B * K))
+    ref_w, ref_n, ref_f = O.wgrad_clip(a, b, C, 0.9, "tn", out_scale=1.0 / B)
+    ref_b, ref_bn, ref_bf = O.colsum_clip(op, None, C, 0.9, "frob", 1.0 / (B * K), None, 0.0)
+    assert_close(out, ref_w, dtype, "weight")
+    assert_elementwise(n, ref_n, dtype, "weight norms")
+    assert_elementwise(f, ref_f, dtype, "weight factors")
+    assert_close(bo, ref_b, dtype, "bias")
+    assert_elementwise(bn, ref_bn, dtype, "bias norms")
+    assert_elementwise(bf, ref_bf, dtype, "bias factors")
+
+
 @pytest.mark.parametrize("sched", ["wide", "unpaired", "narrow", "stream"])
 def test_wgrad_bias_deterministic_and_zero_factors(sched):
     """Repeated calls are bitwise equal; with C = 0 every factor (weight and
