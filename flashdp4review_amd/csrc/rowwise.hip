@@ -1909,7 +1909,11 @@ void launch_colsum_dt(const RedPlan& p, const void* u, const void* v, int64_t B,
 
 // Rows of up to 1024 elements: ln_fwd_kernel, enough wavefronts for ~4 rows
 // each, at most 2 workgroups per CU.  Longer rows: one row per workgroup of
-// NWR wavefronts, grid-stride, about 2048 threads per CU.
+// NWR wavefronts, grid-stride, about 512 threads per CU for rows of 2 or 4
+// wavefronts and 2048 for 16 (each workgroup then walks more rows with the
+// next row's loads in flight).  8192 rows of bf16, threads per CU 2048 / 1024
+// / 512 / 256: H = 2048 22.7 / 17.0 / 15.7 / 19.9 us, H = 4096 27.7 / 26.6 /
+// 25.1 / 31.4 us, H = 8192 49.0 / 50.2 / 50.2 / 50.3 us.
 template <class DT, int VEC>
 void launch_ln_fwd(LnShape sh, const void* x, const void* w, const void* b, int w_dtype,
                    int64_t rows, int64_t H, float eps, void* y, float* mean, float* rstd, int cus,
@@ -1927,7 +1931,8 @@ void launch_ln_fwd(LnShape sh, const void* x, const void* w, const void* b, int 
                          dim3(kLnThreads), 0, s, static_cast<const S*>(x), w, b, w_dtype, rows, H,
                          eps, static_cast<S*>(y), mean, rstd);
     } else {
-      int64_t grid = int64_t(cus) * (2048 / (NWR * kWave));
+      constexpr int kThreadsPerCu = NWR == kSplitWaves ? 2048 : 512;
+      int64_t grid = int64_t(cus) * (kThreadsPerCu / (NWR * kWave));
       if (grid > rows) grid = rows;
       hipLaunchKernelGGL((ln_fwd_split_kernel<DT, EPL, VEC, NWR>),
                          dim3(static_cast<unsigned>(grid)), dim3(NWR * kWave), 0, s,
