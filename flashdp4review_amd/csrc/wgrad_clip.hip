@@ -369,10 +369,23 @@ hipError_t launch_stream(Args a, const Plan& pl, bool noclip, float C, float cla
                          block, Core16<DT>::SMEM, s, a);
     }
   }
-  const unsigned fb = static_cast<unsigned>((a.B + (NT / kWave) - 1) / (NT / kWave));
-  hipLaunchKernelGGL(wgrad_factor_kernel, dim3(fb < 1024 ? fb : 1024), block, 0, s, a.partials,
-                     a.B, per_sample, C, clamp, clip_args_dev, noclip ? 1 : 0, fac_ws, norms,
-                     factors, a.err);
+  // The clipped-sum kernel forms the factors from the partials itself (saving
+  // a launch between the passes) unless the call has no clipping or its
+  // sample groups are larger than it stages.
+  a.fac_parts = 0;
+  if (!noclip && pl.sp.sum_spg <= kSumFacMax) {
+    a.fac_parts = per_sample;
+    a.C = C;
+    a.clamp = clamp;
+    a.clip_args_dev = clip_args_dev;
+    a.norms_out = norms;
+    a.factors_out = factors;
+  } else {
+    const unsigned fb = static_cast<unsigned>((a.B + (NT / kWave) - 1) / (NT / kWave));
+    hipLaunchKernelGGL(wgrad_factor_kernel, dim3(fb < 1024 ? fb : 1024), block, 0, s, a.partials,
+                       a.B, per_sample, C, clamp, clip_args_dev, noclip ? 1 : 0, fac_ws, norms,
+                       factors, a.err);
+  }
   const hipError_t e = DT::code == FDP_BF16 ? launch_clipsum_bf16(a, pl.sp, s) : launch_clipsum_f16(a, pl.sp, s);
   if (e != hipSuccess) return e;
   if (pl.sp.sum_groups > 1) {

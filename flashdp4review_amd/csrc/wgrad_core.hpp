@@ -28,6 +28,8 @@ struct Args {
   int groups;  // number of groups (pass B)
   float* partials;  // [B, tiles]
   const float* factors;  // [B]
+  int fac_parts;         // streamed clipped-sum pass: > 0: it forms the factors itself from
+                         // partials [B, fac_parts] (in place of `factors`)
   float* group_out;      // [groups, M, N] fp32 when groups > 1
   void* out;
   int64_t ldo;

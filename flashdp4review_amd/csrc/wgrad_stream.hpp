@@ -310,6 +310,10 @@ __device__ inline void store_half(const Args& p, int64_t m0, int64_t n0, int h,
 // (bias_finish, run by bias_finish_kernel after this kernel): taken from the
 // fragments of every sample, also of a sample whose clip factor is zero
 // (its fragments are then read for the bias only).
+// Samples per group whose clip factors the clipped-sum kernel forms itself
+// (more: wgrad_factor_kernel forms them before it).
+constexpr int kSumFacMax = 256;
+
 template <class DT, class G, int S, int BOP = 0>
 __global__ __launch_bounds__(NT, 2) void clipsum_kernel(Args p) {
   static_assert(S >= 2 && S <= 4, "ring depth");
@@ -320,9 +324,9 @@ __global__ __launch_bounds__(NT, 2) void clipsum_kernel(Args p) {
   __shared__ __attribute__((aligned(16))) char ring[S * G::STAGE];
   __shared__ float bcol[BOP != 0 ? BW : 1];
   __shared__ float bred[NT / kWave];
+  __shared__ float cfac[kSumFacMax];  // the group's clip factors (fac_parts > 0)
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = (wave >> 1) * G::WM, wn = (wave & 1) * G::WN;
-  (void)lane;
   const int tiles = p.tiles_m * p.tiles_n;
   const int lw = logical_wg(blockIdx.x, gridDim.x);
   const int g = lw / tiles, tile = lw % tiles;
@@ -380,6 +384,32 @@ __global__ __launch_bounds__(NT, 2) void clipsum_kernel(Args p) {
 #pragma unroll
   for (int s = 0; s < S - 1; ++s)
     if (s < nq) issue_next(stage(s));
+  if (p.fac_parts > 0) {
+    // the clip factors of the group's samples, while the first stages load:
+    // wave w takes samples w, w + 4, ... and sums each one's partials
+    // lane-strided, then across the wave (the order of wgrad_factor_kernel);
+    // the workgroup of tile 0 reports them.  (Waiting for these loads also
+    // waits for the stages issued before them.)
+    float C = p.C, clamp = p.clamp;
+    if (p.clip_args_dev != nullptr) {
+      C = p.clip_args_dev[0];
+      clamp = p.clip_args_dev[1];
+    }
+    for (int j = wave; j < nsamp; j += NT / kWave) {
+      const float* part = p.partials + (b0 + j) * p.fac_parts;
+      float s = 0.f;
+      for (int t = lane; t < p.fac_parts; t += kWave) s += part[t];
+      const float n = sqrtf(wave_sum(s));
+      if (lane == 0) {
+        const float c = clip_factor(n, C, clamp);
+        cfac[j] = c;
+        if (tile == 0) {
+          if (p.norms_out) p.norms_out[b0 + j] = n;
+          if (p.factors_out) p.factors_out[b0 + j] = c;
+        }
+      }
+    }
+  }
   for (int base = 0; base < nq; base += S) {
 #pragma unroll
     for (int s = 0; s < S; ++s) {
@@ -390,7 +420,7 @@ __global__ __launch_bounds__(NT, 2) void clipsum_kernel(Args p) {
         dma::barrier();
         if (q + S - 1 < nq) issue_next(stage((s + S - 1) % S));
         if (ck == 0) {  // sample b0 + cu starts: rescale to its factor
-          const float c = p.factors[b0 + cu];
+          const float c = p.fac_parts > 0 ? cfac[cu] : p.factors[b0 + cu];
           live = c != 0.f;  // a zero factor contributes exactly nothing
           if (live) {
             if (any) {
