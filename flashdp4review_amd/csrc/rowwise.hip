@@ -1784,13 +1784,11 @@ void with_ln_shape(LnShape sh, F&& f) {
 }
 
 
-// LayerNorm backward workgroup: 4 waves, about two workgroups per CU, with
-// chunks of at least 32 rows (16 for rows of 1025 .. 4096 elements, see
-// ln_plan).  On a 16x1024x1024 problem one, two and four
-// per CU (chunks of 64, 32 and 16 rows) measured 28.6, 28.1 and 33.8 us per
-// call: a chunk's partials cost 8H bytes against its 6·rows·H bytes of rows,
-// and more chunks also mean more partials for the reduction to read.
-constexpr int ln_bwd_threads(int) { return 256; }
+// LayerNorm backward workgroup of the two-launch path: 8 waves, about one
+// workgroup per CU, chunks of at least 16 rows (ln_plan).  A chunk's partials
+// cost 8H bytes against its 6·rows·H bytes of rows, and more chunks also mean
+// more partials for the reduction to read.
+constexpr int ln_bwd_threads(int) { return 512; }
 
 // The one-launch LayerNorm backward: 8-wave workgroups, one per CU, chunks of
 // at least 32 rows; taken when the last-arriving workgroups' serial work stays
@@ -1829,16 +1827,13 @@ RedPlan ln_plan(int64_t B, int64_t T, int64_t H, int cus) {
     p.total += align_up(sizeof(float2) * size_t(B) * size_t(T));
     return p;
   }
-  // rows of more than kMaxWaveH take one 1024-thread workgroup per CU.
-  // Rows of 1025 .. 4096 elements (one or two rows at a time per workgroup):
-  // chunks of at least 16 rows, so that small batches still give about two
-  // workgroups per CU.  T = 1024 bf16, minimum 32 / 16 rows: B x H = 8 x 2048
-  // 31.2 / 30.7 us, 4 x 4096 44.4 / 35.0, 8 x 3072 44.5 / 40.7, 8 x 1536
-  // 28.7 / 26.5, 2 x 2048 27.8 / 22.3, 16 x 2048 45.0 / 45.2, 8 x 4096 48.6
-  // / 50.0; rows of at most 1024 (four at a time) keep 32 (8 x 1024: 19.7
-  // against 20.3 us).
-  const int64_t min_rows = H > 1024 && H <= kMaxWaveH ? 16 : 32;
-  split_rows(p, B, T, cus, H > kMaxWaveH ? 1 : 2, min_rows);
+  // Rows of more than kMaxWaveH take one 1024-thread workgroup per CU; shorter
+  // ones one 512-thread workgroup (ln_bwd_threads) per CU, with chunks of at
+  // least 16 rows so that small batches still fill the CUs.  T = 1024 bf16,
+  // against 256-thread workgroups, two per CU, chunks of at least 32 rows:
+  // B x H = 8 x 2048 29.1 / 31.2 us, 4 x 4096 32.8 / 44.4, 8 x 3072 38.4 /
+  // 44.5, 2 x 2048 19.4 / 27.8, 8 x 1024 19.0 / 19.7, 16 x 2048 44.5 / 45.0.
+  split_rows(p, B, T, cus, 1, H > kMaxWaveH ? 32 : 16);
   finish_plan(p, B, H, 2);
   return p;
 }
