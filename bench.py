@@ -448,9 +448,10 @@ def weight_and_bias_cost(dev, steps, warmup):
 
 
 def dx_overlap(dev, steps, warmup):
-    """DPLinear backward at cfg2: dX = g W (a plain GEMM) and the clipped dW/db
-    call, one after the other on one stream, or with dX on a second stream
-    (default priority) so that it runs beside the DP kernel's tail."""
+    """DPLinear backward at cfg2: dX = g W (torch's matmul, or the library's own
+    dX kernel fdp_dgrad) and the clipped dW/db call, one after the other on one
+    stream, or with dX on a second stream (default priority) so that it runs
+    beside the DP kernel's tail."""
     from flashdp4review_amd.core import wgrad_clip
     from flashdp4review_amd.layers.utils import NoiseStream
     x, go, _ = cfg2_inputs(dev)
@@ -478,12 +479,22 @@ def dx_overlap(dev, steps, warmup):
             go @ W
         main.wait_stream(side)
 
+    from flashdp4review_amd.core import dgrad
+
+    def serial_own():
+        dgrad(go, W, "nn")
+        dp()
+
     t_dx = median_cuda_time(lambda: go @ W, steps, warmup, reps=3)
+    t_own = median_cuda_time(lambda: dgrad(go, W, "nn"), steps, warmup, reps=3)
     t_dp = median_cuda_time(dp, steps, warmup, reps=3)
     t_ser = median_cuda_time(serial, steps, warmup, reps=3)
+    t_ser_own = median_cuda_time(serial_own, steps, warmup, reps=3)
     t_ovl = median_cuda_time(overlapped, steps, warmup, reps=3)
-    return {"dx_gemm_ms": round(t_dx, 4), "dp_weight_bias_ms": round(t_dp, 4),
-            "serial_ms": round(t_ser, 4), "dx_on_second_stream_ms": round(t_ovl, 4)}
+    return {"dx_gemm_ms": round(t_dx, 4), "dx_fdp_dgrad_ms": round(t_own, 4),
+            "dp_weight_bias_ms": round(t_dp, 4), "serial_ms": round(t_ser, 4),
+            "serial_with_fdp_dgrad_ms": round(t_ser_own, 4),
+            "dx_on_second_stream_ms": round(t_ovl, 4)}
 
 
 def library_gemms_cfg2(dev, steps, warmup):
@@ -551,6 +562,11 @@ def extra_measurements(dev, steps, warmup):
         colsum_clip(g3, None, 1.0, 1.0, norm="frob", out_scale=1.0 / (16 * 1024),
                     noise_scale=0.25, noise_key=(7, 0), out_dtype=torch.bfloat16)
     t3s = median_cuda_time(two_calls, steps, warmup, reps=3)
+    from flashdp4review_amd.core import dgrad
+    W3 = (torch.randn(768, 2304, device=dev) * 0.02).to(torch.bfloat16)  # Conv1D [nx, nf]
+    t3dx = median_cuda_time(lambda: g3 @ W3.t(), steps, warmup, reps=3)
+    t3own = median_cuda_time(lambda: dgrad(g3, W3, "nt"), steps, warmup, reps=3)
+    out["cfg3_dx"] = {"torch_matmul_ms": round(t3dx, 4), "fdp_dgrad_ms": round(t3own, 4)}
     out["cfg3_conv1d_clipped_wgrad"] = {
         "ms": round(t3b, 4), "tflops": round(F3 / t3b / 1e9, 2),
         "frac_bf16_peak": round(F3 / t3b / 1e9 / PEAK_BF16_TFLOPS, 4),

@@ -3,7 +3,8 @@
 Every operator runs on the HIP kernels of libflashdp_hip.so; there is no CPU
 fallback.  ``wgrad_clip``, ``colsum_clip``, ``layernorm_fwd`` and
 ``layernorm_bwd_clip`` are the general entry points the layers use (they add
-out_scale, injected noise and per-sample norm/factor outputs).
+out_scale, injected noise and per-sample norm/factor outputs); ``dgrad`` is
+the layers' input gradient.
 """
 from .wgrad import (
     wgrad_clip,
@@ -31,6 +32,7 @@ from .layernorm import (
     layernorm_bwd_clip_fused,
     layernorm_dwdb_fused,
 )
+from .inputgrad import dgrad, input_grad, set_dgrad
 from .utils import RuntimeAutoTuner, supported_acc_dtypes
 
 __all__ = [
@@ -38,5 +40,5 @@ __all__ = [
     "conv1d_weight_flashdp", "colsum_clip", "linear_bias_grad_clip", "conv1d_bias_grad_clip",
     "layernorm_dw_clip", "layernorm_db_clip", "layernorm_fwd", "layernorm_bwd_clip",
     "layernorm_fwd_fused", "layernorm_bwd_clip_fused", "layernorm_dwdb_fused",
-    "RuntimeAutoTuner", "supported_acc_dtypes",
+    "dgrad", "input_grad", "set_dgrad", "RuntimeAutoTuner", "supported_acc_dtypes",
 ]

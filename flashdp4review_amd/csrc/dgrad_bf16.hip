@@ -1,0 +1,13 @@
+// Input-gradient (dX) kernel instantiations for bf16 operands (one translation
+// unit per dtype so that the builds run in parallel).
+#include "dgrad.hpp"
+
+namespace fdp {
+namespace dg {
+
+hipError_t launch_dgrad_bf16(const DgradArgs& a, bool wkc, hipStream_t s) {
+  return launch_dgrad_t<BF16>(a, wkc, s);
+}
+
+}  // namespace dg
+}  // namespace fdp

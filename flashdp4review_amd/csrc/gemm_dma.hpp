@@ -55,25 +55,37 @@ __host__ __device__ constexpr int row_chunks(int R) { return (R / 8 + 15) / 16 *
 // after the k-tile and column offsets (< 2^31) are added, without wrapping.
 constexpr uint32_t kPadOffset = 0x80000000u;
 
+// Rows of a k-contiguous tile (below) rounded up so that every wave issues
+// whole 1 KB loads: rows of BK 16-bit values, NW waves.
+__host__ __device__ constexpr int kc_rows(int R, int BK, int NW) {
+  return (R + (NW * 1024) / (BK * 2) - 1) / ((NW * 1024) / (BK * 2)) * ((NW * 1024) / (BK * 2));
+}
+
 // Tile geometry: BM x BN outputs, WGM x WGN waves (default 2 x 2), each
 // (BM/WGM) x (BN/WGN); k-tiles of BK rows (a multiple of 16) per LDS stage.
-template <int BM_, int BN_, int BK_ = kBK, int WGM_ = 2, int WGN_ = 2>
+// AKC / BKC: operand A / B is stored with k contiguous ([R, K] rows, e.g. a
+// layer's grad_output [tokens, out] as the first operand of dX = g W) instead
+// of k-strided; such a tile is kept in LDS as rows of BK k-values (below).
+template <int BM_, int BN_, int BK_ = kBK, int WGM_ = 2, int WGN_ = 2, bool AKC_ = false,
+          bool BKC_ = false>
 struct Geom {
   static constexpr int BM = BM_;
   static constexpr int BN = BN_;
   static constexpr int BK = BK_;
   static constexpr int WGM = WGM_;
   static constexpr int WGN = WGN_;
+  static constexpr bool AKC = AKC_;
+  static constexpr bool BKC = BKC_;
   static constexpr int NW = WGM * WGN;    // waves per workgroup
   static constexpr int KS = BK / 16;      // 16-deep MFMA k-steps per k-tile
   static constexpr int WM = BM / WGM;     // wave tile rows
   static constexpr int WN = BN / WGN;     // wave tile columns
   static constexpr int FI = WM / 32;      // 32-row MFMA blocks per wave
   static constexpr int FJ = WN / 32;      // 32-column MFMA blocks per wave
-  static constexpr int ROW_A = row_chunks(BM) * 16;  // LDS bytes per k-row of the A tile
+  static constexpr int ROW_A = row_chunks(BM) * 16;  // LDS bytes per k-row of a k-strided A tile
   static constexpr int ROW_B = row_chunks(BN) * 16;
-  static constexpr int TILE_A = BK * ROW_A;
-  static constexpr int TILE_B = BK * ROW_B;
+  static constexpr int TILE_A = AKC ? kc_rows(BM, BK, NW) * BK * 2 : BK * ROW_A;
+  static constexpr int TILE_B = BKC ? kc_rows(BN, BK, NW) * BK * 2 : BK * ROW_B;
   static constexpr int STAGE = TILE_A + TILE_B;
   static constexpr int LOADS_A = TILE_A / (NW * 64 * 16);  // per wave per k-tile
   static constexpr int LOADS_B = TILE_B / (NW * 64 * 16);
@@ -81,7 +93,15 @@ struct Geom {
   static_assert(LOADS_A * NW * 64 * 16 == TILE_A && LOADS_B * NW * 64 * 16 == TILE_B,
                 "each wave issues whole 1 KB loads");
   static_assert(BM % 32 == 0 && BN % 32 == 0 && WM % 32 == 0 && WN % 32 == 0, "32x32 blocks");
+  static_assert(!(AKC || BKC) || BK == 32, "k-contiguous tiles: rows of 4 chunks, 2 k-steps");
 };
+
+// k-contiguous tile in LDS: row r (one m or n) holds the k-tile's BK = 32
+// values as 4 chunks of 16 bytes, logical chunk c at physical chunk
+// c ^ kc_swz(r).  An MFMA fragment is one ds_read_b128 per lane (rows
+// w0 + lane % 32, chunk 2 ks + lane / 32); the swizzle puts any 16 (and any 8)
+// consecutive rows' reads of one chunk on distinct 16-byte bank groups.
+__host__ __device__ constexpr int kc_swz(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
 
 // One operand's per-thread load state: L buffer loads per k-tile of BK rows.
 //
@@ -139,6 +159,28 @@ struct Operand {
     retile(r0);
     step = static_cast<uint32_t>(BK * ld * 2);
   }
+  // Operand stored [rows, K] with K contiguous (row stride ld, a multiple of 8
+  // elements): the tile's R rows from r0, as rows of BK = 32 values (kc_swz
+  // layout above); slots of the tile's padding rows (R and up) read nothing.
+  // Rows past `rows` read as zeros (the record ends there).  A row's values
+  // past K would be the next row's: callers keep K a multiple of BK.
+  template <int R>
+  __device__ inline void init_kc(const uint16_t* base, int64_t ld, int64_t rows, int64_t r0) {
+    static_assert(BK == 32, "rows of 4 chunks");
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    rsrc = u32x4{static_cast<uint32_t>(a), static_cast<uint32_t>(a >> 32) & 0xffffu,
+                 static_cast<uint32_t>(rows * ld * 2), kRsrcWord3};
+#pragma unroll
+    for (int j = 0; j < L; ++j) {
+      const int slot = (wave * L + j) * 64 + lane;
+      const int r = slot >> 2;
+      const int c = (slot & 3) ^ kc_swz(r);
+      voff[j] = r < R ? static_cast<uint32_t>((int64_t(r) * ld + 8 * c) * 2) : kPadOffset;
+    }
+    col = static_cast<uint32_t>(r0 * ld * 2);
+    step = static_cast<uint32_t>(BK * 2);
+  }
   // The same tile of another sample (same ld, K and columns).  Records past
   // K*ld*2 bytes read as zero.
   __device__ __forceinline__ void retarget(const uint16_t* base, int64_t ld, int64_t K) {
@@ -186,6 +228,18 @@ __device__ __forceinline__ uint32_t frag_off(int w0, int i, int h) {
                                ((m >> 2) & 1) * 8);
 }
 
+// Byte offset inside a k-contiguous tile of this lane's plain read for MFMA
+// rows w0 + 32i .. +31, k-step ks (8 k-values: chunk 2 ks + lane / 32).
+__device__ __forceinline__ uint32_t kc_frag_off(int w0, int i, int ks) {
+  const int lane = threadIdx.x & 63;
+  const int r = w0 + 32 * i + (lane & 31);
+  const int c = 2 * ks + (lane >> 5);
+  return static_cast<uint32_t>((r * 4 + (c ^ kc_swz(r))) * 16);
+}
+
+// Per operand two offsets per fragment: the two transposing half reads of
+// k-step 0 (k-strided tile; later k-steps add 16 rows) or the plain reads of
+// k-steps 0 and 1 (k-contiguous tile).
 template <class G>
 struct FragOffsets {
   uint32_t a[G::FI][2], b[G::FJ][2];
@@ -193,11 +247,13 @@ struct FragOffsets {
 #pragma unroll
     for (int i = 0; i < G::FI; ++i)
 #pragma unroll
-      for (int h = 0; h < 2; ++h) a[i][h] = frag_off<G::BM>(wm, i, h);
+      for (int h = 0; h < 2; ++h)
+        a[i][h] = G::AKC ? kc_frag_off(wm, i, h) : frag_off<G::BM>(wm, i, h);
 #pragma unroll
     for (int j = 0; j < G::FJ; ++j)
 #pragma unroll
-      for (int h = 0; h < 2; ++h) b[j][h] = frag_off<G::BN>(wn, j, h) + G::TILE_A;
+      for (int h = 0; h < 2; ++h)
+        b[j][h] = (G::BKC ? kc_frag_off(wn, j, h) : frag_off<G::BN>(wn, j, h)) + G::TILE_A;
   }
 };
 
@@ -212,6 +268,12 @@ __device__ __forceinline__ uint4 read_frag(const FDP_LDS char* stage, uint32_t o
   v.z = uint32_t(uint16_t(hi[0])) | (uint32_t(uint16_t(hi[1])) << 16);
   v.w = uint32_t(uint16_t(hi[2])) | (uint32_t(uint16_t(hi[3])) << 16);
   return v;
+}
+
+// One lane's 16 bytes of a k-contiguous tile (ds_read_b128).
+__device__ __forceinline__ uint4 read_plain(const FDP_LDS char* stage, uint32_t o) {
+  const u32x4 v = *reinterpret_cast<const FDP_LDS u32x4*>(stage + o);
+  return make_uint4(v[0], v[1], v[2], v[3]);
 }
 
 template <class DT>
@@ -231,11 +293,19 @@ struct Frags {
   uint4 a[G::FI], b[G::FJ];
   __device__ __forceinline__ void load(const FDP_LDS char* st, const FragOffsets<G>& fo, int ks) {
 #pragma unroll
-    for (int j = 0; j < G::FJ; ++j)
-      b[j] = read_frag(st, fo.b[j][0] + ks * 16 * G::ROW_B, fo.b[j][1] + ks * 16 * G::ROW_B);
+    for (int j = 0; j < G::FJ; ++j) {
+      if constexpr (G::BKC)
+        b[j] = read_plain(st, fo.b[j][ks & 1]);
+      else
+        b[j] = read_frag(st, fo.b[j][0] + ks * 16 * G::ROW_B, fo.b[j][1] + ks * 16 * G::ROW_B);
+    }
 #pragma unroll
-    for (int i = 0; i < G::FI; ++i)
-      a[i] = read_frag(st, fo.a[i][0] + ks * 16 * G::ROW_A, fo.a[i][1] + ks * 16 * G::ROW_A);
+    for (int i = 0; i < G::FI; ++i) {
+      if constexpr (G::AKC)
+        a[i] = read_plain(st, fo.a[i][ks & 1]);
+      else
+        a[i] = read_frag(st, fo.a[i][0] + ks * 16 * G::ROW_A, fo.a[i][1] + ks * 16 * G::ROW_A);
+    }
   }
 };
 

@@ -658,6 +658,7 @@ struct PairGeom {
   static constexpr int BK = 32;
   static constexpr int NW = 8, KS = BK / 16;
   static constexpr int WM = 96, WN = 96, FI = 3, FJ = 3;
+  static constexpr bool AKC = false, BKC = false;  // both operands k-strided
   static constexpr int ROW_A = dma::row_chunks(BM) * 16;
   static constexpr int ROW_B = dma::row_chunks(BN) * 16;
   static constexpr int TILE_A = BK * ROW_A;

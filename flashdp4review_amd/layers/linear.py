@@ -1,7 +1,7 @@
 """DPLinear: nn.Linear whose backward clips per-sample weight/bias gradients.
 
 Reference: flashdp/layers/linear.py:11-106.  Backward math (per parameter tensor):
-  dX = g W                                                       (unclipped)
+  dX = g W                                 (unclipped; fdp_dgrad or torch's matmul)
   dW = (1/B) sum_b clip(||g_b^T x_b||_F) g_b^T x_b + (sigma/sqrt(B)) z_W
   db = (1/(B*T)) sum_b clip(||g_b||_F) sum_t g_bt  + (sigma/sqrt(B)) z_b
 (sigma/sqrt(B) is the reference's noise std; set_noise_convention("dpsgd")
@@ -19,7 +19,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 from torch.autograd.function import Function
 
-from ..core import colsum_clip, wgrad_clip
+from ..core import colsum_clip, input_grad, wgrad_clip
 from ..core.utils import RuntimeAutoTuner
 from .utils import DPParameter as Parameter
 from .utils import (NoiseStream, advance_noise, as_btf, exact_fp32, noise_counter, noise_draws,
@@ -83,8 +83,7 @@ class _DPLinearFunction(Function):
         stats = {} if ctx.module is not None else None
         grad_input = grad_weight = grad_bias = None
         if ctx.needs_input_grad[0]:
-            w = weight if weight.dtype == g3.dtype else weight.to(g3.dtype)
-            grad_input = (g3 @ w).reshape(input.shape)
+            grad_input = input_grad(g3, weight, "nn").reshape(input.shape)
         want_bias = ctx.has_bias and ctx.needs_input_grad[2]
         O = g3.shape[-1]
         if ctx.needs_input_grad[1]:

@@ -5,7 +5,7 @@ flashdp/core/transformers_conv1d_clip.py:22-39.  The reference layer routes its
 weight gradient through the Linear helper, which yields g^T x ([nf, nx]) for a
 [nx, nf] weight and fails unless nx == nf, and clips the bias first, in place,
 so that dX and dW see the scaled grad_output.  Here:
-  dX = g W^T                                                     (unclipped)
+  dX = g W^T                               (unclipped; fdp_dgrad or torch's matmul)
   dW = (1/B) sum_b clip(||x_b^T g_b||_F) x_b^T g_b + (sigma/sqrt(B)) z_W
   db = (1/(B*T)) sum_b clip(||g_b||_F) sum_t g_bt  + (sigma/sqrt(B)) z_b
 (sigma/sqrt(B) is the reference's noise std; set_noise_convention("dpsgd")
@@ -21,7 +21,7 @@ import torch
 import torch.nn as nn
 from torch.autograd.function import Function
 
-from ..core import colsum_clip, wgrad_clip
+from ..core import colsum_clip, input_grad, wgrad_clip
 from ..core.utils import RuntimeAutoTuner
 from .utils import DPParameter as Parameter
 from .utils import (NoiseStream, advance_noise, as_btf, exact_fp32, noise_counter, noise_draws,
@@ -98,8 +98,7 @@ class _DPConv1DFunction(Function):
         stats = {} if ctx.module is not None else None
         grad_input = grad_weight = grad_bias = None
         if ctx.needs_input_grad[0]:
-            w = weight if weight.dtype == g3.dtype else weight.to(g3.dtype)
-            grad_input = (g3 @ w.t()).reshape(input.shape)
+            grad_input = input_grad(g3, weight, "nt").reshape(input.shape)
         want_bias = ctx.needs_input_grad[2]
         O = g3.shape[-1]
         if ctx.needs_input_grad[1]:

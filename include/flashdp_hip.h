@@ -282,6 +282,45 @@ int fdp_wgrad_clip_noalloc(const void* a, const void* b, int64_t B, int64_t K, i
                            void* stream);
 
 /* ------------------------------------------------------------------------
+ * Input gradient of a DP Linear or Conv1D layer (the unclipped product of its
+ * backward that reads the same grad_output as the clipped weight gradient):
+ *
+ *   dx[m, n] = sum_k g[m, k] * W(k, n)
+ *
+ *   FDP_DGRAD_NN: W(k, n) = w[k, n], w [K, N] row stride ldw -- a Linear
+ *                 weight [out, in]: grad_input = grad_output @ weight
+ *                 (flashdp/layers/linear.py:62-67);
+ *   FDP_DGRAD_NT: W(k, n) = w[n, k], w [N, K] row stride ldw -- a Conv1D
+ *                 weight [in, out]: grad_input = grad_output @ weight.t()
+ *                 (flashdp/layers/transformers_conv1d.py:70-77).
+ *
+ * g  : [M, K] (M = B*T rows of grad_output, K = out features), row stride ldg.
+ * dx : [M, N], row stride ldo.  g, w and dx share `dtype` (FDP_F16 or
+ *      FDP_BF16); products accumulate in fp32 and dx is rounded once.
+ * Requirements (FDP_ERR_SHAPE / FDP_ERR_ALIGN otherwise, nothing launched):
+ *      K a multiple of 32; ldg and ldw multiples of 8 elements; g and w
+ *      16-byte aligned; g and w each span less than 2 GiB.
+ * workspace: fdp_dgrad_workspace_size bytes, 16-byte aligned.  Its control
+ *      words (the first 256 bytes, the tickets and flags) must be zero before
+ *      the first call; every completed call leaves them zero, so a buffer is
+ *      zero-filled once and reused by calls in stream order.  Its first int is
+ *      a sticky status word, as for fdp_wgrad_clip: nonzero means a bounded
+ *      wait between the two halves of a split contraction expired (the
+ *      affected rows of dx are NaN).  Concurrent calls need separate buffers.
+ * The result is deterministic (fixed summation order).
+ * ---------------------------------------------------------------------- */
+typedef enum fdp_dgrad_layout {
+  FDP_DGRAD_NN = 0,
+  FDP_DGRAD_NT = 1
+} fdp_dgrad_layout;
+
+int fdp_dgrad_workspace_size(int64_t M, int64_t N, int64_t K, int layout, int dtype,
+                             size_t* bytes);
+int fdp_dgrad(const void* g, const void* w, void* dx, int64_t M, int64_t N, int64_t K,
+              int64_t ldg, int64_t ldw, int64_t ldo, int layout, int dtype, void* workspace,
+              size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
  * Clipped per-sample column sums over the middle axis:
  *
  *   S_b[h]  = sum_t u[b,t,h] * (v ? v[b,t,h] : 1)
