@@ -6,13 +6,14 @@ flashdp/layers/transformers_conv1d.py:70-77: ``grad_output @ weight.t()``).
 The library also has a dX kernel of its own for 16-bit operands (fdp_dgrad:
 the clipped products' LDS-DMA / MFMA core with grad_output taken k-contiguous,
 256x192 tiles, a split contraction where the tiles alone would leave CUs
-idle).  It is exact to the bf16 tolerance and deterministic, but on MI355X
-hipBLASLt is faster at every layer shape measured (cfg2's dX 56 against 53 us,
-cfg3's 60.6 against 55.6 us, GPT-2 small 33.7 against 19.9 us), so the layers
+idle).  It is exact to the bf16 tolerance and deterministic, and on MI355X
+about as fast as hipBLASLt at GPT-2's 768-wide inputs (cfg3's dX 54.4 against
+55.6 us, cfg2's 53.6 against 52.4 us) and slower elsewhere (GPT-2 small
+30.8 against 20.2 us, a 2048x2048 Linear 118 against 61 us), so the layers
 keep torch's matmul unless ``set_dgrad("hip")`` selects the kernel:
   "torch" (default) torch's matmul (hipBLASLt);
   "hip"   the HIP kernel for every operand pair it takes.
-Operands the kernel does not take (fp32, K not a multiple of 32, unaligned
+Operands the kernel does not take (fp32, K not a multiple of 64, unaligned
 rows) always use torch's matmul, as the reference does.
 """
 from __future__ import annotations
@@ -44,10 +45,10 @@ def set_dgrad(mode: str) -> str:
 
 def _takes(g2: torch.Tensor, w: torch.Tensor, K: int) -> bool:
     """Operands the kernel takes as they are: 16-bit, one device, K a multiple
-    of 32, rows of 16-byte multiples on 16-byte aligned storage."""
+    of 64, rows of 16-byte multiples on 16-byte aligned storage."""
     return (g2.dtype in (torch.float16, torch.bfloat16) and w.dtype == g2.dtype
             and g2.is_cuda and w.is_cuda and g2.device == w.device
-            and K >= 32 and K % 32 == 0
+            and K >= 64 and K % 64 == 0
             and g2.stride(1) == 1 and g2.stride(0) % 8 == 0 and g2.data_ptr() % 16 == 0
             and w.stride(1) == 1 and w.stride(0) % 8 == 0 and w.data_ptr() % 16 == 0)
 

@@ -35,7 +35,7 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int cus) {
     const int64_t rounds = (tiles * splits + cus - 1) / cus;
     return double(rounds) / splits * (splits > 1 ? 1.06 : 1.0);
   };
-  pl.splits = K >= 64 && cost(2) < cost(1) ? 2 : 1;
+  pl.splits = K >= 2 * kBK && cost(2) < cost(1) ? 2 : 1;
   pl.ticket_off = kAlign;  // the status word sits in the first 256 bytes
   pl.flag_off = pl.ticket_off + align_up(sizeof(unsigned) * size_t(tiles));
   pl.part_off = pl.flag_off + align_up(sizeof(unsigned) * size_t(tiles));
@@ -54,7 +54,7 @@ bool valid16(int dtype) { return dtype == FDP_F16 || dtype == FDP_BF16; }
 int check_shape(int64_t M, int64_t N, int64_t K, int layout, int dtype) {
   if (!valid16(dtype)) return FDP_ERR_DTYPE;
   if (layout != FDP_DGRAD_NN && layout != FDP_DGRAD_NT) return FDP_ERR_ARG;
-  if (M < 1 || N < 1 || K < 32 || K % 32 != 0) return FDP_ERR_SHAPE;
+  if (M < 1 || N < 1 || K < kBK || K % kBK != 0) return FDP_ERR_SHAPE;
   if (M > (int64_t(1) << 30) || N > (int64_t(1) << 30)) return FDP_ERR_SHAPE;
   return FDP_OK;
 }
@@ -108,7 +108,7 @@ extern "C" int fdp_dgrad(const void* g, const void* w, void* dx, int64_t M, int6
   a.tiles_m = pl.tiles_m;
   a.tiles_n = pl.tiles_n;
   a.splits = pl.splits;
-  a.nk = static_cast<int>(K / 32);
+  a.nk = static_cast<int>(K / kBK);
   a.ticket = reinterpret_cast<unsigned*>(ws + pl.ticket_off);
   a.flag = reinterpret_cast<unsigned*>(ws + pl.flag_off);
   a.part = reinterpret_cast<float*>(ws + pl.part_off);

@@ -8,8 +8,10 @@
 // it with torch's matmul); the clipped weight gradient reads the same g.
 //
 // The core is the LDS-DMA / ds_read MFMA core of the clipped products
-// (gemm_dma.hpp): 8 waves of 64 x (BN / 2) outputs each, 3-stage ring of
-// 32-deep k-tiles.  g has k contiguous, so its tiles are kept in LDS as rows
+// (gemm_dma.hpp): 8 waves of 64 x (BN / 2) outputs each, a 2-stage ring of
+// 64-deep k-tiles (a 3-stage ring of 32-deep ones, with half the MFMAs
+// between two workgroup barriers, took 57-61 against 53.6-54.4 us at the
+// cfg2 and cfg3 shapes).  g has k contiguous, so its tiles are kept in LDS as rows
 // of 32 k-values and read with plain ds_read_b128 (Geom::AKC); a Linear weight
 // is k-strided (the clipped products' transposing reads), a Conv1D weight
 // k-contiguous (Geom::BKC).
@@ -33,7 +35,8 @@ namespace fdp {
 namespace dg {
 
 constexpr int kThreads = 512;
-constexpr int kStages = 3;  // a fourth stage measured the same (57.6 vs 56.0 us at cfg2)
+constexpr int kBK = 64;     // k-tile depth
+constexpr int kStages = 2;  // ring stages (64 KB each)
 constexpr int kBM = 256, kBN = 192;  // output tile: 256 rows of g x 192 columns of dX
 constexpr int kXcds = 8;
 
@@ -45,7 +48,7 @@ struct DgradArgs {
   int64_t M, N, K;
   int64_t ldg, ldw, ldo;
   int tiles_m, tiles_n, splits;
-  int nk;             // k-tiles of the whole contraction
+  int nk;             // 64-deep k-tiles of the whole contraction
   unsigned* ticket;   // [tiles_m * tiles_n], zero between launches
   unsigned* flag;     // [tiles], zero between launches
   float* part;        // [tiles, BM * BN] fp32 partials (thread-major), splits == 2
@@ -86,15 +89,15 @@ struct DJob {
 
 template <class DT, int BN, bool WKC>
 __global__ __launch_bounds__(kThreads, 1) void dgrad_kernel(DgradArgs p) {
-  using G = dma::Geom<kBM, BN, 32, 4, 2, true, WKC>;
+  using G = dma::Geom<kBM, BN, kBK, 4, 2, true, WKC>;
   static_assert(G::NW == 8 && G::FI == 2, "8 waves of 64-row blocks");
   constexpr int FI = G::FI, FJ = G::FJ;
   __shared__ __attribute__((aligned(16))) char st0[G::STAGE];
   __shared__ __attribute__((aligned(16))) char st1[G::STAGE];
-  __shared__ __attribute__((aligned(16))) char st2[G::STAGE];
   __shared__ int role, bad_wait;
-  const dma::Stages stages{{(FDP_LDS char*)(st0), (FDP_LDS char*)(st1), (FDP_LDS char*)(st2),
-                            (FDP_LDS char*)(st0)}};
+  static_assert(kStages == 2, "two ring stages");
+  const dma::Stages stages{{(FDP_LDS char*)(st0), (FDP_LDS char*)(st1), (FDP_LDS char*)(st0),
+                            (FDP_LDS char*)(st1)}};
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = (wave >> 1) * 64, wn = (wave & 1) * (BN / 2);
 
@@ -189,48 +192,44 @@ __global__ __launch_bounds__(kThreads, 1) void dgrad_kernel(DgradArgs p) {
   // in LDS (rows of kStageRow bytes, so that the two rows one store
   // instruction writes, 4 apart, fall on different banks) and writes it back
   // as 16-byte row segments.  The ring is free (gemm_pipe ended on a
-  // barrier): waves 0-5 stage two to a ring stage, then waves 6-7 reuse the
-  // first stage.
+  // barrier): four sub-tiles per ring stage.
   constexpr int WN = BN / 2, CH = WN / 8;  // columns, 16-byte chunks per sub-tile row
   constexpr int kStageRow = WN * 2 + 16;
-  static_assert(kStages == 3 && 2 * 64 * kStageRow <= G::STAGE, "two sub-tiles per stage");
-  auto flush = [&](FDP_LDS char* sub) {
+  constexpr int kPerStage = G::STAGE / (64 * kStageRow);  // sub-tiles a ring stage holds
+  static_assert(kPerStage * kStages >= 8, "every wave's sub-tile fits the ring at once");
+  FDP_LDS char* const sub = stages.get(wave / kPerStage) + (wave % kPerStage) * 64 * kStageRow;
 #pragma unroll
-    for (int i = 0; i < FI; ++i)
+  for (int i = 0; i < FI; ++i)
 #pragma unroll
-      for (int j = 0; j < FJ; ++j)
+    for (int j = 0; j < FJ; ++j)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-          const float v = poisoned ? __builtin_nanf("") : acc[i][j][r];
-          *reinterpret_cast<FDP_LDS uint16_t*>(sub + row * kStageRow + (32 * j + (lane & 31)) * 2) =
-              DT::from_f32(v);
-        }
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's writes, read below
-#pragma unroll
-    for (int k = 0; k < CH; ++k) {
-      const int c = lane + 64 * k, row = c / CH, ch = c % CH;
-      const u32x4 v = *reinterpret_cast<const FDP_LDS u32x4*>(sub + row * kStageRow + ch * 16);
-      const int64_t grow = m0 + wm + row, gcol = n0 + wn + ch * 8;
-      if (grow >= p.M) continue;
-      uint16_t* dst = p.out + grow * p.ldo + gcol;
-      if (p.vec_out && gcol + 8 <= p.N) {
-        *reinterpret_cast<uint4*>(dst) = make_uint4(v[0], v[1], v[2], v[3]);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          if (gcol + e < p.N) dst[e] = static_cast<uint16_t>(v[e >> 1] >> (16 * (e & 1)));
+      for (int r = 0; r < 16; ++r) {
+        const int row = 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const float v = poisoned ? __builtin_nanf("") : acc[i][j][r];
+        *reinterpret_cast<FDP_LDS uint16_t*>(sub + row * kStageRow + (32 * j + (lane & 31)) * 2) =
+            DT::from_f32(v);
       }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's writes, read below
+#pragma unroll
+  for (int k = 0; k < CH; ++k) {
+    const int c = lane + 64 * k, row = c / CH, ch = c % CH;
+    const u32x4 v = *reinterpret_cast<const FDP_LDS u32x4*>(sub + row * kStageRow + ch * 16);
+    const int64_t grow = m0 + wm + row, gcol = n0 + wn + ch * 8;
+    if (grow >= p.M) continue;
+    uint16_t* dst = p.out + grow * p.ldo + gcol;
+    if (p.vec_out && gcol + 8 <= p.N) {
+      *reinterpret_cast<uint4*>(dst) = make_uint4(v[0], v[1], v[2], v[3]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (gcol + e < p.N) dst[e] = static_cast<uint16_t>(v[e >> 1] >> (16 * (e & 1)));
     }
-  };
-  if (wave < 6) flush(stages.get(wave >> 1) + (wave & 1) * 64 * kStageRow);
-  __syncthreads();
-  if (wave >= 6) flush(stages.get(0) + (wave & 1) * 64 * kStageRow);
+  }
 }
 
 // Instantiated per dtype in dgrad_{bf16,f16}.hip.  (A 256-wide tile needs
 // 128 accumulators per thread and spills beside the double-buffered fragments
-// at two waves per SIMD; 192 columns keep 96 and 205 VGPRs.)
+// at two waves per SIMD; 192 columns keep 96 and about 200 VGPRs.)
 template <class DT>
 hipError_t launch_dgrad_t(const DgradArgs& a, bool wkc, hipStream_t s) {
   const dim3 grid(static_cast<unsigned>(a.tiles_m * a.tiles_n * a.splits)), block(kThreads);

@@ -93,15 +93,18 @@ struct Geom {
   static_assert(LOADS_A * NW * 64 * 16 == TILE_A && LOADS_B * NW * 64 * 16 == TILE_B,
                 "each wave issues whole 1 KB loads");
   static_assert(BM % 32 == 0 && BN % 32 == 0 && WM % 32 == 0 && WN % 32 == 0, "32x32 blocks");
-  static_assert(!(AKC || BKC) || BK == 32, "k-contiguous tiles: rows of 4 chunks, 2 k-steps");
+  static_assert(!(AKC || BKC) || BK == 32 || BK == 64, "k-contiguous tiles: rows of 4 or 8 chunks");
 };
 
-// k-contiguous tile in LDS: row r (one m or n) holds the k-tile's BK = 32
-// values as 4 chunks of 16 bytes, logical chunk c at physical chunk
-// c ^ kc_swz(r).  An MFMA fragment is one ds_read_b128 per lane (rows
+// k-contiguous tile in LDS: row r (one m or n) holds the k-tile's BK = 32 or
+// 64 values as 4 or 8 chunks of 16 bytes, logical chunk c at physical chunk
+// c ^ kc_swz<BK>(r).  An MFMA fragment is one ds_read_b128 per lane (rows
 // w0 + lane % 32, chunk 2 ks + lane / 32); the swizzle puts any 16 (and any 8)
 // consecutive rows' reads of one chunk on distinct 16-byte bank groups.
-__host__ __device__ constexpr int kc_swz(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
+template <int BK>
+__host__ __device__ constexpr int kc_swz(int r) {
+  return BK == 32 ? ((r >> 1) ^ (r >> 2)) & 3 : ((r >> 1) ^ ((r & 1) << 2)) & 7;
+}
 
 // One operand's per-thread load state: L buffer loads per k-tile of BK rows.
 //
@@ -160,13 +163,14 @@ struct Operand {
     step = static_cast<uint32_t>(BK * ld * 2);
   }
   // Operand stored [rows, K] with K contiguous (row stride ld, a multiple of 8
-  // elements): the tile's R rows from r0, as rows of BK = 32 values (kc_swz
+  // elements): the tile's R rows from r0, as rows of BK values (kc_swz
   // layout above); slots of the tile's padding rows (R and up) read nothing.
   // Rows past `rows` read as zeros (the record ends there).  A row's values
   // past K would be the next row's: callers keep K a multiple of BK.
   template <int R>
   __device__ inline void init_kc(const uint16_t* base, int64_t ld, int64_t rows, int64_t r0) {
-    static_assert(BK == 32, "rows of 4 chunks");
+    static_assert(BK == 32 || BK == 64, "rows of 4 or 8 chunks");
+    constexpr int CPK = BK / 8;  // 16-byte chunks per row
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint64_t a = reinterpret_cast<uint64_t>(base);
     rsrc = u32x4{static_cast<uint32_t>(a), static_cast<uint32_t>(a >> 32) & 0xffffu,
@@ -174,8 +178,8 @@ struct Operand {
 #pragma unroll
     for (int j = 0; j < L; ++j) {
       const int slot = (wave * L + j) * 64 + lane;
-      const int r = slot >> 2;
-      const int c = (slot & 3) ^ kc_swz(r);
+      const int r = slot / CPK;
+      const int c = (slot % CPK) ^ kc_swz<BK>(r);
       voff[j] = r < R ? static_cast<uint32_t>((int64_t(r) * ld + 8 * c) * 2) : kPadOffset;
     }
     col = static_cast<uint32_t>(r0 * ld * 2);
@@ -229,17 +233,19 @@ __device__ __forceinline__ uint32_t frag_off(int w0, int i, int h) {
 }
 
 // Byte offset inside a k-contiguous tile of this lane's plain read for MFMA
-// rows w0 + 32i .. +31, k-step ks (8 k-values: chunk 2 ks + lane / 32).
-__device__ __forceinline__ uint32_t kc_frag_off(int w0, int i, int ks) {
+// rows w0 + 32i .. +31 at k-step 0 (8 k-values: chunk lane / 32).  Chunk
+// 2 ks + h of a row sits at physical chunk (2 ks) ^ (h ^ kc_swz(r)), and a
+// row is 64 or 128 bytes, so k-step ks reads at this offset ^ (ks << 5).
+template <int BK>
+__device__ __forceinline__ uint32_t kc_frag_off(int w0, int i) {
   const int lane = threadIdx.x & 63;
   const int r = w0 + 32 * i + (lane & 31);
-  const int c = 2 * ks + (lane >> 5);
-  return static_cast<uint32_t>((r * 4 + (c ^ kc_swz(r))) * 16);
+  return static_cast<uint32_t>(r * (BK * 2) + (((lane >> 5) ^ kc_swz<BK>(r)) * 16));
 }
 
 // Per operand two offsets per fragment: the two transposing half reads of
-// k-step 0 (k-strided tile; later k-steps add 16 rows) or the plain reads of
-// k-steps 0 and 1 (k-contiguous tile).
+// k-step 0 (k-strided tile; later k-steps add 16 rows), or the plain read of
+// k-step 0 (k-contiguous tile; [1] unused).
 template <class G>
 struct FragOffsets {
   uint32_t a[G::FI][2], b[G::FJ][2];
@@ -248,12 +254,12 @@ struct FragOffsets {
     for (int i = 0; i < G::FI; ++i)
 #pragma unroll
       for (int h = 0; h < 2; ++h)
-        a[i][h] = G::AKC ? kc_frag_off(wm, i, h) : frag_off<G::BM>(wm, i, h);
+        a[i][h] = G::AKC ? kc_frag_off<G::BK>(wm, i) : frag_off<G::BM>(wm, i, h);
 #pragma unroll
     for (int j = 0; j < G::FJ; ++j)
 #pragma unroll
       for (int h = 0; h < 2; ++h)
-        b[j][h] = (G::BKC ? kc_frag_off(wn, j, h) : frag_off<G::BN>(wn, j, h)) + G::TILE_A;
+        b[j][h] = (G::BKC ? kc_frag_off<G::BK>(wn, j) : frag_off<G::BN>(wn, j, h)) + G::TILE_A;
   }
 };
 
@@ -295,14 +301,14 @@ struct Frags {
 #pragma unroll
     for (int j = 0; j < G::FJ; ++j) {
       if constexpr (G::BKC)
-        b[j] = read_plain(st, fo.b[j][ks & 1]);
+        b[j] = read_plain(st, fo.b[j][0] ^ (ks << 5));
       else
         b[j] = read_frag(st, fo.b[j][0] + ks * 16 * G::ROW_B, fo.b[j][1] + ks * 16 * G::ROW_B);
     }
 #pragma unroll
     for (int i = 0; i < G::FI; ++i) {
       if constexpr (G::AKC)
-        a[i] = read_plain(st, fo.a[i][ks & 1]);
+        a[i] = read_plain(st, fo.a[i][0] ^ (ks << 5));
       else
         a[i] = read_frag(st, fo.a[i][0] + ks * 16 * G::ROW_A, fo.a[i][1] + ks * 16 * G::ROW_A);
     }

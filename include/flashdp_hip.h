@@ -298,7 +298,7 @@ int fdp_wgrad_clip_noalloc(const void* a, const void* b, int64_t B, int64_t K, i
  * dx : [M, N], row stride ldo.  g, w and dx share `dtype` (FDP_F16 or
  *      FDP_BF16); products accumulate in fp32 and dx is rounded once.
  * Requirements (FDP_ERR_SHAPE / FDP_ERR_ALIGN otherwise, nothing launched):
- *      K a multiple of 32; ldg and ldw multiples of 8 elements; g and w
+ *      K a multiple of 64; ldg and ldw multiples of 8 elements; g and w
  *      16-byte aligned; g and w each span less than 2 GiB.
  * workspace: fdp_dgrad_workspace_size bytes, 16-byte aligned.  Its control
  *      words (the first 256 bytes, the tickets and flags) must be zero before

@@ -175,7 +175,7 @@ def test_dgrad_validation_codes():
     n = q(8192, 768, 3072, 0, 2)
     assert 128 * 256 * 192 * 4 <= n < 128 * 256 * 192 * 4 + 4096
     with pytest.raises(ValueError):
-        q(8192, 768, 3000, 0, 2)  # K % 32 != 0
+        q(8192, 768, 3040, 0, 2)  # K % 64 != 0
     with pytest.raises(KeyError):
         q(8192, 768, 3072, 0, 0)  # fp32 is torch's matmul
     with pytest.raises(ValueError):
@@ -187,7 +187,7 @@ def test_dgrad_validation_codes():
         a = {**args, **kw}
         return L.fdp_dgrad(a["g"], a["w"], a["dx"], a["M"], a["N"], a["K"], a["ldg"], a["ldw"],
                            a["ldo"], a["layout"], a["dtype"], a["ws"], a["nb"], a["stream"])
-    assert call(K=48) == 2
+    assert call(K=96) == 2
     assert call(ldg=32) == 2          # row stride below K
     assert call(ldw=32) == 2          # NN weight rows hold N values
     assert call(ldg=68) == 6          # 16-byte rows

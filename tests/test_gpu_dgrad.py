@@ -50,9 +50,9 @@ def call(g, w, layout, ws=None, ldg=None):
 
 
 SHAPES = [
-    (300, 64, 100),      # ragged rows and columns, one tile, split over K
-    (1000, 96, 200),     # several tiles
-    (17, 32, 40),        # fewer rows than a tile, the shortest contraction
+    (300, 128, 100),     # ragged rows and columns, one tile, split over K
+    (1000, 192, 200),    # several tiles
+    (17, 64, 40),        # fewer rows than a tile, the shortest contraction (no split)
     (4096, 768, 768),    # GPT-2 small Linear
     (8192, 3072, 768),   # cfg2's dX (MLP-up, Linear): 128 tiles, split in two
     (16384, 2304, 768),  # cfg3's dX (c_attn, Conv1D): 256 tiles, one pass
@@ -87,7 +87,7 @@ def test_dgrad_deterministic_and_workspace_reuse(layout):
     for _ in range(3):
         again, _ = call(g, w, layout, ws=ws)
         assert torch.equal(first, again)
-    g2, w2 = make(1000, 96, 200, torch.bfloat16, layout, seed=2)
+    g2, w2 = make(1000, 192, 200, torch.bfloat16, layout, seed=2)
     out2, _ = call(g2, w2, layout, ws=ws)
     assert_close(out2, ref_dx(g2, w2, layout), torch.bfloat16, "dgrad after reuse")
 
@@ -144,8 +144,8 @@ def test_layers_default_to_torch_matmul():
 
 
 def test_dgrad_rejects_unsupported_operands():
-    g, w = make(256, 100, 64, torch.bfloat16, "nn")
-    with pytest.raises(ValueError):  # K % 32 != 0
+    g, w = make(256, 96, 64, torch.bfloat16, "nn")
+    with pytest.raises(ValueError):  # K % 64 != 0
         core.dgrad(g, w, "nn")
     g32 = torch.randn(256, 64, device=DEV)
     with pytest.raises(KeyError):
