@@ -12,7 +12,7 @@
 // 64-deep k-tiles (a 3-stage ring of 32-deep ones, with half the MFMAs
 // between two workgroup barriers, took 57-61 against 53.6-54.4 us at the
 // cfg2 and cfg3 shapes).  g has k contiguous, so its tiles are kept in LDS as rows
-// of 32 k-values and read with plain ds_read_b128 (Geom::AKC); a Linear weight
+// of 64 k-values and read with plain ds_read_b128 (Geom::AKC); a Linear weight
 // is k-strided (the clipped products' transposing reads), a Conv1D weight
 // k-contiguous (Geom::BKC).
 //

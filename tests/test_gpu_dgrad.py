@@ -135,8 +135,8 @@ def test_layer_input_grad_on_the_kernel(cls):
 
 
 def test_layers_default_to_torch_matmul():
-    """hipBLASLt is faster at every measured layer shape: the layers call the
-    kernel only when set_dgrad("hip") selects it."""
+    """hipBLASLt is as fast or faster at every measured layer shape: the layers
+    call the kernel only when set_dgrad("hip") selects it."""
     from flashdp4review_amd.core import inputgrad as D
     assert D._mode == "torch"
     with pytest.raises(ValueError):
