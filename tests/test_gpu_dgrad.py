@@ -153,3 +153,26 @@ def test_dgrad_rejects_unsupported_operands():
     # the layer falls back to torch's matmul for such shapes
     out = core.input_grad(g, w, "nn")
     np.testing.assert_allclose(out.float().cpu().numpy(), ref_dx(g, w, "nn"), rtol=0, atol=2e-3)
+
+
+def test_dgrad_graph_replays_match_eager():
+    """fdp_dgrad records kernels only (no memset) and its control words clear
+    themselves, so a captured call replays exactly: three replays, with eager
+    calls and synchronisations between them, each equal to the eager result."""
+    g, w = make(8192, 3072, 768, torch.bfloat16, "nn", seed=3)  # the split plan
+    eager = core.dgrad(g, w, "nn")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        core.dgrad(g, w, "nn")  # warm-up on the capture stream (its workspace)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            out = core.dgrad(g, w, "nn")
+    torch.cuda.current_stream().wait_stream(s)
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+        assert torch.equal(core.dgrad(g, w, "nn"), eager)
+        torch.cuda.synchronize()
