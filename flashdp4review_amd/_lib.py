@@ -99,9 +99,8 @@ SIGNATURES = {
                                         _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_f, _c_f, _c_p,
                                         _c_f, _c_p, _c_f, _c_key, _c_p, _c_i64, _c_int, _c_p, _c_p,
                                         _c_int, _c_p]),
-    "fdp_dgrad_workspace_size": (_c_int, [_c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_sz_p]),
     "fdp_dgrad": (_c_int, [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
-                           _c_int, _c_int, _c_p, ctypes.c_size_t, _c_p]),
+                           _c_int, _c_int, _c_p]),
     "fdp_colsum_clip_workspace_size": (_c_int, [_c_i64, _c_i64, _c_i64, _c_int, _c_sz_p]),
     "fdp_colsum_clip": (_c_int, [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_f, _c_f,
                                  _c_p, _c_f, _c_p, _c_f, _c_key, _c_p, _c_int, _c_p, _c_p, _c_p,

@@ -32,7 +32,7 @@ from .layernorm import (
     layernorm_bwd_clip_fused,
     layernorm_dwdb_fused,
 )
-from .inputgrad import dgrad, input_grad, set_dgrad
+from .inputgrad import dgrad, dgrad_choices, input_grad, set_dgrad
 from .utils import RuntimeAutoTuner, supported_acc_dtypes
 
 __all__ = [
@@ -40,5 +40,5 @@ __all__ = [
     "conv1d_weight_flashdp", "colsum_clip", "linear_bias_grad_clip", "conv1d_bias_grad_clip",
     "layernorm_dw_clip", "layernorm_db_clip", "layernorm_fwd", "layernorm_bwd_clip",
     "layernorm_fwd_fused", "layernorm_bwd_clip_fused", "layernorm_dwdb_fused",
-    "dgrad", "input_grad", "set_dgrad", "RuntimeAutoTuner", "supported_acc_dtypes",
+    "dgrad", "dgrad_choices", "input_grad", "set_dgrad", "RuntimeAutoTuner", "supported_acc_dtypes",
 ]

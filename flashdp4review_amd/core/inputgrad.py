@@ -5,13 +5,18 @@ The reference forms a DP layer's grad_input with torch's matmul
 flashdp/layers/transformers_conv1d.py:70-77: ``grad_output @ weight.t()``).
 The library also has a dX kernel of its own for 16-bit operands (fdp_dgrad:
 the clipped products' LDS-DMA / MFMA core with grad_output taken k-contiguous,
-256x192 tiles, a split contraction where the tiles alone would leave CUs
-idle).  It is exact to the bf16 tolerance and deterministic, and on MI355X
-about as fast as hipBLASLt at GPT-2's 768-wide inputs (cfg3's dX 54.4 against
-55.6 us, cfg2's 53.6 against 52.4 us) and slower elsewhere (GPT-2 small
-30.8 against 20.2 us, a 2048x2048 Linear 118 against 61 us), so the layers
-keep torch's matmul unless ``set_dgrad("hip")`` selects the kernel:
-  "torch" (default) torch's matmul (hipBLASLt);
+256x192 or 128x192 output tiles, no workspace), exact to the bf16 tolerance
+and deterministic.  On MI355X it is faster than hipBLASLt at some layer shapes
+(GPT-2 small's attention projection, 8192x768x768: 15.8 against 20.3 us) and
+slower at others (d = 2048 layers, where 192-column tiles leave CUs idle), so
+the path is chosen per shape (``set_dgrad``):
+  "auto"  (default) the first call of each (device, M, N, K, layout, dtype)
+          times both paths on the current stream (a few calls each, outside
+          HIP-graph capture) and keeps the faster; the reference's layers
+          choose between implementations by timing in the same way
+          (flashdp/core/utils.py:15-47); under capture an untimed shape
+          takes torch's matmul;
+  "torch" torch's matmul (hipBLASLt) always;
   "hip"   the HIP kernel for every operand pair it takes.
 Operands the kernel does not take (fp32, K not a multiple of 64, unaligned
 rows) always use torch's matmul, as the reference does.
@@ -23,10 +28,10 @@ import os
 import torch
 
 from .. import _lib
-from .wgrad import _persistent_workspace, _raise_expired
 
-_MODES = ("torch", "hip")
-_mode = os.environ.get("FDP_DGRAD", "torch")
+_MODES = ("auto", "torch", "hip")
+_mode = os.environ.get("FDP_DGRAD", "auto")
+_choice: dict = {}  # (device, M, N, K, layout, dtype) -> "hip" | "torch" ("auto" mode)
 if _mode not in _MODES:
     raise ValueError(f"FDP_DGRAD must be one of {_MODES}, got {_mode!r}")
 
@@ -34,13 +39,47 @@ LAYOUT_NN, LAYOUT_NT = 0, 1  # fdp_dgrad_layout
 
 
 def set_dgrad(mode: str) -> str:
-    """Input-gradient path of DPLinear / DPConv1D ("torch" or "hip"); returns
-    the previous mode."""
+    """Input-gradient path of DPLinear / DPConv1D ("auto", "torch" or "hip");
+    returns the previous mode."""
     global _mode
     if mode not in _MODES:
         raise ValueError(f"dgrad mode must be one of {_MODES}, got {mode!r}")
     prev, _mode = _mode, mode
     return prev
+
+
+def dgrad_choices() -> dict:
+    """The "auto" mode's choices so far: (device, M, N, K, layout, dtype) -> path."""
+    return dict(_choice)
+
+
+def _median_us(fn, reps: int = 5, warmup: int = 2) -> float:
+    for _ in range(warmup):
+        fn()
+    ts = []
+    for _ in range(reps):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        fn()
+        end.record()
+        end.synchronize()
+        ts.append(start.elapsed_time(end))
+    return sorted(ts)[len(ts) // 2] * 1e3
+
+
+def _auto_choice(grad_output, weight, layout, M, N, K) -> str:
+    key = (grad_output.device.index, M, N, K, layout, grad_output.dtype)
+    c = _choice.get(key)
+    if c is not None:
+        return c
+    if torch.cuda.is_current_stream_capturing():
+        return "torch"
+    w = weight if layout == "nn" else weight.t()
+    t_torch = _median_us(lambda: grad_output @ w)
+    t_hip = _median_us(lambda: dgrad(grad_output, weight, layout))
+    c = "hip" if t_hip < t_torch else "torch"
+    _choice[key] = c
+    return c
 
 
 def _takes(g2: torch.Tensor, w: torch.Tensor, K: int) -> bool:
@@ -78,29 +117,23 @@ def dgrad(grad_output: torch.Tensor, weight: torch.Tensor, layout: str = "nn") -
     w = weight if weight.stride(1) == 1 and weight.stride(0) % 8 == 0 else weight.contiguous()
     M = g2.shape[0]
     out = torch.empty(M, N, dtype=grad_output.dtype, device=dev)
-    L = _lib.lib()
     lay = LAYOUT_NN if layout == "nn" else LAYOUT_NT
-    nbytes = _lib.size_query(L.fdp_dgrad_workspace_size, M, N, K, lay, dt)
-    stream = _lib.stream_handle(dev)
-    ws = _persistent_workspace(nbytes, dev, stream, "dgrad")
-    if ws.event is not None:
-        probed = ws.take_probe()
-        if probed != 0:
-            _raise_expired(ws, "reported asynchronously for an earlier call on this stream",
-                           probed)
-    st = L.fdp_dgrad(g2.data_ptr(), w.data_ptr(), out.data_ptr(), M, N, K, g2.stride(0),
-                     w.stride(0), N, lay, dt, ws.buf.data_ptr(), ws.buf.numel(), stream)
+    st = _lib.lib().fdp_dgrad(g2.data_ptr(), w.data_ptr(), out.data_ptr(), M, N, K,
+                              g2.stride(0), w.stride(0), N, lay, dt, _lib.stream_handle(dev))
     _lib.check(st, "fdp_dgrad")
-    ws.queue_probe()
     return out.reshape(*grad_output.shape[:-1], N)
 
 
 def input_grad(grad_output: torch.Tensor, weight: torch.Tensor, layout: str = "nn") -> torch.Tensor:
-    """A DP layer's grad_input: the HIP kernel in "hip" mode for the operands
-    it takes, torch's matmul otherwise."""
+    """A DP layer's grad_input: the HIP kernel or torch's matmul, by the mode
+    (see the module docstring); torch's matmul for operands the kernel does
+    not take."""
     if weight.dtype != grad_output.dtype:  # AMP: the weight in grad_output's dtype
         weight = weight.to(grad_output.dtype)
     K = grad_output.shape[-1]
-    if _mode == "hip" and _takes(grad_output.reshape(-1, K), weight, K):
-        return dgrad(grad_output, weight, layout)
+    if _mode != "torch" and _takes(grad_output.reshape(-1, K), weight, K):
+        N = weight.shape[1] if layout == "nn" else weight.shape[0]
+        M = grad_output.numel() // K
+        if _mode == "hip" or _auto_choice(grad_output, weight, layout, M, N, K) == "hip":
+            return dgrad(grad_output, weight, layout)
     return grad_output @ (weight if layout == "nn" else weight.t())

@@ -40,8 +40,7 @@ class _Workspace:
     each leaves the control words valid (a zero-filled head is valid), so the
     buffer is reused with FDP_WGRAD_CLEAN_WORKSPACE and no clearing kernel."""
 
-    def __init__(self, nbytes: int, dev: torch.device, kind: str = "wgrad"):
-        self.kind = kind  # "wgrad" (fdp_wgrad_clip) or "dgrad" (fdp_dgrad)
+    def __init__(self, nbytes: int, dev: torch.device):
         self.buf = torch.zeros(max(int(nbytes), 4096), dtype=torch.uint8, device=dev)
         self.status_host = torch.zeros(1, dtype=torch.int32, pin_memory=True)
         self.event = None
@@ -70,11 +69,8 @@ class _Workspace:
             self.event.record()
 
 
-def _persistent_workspace(nbytes: int, dev: torch.device, stream: int,
-                          kind: str = "wgrad") -> _Workspace:
-    """The zero-filled workspace of `kind` ("wgrad": fdp_wgrad_clip and
-    fdp_wgrad_bias_clip; "dgrad": fdp_dgrad) for (device, stream)."""
-    key = (dev.index, stream, kind)
+def _persistent_workspace(nbytes: int, dev: torch.device, stream: int) -> _Workspace:
+    key = (dev.index, stream)
     ws = _ws_cache.get(key)  # (a dict read is atomic; the lock guards replacement)
     if ws is not None and ws.buf.numel() >= nbytes:
         return ws
@@ -83,7 +79,7 @@ def _persistent_workspace(nbytes: int, dev: torch.device, stream: int,
         if ws is None or ws.buf.numel() < nbytes:
             if len(_ws_cache) >= 16:
                 _ws_cache.clear()
-            ws = _Workspace(nbytes, dev, kind)
+            ws = _Workspace(nbytes, dev)
             _ws_cache[key] = ws
         _install_step_check()
         return ws
@@ -199,10 +195,9 @@ def release_workspaces() -> None:
 def _raise_expired(ws: _Workspace, when: str, status: int = 1) -> None:
     del status  # every nonzero status is an expired wait
     ws.status_word().zero_()  # stream-ordered: later calls see a clear status word
-    what = ("fdp_dgrad: a bounded wait between the two halves of a split contraction"
-            if ws.kind == "dgrad" else
-            "fdp_wgrad_clip: a bounded inter-workgroup wait of the single-pass kernel")
-    raise _lib.FlashDPError(f"{what} timed out ({when}); the results of that call are NaN")
+    raise _lib.FlashDPError(
+        f"fdp_wgrad_clip: a bounded inter-workgroup wait of the single-pass kernel timed out "
+        f"({when}); the results of that call are NaN")
 
 
 def wgrad_status(device=None, clear: bool = True) -> int:
@@ -210,7 +205,7 @@ def wgrad_status(device=None, clear: bool = True) -> int:
     (nonzero: a bounded wait of an earlier call timed out and its outputs are
     NaN); ``clear`` resets it."""
     dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
-    ws = _ws_cache.get((dev.index, _lib.stream_handle(dev), "wgrad"))
+    ws = _ws_cache.get((dev.index, _lib.stream_handle(dev)))
     if ws is None:
         return 0
     torch.cuda.synchronize(dev)

@@ -16,17 +16,10 @@
 // is k-strided (the clipped products' transposing reads), a Conv1D weight
 // k-contiguous (Geom::BKC).
 //
-// Work map: one workgroup per (output tile, k-split).  A layer whose tiles
-// fill less of the chip (cfg2: 8192 x 768 outputs = 128 tiles of 256 x 192 on
-// 256 CUs) splits the contraction: each split contracts a contiguous range of
-// k-tiles (at most two splits).  The tile's two splits meet at a
-// self-resetting ticket: the first to arrive publishes its fp32 partial
-// (agent-coherent 16-byte stores) and raises its flag; the second waits for
-// that flag -- set by a workgroup that already holds a CU and waits on
-// nothing, so the wait ends -- adds the partial (p0 + p1 is the same fp32 sum
-// whichever split arrives last: deterministic) and stores dX.  It then clears
-// the flags and the ticket, so the control words are zero after every
-// completed launch.
+// Work map: one workgroup per output tile of 256 or 128 rows of g by 192
+// columns of dX (the host picks the height that needs the fewer rounds of
+// workgroups over the CUs: cfg2's 8192 x 768 outputs are 128 tiles of 256
+// rows but 256 of 128), XCD-contiguous.  No workgroup waits for another.
 #pragma once
 
 #include "gemm_dma.hpp"
@@ -38,6 +31,7 @@ constexpr int kThreads = 512;
 constexpr int kBK = 64;     // k-tile depth
 constexpr int kStages = 2;  // ring stages (64 KB each)
 constexpr int kBM = 256, kBN = 192;  // output tile: 256 rows of g x 192 columns of dX
+constexpr int kBMHalf = 128;         // or 128 rows (32 per wave), when 256 leave CUs idle
 constexpr int kXcds = 8;
 
 struct DgradArgs {
@@ -47,19 +41,14 @@ struct DgradArgs {
   int vec_out;        // out rows are 16-byte aligned (ldo % 8 == 0, out 16-byte aligned)
   int64_t M, N, K;
   int64_t ldg, ldw, ldo;
-  int tiles_m, tiles_n, splits;
-  int nk;             // 64-deep k-tiles of the whole contraction
-  unsigned* ticket;   // [tiles_m * tiles_n], zero between launches
-  unsigned* flag;     // [tiles], zero between launches
-  float* part;        // [tiles, BM * BN] fp32 partials (thread-major), splits == 2
-  int* err;           // sticky status word: a bounded wait expired
-  unsigned spin_limit;
+  int tiles_m, tiles_n;
+  int nk;             // 64-deep k-tiles of the contraction
 };
 
 // Hardware workgroup -> logical item, XCD-contiguous: workgroups are dealt
 // round-robin to the 8 XCDs, so item ranges [x * n / 8, (x + 1) * n / 8) run
-// on XCD x and neighbouring items (the n-tiles and splits of one row band of
-// g) share that XCD's L2.
+// on XCD x and neighbouring items (the n-tiles of one row band of g) share
+// that XCD's L2.
 __device__ __forceinline__ int item_of(int hw, int n) {
   if (n % kXcds != 0) return hw;
   return (hw % kXcds) * (n / kXcds) + hw / kXcds;
@@ -69,17 +58,11 @@ template <class G, bool WKC>
 struct DJob {
   dma::Operand<G::LOADS_A, G::BK> a;
   dma::Operand<G::LOADS_B, G::BK> b;
-  // output tile (m0, n0), contraction from k-tile kt0 on
-  __device__ __forceinline__ void init(const DgradArgs& p, int64_t m0, int64_t n0, int kt0) {
+  // output tile (m0, n0)
+  __device__ __forceinline__ void init(const DgradArgs& p, int64_t m0, int64_t n0) {
     a.template init_kc<G::BM>(p.g, p.ldg, p.M, m0);
-    a.col += static_cast<uint32_t>(kt0 * G::BK * 2);
-    if constexpr (WKC) {
-      b.template init_kc<G::BN>(p.w, p.ldw, p.N, n0);
-      b.col += static_cast<uint32_t>(kt0 * G::BK * 2);
-    } else {
-      b.template init<G::BN>(p.w, p.ldw, p.K, n0);
-      b.col += static_cast<uint32_t>(int64_t(kt0) * G::BK * p.ldw * 2);
-    }
+    if constexpr (WKC) b.template init_kc<G::BN>(p.w, p.ldw, p.N, n0);
+    else b.template init<G::BN>(p.w, p.ldw, p.K, n0);
   }
   __device__ __forceinline__ void issue(FDP_LDS char* stage, int kt) const {
     a.issue(stage, kt);
@@ -87,26 +70,22 @@ struct DJob {
   }
 };
 
-template <class DT, int BN, bool WKC>
+template <class DT, int BM, int BN, bool WKC>
 __global__ __launch_bounds__(kThreads, 1) void dgrad_kernel(DgradArgs p) {
-  using G = dma::Geom<kBM, BN, kBK, 4, 2, true, WKC>;
-  static_assert(G::NW == 8 && G::FI == 2, "8 waves of 64-row blocks");
+  using G = dma::Geom<BM, BN, kBK, 4, 2, true, WKC>;
+  static_assert(G::NW == 8, "8 waves: 4 along g's rows, 2 along dX's columns");
+  constexpr int WMR = G::WM;  // rows of g per wave (BM / 4)
   constexpr int FI = G::FI, FJ = G::FJ;
   __shared__ __attribute__((aligned(16))) char st0[G::STAGE];
   __shared__ __attribute__((aligned(16))) char st1[G::STAGE];
-  __shared__ int role, bad_wait;
   static_assert(kStages == 2, "two ring stages");
   const dma::Stages stages{{(FDP_LDS char*)(st0), (FDP_LDS char*)(st1), (FDP_LDS char*)(st0),
                             (FDP_LDS char*)(st1)}};
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = (wave >> 1) * 64, wn = (wave & 1) * (BN / 2);
+  const int wm = (wave >> 1) * WMR, wn = (wave & 1) * (BN / 2);
 
-  const int tiles = p.tiles_m * p.tiles_n;
-  const int item = item_of(blockIdx.x, tiles * p.splits);
-  const int split = item % p.splits, tile = item / p.splits;
-  const int64_t m0 = int64_t(tile / p.tiles_n) * G::BM, n0 = int64_t(tile % p.tiles_n) * BN;
-  const int kt0 = static_cast<int>((int64_t(split) * p.nk) / p.splits);
-  const int kt1 = static_cast<int>((int64_t(split + 1) * p.nk) / p.splits);
+  const int tile = item_of(blockIdx.x, p.tiles_m * p.tiles_n);
+  const int64_t m0 = int64_t(tile / p.tiles_n) * BM, n0 = int64_t(tile % p.tiles_n) * BN;
 
   f32x16 acc[FI][FJ];
 #pragma unroll
@@ -119,85 +98,21 @@ __global__ __launch_bounds__(kThreads, 1) void dgrad_kernel(DgradArgs p) {
     dma::FragOffsets<G> fo;
     fo.init(wm, wn);
     DJob<G, WKC> job;
-    job.init(p, m0, n0, kt0);
-    dma::gemm_pipe<DT, G, kStages>(job, kt1 - kt0, fo, stages, acc);
+    job.init(p, m0, n0);
+    dma::gemm_pipe<DT, G, kStages>(job, p.nk, fo, stages, acc);
   }
 
-  bool poisoned = false;
-  if (p.splits > 1) {
-    // ---- the tile's splits meet at its ticket
-    if (threadIdx.x == 0) {
-      const unsigned t =
-          __hip_atomic_fetch_add(p.ticket + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      role = t + 1 == unsigned(p.splits);
-    }
-    __syncthreads();
-    const uint32_t span = static_cast<uint32_t>(sizeof(float) * G::BM * BN);
-    if (!role) {
-      // publish: chunk q of this thread at (q * 512 + tid) * 16 bytes
-      const CoherentSpan out(p.part + int64_t(tile) * (G::BM * BN), span);
-#pragma unroll
-      for (int i = 0; i < FI; ++i)
-#pragma unroll
-        for (int j = 0; j < FJ; ++j)
-#pragma unroll
-          for (int r = 0; r < 16; r += 4) {
-            const int q = ((i * FJ + j) * 16 + r) / 4;
-            out.store4(static_cast<uint32_t>((q * kThreads + threadIdx.x) * 16),
-                       f32x4{acc[i][j][r], acc[i][j][r + 1], acc[i][j][r + 2], acc[i][j][r + 3]});
-          }
-      wait_stores();
-      __syncthreads();
-      if (threadIdx.x == 0)
-        __hip_atomic_store(p.flag + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      return;
-    }
-    // second split: wait for the first's flag (bounded), then clear it and
-    // the ticket for the next launch
-    if (threadIdx.x == 0) {
-      int bad = 0;
-      for (unsigned spins = 0;; ++spins) {
-        if (__hip_atomic_load(p.flag + tile, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u)
-          break;
-        if (spins >= p.spin_limit) {
-          bad = 1;
-          break;
-        }
-        __builtin_amdgcn_s_sleep(2);
-      }
-      if (bad) atomicOr(p.err, 1);
-      __hip_atomic_store(p.flag + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(p.ticket + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      bad_wait = bad;
-    }
-    __syncthreads();
-    poisoned = bad_wait != 0;
-    // the other split's partial (splits == 2; p0 + p1 in either order is the
-    // same fp32 sum, so the result does not depend on which split came last)
-    const CoherentSpan in(p.part + int64_t(tile) * (G::BM * BN), span);
-#pragma unroll
-    for (int i = 0; i < FI; ++i)
-#pragma unroll
-      for (int j = 0; j < FJ; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; r += 4) {
-          const int q = ((i * FJ + j) * 16 + r) / 4;
-          const f32x4 v = in.load4(static_cast<uint32_t>((q * kThreads + threadIdx.x) * 16));
-#pragma unroll
-          for (int c = 0; c < 4; ++c) acc[i][j][r + c] = v[c] + acc[i][j][r + c];
-        }
-  }
-
-  // ---- store dX in g's dtype.  Each wave stages its 64 x (BN/2) sub-tile
+  // ---- store dX in g's dtype.  Each wave stages its WMR x (BN/2) sub-tile
   // in LDS (rows of kStageRow bytes, so that the two rows one store
   // instruction writes, 4 apart, fall on different banks) and writes it back
   // as 16-byte row segments.  The ring is free (gemm_pipe ended on a
   // barrier): four sub-tiles per ring stage.
   constexpr int WN = BN / 2, CH = WN / 8;  // columns, 16-byte chunks per sub-tile row
   constexpr int kStageRow = WN * 2 + 16;
-  constexpr int kPerStage = G::STAGE / (64 * kStageRow);  // sub-tiles a ring stage holds
+  constexpr int kPerStage = G::STAGE / (WMR * kStageRow);  // sub-tiles a ring stage holds
   static_assert(kPerStage * kStages >= 8, "every wave's sub-tile fits the ring at once");
-  FDP_LDS char* const sub = stages.get(wave / kPerStage) + (wave % kPerStage) * 64 * kStageRow;
+  static_assert(WMR * CH % 64 == 0, "whole rounds of 16-byte chunks per wave");
+  FDP_LDS char* const sub = stages.get(wave / kPerStage) + (wave % kPerStage) * WMR * kStageRow;
 #pragma unroll
   for (int i = 0; i < FI; ++i)
 #pragma unroll
@@ -205,13 +120,12 @@ __global__ __launch_bounds__(kThreads, 1) void dgrad_kernel(DgradArgs p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int row = 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        const float v = poisoned ? __builtin_nanf("") : acc[i][j][r];
         *reinterpret_cast<FDP_LDS uint16_t*>(sub + row * kStageRow + (32 * j + (lane & 31)) * 2) =
-            DT::from_f32(v);
+            DT::from_f32(acc[i][j][r]);
       }
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's writes, read below
 #pragma unroll
-  for (int k = 0; k < CH; ++k) {
+  for (int k = 0; k < WMR * CH / 64; ++k) {
     const int c = lane + 64 * k, row = c / CH, ch = c % CH;
     const u32x4 v = *reinterpret_cast<const FDP_LDS u32x4*>(sub + row * kStageRow + ch * 16);
     const int64_t grow = m0 + wm + row, gcol = n0 + wn + ch * 8;
@@ -231,15 +145,20 @@ __global__ __launch_bounds__(kThreads, 1) void dgrad_kernel(DgradArgs p) {
 // 128 accumulators per thread and spills beside the double-buffered fragments
 // at two waves per SIMD; 192 columns keep 96 and about 200 VGPRs.)
 template <class DT>
-hipError_t launch_dgrad_t(const DgradArgs& a, bool wkc, hipStream_t s) {
-  const dim3 grid(static_cast<unsigned>(a.tiles_m * a.tiles_n * a.splits)), block(kThreads);
-  if (wkc) hipLaunchKernelGGL((dgrad_kernel<DT, kBN, true>), grid, block, 0, s, a);
-  else hipLaunchKernelGGL((dgrad_kernel<DT, kBN, false>), grid, block, 0, s, a);
+hipError_t launch_dgrad_t(const DgradArgs& a, int bm, bool wkc, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>(a.tiles_m * a.tiles_n)), block(kThreads);
+  if (bm == kBM) {
+    if (wkc) hipLaunchKernelGGL((dgrad_kernel<DT, kBM, kBN, true>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((dgrad_kernel<DT, kBM, kBN, false>), grid, block, 0, s, a);
+  } else {
+    if (wkc) hipLaunchKernelGGL((dgrad_kernel<DT, kBMHalf, kBN, true>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((dgrad_kernel<DT, kBMHalf, kBN, false>), grid, block, 0, s, a);
+  }
   return hipGetLastError();
 }
 
-hipError_t launch_dgrad_bf16(const DgradArgs& a, bool wkc, hipStream_t s);
-hipError_t launch_dgrad_f16(const DgradArgs& a, bool wkc, hipStream_t s);
+hipError_t launch_dgrad_bf16(const DgradArgs& a, int bm, bool wkc, hipStream_t s);
+hipError_t launch_dgrad_f16(const DgradArgs& a, int bm, bool wkc, hipStream_t s);
 
 }  // namespace dg
 }  // namespace fdp

@@ -5,8 +5,8 @@
 namespace fdp {
 namespace dg {
 
-hipError_t launch_dgrad_f16(const DgradArgs& a, bool wkc, hipStream_t s) {
-  return launch_dgrad_t<F16>(a, wkc, s);
+hipError_t launch_dgrad_f16(const DgradArgs& a, int bm, bool wkc, hipStream_t s) {
+  return launch_dgrad_t<F16>(a, bm, wkc, s);
 }
 
 }  // namespace dg

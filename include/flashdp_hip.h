@@ -300,25 +300,18 @@ int fdp_wgrad_clip_noalloc(const void* a, const void* b, int64_t B, int64_t K, i
  * Requirements (FDP_ERR_SHAPE / FDP_ERR_ALIGN otherwise, nothing launched):
  *      K a multiple of 64; ldg and ldw multiples of 8 elements; g and w
  *      16-byte aligned; g and w each span less than 2 GiB.
- * workspace: fdp_dgrad_workspace_size bytes, 16-byte aligned.  Its control
- *      words (the first 256 bytes, the tickets and flags) must be zero before
- *      the first call; every completed call leaves them zero, so a buffer is
- *      zero-filled once and reused by calls in stream order.  Its first int is
- *      a sticky status word, as for fdp_wgrad_clip: nonzero means a bounded
- *      wait between the two halves of a split contraction expired (the
- *      affected rows of dx are NaN).  Concurrent calls need separate buffers.
- * The result is deterministic (fixed summation order).
+ * No workspace: each workgroup forms whole output tiles and waits for no
+ * other, so the call only enqueues one kernel on `stream` (it may be
+ * captured into a HIP graph).  The result is deterministic (fixed summation
+ * order).
  * ---------------------------------------------------------------------- */
 typedef enum fdp_dgrad_layout {
   FDP_DGRAD_NN = 0,
   FDP_DGRAD_NT = 1
 } fdp_dgrad_layout;
 
-int fdp_dgrad_workspace_size(int64_t M, int64_t N, int64_t K, int layout, int dtype,
-                             size_t* bytes);
 int fdp_dgrad(const void* g, const void* w, void* dx, int64_t M, int64_t N, int64_t K,
-              int64_t ldg, int64_t ldw, int64_t ldo, int layout, int dtype, void* workspace,
-              size_t workspace_bytes, void* stream);
+              int64_t ldg, int64_t ldw, int64_t ldo, int layout, int dtype, void* stream);
 
 /* ------------------------------------------------------------------------
  * Clipped per-sample column sums over the middle axis:

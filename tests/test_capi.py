@@ -169,29 +169,19 @@ def test_dgrad_validation_codes():
     """fdp_dgrad checks sizes, layout, dtype, strides and alignment on the host
     and launches nothing on a bad call."""
     L = _lib.lib()
-    q = lambda *a: _lib.size_query(L.fdp_dgrad_workspace_size, *a)  # noqa: E731
-    # cfg2 (M = 8192, N = 768, K = 3072): 128 tiles of 256 x 192, split in two over
-    # K on 256 CUs: one fp32 partial per tile after the control words
-    n = q(8192, 768, 3072, 0, 2)
-    assert 128 * 256 * 192 * 4 <= n < 128 * 256 * 192 * 4 + 4096
-    with pytest.raises(ValueError):
-        q(8192, 768, 3040, 0, 2)  # K % 64 != 0
-    with pytest.raises(KeyError):
-        q(8192, 768, 3072, 0, 0)  # fp32 is torch's matmul
-    with pytest.raises(ValueError):
-        q(8192, 768, 3072, 2, 2)  # no such layout
     args = dict(g=16, w=16, dx=16, M=64, N=64, K=64, ldg=64, ldw=64, ldo=64, layout=0, dtype=2,
-                ws=16, nb=0, stream=None)
+                stream=None)
 
     def call(**kw):
         a = {**args, **kw}
         return L.fdp_dgrad(a["g"], a["w"], a["dx"], a["M"], a["N"], a["K"], a["ldg"], a["ldw"],
-                           a["ldo"], a["layout"], a["dtype"], a["ws"], a["nb"], a["stream"])
-    assert call(K=96) == 2
+                           a["ldo"], a["layout"], a["dtype"], a["stream"])
+    assert call(K=96) == 2            # K % 64 != 0
+    assert call(dtype=0) == 1         # fp32 is torch's matmul
+    assert call(layout=2) == 3        # no such layout
     assert call(ldg=32) == 2          # row stride below K
     assert call(ldw=32) == 2          # NN weight rows hold N values
     assert call(ldg=68) == 6          # 16-byte rows
     assert call(g=24) == 6            # 16-byte aligned operands
     assert call(g=None) == 3
     assert call(M=1 << 22, ldg=1 << 9) == 2  # g spans 2^32 bytes (32-bit buffer records)
-    assert call(nb=0) == 4            # workspace too small
