@@ -65,6 +65,7 @@ extern "C" int fdp_dgrad(const void* g, const void* w, void* dx, int64_t M, int6
       reinterpret_cast<uintptr_t>(w) % 16 != 0 || reinterpret_cast<uintptr_t>(dx) % 2 != 0)
     return FDP_ERR_ALIGN;
   const Plan pl = cached_plan(M, N, fdp::host::device_cus());
+  if (int64_t(pl.tiles_m) * pl.tiles_n >= (int64_t(1) << 30)) return FDP_ERR_SHAPE;  // grid size
 
   DgradArgs a{};
   a.g = static_cast<const uint16_t*>(g);

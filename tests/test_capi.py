@@ -185,3 +185,5 @@ def test_dgrad_validation_codes():
     assert call(g=24) == 6            # 16-byte aligned operands
     assert call(g=None) == 3
     assert call(M=1 << 22, ldg=1 << 9) == 2  # g spans 2^32 bytes (32-bit buffer records)
+    # 2^23 rows x 2^23 columns: g and w each 1 GiB, but about 2^31 output tiles
+    assert call(M=1 << 23, N=1 << 23, K=64, ldw=1 << 23, ldo=1 << 23) == 2
