@@ -59,8 +59,7 @@ extern "C" int fdp_dgrad(const void* g, const void* w, void* dx, int64_t M, int6
   const int64_t wrows = layout == FDP_DGRAD_NN ? K : N, wcols = layout == FDP_DGRAD_NN ? N : K;
   if (ldg < K || ldw < wcols || ldo < N) return FDP_ERR_SHAPE;
   // 32-bit buffer records: each operand spans less than 2 GiB
-  if (M * ldg * 2 >= (int64_t(1) << 31) || wrows * ldw * 2 >= (int64_t(1) << 31))
-    return FDP_ERR_SHAPE;
+  if (!fdp::fits_record(M, ldg) || !fdp::fits_record(wrows, ldw)) return FDP_ERR_SHAPE;
   if (ldg % 8 != 0 || ldw % 8 != 0 || reinterpret_cast<uintptr_t>(g) % 16 != 0 ||
       reinterpret_cast<uintptr_t>(w) % 16 != 0 || reinterpret_cast<uintptr_t>(dx) % 2 != 0)
     return FDP_ERR_ALIGN;

@@ -19,6 +19,15 @@ typedef __attribute__((__vector_size__(4 * sizeof(unsigned)))) unsigned u32x4;
 
 constexpr int kWave = 64;
 
+// Whether `extra + rows * ld` 16-bit elements fit one 32-bit buffer record
+// (fewer than 2^31 bytes); every factor is bounded first, so the product
+// cannot overflow for any caller-supplied size.
+inline bool fits_record(int64_t rows, int64_t ld, int64_t extra = 0) {
+  constexpr int64_t lim = int64_t(1) << 30;  // elements of 2 bytes
+  return rows >= 0 && ld >= 0 && extra >= 0 && rows < lim && ld < lim && extra < lim &&
+         extra + rows * ld < lim;
+}
+
 // ---------------------------------------------------------------- dtype tags
 struct F32 {
   using storage = float;

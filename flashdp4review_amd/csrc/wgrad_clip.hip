@@ -628,7 +628,10 @@ int wgrad_clip_impl(const void* a, const void* b, int64_t B, int64_t K, int64_t 
   }
 
   hipError_t e;
-  if (layout == FDP_LAYOUT_TN && vec && dtype != FDP_F32 && K > 0) {
+  // the streamed kernels address a sample's operands through 32-bit buffer
+  // records; larger samples take the generic schedule (64-bit addressing)
+  if (layout == FDP_LAYOUT_TN && vec && dtype != FDP_F32 && K > 0 && fits_record(K, lda) &&
+      fits_record(K, ldb)) {
     args.group_out = pl.sp.sum_groups > 1 ? reinterpret_cast<float*>(ws + pl.off_group) : nullptr;
     e = dtype == FDP_BF16 ? launch_stream<BF16>(args, pl, noclip, C, clamp, clip_args_dev, norms,
                                                 factors, fac_ws, s)

@@ -1678,8 +1678,7 @@ inline host::ShapeCache<WorkMapKey, WorkMap>& work_map_cache() {
 template <class DT, int BOP = 0>
 hipError_t try_grouped(Args a, int cus, bool plain, bool clean, hipStream_t s) {
   const int tiles = a.tiles_m * a.tiles_n;
-  if (a.K * a.lda * 2 >= (int64_t(1) << 31) || a.K * a.ldb * 2 >= (int64_t(1) << 31))
-    return hipErrorNotSupported;
+  if (!fits_record(a.K, a.lda) || !fits_record(a.K, a.ldb)) return hipErrorNotSupported;
   const GroupPlan gp = group_plan(a.B, tiles, 2 * cus);
   if (gp.chunk == 0) return hipErrorNotSupported;
   KernelFn grouped[kGroupUnits] = {&wgrad_group_kernel<DT, 1, BOP>, &wgrad_group_kernel<DT, 2, BOP>,

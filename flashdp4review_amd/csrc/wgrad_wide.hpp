@@ -1304,12 +1304,12 @@ struct WidePlan {
 // inside one 32-bit buffer record ((sab + K * lda) * 2 bytes): checked here for
 // contiguous operands, by the caller for the strides of the call.
 inline bool pair_records_fit(int64_t K, int64_t ld, int64_t ds) {
-  return ds >= 0 && (ds + K * ld) * 2 < (int64_t(1) << 31);
+  return fits_record(K, ld, ds);
 }
 inline WidePlan wide_plan(int64_t B, int64_t K, int64_t M, int64_t N, int64_t lda, int64_t ldb,
                           int cus, double min_fill) {
   WidePlan w{};
-  if (K * lda * 2 >= (int64_t(1) << 31) || K * ldb * 2 >= (int64_t(1) << 31)) return w;
+  if (!fits_record(K, lda) || !fits_record(K, ldb)) return w;
   const double fill = double(M) * double(N) * double(B) / (double(cus) * 73728.0);
   if (fill < min_fill) return w;
   int64_t best_tiles = 0;

@@ -185,5 +185,8 @@ def test_dgrad_validation_codes():
     assert call(g=24) == 6            # 16-byte aligned operands
     assert call(g=None) == 3
     assert call(M=1 << 22, ldg=1 << 9) == 2  # g spans 2^32 bytes (32-bit buffer records)
+    # strides whose byte spans overflow 64-bit arithmetic are refused, not wrapped
+    assert call(M=2, ldg=1 << 62) == 2
+    assert call(ldw=1 << 62) == 2
     # 2^23 rows x 2^23 columns: g and w each 1 GiB, but about 2^31 output tiles
     assert call(M=1 << 23, N=1 << 23, K=64, ldw=1 << 23, ldo=1 << 23) == 2

@@ -283,6 +283,30 @@ def test_wgrad_stream_zero_factors():
     assert_elementwise(norms, norms_ref, torch.bfloat16, "norms")
 
 
+def test_wgrad_operand_rows_past_a_buffer_record():
+    """A sample operand whose rows span 4 GiB (the last 128 columns of
+    [8192, 262144] bf16 rows, lda = 2^18) is more than a 32-bit buffer record
+    addresses: the call takes the generic schedule (64-bit addressing) instead
+    of the single-pass or streamed kernels, and matches the oracle.  Clipping
+    is active (norm about 160 against C = 1)."""
+    K, M, N, W = 8192, 128, 64, 1 << 18
+    gen = torch.Generator().manual_seed(61)
+    big = torch.zeros(K, W, dtype=torch.bfloat16, device=DEV)
+    big[:, W - M:] = torch.randn(K, M, generator=gen).to(torch.bfloat16).to(DEV)
+    a = big[:, W - M:].unsqueeze(0)  # [1, K, M], lda = W
+    b = (torch.randn(1, K, N, generator=gen) * 0.02).to(torch.bfloat16).to(DEV)
+    assert a.stride(1) == W
+    ref, nref, fref = O.wgrad_clip(a.contiguous(), b, 1.0, 1.0, "tn")
+    assert float(fref.max()) < 0.1
+    for tp in (False, True):
+        out, n, f = core.wgrad_clip(a, b, 1.0, 1.0, out_dtype=torch.float32, two_pass=tp,
+                                    return_stats=True, check=True)
+        assert_close(out, ref, torch.bfloat16, f"4 GiB operand rows, two_pass={tp}")
+        assert_elementwise(n, nref, torch.bfloat16, "norms")
+        assert_elementwise(f, fref, torch.bfloat16, "factors")
+    del big
+
+
 def test_wgrad_workspace_reused_across_shapes():
     """Consecutive calls of different shapes share the cached per-stream workspace;
     each shape lays it out differently (one call's partial norms sit where the
