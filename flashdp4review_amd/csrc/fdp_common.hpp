@@ -20,12 +20,16 @@ typedef __attribute__((__vector_size__(4 * sizeof(unsigned)))) unsigned u32x4;
 constexpr int kWave = 64;
 
 // Whether `extra + rows * ld` 16-bit elements fit one 32-bit buffer record
-// (fewer than 2^31 bytes); every factor is bounded first, so the product
-// cannot overflow for any caller-supplied size.
+// (fewer than 2^31 bytes), with `rows` rounded up to 128, the deepest padding
+// of a sample's rows in any tile: the padding rows' byte offsets (rows * ld * 2
+// and up, which read as zeros past the record) then stay below 2^32 and cannot
+// wrap back into it.  Every factor is bounded first, so the products cannot
+// overflow for any caller-supplied size.
 inline bool fits_record(int64_t rows, int64_t ld, int64_t extra = 0) {
   constexpr int64_t lim = int64_t(1) << 30;  // elements of 2 bytes
-  return rows >= 0 && ld >= 0 && extra >= 0 && rows < lim && ld < lim && extra < lim &&
-         extra + rows * ld < lim;
+  if (rows < 0 || ld < 0 || extra < 0 || rows >= lim || ld >= lim || extra >= lim) return false;
+  const int64_t padded = (rows + 127) / 128 * 128;
+  return extra + padded * ld < lim;
 }
 
 // ---------------------------------------------------------------- dtype tags

@@ -307,6 +307,26 @@ def test_wgrad_operand_rows_past_a_buffer_record():
     del big
 
 
+def test_wgrad_padding_rows_never_wrap_into_a_record():
+    """K = 1 with a row stride of 2^29 elements: a 64-deep k-tile's padding rows
+    k = 1..63 lie k * 2^30 bytes on, and 32-bit offsets would wrap every fourth
+    one back to row 0 inside the operand's record.  Such a stride takes the
+    generic schedule, and the sum counts row 0 once."""
+    B, M, N, LD = 4, 256, 256, 1 << 29
+    gen = torch.Generator().manual_seed(62)
+    flat = torch.randn(B * M, generator=gen).to(torch.bfloat16).to(DEV)
+    a = flat.as_strided((B, 1, M), (M, LD, 1))
+    b = (torch.randn(B, 1, N, generator=gen) * 0.02).to(torch.bfloat16).to(DEV)
+    assert a.stride(1) == LD
+    ref, nref, fref = O.wgrad_clip(a.contiguous(), b, 0.05, 1.0, "tn")
+    for tp in (False, True):
+        out, n, f = core.wgrad_clip(a, b, 0.05, 1.0, out_dtype=torch.float32, two_pass=tp,
+                                    return_stats=True, check=True)
+        assert_close(out, ref, torch.bfloat16, f"K=1, lda=2^29, two_pass={tp}")
+        assert_elementwise(n, nref, torch.bfloat16, "norms")
+        assert_elementwise(f, fref, torch.bfloat16, "factors")
+
+
 def test_wgrad_workspace_reused_across_shapes():
     """Consecutive calls of different shapes share the cached per-stream workspace;
     each shape lays it out differently (one call's partial norms sit where the
