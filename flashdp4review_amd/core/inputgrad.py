@@ -87,7 +87,7 @@ def _takes(g2: torch.Tensor, w: torch.Tensor, K: int) -> bool:
     of 64, rows of 16-byte multiples on 16-byte aligned storage."""
     return (g2.dtype in (torch.float16, torch.bfloat16) and w.dtype == g2.dtype
             and g2.is_cuda and w.is_cuda and g2.device == w.device
-            and K >= 64 and K % 64 == 0
+            and K >= 64 and K % 64 == 0 and g2.shape[0] > 0 and w.numel() > 0
             and g2.stride(1) == 1 and g2.stride(0) % 8 == 0 and g2.data_ptr() % 16 == 0
             and w.stride(1) == 1 and w.stride(0) % 8 == 0 and w.data_ptr() % 16 == 0)
 
@@ -112,11 +112,15 @@ def dgrad(grad_output: torch.Tensor, weight: torch.Tensor, layout: str = "nn") -
         raise KeyError(f"weight dtype {weight.dtype} differs from grad_output's "
                        f"{grad_output.dtype}")
     g2 = grad_output.reshape(-1, K)
-    if g2.stride(1) != 1 or g2.stride(0) % 8 != 0 or g2.data_ptr() % 16 != 0:
-        g2 = g2.contiguous()
-    w = weight if weight.stride(1) == 1 and weight.stride(0) % 8 == 0 else weight.contiguous()
     M = g2.shape[0]
     out = torch.empty(M, N, dtype=grad_output.dtype, device=dev)
+    if M == 0 or N == 0:
+        return out.reshape(*grad_output.shape[:-1], N)
+    if g2.stride(1) != 1 or g2.stride(0) % 8 != 0 or g2.data_ptr() % 16 != 0:
+        g2 = g2.contiguous()
+    w = weight
+    if w.stride(1) != 1 or w.stride(0) % 8 != 0 or w.data_ptr() % 16 != 0:
+        w = w.contiguous()
     lay = LAYOUT_NN if layout == "nn" else LAYOUT_NT
     st = _lib.lib().fdp_dgrad(g2.data_ptr(), w.data_ptr(), out.data_ptr(), M, N, K,
                               g2.stride(0), w.stride(0), N, lay, dt, _lib.stream_handle(dev))

@@ -168,6 +168,24 @@ def test_dgrad_rejects_unsupported_operands():
     np.testing.assert_allclose(out.float().cpu().numpy(), ref_dx(g, w, "nn"), rtol=0, atol=2e-3)
 
 
+def test_dgrad_empty_batch_and_misaligned_weight():
+    """An empty batch gives an empty dX on either path (no launch); a weight
+    view whose storage is not 16-byte aligned is copied, not refused."""
+    g, w = make(512, 128, 264, torch.bfloat16, "nn", seed=7)
+    empty = g[:0].reshape(0, 1, 128)
+    assert core.dgrad(empty, w, "nn").shape == (0, 1, 264)
+    prev = core.set_dgrad("hip")
+    try:
+        assert core.input_grad(empty, w, "nn").shape == (0, 1, 264)
+    finally:
+        core.set_dgrad(prev)
+    wide = torch.zeros(128, 264 + 8, dtype=torch.bfloat16, device=DEV)
+    wide[:, 1:265] = w
+    wv = wide[:, 1:265]  # row stride 272, storage 2 bytes past a 16-byte boundary
+    assert wv.data_ptr() % 16 != 0
+    assert torch.equal(core.dgrad(g, wv, "nn"), call(g, w, "nn"))
+
+
 def test_dgrad_graph_replays_match_eager():
     """fdp_dgrad records one kernel and no memset, so a captured call replays
     exactly: three replays, with eager calls and synchronisations between
