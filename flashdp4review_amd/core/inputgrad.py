@@ -19,7 +19,8 @@ the path is chosen per shape (``set_dgrad``):
   "torch" torch's matmul (hipBLASLt) always;
   "hip"   the HIP kernel for every operand pair it takes.
 Operands the kernel does not take (fp32, K not a multiple of 64, unaligned
-rows) always use torch's matmul, as the reference does.
+rows, an operand of 2^30 elements or more) always use torch's matmul, as the
+reference does.
 """
 from __future__ import annotations
 
@@ -82,14 +83,22 @@ def _auto_choice(grad_output, weight, layout, M, N, K) -> str:
     return c
 
 
+def _fits_record(rows: int, ld: int) -> bool:
+    """The operand fits one 32-bit buffer record: rows rounded up to 128, times
+    the row stride, below 2^30 elements (fdp_dgrad's own check)."""
+    return (rows + 127) // 128 * 128 * ld < (1 << 30)
+
+
 def _takes(g2: torch.Tensor, w: torch.Tensor, K: int) -> bool:
     """Operands the kernel takes as they are: 16-bit, one device, K a multiple
-    of 64, rows of 16-byte multiples on 16-byte aligned storage."""
+    of 64, rows of 16-byte multiples on 16-byte aligned storage, each operand
+    within one 32-bit buffer record."""
     return (g2.dtype in (torch.float16, torch.bfloat16) and w.dtype == g2.dtype
             and g2.is_cuda and w.is_cuda and g2.device == w.device
             and K >= 64 and K % 64 == 0 and g2.shape[0] > 0 and w.numel() > 0
             and g2.stride(1) == 1 and g2.stride(0) % 8 == 0 and g2.data_ptr() % 16 == 0
-            and w.stride(1) == 1 and w.stride(0) % 8 == 0 and w.data_ptr() % 16 == 0)
+            and w.stride(1) == 1 and w.stride(0) % 8 == 0 and w.data_ptr() % 16 == 0
+            and _fits_record(g2.shape[0], g2.stride(0)) and _fits_record(w.shape[0], w.stride(0)))
 
 
 def dgrad(grad_output: torch.Tensor, weight: torch.Tensor, layout: str = "nn") -> torch.Tensor:

@@ -125,7 +125,10 @@ int fdp_version(void);
  *            stride_ab / stride_bb and row strides lda / ldb in elements
  *            (row = the contiguous dimension's parent: for TN, a row of a_b
  *            is one k; for NN, one m).  The innermost dimension must be
- *            contiguous.
+ *            contiguous.  The single-pass and streamed kernels address one
+ *            sample's operand through a 32-bit buffer record: a sample whose
+ *            K (rounded up to 128) times its row stride reaches 2^30 elements
+ *            takes the generic two-pass schedule (64-bit addressing) instead.
  * out      : [M, N] row-major with row stride ldo, dtype `out_dtype`.
  * noise    : NULL or [M, N] contiguous, dtype `out_dtype`.
  * noise_key: NULL, or the in-kernel draw used when `noise` is NULL.

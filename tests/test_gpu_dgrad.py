@@ -186,6 +186,22 @@ def test_dgrad_empty_batch_and_misaligned_weight():
     assert torch.equal(core.dgrad(g, wv, "nn"), call(g, w, "nn"))
 
 
+def test_input_grad_past_a_buffer_record_takes_torch():
+    """grad_output of 2^30 elements (2^24 rows of 64) is more than one of the
+    kernel's 32-bit buffer records addresses: fdp_dgrad refuses it, and the
+    layers' input gradient takes torch's matmul even in "hip" mode."""
+    g = torch.empty(1 << 24, 64, dtype=torch.bfloat16, device=DEV).normal_(0.0, 0.02)
+    w = (torch.randn(64, 64) * 0.02).to(torch.bfloat16).to(DEV)
+    with pytest.raises(ValueError):
+        core.dgrad(g, w, "nn")
+    prev = core.set_dgrad("hip")
+    try:
+        out = core.input_grad(g, w, "nn")
+    finally:
+        core.set_dgrad(prev)
+    assert torch.equal(out, g @ w)
+
+
 def test_dgrad_graph_replays_match_eager():
     """fdp_dgrad records one kernel and no memset, so a captured call replays
     exactly: three replays, with eager calls and synchronisations between
